@@ -1,0 +1,162 @@
+"""Fused-block latency on one MI355X, with its roofline fraction and the CPU path.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload NAME] [--no-cpu]
+                    [--blocks | --no-blocks]
+
+A step is one launch of the fused block over one batch of synthetic
+(seeded) inputs that are already resident in HBM.  W untimed steps, then K
+timed steps back to back on the launch stream, bracketed by a device
+synchronize on both sides; HIP events recorded on that same stream give the
+average device time per step.  The JSON line's ``value`` is that latency in
+microseconds (lower is better).
+
+``roofline`` relates the algorithmic work of one launch (compulsory HBM
+bytes, or MFMA FLOPs, of the fused block) to the measured launch duration and
+the MI355X published peak.  ``cpu_baseline`` times the CPU restatement of the
+reference's execution path (the oracle: unfused scalar loop nests, one
+thread) on a bounded sample of the same workload on this host.  ``blocks``
+repeats the GPU measurement for every other configuration.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "npu-dialect_amd"))
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--workload", default=None)
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--blocks", dest="blocks", action="store_true", default=True)
+    ap.add_argument("--no-blocks", dest="blocks", action="store_false")
+    return ap.parse_args()
+
+
+def time_gpu(w, steps, warmup):
+    """Returns (avg seconds per launch from HIP events, wall seconds, outputs)."""
+    import torch
+
+    from npu_amd import configs
+    d = configs.to_device(w.make_inputs())
+    o = w.make_outputs(d)
+    stream = torch.cuda.current_stream()
+    for _ in range(warmup):
+        w.run(d, o, stream)
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    start.record(stream)
+    for _ in range(steps):
+        w.run(d, o, stream)
+    end.record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    return start.elapsed_time(end) * 1e-3 / steps, wall, o
+
+
+def cpu_sample(w, budget_s=30.0):
+    """Times the oracle on a bounded sample; returns the cpu_baseline object.
+
+    Batched workloads time one image first; if the whole batch is estimated
+    to fit the budget it is timed in full, otherwise as many images as fit,
+    scaled to the batch (images are independent)."""
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import refs
+
+    inp = w.make_inputs()
+    n = w.units
+    if w.unit_name == "images" and n > 1:
+        t0 = time.perf_counter()
+        refs.run_oracle(w.name, inp, images=[0])
+        one = time.perf_counter() - t0
+        k = max(1, min(n, int(budget_s / max(one, 1e-6))))
+        imgs = list(range(k))
+    else:
+        k, imgs = n, None
+    t0 = time.perf_counter()
+    refs.run_oracle(w.name, inp, images=imgs)
+    dt = time.perf_counter() - t0
+    if imgs is not None and k < n:
+        sample = f"{k} of {n} images (images are independent), scaled x{n / k:g}"
+        dt *= n / k
+    else:
+        sample = "the full workload"
+    return {"value": dt * 1e6, "unit": "us", "cores": 1, "kind": "port",
+            "sample": sample + "; unfused scalar loop nests, -O2 -ffp-contract=off, 1 thread",
+            "host": host_cpu()}
+
+
+def host_cpu():
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return f"{line.split(':', 1)[1].strip()} ({os.cpu_count()} logical CPUs visible)"
+    except OSError:
+        pass
+    return f"{os.cpu_count()} logical CPUs"
+
+
+def main():
+    args = parse()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one GPU only: the fused blocks are single-GPU kernels and "
+              "this build has no multi-GPU path (run with --gpus 1)", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+
+    from npu_amd import configs
+    import npu_amd
+    npu_amd.lib()  # fail loudly if the HIP library is missing
+    torch.cuda.set_device(0)
+
+    name = args.workload or configs.HEADLINE
+    w = configs.by_name(name)
+    sec, wall, _ = time_gpu(w, args.steps, args.warmup)
+    line = {
+        "metric": "fused-block latency",
+        "value": round(sec * 1e6, 3),
+        "unit": "us",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": sec * 1e3,
+        "higher_is_better": False,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": w.dtype,
+        "data": "synthetic: SplitMix64-seeded inputs, distributions of the configuration",
+        "config": {"workload": w.name, "desc": w.desc, "batch": w.units,
+                   "parallelism": "single GPU"},
+        "throughput": {"value": w.units / sec, "unit": f"{w.unit_name}/s"},
+        "wall_s_timed_region": wall,
+        "roofline": dict(w.roofline(sec), traffic=None,
+                         flops=w.flops, bytes=w.bytes, floor_us=w.floor_s() * 1e6),
+    }
+    if not args.no_cpu:
+        line["cpu_baseline"] = cpu_sample(w)
+    if args.blocks:
+        blocks = []
+        for other in configs.all_workloads():
+            if other.name == w.name:
+                continue
+            s, _, _ = time_gpu(other, max(20, args.steps // 2), max(5, args.warmup // 2))
+            rl = other.roofline(s)
+            blocks.append({"workload": other.name, "latency_us": round(s * 1e6, 3),
+                           "bound": rl["bound"], "frac": round(rl["frac"], 4),
+                           "floor_us": round(other.floor_s() * 1e6, 3)})
+        line["blocks"] = blocks
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,121 @@
+/*
+ * npu_amd.h -- C-ABI of the MI355X (gfx950) execution backend for the fused
+ * tile groups produced by NPU-Dialect's npu-fusion / npu-outline-fused-groups
+ * / npu-spatial-tiling / npu-temporal-tiling / npu-bufferize pipeline.
+ *
+ * The unit of execution is one outlined group, i.e. one
+ *   func.func private @fused_<ops>_<idx>(ext inputs...) -> (ext outputs...)
+ *       attributes {npu.fused_kernel}
+ * (lib/Transforms/OutlineFusedGroupsPass.cpp:259-283) together with the
+ * spatial / temporal tile loops wrapped around its func.call
+ * (lib/Transforms/FusionPass.cpp:330-357, SpatialTilingPass.cpp:146-166,
+ * OutlineFusedGroupsPass.cpp:306-316).  One call here replaces the whole
+ * tile-loop nest: the loop bounds become the launch grid.
+ *
+ * Conventions (all entry points):
+ *  - Buffers are device pointers in HBM, owned by the caller
+ *    (destination-passing style, as linalg's `outs`, test/matmul_relu.mlir:10-11;
+ *    the caller allocates, tools/harness/e2e_verify.py:195-203).  The library
+ *    never frees caller memory.
+ *  - Every call is asynchronous on the caller's HIP stream (`npu_stream` is a
+ *    hipStream_t; NULL = the null stream).  Launches on distinct streams may
+ *    run concurrently; the library keeps no per-call device state.
+ *  - Errors are returned as npu_status; nothing throws across the ABI.  Shape,
+ *    dtype and layout mismatches are rejected before any launch, and
+ *    npu_last_error() (thread-local) says why.
+ *  - No entry point allocates device memory.
+ */
+#ifndef NPU_AMD_H
+#define NPU_AMD_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---------------------------------------------------------------------- */
+/* Status codes.  Replace the reference's diagnostics / exit codes
+ * (lib/Transforms/BufferizePass.cpp:63-65, tools/npu-opt/npu-opt.cpp:65-66). */
+typedef int32_t npu_status;
+#define NPU_OK 0
+#define NPU_ERR_INVALID_ARG 1  /* null pointer, bad rank/shape/dtype       */
+#define NPU_ERR_UNSUPPORTED 2  /* valid linalg, not handled by a kernel     */
+#define NPU_ERR_HIP 3          /* a HIP runtime call failed                 */
+#define NPU_ERR_OOM 4          /* reserved: no entry point allocates        */
+
+typedef void *npu_stream; /* hipStream_t */
+
+/* Element types of memref descriptors. */
+#define NPU_F32 0
+#define NPU_BF16 1
+#define NPU_I8 2
+#define NPU_I32 3
+
+#define NPU_MAX_RANK 4
+
+/* Strided memref descriptor: the field order of MLIR's ranked memref C
+ * interface ({allocated, aligned, offset, sizes[R], strides[R]}, which the
+ * reference harness relies on through llvm.emit_c_interface,
+ * tools/harness/e2e_verify.py:221), at a fixed maximum rank, followed by the
+ * rank and element type.  Offsets and strides are in elements.  Kernels
+ * require the row-major contiguous layout of their operand; other layouts are
+ * rejected with NPU_ERR_UNSUPPORTED. */
+typedef struct npu_memref {
+  void *allocated;
+  void *aligned;
+  int64_t offset;
+  int64_t sizes[NPU_MAX_RANK];
+  int64_t strides[NPU_MAX_RANK];
+  int32_t rank;
+  int32_t dtype;
+} npu_memref;
+
+/* Epilogue activation of a `linalg.generic` consumer. */
+#define NPU_ACT_NONE 0
+#define NPU_ACT_RELU 1  /* arith.maximumf(x, 0), test/matmul_relu.mlir:15-25 */
+#define NPU_ACT_RELU6 2 /* minimumf(maximumf(x, 0), 6)                        */
+
+/* ---------------------------------------------------------------------- */
+/* Library information and errors. */
+const char *npu_version(void);
+const char *npu_last_error(void);
+const char *npu_status_string(npu_status s);
+/* Number of visible HIP devices (0 when none), or -1 when the runtime fails. */
+int32_t npu_device_count(void);
+
+/* ---------------------------------------------------------------------- */
+/* Fused-group entry points.  Each names the op chain of the outlined group it
+ * replaces; the outliner's own symbol is `fused_` + the short op names +
+ * `_<idx>` (OutlineFusedGroupsPass.cpp:69-82, 259-263).  The mapping from
+ * outlined chains to these entry points is the group classifier of the
+ * host lowering. */
+
+/* Group `fill -> matmul -> generic(bias add, act)`
+ * (test/matmul_relu.mlir:6-28 plus a broadcast bias; outlined as
+ * @fused_fill_matmul_generic_<idx> after elementwise fusion,
+ * FusionPass.cpp:458-499).
+ *   A    f32 [M,K]      B f32 [K,N]      bias f32 [N] (aligned may be NULL: no bias)
+ *   out  f32 [M,N] = act(A @ B + bias)
+ * Requires K % 4 == 0. */
+npu_status fused_matmul_bias_act(const npu_memref *A, const npu_memref *B,
+                                 const npu_memref *bias, const npu_memref *out,
+                                 int32_t act, npu_stream stream);
+
+/* Group `pad -> fill -> conv_2d_nhwc_fhwc -> generic(bias add, act)`
+ * (NHWC restatement of test/conv2d_relu.mlir:7-42; the zero pad is folded
+ * into predicated halo loads instead of a materialised tensor.pad).
+ *   x    [N,H,W,C]  f32 or bf16      w [F,KH,KW,C] same dtype
+ *   bias f32 [F] (aligned may be NULL)
+ *   out  [N,Ho,Wo,F] same dtype as x (bf16: fp32 accumulate, one rounding)
+ * Stride 1, symmetric zero padding `pad`; Ho = H + 2*pad - KH + 1.
+ * Requires C % 16 == 0 (f32) / C % 32 == 0 (bf16) and F % 16 == 0. */
+npu_status fused_conv2d_nhwc_bias_act(const npu_memref *x, const npu_memref *w,
+                                      const npu_memref *bias,
+                                      const npu_memref *out, int32_t pad,
+                                      int32_t act, npu_stream stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* NPU_AMD_H */

@@ -1,0 +1,88 @@
+// k_matmul.hip -- group `fill -> matmul -> generic(bias, act)` in f32.
+//
+// Replaces the tile loops the reference wraps around the outlined call
+// (FusionPass.cpp:306-359 tile-and-fuse of the consumer generic, then
+// OutlineFusedGroupsPass.cpp:306-316): one launch covers the whole output.
+//
+// Decomposition.  The matmul+bias+ReLU shape (256x512 . 512x256) has only
+// 256 output tiles of 16x16, one per CU, so each workgroup owns one 16x16
+// tile and splits K across its 4 waves (split-K inside the workgroup; the
+// reference's analogue is a K split with a reduce penalty,
+// CostModel.cpp:798-812).  Each wave runs v_mfma_f32_16x16x4_f32 over its K
+// share, the partial tiles meet in LDS, and the epilogue (bias add, act) is
+// applied once while the tile is in registers: the matmul result never
+// reaches HBM.
+#include "kernels.hpp"
+#include "npu_device.hpp"
+
+namespace npu {
+
+namespace {
+
+constexpr int kWaves = 4;
+constexpr int kBatch = 4;  // K chunks whose loads are issued before their MFMAs
+
+__global__ __launch_bounds__(kWaves * 64) void matmul_bias_act_f32_kernel(
+    const float *__restrict__ A, const float *__restrict__ B,
+    const float *__restrict__ bias, float *__restrict__ out, int M, int N, int K,
+    int act) {
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int r = lane & 15, q = lane >> 4;
+  const int m0 = blockIdx.y * 16, n0 = blockIdx.x * 16;
+  const int arow = m0 + r, bcol = n0 + r;
+  const bool arow_ok = arow < M, bcol_ok = bcol < N;
+
+  // K is walked in chunks of 16 (four MFMA k-steps); waves take contiguous
+  // chunk ranges.
+  const int nchunks = (K + 15) >> 4;
+  const int c_begin = (wave * nchunks) / kWaves;
+  const int c_end = ((wave + 1) * nchunks) / kWaves;
+
+  f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+  for (int c = c_begin; c < c_end; c += kBatch) {
+    Frag16 a[kBatch], b[kBatch];
+#pragma unroll
+    for (int t = 0; t < kBatch; ++t) {
+      a[t] = frag_zero();
+      b[t] = frag_zero();
+      const int k = (c + t) * 16 + 4 * q;  // K % 4 == 0: the run is all in or all out
+      if (c + t < c_end && k < K) {
+        if (arow_ok) a[t] = load16(A + (size_t)arow * K + k);
+        if (bcol_ok) {
+#pragma unroll
+          for (int s = 0; s < 4; ++s) b[t].f[s] = B[(size_t)(k + s) * N + bcol];
+        }
+      }
+    }
+#pragma unroll
+    for (int t = 0; t < kBatch; ++t) MfmaF32::mma(acc, a[t], b[t]);
+  }
+
+  // Split-K reduction through LDS, then the fused epilogue.
+  __shared__ float red[kWaves][256];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) red[wave][(4 * q + i) * 16 + r] = acc[i];
+  __syncthreads();
+  for (int e = threadIdx.x; e < 256; e += blockDim.x) {
+    float s = red[0][e];
+#pragma unroll
+    for (int w = 1; w < kWaves; ++w) s += red[w][e];
+    const int row = m0 + (e >> 4), col = n0 + (e & 15);
+    if (row < M && col < N) {
+      if (bias) s += bias[col];
+      out[(size_t)row * N + col] = act_apply(s, act);
+    }
+  }
+}
+
+}  // namespace
+
+hipError_t launch_matmul_bias_act_f32(const MatmulArgs &a, hipStream_t s) {
+  dim3 grid((a.N + 15) / 16, (a.M + 15) / 16);
+  hipLaunchKernelGGL(matmul_bias_act_f32_kernel, grid, dim3(kWaves * 64), 0, s, a.A,
+                     a.B, a.bias, a.out, a.M, a.N, a.K, a.act);
+  return hipGetLastError();
+}
+
+}  // namespace npu

@@ -1,0 +1,68 @@
+"""Loads libnpu_amd.so (the HIP kernels and their extern "C" ABI) with ctypes.
+
+The library is built in-tree by ``make -C npu-dialect_amd``; there is no
+fallback.  If the shared object is missing or lacks a symbol the headers
+declare, loading fails with an error naming the file, so a GPU run can never
+silently execute anything but the HIP path.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+import subprocess
+
+PKG_DIR = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(PKG_DIR, "libnpu_amd.so")
+SRC_DIR = os.path.dirname(PKG_DIR)
+
+# Every extern "C" symbol of include/npu_amd.h, with its ctypes signature.
+_I32, _I64, _P = C.c_int32, C.c_int64, C.c_void_p
+
+
+class NpuMemref(C.Structure):
+    """npu_memref: {allocated, aligned, offset, sizes[4], strides[4], rank, dtype}."""
+
+    _fields_ = [
+        ("allocated", C.c_void_p),
+        ("aligned", C.c_void_p),
+        ("offset", C.c_int64),
+        ("sizes", C.c_int64 * 4),
+        ("strides", C.c_int64 * 4),
+        ("rank", C.c_int32),
+        ("dtype", C.c_int32),
+    ]
+
+
+_MR = C.POINTER(NpuMemref)
+
+SIGNATURES = {
+    "npu_version": (C.c_char_p, []),
+    "npu_last_error": (C.c_char_p, []),
+    "npu_status_string": (C.c_char_p, [_I32]),
+    "npu_device_count": (_I32, []),
+    "fused_matmul_bias_act": (_I32, [_MR, _MR, _MR, _MR, _I32, _P]),
+    "fused_conv2d_nhwc_bias_act": (_I32, [_MR, _MR, _MR, _MR, _I32, _I32, _P]),
+}
+
+_lib = None
+
+
+def build() -> None:
+    """Compile every HIP source for gfx950 into libnpu_amd.so (always rebuilds)."""
+    subprocess.run(["make", "-s", "-B", "-j8", "-C", SRC_DIR], check=True)
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise RuntimeError(
+                f"libnpu_amd.so not found at {LIB_PATH}: build it with `make -C {SRC_DIR}` "
+                "(the HIP path has no fallback)")
+        handle = C.CDLL(LIB_PATH)
+        for name, (res, args) in SIGNATURES.items():
+            fn = getattr(handle, name)  # AttributeError names a missing export
+            fn.restype = res
+            fn.argtypes = args
+        _lib = handle
+    return _lib

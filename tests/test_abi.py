@@ -1,0 +1,97 @@
+"""The C-ABI library loads and exports every symbol include/*.h declares, and
+rejects bad descriptors with a status before any launch (CPU-only: these
+calls return before touching the GPU)."""
+import ctypes as C
+import glob
+import os
+import re
+
+import pytest
+
+import npu_amd
+from npu_amd import _lib
+from npu_amd.memref import BF16, F32, I8
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def declared_functions():
+    names = set()
+    for h in glob.glob(os.path.join(ROOT, "include", "*.h")):
+        text = open(h).read()
+        text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+        for m in re.finditer(r"^\s*[A-Za-z_][\w\s\*]*?\b([a-z_][a-z0-9_]*)\s*\(", text, re.M):
+            if m.group(1) not in ("if", "return", "sizeof"):
+                names.add(m.group(1))
+    return names
+
+
+def test_header_declares_entry_points():
+    names = declared_functions()
+    assert {"fused_matmul_bias_act", "fused_conv2d_nhwc_bias_act", "npu_last_error"} <= names
+
+
+def test_library_exports_every_declared_symbol():
+    lib = npu_amd.lib()
+    missing = [n for n in sorted(declared_functions()) if not hasattr(lib, n)]
+    assert not missing, f"declared in include/ but not exported: {missing}"
+    assert set(_lib.SIGNATURES) == declared_functions()
+
+
+def test_version_and_status_strings():
+    lib = npu_amd.lib()
+    assert b"gfx950" in lib.npu_version()
+    assert lib.npu_status_string(0) == b"ok"
+    assert lib.npu_status_string(2) == b"unsupported"
+
+
+def _mr(shape, dtype=F32, ptr=0x10000, strides=None):
+    m = _lib.NpuMemref()
+    m.allocated = m.aligned = ptr
+    m.offset = 0
+    st = strides or [int(__import__("numpy").prod(shape[i + 1:])) for i in range(len(shape))]
+    for i, (s, t) in enumerate(zip(shape, st)):
+        m.sizes[i], m.strides[i] = s, t
+    m.rank, m.dtype = len(shape), dtype
+    return m
+
+
+def _err():
+    return npu_amd.lib().npu_last_error().decode()
+
+
+def test_matmul_rejects_bad_descriptors():
+    lib = npu_amd.lib()
+    A, B, b, o = _mr([8, 16]), _mr([16, 4]), _mr([4]), _mr([8, 4])
+    call = lambda *a: lib.fused_matmul_bias_act(*[C.byref(x) if x is not None else None for x in a[:4]], a[4], None)
+    assert call(None, B, b, o, 1) == 1 and "A" in _err()
+    assert call(A, _mr([15, 4]), b, o, 1) == 1 and "expected K" in _err()
+    assert call(A, B, b, _mr([8, 5]), 1) == 1 and "out" in _err()
+    assert call(A, B, _mr([5]), o, 1) == 1 and "bias" in _err()
+    assert call(A, _mr([16, 4], BF16), b, o, 1) == 1 and "dtype" in _err()
+    assert call(A, B, b, o, 7) == 1 and "act" in _err()
+    assert call(_mr([8, 6]), _mr([6, 4]), b, o, 1) == 2 and "multiple of 4" in _err()
+    assert call(A, _mr([16, 4], strides=[1, 16]), b, o, 1) == 2 and "contiguous" in _err()
+    assert call(_mr([8, 16], ptr=0x10004), B, b, o, 1) == 2 and "aligned" in _err()
+
+
+def test_conv_rejects_bad_descriptors():
+    lib = npu_amd.lib()
+    x, w, b, o = _mr([1, 8, 8, 16]), _mr([16, 3, 3, 16]), _mr([16]), _mr([1, 8, 8, 16])
+    call = lambda x_, w_, b_, o_, pad=1, act=1: lib.fused_conv2d_nhwc_bias_act(
+        C.byref(x_), C.byref(w_), C.byref(b_), C.byref(o_), pad, act, None)
+    assert call(x, w, b, _mr([1, 7, 8, 16])) == 1 and "out" in _err()
+    assert call(x, _mr([16, 3, 3, 8]), b, o) == 1 and "channels" in _err()
+    assert call(_mr([1, 8, 8, 16], I8), w, b, o) == 2 and "f32 or bf16" in _err()
+    assert call(_mr([1, 8, 8, 24]), _mr([16, 3, 3, 24]), b, o) == 2 and "multiple of 16" in _err()
+    assert call(x, _mr([8, 3, 3, 16]), _mr([8]), _mr([1, 8, 8, 8])) == 2 and "F = 8" in _err()
+    assert call(x, w, b, o, pad=-1) == 1 and "negative" in _err()
+    xb = _mr([1, 8, 8, 16], BF16)
+    assert call(xb, _mr([16, 3, 3, 16], BF16), b, _mr([1, 8, 8, 16], BF16)) == 2 and "32" in _err()
+
+
+def test_python_mirror_raises_with_library_message():
+    torch = pytest.importorskip("torch")
+    A = torch.zeros(4, 6)  # host tensors: validation fails before any launch
+    with pytest.raises(npu_amd.NpuError, match="multiple of 4"):
+        npu_amd.fused_matmul_bias_act(A, torch.zeros(6, 4), None, torch.zeros(4, 4), "relu", 0)
