@@ -115,6 +115,73 @@ npu_status fused_conv2d_nhwc_bias_act(const npu_memref *x, const npu_memref *w,
                                       const npu_memref *out, int32_t pad,
                                       int32_t act, npu_stream stream);
 
+/* Group chain of the int8 ResNet-50 bottleneck (int8 restatement of
+ * test/resnet50_block.mlir:5-105, NHWC, zero points 0), fused across both
+ * tensor.pads into one launch:
+ *   y1  = clamp(apply_scale(conv1x1(x, w1), m1, s1), 0, 127)
+ *   y2  = clamp(apply_scale(conv3x3(pad1(y1), w2), m2, s2), 0, 127)
+ *   out = clamp(apply_scale(conv1x1(y2, w3), m3, s3) + x, 0, 127)
+ * apply_scale is TOSA apply_scale_32 with single rounding:
+ *   (int64(acc) * m + (1 << (s - 1))) >> s, per output channel.
+ *   x i8 [N,H,W,C]; w1 i8 [M1,C]; w2 i8 [M1,3,3,M1]; w3 i8 [C,M1];
+ *   m1,s1,m2,s2 i32 [M1]; m3,s3 i32 [C]; out i8 [N,H,W,C].
+ * Supported (C, M1): (256,64), (128,64), (64,64).  Precondition (TOSA):
+ * every shift is in [2, 62]. */
+npu_status fused_qbottleneck_i8(const npu_memref *x, const npu_memref *w1,
+                                const npu_memref *w2, const npu_memref *w3,
+                                const npu_memref *m1, const npu_memref *s1,
+                                const npu_memref *m2, const npu_memref *s2,
+                                const npu_memref *m3, const npu_memref *s3,
+                                const npu_memref *out, npu_stream stream);
+
+/* Group chain of the MobileNetV2 inverted residual block (NHWC restatement
+ * of test/mobilenet_block.mlir:8-94 with a true depthwise stage), fused
+ * across the tensor.pad into one launch, f32:
+ *   e   = relu6(conv1x1(x, we))
+ *   d   = relu6(depthwise_conv_2d_nhwc_hwc(pad1(e), wdw))
+ *   out = conv1x1(d, wp) + x
+ *   x f32 [N,H,W,C]; we f32 [E,C]; wdw f32 [3,3,E]; wp f32 [C,E];
+ *   out f32 [N,H,W,C].
+ * Supported (C, E): (24,144), (16,96), (32,192). */
+npu_status fused_irb_f32(const npu_memref *x, const npu_memref *we,
+                         const npu_memref *wdw, const npu_memref *wp,
+                         const npu_memref *out, npu_stream stream);
+
+/* Groups of one Llama decoder layer (bf16 storage, f32 accumulation and
+ * elementwise math; bf16 rounding at each group output and at the
+ * normalised matmul inputs).  The reference's llama_attention.mlir:5-67
+ * replaces softmax by ReLU and has no RMSNorm, RoPE or gating; these groups
+ * implement the real layer.  Row-major [S, D] activations, D = H * 64,
+ * weights [K, N] as linalg.matmul takes them.  Requires S % 64 == 0 for the
+ * matmul groups, K % 32 == 0 and N % 64 == 0.
+ *
+ * QKV: xn = bf16(rmsnorm(x) * g1) with inv = 1/sqrt(mean(x^2) + eps);
+ *      Q = bf16(rope(xn @ wq)), K = bf16(rope(xn @ wk)), V = bf16(xn @ wv).
+ *      RoPE rotates interleaved pairs (2t, 2t+1) of each 64-wide head by the
+ *      tables cos_t / sin_t f32 [S, 32]. */
+npu_status fused_llama_qkv_rope(const npu_memref *x, const npu_memref *g1,
+                                const npu_memref *wq, const npu_memref *wk,
+                                const npu_memref *wv, const npu_memref *cos_t,
+                                const npu_memref *sin_t, const npu_memref *Q,
+                                const npu_memref *K, const npu_memref *V,
+                                float eps, npu_stream stream);
+/* Causal attention per head (head dim 64): A = bf16(softmax(Q K^T * scale
+ * with keys j <= i) @ V).  Q, K, V, A bf16 [S, H*64]. */
+npu_status fused_llama_attention(const npu_memref *Q, const npu_memref *K,
+                                 const npu_memref *V, const npu_memref *A,
+                                 int32_t n_heads, float scale,
+                                 npu_stream stream);
+/* out = bf16(res + a @ w); a [S, K], w [K, N], res and out [S, N]. */
+npu_status fused_llama_matmul_residual(const npu_memref *a, const npu_memref *w,
+                                       const npu_memref *res,
+                                       const npu_memref *out, npu_stream stream);
+/* hn = bf16(rmsnorm(h) * g2); act = bf16(silu(hn @ wg) * (hn @ wu));
+ * h [S, D], wg / wu [D, F], act [S, F]. */
+npu_status fused_llama_rmsnorm_swiglu(const npu_memref *h, const npu_memref *g2,
+                                      const npu_memref *wg, const npu_memref *wu,
+                                      const npu_memref *act, float eps,
+                                      npu_stream stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -209,4 +209,237 @@ npu_status fused_conv2d_nhwc_bias_act(const npu_memref *x, const npu_memref *w,
   return hip_status(e, "fused_conv2d_nhwc_bias_act launch");
 }
 
+npu_status fused_qbottleneck_i8(const npu_memref *x, const npu_memref *w1,
+                                const npu_memref *w2, const npu_memref *w3,
+                                const npu_memref *m1, const npu_memref *s1,
+                                const npu_memref *m2, const npu_memref *s2,
+                                const npu_memref *m3, const npu_memref *s3,
+                                const npu_memref *out, npu_stream stream) {
+  const void *px, *pw1, *pw2, *pw3, *pm1, *ps1, *pm2, *ps2, *pm3, *ps3, *po;
+  NPU_TRY(check_memref(x, "x", 4, NPU_I8, &px));
+  const int64_t N = x->sizes[0], H = x->sizes[1], W = x->sizes[2], C = x->sizes[3];
+  NPU_TRY(check_memref(w1, "w1", 2, NPU_I8, &pw1));
+  const int64_t M1 = w1->sizes[0];
+  if (w1->sizes[1] != C)
+    return fail(NPU_ERR_INVALID_ARG, "w1: [%lld,%lld], expected [M1,%lld]",
+                (long long)w1->sizes[0], (long long)w1->sizes[1], (long long)C);
+  NPU_TRY(check_memref(w2, "w2", 4, NPU_I8, &pw2));
+  if (w2->sizes[0] != M1 || w2->sizes[1] != 3 || w2->sizes[2] != 3 || w2->sizes[3] != M1)
+    return fail(NPU_ERR_INVALID_ARG, "w2: expected [%lld,3,3,%lld]", (long long)M1,
+                (long long)M1);
+  NPU_TRY(check_memref(w3, "w3", 2, NPU_I8, &pw3));
+  if (w3->sizes[0] != C || w3->sizes[1] != M1)
+    return fail(NPU_ERR_INVALID_ARG, "w3: expected [%lld,%lld]", (long long)C, (long long)M1);
+  const npu_memref *qm[6] = {m1, s1, m2, s2, m3, s3};
+  const char *qn[6] = {"m1", "s1", "m2", "s2", "m3", "s3"};
+  const void **qp[6] = {&pm1, &ps1, &pm2, &ps2, &pm3, &ps3};
+  for (int i = 0; i < 6; ++i) {
+    NPU_TRY(check_memref(qm[i], qn[i], 1, NPU_I32, qp[i]));
+    const int64_t want = i < 4 ? M1 : C;
+    if (qm[i]->sizes[0] != want)
+      return fail(NPU_ERR_INVALID_ARG, "%s: size %lld, expected %lld", qn[i],
+                  (long long)qm[i]->sizes[0], (long long)want);
+  }
+  NPU_TRY(check_memref(out, "out", 4, NPU_I8, &po));
+  for (int d = 0; d < 4; ++d)
+    if (out->sizes[d] != x->sizes[d])
+      return fail(NPU_ERR_INVALID_ARG, "out: size[%d] = %lld, expected %lld", d,
+                  (long long)out->sizes[d], (long long)x->sizes[d]);
+  if (!npu::qbottleneck_supported((int)C, (int)M1))
+    return fail(NPU_ERR_UNSUPPORTED, "(C, M1) = (%lld, %lld) has no kernel instance",
+                (long long)C, (long long)M1);
+  npu::QBottleneckArgs a{static_cast<const int8_t *>(px), static_cast<const int8_t *>(pw1),
+                         static_cast<const int8_t *>(pw2), static_cast<const int8_t *>(pw3),
+                         static_cast<const int32_t *>(pm1), static_cast<const int32_t *>(ps1),
+                         static_cast<const int32_t *>(pm2), static_cast<const int32_t *>(ps2),
+                         static_cast<const int32_t *>(pm3), static_cast<const int32_t *>(ps3),
+                         const_cast<int8_t *>(static_cast<const int8_t *>(po)),
+                         (int)N, (int)H, (int)W, (int)C, (int)M1};
+  return hip_status(npu::launch_qbottleneck_i8(a, static_cast<hipStream_t>(stream)),
+                    "fused_qbottleneck_i8 launch");
+}
+
+npu_status fused_irb_f32(const npu_memref *x, const npu_memref *we, const npu_memref *wdw,
+                         const npu_memref *wp, const npu_memref *out, npu_stream stream) {
+  const void *px, *pwe, *pwdw, *pwp, *po;
+  NPU_TRY(check_memref(x, "x", 4, NPU_F32, &px));
+  const int64_t N = x->sizes[0], H = x->sizes[1], W = x->sizes[2], C = x->sizes[3];
+  NPU_TRY(check_memref(we, "we", 2, NPU_F32, &pwe));
+  const int64_t E = we->sizes[0];
+  if (we->sizes[1] != C)
+    return fail(NPU_ERR_INVALID_ARG, "we: [%lld,%lld], expected [E,%lld]",
+                (long long)we->sizes[0], (long long)we->sizes[1], (long long)C);
+  NPU_TRY(check_memref(wdw, "wdw", 3, NPU_F32, &pwdw));
+  if (wdw->sizes[0] != 3 || wdw->sizes[1] != 3 || wdw->sizes[2] != E)
+    return fail(NPU_ERR_INVALID_ARG, "wdw: expected [3,3,%lld]", (long long)E);
+  NPU_TRY(check_memref(wp, "wp", 2, NPU_F32, &pwp));
+  if (wp->sizes[0] != C || wp->sizes[1] != E)
+    return fail(NPU_ERR_INVALID_ARG, "wp: expected [%lld,%lld]", (long long)C, (long long)E);
+  NPU_TRY(check_memref(out, "out", 4, NPU_F32, &po));
+  for (int d = 0; d < 4; ++d)
+    if (out->sizes[d] != x->sizes[d])
+      return fail(NPU_ERR_INVALID_ARG, "out: size[%d] = %lld, expected %lld", d,
+                  (long long)out->sizes[d], (long long)x->sizes[d]);
+  if (!npu::irb_supported((int)C, (int)E))
+    return fail(NPU_ERR_UNSUPPORTED, "(C, E) = (%lld, %lld) has no kernel instance",
+                (long long)C, (long long)E);
+  npu::IrbArgs a{static_cast<const float *>(px), static_cast<const float *>(pwe),
+                 static_cast<const float *>(pwdw), static_cast<const float *>(pwp),
+                 const_cast<float *>(static_cast<const float *>(po)), (int)N, (int)H, (int)W,
+                 (int)C, (int)E};
+  return hip_status(npu::launch_irb_f32(a, static_cast<hipStream_t>(stream)),
+                    "fused_irb_f32 launch");
+}
+
+}  // extern "C"
+
+namespace {
+
+// A 2-D operand of exactly [d0, d1].
+npu_status check_2d(const npu_memref *m, const char *name, int32_t dtype, int64_t d0, int64_t d1,
+                    const void **ptr) {
+  NPU_TRY(check_memref(m, name, 2, dtype, ptr));
+  if (m->sizes[0] != d0 || m->sizes[1] != d1)
+    return fail(NPU_ERR_INVALID_ARG, "%s: [%lld,%lld], expected [%lld,%lld]", name,
+                (long long)m->sizes[0], (long long)m->sizes[1], (long long)d0, (long long)d1);
+  return NPU_OK;
+}
+
+npu_status check_1d(const npu_memref *m, const char *name, int32_t dtype, int64_t d0,
+                    const void **ptr) {
+  NPU_TRY(check_memref(m, name, 1, dtype, ptr));
+  if (m->sizes[0] != d0)
+    return fail(NPU_ERR_INVALID_ARG, "%s: size %lld, expected %lld", name,
+                (long long)m->sizes[0], (long long)d0);
+  return NPU_OK;
+}
+
+npu_status check_gemm_dims(int64_t S, int64_t K, int64_t N) {
+  if (S % 64 != 0) return fail(NPU_ERR_UNSUPPORTED, "S = %lld must be a multiple of 64", (long long)S);
+  if (K % 32 != 0) return fail(NPU_ERR_UNSUPPORTED, "K = %lld must be a multiple of 32", (long long)K);
+  if (N % 64 != 0) return fail(NPU_ERR_UNSUPPORTED, "N = %lld must be a multiple of 64", (long long)N);
+  return NPU_OK;
+}
+
+npu_status check_eps(float eps) {
+  if (!(eps >= 0.0f)) return fail(NPU_ERR_INVALID_ARG, "eps must be >= 0");
+  return NPU_OK;
+}
+
+const uint16_t *u16(const void *p) { return static_cast<const uint16_t *>(p); }
+uint16_t *u16w(const void *p) { return const_cast<uint16_t *>(static_cast<const uint16_t *>(p)); }
+
+}  // namespace
+
+extern "C" {
+
+npu_status fused_llama_qkv_rope(const npu_memref *x, const npu_memref *g1, const npu_memref *wq,
+                                const npu_memref *wk, const npu_memref *wv,
+                                const npu_memref *cos_t, const npu_memref *sin_t,
+                                const npu_memref *Q, const npu_memref *K, const npu_memref *V,
+                                float eps, npu_stream stream) {
+  const void *px, *pg, *pq, *pk, *pv, *pc, *ps, *oq, *ok, *ov;
+  NPU_TRY(check_memref(x, "x", 2, NPU_BF16, &px));
+  const int64_t S = x->sizes[0], D = x->sizes[1];
+  if (D % 64 != 0) return fail(NPU_ERR_UNSUPPORTED, "D = %lld must be a multiple of 64", (long long)D);
+  NPU_TRY(check_1d(g1, "g1", NPU_F32, D, &pg));
+  NPU_TRY(check_2d(wq, "wq", NPU_BF16, D, D, &pq));
+  NPU_TRY(check_2d(wk, "wk", NPU_BF16, D, D, &pk));
+  NPU_TRY(check_2d(wv, "wv", NPU_BF16, D, D, &pv));
+  NPU_TRY(check_2d(cos_t, "cos_t", NPU_F32, S, 32, &pc));
+  NPU_TRY(check_2d(sin_t, "sin_t", NPU_F32, S, 32, &ps));
+  NPU_TRY(check_2d(Q, "Q", NPU_BF16, S, D, &oq));
+  NPU_TRY(check_2d(K, "K", NPU_BF16, S, D, &ok));
+  NPU_TRY(check_2d(V, "V", NPU_BF16, S, D, &ov));
+  NPU_TRY(check_gemm_dims(S, D, D));
+  NPU_TRY(check_eps(eps));
+  npu::LlamaGemmArgs a{};
+  a.A = u16(px);
+  a.gamma = static_cast<const float *>(pg);
+  a.eps = eps;
+  a.B[0] = u16(pq); a.B[1] = u16(pk); a.B[2] = u16(pv);
+  a.nparts = 3;
+  a.M = (int)S; a.K = (int)D; a.Npart = (int)D; a.Dh = 64;
+  a.cos_t = static_cast<const float *>(pc);
+  a.sin_t = static_cast<const float *>(ps);
+  a.out[0] = u16w(oq); a.out[1] = u16w(ok); a.out[2] = u16w(ov);
+  return hip_status(npu::launch_llama_gemm(a, npu::kProRmsnorm, npu::kEpiQkvRope,
+                                           static_cast<hipStream_t>(stream)),
+                    "fused_llama_qkv_rope launch");
+}
+
+npu_status fused_llama_attention(const npu_memref *Q, const npu_memref *K, const npu_memref *V,
+                                 const npu_memref *A, int32_t n_heads, float scale,
+                                 npu_stream stream) {
+  const void *pq, *pk, *pv, *pa;
+  NPU_TRY(check_memref(Q, "Q", 2, NPU_BF16, &pq));
+  const int64_t S = Q->sizes[0], D = Q->sizes[1];
+  if (n_heads <= 0 || D != (int64_t)n_heads * 64)
+    return fail(NPU_ERR_UNSUPPORTED, "D = %lld must equal n_heads * 64 (n_heads = %d)",
+                (long long)D, n_heads);
+  NPU_TRY(check_2d(K, "K", NPU_BF16, S, D, &pk));
+  NPU_TRY(check_2d(V, "V", NPU_BF16, S, D, &pv));
+  NPU_TRY(check_2d(A, "A", NPU_BF16, S, D, &pa));
+  if (!(scale > 0.0f)) return fail(NPU_ERR_INVALID_ARG, "scale must be positive");
+  return hip_status(npu::launch_llama_attention(u16(pq), u16(pk), u16(pv), u16w(pa), (int)S,
+                                                n_heads, scale, static_cast<hipStream_t>(stream)),
+                    "fused_llama_attention launch");
+}
+
+npu_status fused_llama_matmul_residual(const npu_memref *am, const npu_memref *w,
+                                       const npu_memref *res, const npu_memref *out,
+                                       npu_stream stream) {
+  const void *pa, *pw, *pr, *po;
+  NPU_TRY(check_memref(am, "a", 2, NPU_BF16, &pa));
+  const int64_t S = am->sizes[0], Kd = am->sizes[1];
+  NPU_TRY(check_memref(w, "w", 2, NPU_BF16, &pw));
+  const int64_t N = w->sizes[1];
+  if (w->sizes[0] != Kd)
+    return fail(NPU_ERR_INVALID_ARG, "w: sizes[0] = %lld, expected K = %lld",
+                (long long)w->sizes[0], (long long)Kd);
+  NPU_TRY(check_2d(res, "res", NPU_BF16, S, N, &pr));
+  NPU_TRY(check_2d(out, "out", NPU_BF16, S, N, &po));
+  NPU_TRY(check_gemm_dims(S, Kd, N));
+  npu::LlamaGemmArgs a{};
+  a.A = u16(pa);
+  a.B[0] = a.B[1] = a.B[2] = u16(pw);
+  a.nparts = 1;
+  a.M = (int)S; a.K = (int)Kd; a.Npart = (int)N; a.Dh = 64;
+  a.res = u16(pr);
+  a.out[0] = a.out[1] = a.out[2] = u16w(po);
+  return hip_status(npu::launch_llama_gemm(a, npu::kProPlain, npu::kEpiResidual,
+                                           static_cast<hipStream_t>(stream)),
+                    "fused_llama_matmul_residual launch");
+}
+
+npu_status fused_llama_rmsnorm_swiglu(const npu_memref *h, const npu_memref *g2,
+                                      const npu_memref *wg, const npu_memref *wu,
+                                      const npu_memref *act, float eps, npu_stream stream) {
+  const void *ph, *pg, *pwg, *pwu, *po;
+  NPU_TRY(check_memref(h, "h", 2, NPU_BF16, &ph));
+  const int64_t S = h->sizes[0], D = h->sizes[1];
+  NPU_TRY(check_1d(g2, "g2", NPU_F32, D, &pg));
+  NPU_TRY(check_memref(wg, "wg", 2, NPU_BF16, &pwg));
+  const int64_t F = wg->sizes[1];
+  if (wg->sizes[0] != D)
+    return fail(NPU_ERR_INVALID_ARG, "wg: sizes[0] = %lld, expected D = %lld",
+                (long long)wg->sizes[0], (long long)D);
+  NPU_TRY(check_2d(wu, "wu", NPU_BF16, D, F, &pwu));
+  NPU_TRY(check_2d(act, "act", NPU_BF16, S, F, &po));
+  NPU_TRY(check_gemm_dims(S, D, F));
+  if (D % 8 != 0) return fail(NPU_ERR_UNSUPPORTED, "D must be a multiple of 8");
+  NPU_TRY(check_eps(eps));
+  npu::LlamaGemmArgs a{};
+  a.A = u16(ph);
+  a.gamma = static_cast<const float *>(pg);
+  a.eps = eps;
+  a.B[0] = u16(pwg); a.B[1] = u16(pwu); a.B[2] = u16(pwu);
+  a.nparts = 2;
+  a.M = (int)S; a.K = (int)D; a.Npart = (int)F; a.Dh = 64;
+  a.out[0] = a.out[1] = a.out[2] = u16w(po);
+  return hip_status(npu::launch_llama_gemm(a, npu::kProRmsnorm, npu::kEpiSwiglu,
+                                           static_cast<hipStream_t>(stream)),
+                    "fused_llama_rmsnorm_swiglu launch");
+}
+
 }  // extern "C"

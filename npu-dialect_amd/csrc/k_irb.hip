@@ -1,0 +1,152 @@
+// k_irb.hip -- MobileNetV2 inverted residual block as ONE fused group (f32):
+//   e   = relu6(conv1x1(x, we))                 expand  C -> E   (MFMA)
+//   d   = relu6(depthwise3x3(pad1(e), wdw))     E channels       (VALU)
+//   out = conv1x1(d, wp) + x                    project E -> C   (MFMA)
+// (NHWC restatement of test/mobilenet_block.mlir:8-94, with a true depthwise
+// stage where the reference models it as a full conv, :45-53).
+//
+// Vertical fusion with the intermediates in LDS: a workgroup owns an 8x8
+// output tile, stages the 10x10 x halo, recomputes the expand conv on the
+// halo (the tensor.pad before the depthwise conv becomes zeros written for
+// out-of-image halo pixels), and keeps the E-channel tile in LDS.  The
+// depthwise result is computed directly in the A-operand layout of the
+// project MFMA (each lane produces the 4 consecutive channels of one pixel
+// that it feeds), so d never leaves registers.  HBM sees x and out once: the
+// E-channel intermediates (6x the block's own bytes) never reach it.
+#include "kernels.hpp"
+#include "npu_device.hpp"
+
+namespace npu {
+
+namespace {
+
+constexpr int TH = 8, TW = 8;        // output tile
+constexpr int HW = TW + 2;           // halo tile width (and height)
+constexpr int HP = HW * (TH + 2);    // 100 halo pixels
+constexpr int HPB = (HP + 15) / 16;  // 7 blocks of 16 rows
+
+__device__ __forceinline__ float relu6(float v) { return act_apply(v, 2); }
+
+template <int C, int E>
+__global__ __launch_bounds__(256) void irb_kernel(const float *__restrict__ x,
+                                                  const float *__restrict__ we,
+                                                  const float *__restrict__ wdw,
+                                                  const float *__restrict__ wp,
+                                                  float *__restrict__ out, int H, int W,
+                                                  int tiles_w) {
+  static_assert(C % 4 == 0 && E % 16 == 0, "C must be a multiple of 4, E of 16");
+  constexpr int KC1 = (C + 15) / 16;  // expand reduction chunks (C padded to 16)
+  constexpr int XS = KC1 * 16 + 4;    // LDS row strides in floats (+4 against bank conflicts)
+  constexpr int ES = E + 4;
+  constexpr int FB1 = E / 16;         // expand filter blocks
+  constexpr int KC2 = E / 16;         // project reduction chunks
+  constexpr int FB2 = (C + 15) / 16;  // project filter blocks
+  __shared__ __attribute__((aligned(16))) float xs[HPB * 16 * XS];
+  __shared__ __attribute__((aligned(16))) float es[HP * ES];
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int r = lane & 15, q = lane >> 4;
+  const int n = blockIdx.y;
+  const int ty0 = (blockIdx.x / tiles_w) * TH, tx0 = (blockIdx.x % tiles_w) * TW;
+
+  // ---- x halo tile, zero-padded to KC1*16 channels and 112 rows.
+  constexpr int XV = KC1 * 4;  // float4 columns per row
+  for (int idx = tid; idx < HPB * 16 * XV; idx += 256) {
+    const int hp = idx / XV, c = (idx - hp * XV) * 4;
+    const int iy = ty0 + hp / HW - 1, ix = tx0 + hp % HW - 1;
+    f32x4 v = {0.f, 0.f, 0.f, 0.f};
+    if (hp < HP && c < C && iy >= 0 && iy < H && ix >= 0 && ix < W)
+      v = *reinterpret_cast<const f32x4 *>(x + ((size_t)(n * H + iy) * W + ix) * C + c);
+    *reinterpret_cast<f32x4 *>(xs + hp * XS + c) = v;
+  }
+  __syncthreads();
+
+  // ---- expand on the halo: 7 pixel blocks x FB1 filter blocks, round-robin.
+  for (int t = wave; t < HPB * FB1; t += 4) {
+    const int pb = t / FB1, fb = t - pb * FB1;
+    const int f = fb * 16 + r;
+    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int kc = 0; kc < KC1; ++kc) {
+      const int k = kc * 16 + 4 * q;
+      const Frag16 a = load16(xs + (pb * 16 + r) * XS + k);
+      const Frag16 b = k < C ? load16(we + f * C + k) : frag_zero();
+      MfmaF32::mma(acc, a, b);
+    }
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int hp = pb * 16 + 4 * q + e;
+      if (hp < HP) {
+        const int iy = ty0 + hp / HW - 1, ix = tx0 + hp % HW - 1;
+        const bool inside = iy >= 0 && iy < H && ix >= 0 && ix < W;
+        es[hp * ES + f] = inside ? relu6(acc[e]) : 0.0f;
+      }
+    }
+  }
+  __syncthreads();
+
+  // ---- depthwise (in registers, A-operand layout) + project + residual.
+  // Wave w owns output pixels 16w .. 16w+15.
+  const int p = wave * 16 + r;
+  const int hbase = (p / TW) * HW + (p % TW);
+  f32x4 acc2[FB2];
+#pragma unroll
+  for (int fb = 0; fb < FB2; ++fb) acc2[fb] = f32x4{0.f, 0.f, 0.f, 0.f};
+  for (int kc = 0; kc < KC2; ++kc) {
+    const int e0 = kc * 16 + 4 * q;
+    f32x4 d = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int t = 0; t < 9; ++t) {
+      const int hidx = hbase + (t / 3) * HW + (t % 3);
+      const f32x4 ev = *reinterpret_cast<const f32x4 *>(es + hidx * ES + e0);
+      const f32x4 wv = *reinterpret_cast<const f32x4 *>(wdw + t * E + e0);
+      d += ev * wv;
+    }
+    Frag16 a;
+    a.f = f32x4{relu6(d[0]), relu6(d[1]), relu6(d[2]), relu6(d[3])};
+#pragma unroll
+    for (int fb = 0; fb < FB2; ++fb) {
+      const int c = fb * 16 + r;
+      const Frag16 b = c < C ? load16(wp + c * E + e0) : frag_zero();
+      MfmaF32::mma(acc2[fb], a, b);
+    }
+  }
+#pragma unroll
+  for (int fb = 0; fb < FB2; ++fb) {
+    const int c = fb * 16 + r;
+    if (c >= C) continue;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int pe = wave * 16 + 4 * q + e;
+      const int oy = ty0 + pe / TW, ox = tx0 + pe % TW;
+      if (oy < H && ox < W) {
+        const float res = xs[((pe / TW + 1) * HW + (pe % TW) + 1) * XS + c];
+        out[((size_t)(n * H + oy) * W + ox) * C + c] = acc2[fb][e] + res;
+      }
+    }
+  }
+}
+
+template <int C, int E>
+hipError_t launch_irb_t(const IrbArgs &a, hipStream_t s) {
+  const int tiles_w = (a.W + TW - 1) / TW, tiles_h = (a.H + TH - 1) / TH;
+  dim3 grid(tiles_w * tiles_h, a.N);
+  hipLaunchKernelGGL((irb_kernel<C, E>), grid, dim3(256), 0, s, a.x, a.we, a.wdw, a.wp, a.out,
+                     a.H, a.W, tiles_w);
+  return hipGetLastError();
+}
+
+}  // namespace
+
+bool irb_supported(int C, int E) {
+  return (C == 24 && E == 144) || (C == 16 && E == 96) || (C == 32 && E == 192);
+}
+
+hipError_t launch_irb_f32(const IrbArgs &a, hipStream_t s) {
+  if (a.C == 24 && a.E == 144) return launch_irb_t<24, 144>(a, s);
+  if (a.C == 16 && a.E == 96) return launch_irb_t<16, 96>(a, s);
+  if (a.C == 32 && a.E == 192) return launch_irb_t<32, 192>(a, s);
+  return hipErrorInvalidValue;
+}
+
+}  // namespace npu

@@ -24,4 +24,39 @@ struct ConvArgs {
 hipError_t launch_conv2d_nhwc_f32(const ConvArgs &a, hipStream_t s);
 hipError_t launch_conv2d_nhwc_bf16(const ConvArgs &a, hipStream_t s);
 
+struct QBottleneckArgs {
+  const int8_t *x, *w1, *w2, *w3;
+  const int32_t *m1, *s1, *m2, *s2, *m3, *s3;
+  int8_t *out;
+  int N, H, W, C, M1;
+};
+bool qbottleneck_supported(int C, int M1);
+hipError_t launch_qbottleneck_i8(const QBottleneckArgs &a, hipStream_t s);
+
+struct IrbArgs {
+  const float *x, *we, *wdw, *wp;
+  float *out;
+  int N, H, W, C, E;
+};
+bool irb_supported(int C, int E);
+hipError_t launch_irb_f32(const IrbArgs &a, hipStream_t s);
+
+// Llama layer GEMM variants: A prologue and epilogue kinds.
+enum { kProPlain = 0, kProRmsnorm = 1 };
+enum { kEpiQkvRope = 0, kEpiResidual = 1, kEpiSwiglu = 2 };
+struct LlamaGemmArgs {
+  const uint16_t *A;      // [M][K] bf16
+  const float *gamma;     // [K] (RMSNorm prologue)
+  float eps;
+  const uint16_t *B[3];   // each [K][Npart] bf16; QKV: 3 parts, SwiGLU: gate, up
+  int nparts;
+  int M, K, Npart, Dh;
+  const float *cos_t, *sin_t;  // [M][Dh/2] (RoPE epilogue)
+  const uint16_t *res;    // [M][Npart] (residual epilogue)
+  uint16_t *out[3];       // each [M][Npart]
+};
+hipError_t launch_llama_gemm(const LlamaGemmArgs &a, int pro, int epi, hipStream_t s);
+hipError_t launch_llama_attention(const uint16_t *Q, const uint16_t *K, const uint16_t *V,
+                                  uint16_t *O, int S, int H, float scale, hipStream_t s);
+
 }  // namespace npu

@@ -147,12 +147,164 @@ def conv3x3_bias_relu(N=1, dtype="f32", H=56, W=56, C=64, F=64,
         meta={"N": N, "H": H, "W": W, "C": C, "F": F})
 
 
+# ------------------------------------------------------------------ C3
+def irb(N=1, H=56, W=56, C=24, E=144, seed=rng.SEED_BASE + 3) -> Workload:
+    def make_inputs():
+        return {
+            "x": rng.uniform(seed, 0, (N, H, W, C), 0.0, 1.0),
+            "we": rng.normal(seed, 1, (E, C), 0.0, math.sqrt(2.0 / C)),
+            "wdw": rng.normal(seed, 2, (3, 3, E), 0.0, math.sqrt(2.0 / 9)),
+            "wp": rng.normal(seed, 3, (C, E), 0.0, math.sqrt(2.0 / E)),
+        }
+
+    def make_outputs(d):
+        import torch
+        return {"out": torch.empty((N, H, W, C), dtype=torch.float32, device="cuda")}
+
+    def run(d, o, stream):
+        groups.fused_irb_f32(d["x"], d["we"], d["wdw"], d["wp"], o["out"], stream)
+
+    P = N * H * W
+    return Workload(
+        name=f"mbv2_irb_f32_n{N}", config=3, dtype="f32",
+        flops=2 * P * (C * E + 9 * E + E * C),
+        bytes=4 * (2 * P * C + E * C + 9 * E + C * E),
+        make_inputs=make_inputs, make_outputs=make_outputs, run=run,
+        desc=f"MobileNetV2 IRB 1x1 {C}->{E} ReLU6, dw3x3 ReLU6, 1x1 {E}->{C}, +x; NHWC "
+             f"{N}x{H}x{W} f32", units=N, meta={"N": N, "H": H, "W": W, "C": C, "E": E})
+
+
+# ------------------------------------------------------------------ C4
+def quant_multiplier(real):
+    """Fixed-point (multiplier, shift) with real ~= m * 2^-shift, m in [2^30, 2^31)."""
+    real = np.asarray(real, np.float64)
+    frac, exp = np.frexp(real)                      # real = frac * 2^exp, frac in [0.5, 1)
+    m = np.rint(frac * 2.0 ** 31).astype(np.int64)
+    exp = exp + (m == 2 ** 31)
+    m = np.where(m == 2 ** 31, 2 ** 30, m)
+    shift = 31 - exp
+    if np.any(shift < 2) or np.any(shift > 62):
+        raise ValueError("requant scale out of the apply_scale range")
+    return m.astype(np.int32), shift.astype(np.int32)
+
+
+def requant_np(acc, m, s):
+    acc = np.asarray(acc, np.int64)
+    return (acc * m.astype(np.int64) + (np.int64(1) << (s.astype(np.int64) - 1))) >> s
+
+
+def _quantize_per_channel(wf):
+    flat = wf.reshape(wf.shape[0], -1).astype(np.float64)
+    sc = np.abs(flat).max(1) / 127.0
+    q = np.clip(np.rint(flat / sc[:, None]), -127, 127).astype(np.int8)
+    return q.reshape(wf.shape), sc
+
+
+def qbottleneck(N=32, H=56, W=56, C=256, M1=64, seed=rng.SEED_BASE + 4) -> Workload:
+    """int8 ResNet-50 bottleneck.  Weights: He-normal floats quantized per
+    output channel, symmetric, to [-127, 127].  Activations: int8 with zero
+    point 0 and scale 1/127 for x and the output (so the residual adds
+    directly).  Requant multipliers come from float scales calibrated once on
+    image 0 (99.9th percentile of each post-ReLU activation mapped to 127)."""
+
+    def make_inputs():
+        x = rng.randint(seed, 0, (N, H, W, C), 0, 127).astype(np.int8)
+        w1, sw1 = _quantize_per_channel(rng.normal(seed, 1, (M1, C), 0, math.sqrt(2 / C)))
+        w2, sw2 = _quantize_per_channel(rng.normal(seed, 2, (M1, 3, 3, M1), 0,
+                                                   math.sqrt(2 / (9 * M1))))
+        w3, sw3 = _quantize_per_channel(rng.normal(seed, 3, (C, M1), 0, math.sqrt(2 / M1)))
+        sx = 1.0 / 127
+        x0 = x[0].astype(np.int64).reshape(-1, C)
+        acc1 = x0 @ w1.astype(np.int64).T
+        sy1 = np.percentile(np.maximum(acc1 * (sx * sw1), 0), 99.9) / 127
+        m1, s1 = quant_multiplier(sx * sw1 / sy1)
+        y1 = np.clip(requant_np(acc1, m1, s1), 0, 127).reshape(H, W, M1)
+        y1p = np.pad(y1, ((1, 1), (1, 1), (0, 0)))
+        cols = np.concatenate([y1p[kh:kh + H, kw:kw + W] for kh in range(3) for kw in range(3)],
+                              -1).reshape(-1, 9 * M1)
+        acc2 = cols @ w2.reshape(M1, -1).astype(np.int64).T
+        sy2 = np.percentile(np.maximum(acc2 * (sy1 * sw2), 0), 99.9) / 127
+        m2, s2 = quant_multiplier(sy1 * sw2 / sy2)
+        m3, s3 = quant_multiplier(sy2 * sw3 / sx)
+        return {"x": x, "w1": w1, "w2": w2, "w3": w3, "m1": m1, "s1": s1, "m2": m2, "s2": s2,
+                "m3": m3, "s3": s3}
+
+    def make_outputs(d):
+        import torch
+        return {"out": torch.empty((N, H, W, C), dtype=torch.int8, device="cuda")}
+
+    def run(d, o, stream):
+        groups.fused_qbottleneck_i8(d["x"], d["w1"], d["w2"], d["w3"], d["m1"], d["s1"],
+                                    d["m2"], d["s2"], d["m3"], d["s3"], o["out"], stream)
+
+    P = N * H * W
+    wbytes = M1 * C + 9 * M1 * M1 + C * M1
+    return Workload(
+        name=f"qbottleneck_i8_n{N}", config=4, dtype="i8",
+        flops=2 * P * (C * M1 + 9 * M1 * M1 + M1 * C),
+        bytes=2 * P * C + wbytes + 4 * (4 * M1 + 2 * C),
+        make_inputs=make_inputs, make_outputs=make_outputs, run=run,
+        desc=f"int8 bottleneck 1x1 {C}->{M1}, 3x3 {M1}->{M1}, 1x1 {M1}->{C} + residual, "
+             f"NHWC {N}x{H}x{W}", units=N, meta={"N": N, "H": H, "W": W, "C": C, "M1": M1})
+
+
+# ------------------------------------------------------------------ C5
+def rope_tables(S, Dh, theta=10000.0):
+    """cos/sin of position * theta^(-2t/Dh), t < Dh/2, in float64 rounded to f32."""
+    inv = theta ** (-np.arange(0, Dh, 2, dtype=np.float64) / Dh)
+    ang = np.arange(S, dtype=np.float64)[:, None] * inv[None, :]
+    return np.cos(ang).astype(np.float32), np.sin(ang).astype(np.float32)
+
+
+def llama_layer(S=512, D=512, H=8, F=1408, eps=1e-5, seed=rng.SEED_BASE + 5) -> Workload:
+    """One Llama decoder layer, bf16: x ~ N(0,1), weights ~ N(0, 0.02), RMSNorm
+    gains ~ U(0.5, 1.5) (f32), RoPE theta 10000, causal attention."""
+    Dh = D // H
+
+    def make_inputs():
+        bf = lambda t, shape, sd: rng.to_bf16_bits(rng.normal(seed, t, shape, 0.0, sd))
+        c, s = rope_tables(S, Dh)
+        return {
+            "x": bf(0, (S, D), 1.0),
+            "wq": bf(1, (D, D), 0.02), "wk": bf(2, (D, D), 0.02), "wv": bf(3, (D, D), 0.02),
+            "wo": bf(4, (D, D), 0.02), "wg": bf(5, (D, F), 0.02), "wu": bf(6, (D, F), 0.02),
+            "wd": bf(7, (F, D), 0.02),
+            "g1": rng.uniform(seed, 8, (D,), 0.5, 1.5), "g2": rng.uniform(seed, 9, (D,), 0.5, 1.5),
+            "cos_t": c, "sin_t": s,
+        }
+
+    def make_outputs(d):
+        import torch
+        e = lambda *shape: torch.empty(shape, dtype=torch.bfloat16, device="cuda")
+        return {"Q": e(S, D), "K": e(S, D), "V": e(S, D), "A": e(S, D), "h": e(S, D),
+                "act": e(S, F), "out": e(S, D)}
+
+    def run(d, o, stream):
+        groups.llama_layer(d, o, H, eps, stream)
+
+    pairs = S * (S + 1) // 2  # causal (query, key) pairs
+    flops = 2 * S * D * 3 * D + 2 * H * Dh * pairs * 2 + 2 * S * D * D + 2 * S * D * 2 * F \
+        + 2 * S * F * D
+    wbytes = 2 * (4 * D * D + 3 * D * F)
+    return Workload(
+        name=f"llama_layer_bf16_s{S}", config=5, dtype="bf16", flops=flops,
+        bytes=wbytes + 4 * 2 * D + 2 * 4 * S * (Dh // 2) + 2 * 2 * S * D,
+        make_inputs=make_inputs, make_outputs=make_outputs, run=run,
+        desc=f"Llama decoder layer bf16: S={S}, d_model={D}, {H} heads x {Dh}, SwiGLU {F}, "
+             "RMSNorm, RoPE, causal attention (5 fused groups)",
+        units=1, unit_name="layers",
+        meta={"S": S, "D": D, "H": H, "F": F, "eps": eps})
+
+
 def all_workloads() -> list:
     """Every configuration this backend runs, in configuration order."""
     return [
         matmul_bias_relu(),
         conv3x3_bias_relu(1, "f32"), conv3x3_bias_relu(32, "f32"),
         conv3x3_bias_relu(1, "bf16"), conv3x3_bias_relu(32, "bf16"),
+        irb(1), irb(32),
+        qbottleneck(32),
+        llama_layer(),
     ]
 
 

@@ -21,6 +21,10 @@ ACT = {"none": 0, "relu": 1, "relu6": 2}
 OUTLINED_NAMES = {
     "fused_fill_matmul_generic": "fused_matmul_bias_act",
     "fused_pad_fill_conv2d_nhwc_generic": "fused_conv2d_nhwc_bias_act",
+    "fused_fill_conv2d_nhwc_generic_pad_fill_conv2d_nhwc_generic_fill_conv2d_nhwc_generic":
+        "fused_qbottleneck_i8",
+    "fused_fill_conv2d_nhwc_generic_pad_fill_dwconv2d_generic_fill_conv2d_nhwc_generic":
+        "fused_irb_f32",
 }
 
 
@@ -65,3 +69,65 @@ def fused_conv2d_nhwc_bias_act(x, w, bias, out, pad=1, act="relu", stream=None):
                                                ACT[act], _stream(stream))
     _check(st, "fused_conv2d_nhwc_bias_act")
     return out
+
+
+def fused_qbottleneck_i8(x, w1, w2, w3, m1, s1, m2, s2, m3, s3, out, stream=None):
+    """int8 bottleneck: three convs with per-channel requant, residual, ReLU."""
+    ms = [from_tensor(t) for t in (x, w1, w2, w3, m1, s1, m2, s2, m3, s3, out)]
+    st = _lib.lib().fused_qbottleneck_i8(*[ref(m) for m in ms], _stream(stream))
+    _check(st, "fused_qbottleneck_i8")
+    return out
+
+
+def fused_irb_f32(x, we, wdw, wp, out, stream=None):
+    """MobileNetV2 inverted residual: expand, ReLU6, depthwise 3x3, ReLU6, project, +x."""
+    ms = [from_tensor(t) for t in (x, we, wdw, wp, out)]
+    st = _lib.lib().fused_irb_f32(*[ref(m) for m in ms], _stream(stream))
+    _check(st, "fused_irb_f32")
+    return out
+
+
+def fused_llama_qkv_rope(x, g1, wq, wk, wv, cos_t, sin_t, Q, K, V, eps=1e-5, stream=None):
+    """Q, K, V = rope(rmsnorm(x)*g1 @ wq), rope(... @ wk), (... @ wv); bf16."""
+    ms = [from_tensor(t) for t in (x, g1, wq, wk, wv, cos_t, sin_t, Q, K, V)]
+    st = _lib.lib().fused_llama_qkv_rope(*[ref(m) for m in ms], float(eps), _stream(stream))
+    _check(st, "fused_llama_qkv_rope")
+    return Q, K, V
+
+
+def fused_llama_attention(Q, K, V, A, n_heads, scale, stream=None):
+    """A = causal softmax(Q K^T * scale) V per head (head dim 64); bf16."""
+    ms = [from_tensor(t) for t in (Q, K, V, A)]
+    st = _lib.lib().fused_llama_attention(*[ref(m) for m in ms], int(n_heads), float(scale),
+                                          _stream(stream))
+    _check(st, "fused_llama_attention")
+    return A
+
+
+def fused_llama_matmul_residual(a, w, res, out, stream=None):
+    """out = res + a @ w; bf16."""
+    ms = [from_tensor(t) for t in (a, w, res, out)]
+    st = _lib.lib().fused_llama_matmul_residual(*[ref(m) for m in ms], _stream(stream))
+    _check(st, "fused_llama_matmul_residual")
+    return out
+
+
+def fused_llama_rmsnorm_swiglu(h, g2, wg, wu, act, eps=1e-5, stream=None):
+    """act = silu(rmsnorm(h)*g2 @ wg) * (rmsnorm(h)*g2 @ wu); bf16."""
+    ms = [from_tensor(t) for t in (h, g2, wg, wu, act)]
+    st = _lib.lib().fused_llama_rmsnorm_swiglu(*[ref(m) for m in ms], float(eps), _stream(stream))
+    _check(st, "fused_llama_rmsnorm_swiglu")
+    return act
+
+
+def llama_layer(p, bufs, n_heads, eps=1e-5, stream=None):
+    """One decoder layer as its five groups.  ``p``: x, g1, g2, wq, wk, wv, wo,
+    wg, wu, wd, cos_t, sin_t; ``bufs``: Q, K, V, A, h, act, out (caller-owned)."""
+    fused_llama_qkv_rope(p["x"], p["g1"], p["wq"], p["wk"], p["wv"], p["cos_t"], p["sin_t"],
+                         bufs["Q"], bufs["K"], bufs["V"], eps, stream)
+    dh = p["x"].shape[1] // n_heads
+    fused_llama_attention(bufs["Q"], bufs["K"], bufs["V"], bufs["A"], n_heads, dh ** -0.5, stream)
+    fused_llama_matmul_residual(bufs["A"], p["wo"], p["x"], bufs["h"], stream)
+    fused_llama_rmsnorm_swiglu(bufs["h"], p["g2"], p["wg"], p["wu"], bufs["act"], eps, stream)
+    fused_llama_matmul_residual(bufs["act"], p["wd"], bufs["h"], bufs["out"], stream)
+    return bufs["out"]

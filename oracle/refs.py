@@ -4,7 +4,8 @@ TEST INFRASTRUCTURE ONLY (see oracle.py).  ``reference(name, inputs)`` runs
 the unfused CPU restatement of the workload's linalg chain and returns
 ``{output_name: (expected, mag)}`` where ``mag`` is the chain evaluated on
 absolute values (the scale of the per-element error bound) or None for
-integer outputs that must match bit for bit.
+integer outputs that must match bit for bit.  ``run_oracle`` runs only the
+restatement (what the CPU baseline times).
 """
 from __future__ import annotations
 
@@ -23,6 +24,13 @@ def _absf(x):
     return np.abs(np.asarray(x, np.float32))
 
 
+def _sel(images):
+    if images is None:
+        return lambda a: a
+    return lambda a: np.ascontiguousarray(a[list(images)])
+
+
+# ------------------------------------------------------------ per group
 def matmul_bias_act(A, B, bias, act="relu"):
     out = oracle.block_matmul_bias_act(A, B, bias, act)
     mag = np.abs(A).astype(np.float64) @ np.abs(B).astype(np.float64)
@@ -40,22 +48,130 @@ def conv_bias_act(x, w, bias, pad=1, act="relu"):
     return out, mag
 
 
+def irb(x, we, wdw, wp):
+    out = oracle.block_irb(x, we, wdw, wp)
+    ax = np.abs(x)
+    me = oracle.conv2d_nhwc_fhwc(ax, np.abs(we)[:, None, None, :])
+    md = oracle.depthwise_conv2d_nhwc_hwc(oracle.pad_nhwc(me, (1, 1, 1, 1)), np.abs(wdw))
+    mag = oracle.conv2d_nhwc_fhwc(md, np.abs(wp)[:, None, None, :]).astype(np.float64) + ax
+    return out, mag
+
+
+def qbottleneck(inp, images=None):
+    s = _sel(images)
+    return oracle.block_qbottleneck(s(inp["x"]), inp["w1"], inp["w2"], inp["w3"], inp["m1"],
+                                    inp["s1"], inp["m2"], inp["s2"], inp["m3"], inp["s3"])
+
+
+# ------------------------------------------------------------ Llama layer
+LLAMA_HEADS, LLAMA_EPS = 8, 1e-5
+
+
+def _f64(x):
+    return _bf(x).astype(np.float64) if x.dtype == np.uint16 else np.asarray(x, np.float64)
+
+
+def llama_stages(inp, H, eps):
+    """The oracle's five sub-group outputs of one decoder layer."""
+    x = inp["x"]
+    S, D = x.shape
+    Q, K, V = oracle.llama_qkv(x, inp["g1"], inp["wq"], inp["wk"], inp["wv"], inp["cos_t"],
+                               inp["sin_t"], H, eps)
+    A = oracle.llama_attention(Q, K, V, H, float((D // H) ** -0.5))
+    h = oracle.llama_matmul_residual(A, inp["wo"], x)
+    act = oracle.llama_swiglu(h, inp["g2"], inp["wg"], inp["wu"], eps)
+    out = oracle.llama_matmul_residual(act, inp["wd"], h)
+    return {"Q": Q, "K": K, "V": V, "A": A, "h": h, "act": act, "out": out}
+
+
+def normed_bf16(x, g, eps):
+    """bf16(rmsnorm(x) * g) exactly as the oracle's sub-groups form the matmul input."""
+    return oracle.trunc_bf16(oracle.rmsnorm(oracle.ext_bf16(x), g, eps))
+
+
+def mag_qkv(xn, w, cos_t, sin_t, rope):
+    m = np.abs(_f64(xn)) @ np.abs(_f64(w))
+    if not rope:
+        return m
+    S, D = m.shape
+    mp = m.reshape(S, D // 2, 2)
+    Dh = 2 * cos_t.shape[1]
+    c = np.abs(np.tile(cos_t, (1, D // Dh))).astype(np.float64)
+    s = np.abs(np.tile(sin_t, (1, D // Dh))).astype(np.float64)
+    out = np.empty_like(mp)
+    out[..., 0] = mp[..., 0] * c + mp[..., 1] * s
+    out[..., 1] = mp[..., 0] * s + mp[..., 1] * c
+    return out.reshape(S, D)
+
+
+def mag_attention(Q, K, V, H):
+    q, k, v = _f64(Q), _f64(K), _f64(V)
+    S, D = q.shape
+    Dh = D // H
+    mag = np.empty((S, D))
+    mask = np.triu(np.ones((S, S), bool), 1)
+    for h in range(H):
+        sl = slice(h * Dh, (h + 1) * Dh)
+        s = (q[:, sl] @ k[:, sl].T) * Dh ** -0.5
+        s[mask] = -np.inf
+        p = np.exp(s - s.max(1, keepdims=True))
+        p /= p.sum(1, keepdims=True)
+        mag[:, sl] = p @ np.abs(v[:, sl])
+    return mag
+
+
+def mag_residual(a, w, res):
+    return np.abs(_f64(res)) + np.abs(_f64(a)) @ np.abs(_f64(w))
+
+
+def mag_swiglu(hn, wg, wu):
+    g, u = _f64(hn) @ _f64(wg), _f64(hn) @ _f64(wu)
+    mg, mu = np.abs(_f64(hn)) @ np.abs(_f64(wg)), np.abs(_f64(hn)) @ np.abs(_f64(wu))
+    sg = g / (1 + np.exp(-g))
+    return mg * np.abs(u) + np.abs(sg) * mu + np.abs(sg * u)
+
+
+def llama_reference(inp, H, eps):
+    """{name: (expected, mag)} for the layer's h and out."""
+    st = llama_stages(inp, H, eps)
+    hn = normed_bf16(st["h"], inp["g2"], eps)
+    m_h = mag_residual(st["A"], inp["wo"], inp["x"])
+    m_act = mag_swiglu(hn, inp["wg"], inp["wu"])
+    m_out = np.abs(_f64(st["h"])) + m_h + m_act @ np.abs(_f64(inp["wd"]))
+    return {"h": (st["h"], m_h), "out": (st["out"], m_out)}
+
+
+# ------------------------------------------------------------ registry
 def run_oracle(workload_name: str, inp: dict, images=None) -> dict:
-    """Only the oracle's outputs (what the CPU baseline times)."""
-    sel = (lambda a: a) if images is None else (lambda a: np.ascontiguousarray(a[list(images)]))
+    s = _sel(images)
     if workload_name.startswith("matmul_bias_relu"):
         return {"out": oracle.block_matmul_bias_act(inp["A"], inp["B"], inp["bias"], "relu")}
     if workload_name.startswith("conv3x3_bias_relu"):
-        return {"out": oracle.block_conv_bias_act(sel(inp["x"]), inp["w"], inp["bias"], 1, "relu")}
+        return {"out": oracle.block_conv_bias_act(s(inp["x"]), inp["w"], inp["bias"], 1, "relu")}
+    if workload_name.startswith("mbv2_irb"):
+        return {"out": oracle.block_irb(s(inp["x"]), inp["we"], inp["wdw"], inp["wp"])}
+    if workload_name.startswith("qbottleneck"):
+        return {"out": qbottleneck(inp, images)}
+    if workload_name.startswith("llama_layer"):
+        st = oracle.block_llama_layer(inp["x"], inp["g1"], inp["g2"], inp["wq"], inp["wk"],
+                                      inp["wv"], inp["wo"], inp["wg"], inp["wu"], inp["wd"],
+                                      inp["cos_t"], inp["sin_t"], LLAMA_HEADS, LLAMA_EPS)
+        return {"h": st[0], "out": st[1]}
     raise KeyError(workload_name)
 
 
 def reference(workload_name: str, inp: dict, images=None) -> dict:
     """Expected outputs of a named workload; ``images`` restricts batched
     workloads to a subset of batch indices (each image is independent)."""
-    sel = (lambda a: a) if images is None else (lambda a: np.ascontiguousarray(a[list(images)]))
+    s = _sel(images)
     if workload_name.startswith("matmul_bias_relu"):
         return {"out": matmul_bias_act(inp["A"], inp["B"], inp["bias"], "relu")}
     if workload_name.startswith("conv3x3_bias_relu"):
-        return {"out": conv_bias_act(sel(inp["x"]), inp["w"], inp["bias"], 1, "relu")}
+        return {"out": conv_bias_act(s(inp["x"]), inp["w"], inp["bias"], 1, "relu")}
+    if workload_name.startswith("mbv2_irb"):
+        return {"out": irb(s(inp["x"]), inp["we"], inp["wdw"], inp["wp"])}
+    if workload_name.startswith("qbottleneck"):
+        return {"out": (qbottleneck(inp, images), None)}
+    if workload_name.startswith("llama_layer"):
+        return llama_reference(inp, LLAMA_HEADS, LLAMA_EPS)
     raise KeyError(workload_name)

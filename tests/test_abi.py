@@ -95,3 +95,23 @@ def test_python_mirror_raises_with_library_message():
     A = torch.zeros(4, 6)  # host tensors: validation fails before any launch
     with pytest.raises(npu_amd.NpuError, match="multiple of 4"):
         npu_amd.fused_matmul_bias_act(A, torch.zeros(6, 4), None, torch.zeros(4, 4), "relu", 0)
+
+
+def test_qbottleneck_rejects_bad_descriptors():
+    lib = npu_amd.lib()
+    from npu_amd.memref import I32
+    x, w1, w2, w3 = _mr([1, 8, 8, 256], I8), _mr([64, 256], I8), _mr([64, 3, 3, 64], I8), _mr([256, 64], I8)
+    q = [_mr([64], I32), _mr([64], I32), _mr([64], I32), _mr([64], I32), _mr([256], I32), _mr([256], I32)]
+    o = _mr([1, 8, 8, 256], I8)
+
+    def call(*a):
+        return lib.fused_qbottleneck_i8(*[C.byref(m) for m in a], None)
+
+    assert call(x, w1, w2, w3, *q, _mr([1, 8, 8, 128], I8)) == 1 and "out" in _err()
+    assert call(x, _mr([64, 128], I8), w2, w3, *q, o) == 1 and "w1" in _err()
+    assert call(x, w1, _mr([64, 3, 3, 32], I8), w3, *q, o) == 1 and "w2" in _err()
+    assert call(x, w1, w2, w3, *q[:4], _mr([64], I32), q[5], o) == 1 and "m3" in _err()
+    assert call(x, w1, w2, w3, _mr([64], F32), *q[1:], o) == 1 and "dtype" in _err()
+    xx, ww1 = _mr([1, 8, 8, 192], I8), _mr([64, 192], I8)
+    assert call(xx, ww1, w2, _mr([192, 64], I8), *q[:4], _mr([192], I32), _mr([192], I32),
+                _mr([1, 8, 8, 192], I8)) == 2 and "no kernel instance" in _err()

@@ -146,3 +146,217 @@ def test_c2_reference_kat_fills(cuda):
     out = torch.empty(1, 4, 4, 16, device="cuda")
     groups.fused_conv2d_nhwc_bias_act(x, w, None, out, 0, "none")
     np.testing.assert_allclose(_host(out), 16 * 9 * 0.01 * 0.02, atol=1e-5)
+
+
+# ------------------------------------------------------------------ C4
+def _qb_inputs(N, H, W, C, M1, seed):
+    x = rng.randint(seed, 0, (N, H, W, C), 0, 127).astype(np.int8)
+    w1 = rng.randint(seed, 1, (M1, C), -127, 127).astype(np.int8)
+    w2 = rng.randint(seed, 2, (M1, 3, 3, M1), -127, 127).astype(np.int8)
+    w3 = rng.randint(seed, 3, (C, M1), -127, 127).astype(np.int8)
+    q = {}
+    for i, (k, n, sh) in enumerate((("1", M1, 24), ("2", M1, 26), ("3", C, 26))):
+        q["m" + k] = rng.randint(seed, 4 + i, (n,), 2 ** 30, 2 ** 31 - 1).astype(np.int32)
+        q["s" + k] = rng.randint(seed, 7 + i, (n,), sh, sh + 3).astype(np.int32)
+    return dict(x=x, w1=w1, w2=w2, w3=w3, **q)
+
+
+def _qb_run(inp):
+    d = configs.to_device(inp)
+    out = torch.empty_like(d["x"])
+    groups.fused_qbottleneck_i8(d["x"], d["w1"], d["w2"], d["w3"], d["m1"], d["s1"], d["m2"],
+                                d["s2"], d["m3"], d["s3"], out)
+    torch.cuda.synchronize()
+    return _host(out)
+
+
+def test_c4_qbottleneck_config_n32(cuda):
+    w = configs.qbottleneck(32)
+    arrs, out = _run_workload(w)
+    imgs = [0, 13, 31]
+    ref = refs.qbottleneck(arrs, imgs)
+    assert np.array_equal(out["out"][imgs], ref), "int8 bottleneck must be bit-exact"
+    # whole batch: output range and batch-permutation commutation (bit-exact)
+    assert out["out"].min() >= 0
+    d = configs.to_device(arrs)
+    perm = torch.arange(31, -1, -1, device="cuda")
+    inp2 = dict(arrs, x=_host(d["x"][perm].contiguous()))
+    assert np.array_equal(_qb_run(inp2), out["out"][::-1])
+
+
+@pytest.mark.parametrize("N,H,W,C,M1", [
+    (2, 9, 13, 256, 64),   # ragged tiles on both spatial dims
+    (1, 8, 8, 64, 64),     # exactly one tile
+    (3, 5, 3, 128, 64),    # image smaller than a tile
+    (1, 1, 1, 256, 64),    # single pixel: only the centre tap sees data
+])
+def test_c4_qbottleneck_shapes(cuda, N, H, W, C, M1):
+    inp = _qb_inputs(N, H, W, C, M1, 21 + H)
+    ref = oracle.block_qbottleneck(**inp)
+    assert np.array_equal(_qb_run(inp), ref)
+
+
+def test_c4_requant_extremes(cuda):
+    """Shifts at both ends of the TOSA range and multipliers at the int32
+    limits: the kernel's 64-bit rounding must match the oracle bit for bit."""
+    N, H, W, C, M1 = 1, 8, 8, 256, 64
+    inp = _qb_inputs(N, H, W, C, M1, 77)
+    inp["m1"][:] = 2 ** 31 - 1
+    inp["s1"][:] = rng.randint(78, 0, (M1,), 36, 62).astype(np.int32)
+    inp["m2"][:8] = 0
+    inp["s2"][:] = 30
+    # low end of the shift range with multipliers small enough that the
+    # rescaled value still fits int32 (the apply_scale precondition)
+    inp["m3"][:] = rng.randint(79, 0, (C,), 1, 4096).astype(np.int32)
+    inp["s3"][:] = 2
+    ref = oracle.block_qbottleneck(**inp)
+    assert np.array_equal(_qb_run(inp), ref)
+
+
+# ------------------------------------------------------------------ C3
+def test_c3_irb_config_n1(cuda):
+    w = configs.irb(1)
+    arrs, out = _run_workload(w)
+    ref, mag = refs.reference(w.name, arrs)["out"]
+    check_bound(out["out"], ref, mag, RTOL_F32, what=w.name)
+
+
+def test_c3_irb_config_n32(cuda):
+    w = configs.irb(32)
+    arrs, out = _run_workload(w)
+    imgs = [0, 9, 31]
+    ref, mag = refs.reference(w.name, arrs, images=imgs)["out"]
+    check_bound(out["out"][imgs], ref, mag, RTOL_F32, what=w.name)
+    assert np.isfinite(out["out"]).all()
+
+
+@pytest.mark.parametrize("N,H,W,C,E", [
+    (2, 9, 13, 24, 144),   # ragged tiles
+    (1, 3, 5, 24, 144),    # image smaller than a tile
+    (2, 8, 8, 16, 96),     # other block widths of the network
+    (1, 10, 7, 32, 192),
+])
+def test_c3_irb_shapes(cuda, N, H, W, C, E):
+    x = rng.uniform(31, 0, (N, H, W, C), 0, 1)
+    we = rng.normal(31, 1, (E, C), 0, math.sqrt(2 / C))
+    wdw = rng.normal(31, 2, (3, 3, E), 0, math.sqrt(2 / 9))
+    wp = rng.normal(31, 3, (C, E), 0, math.sqrt(2 / E))
+    d = configs.to_device({"x": x, "we": we, "wdw": wdw, "wp": wp})
+    out = torch.empty_like(d["x"])
+    groups.fused_irb_f32(d["x"], d["we"], d["wdw"], d["wp"], out)
+    torch.cuda.synchronize()
+    ref, mag = refs.irb(x, we, wdw, wp)
+    check_bound(_host(out), ref, mag, RTOL_F32, what=f"irb {N}x{H}x{W}x{C}/{E}")
+
+
+def test_c3_irb_relu6_clamps_both_sides(cuda):
+    """Large weights drive the expand and depthwise stages past 6 and below 0."""
+    N, H, W, C, E = 1, 8, 8, 24, 144
+    x = rng.uniform(32, 0, (N, H, W, C), 0, 4)
+    we = rng.normal(32, 1, (E, C), 0, 2.0)
+    wdw = rng.normal(32, 2, (3, 3, E), 0, 2.0)
+    wp = rng.normal(32, 3, (C, E), 0, 0.1)
+    d = configs.to_device({"x": x, "we": we, "wdw": wdw, "wp": wp})
+    out = torch.empty_like(d["x"])
+    groups.fused_irb_f32(d["x"], d["we"], d["wdw"], d["wp"], out)
+    torch.cuda.synchronize()
+    ref, mag = refs.irb(x, we, wdw, wp)
+    check_bound(_host(out), ref, mag, RTOL_F32, what="irb clamps")
+
+
+# ------------------------------------------------------------------ C5
+LL_H, LL_EPS = 8, 1e-5
+
+
+@pytest.fixture(scope="module")
+def llama_case():
+    w = configs.llama_layer()
+    inp = w.make_inputs()
+    return w, inp, refs.llama_stages(inp, LL_H, LL_EPS)
+
+
+def _bf_dev(shape):
+    return torch.empty(shape, dtype=torch.bfloat16, device="cuda")
+
+
+def test_c5_stage_qkv_rope(cuda, llama_case):
+    w, inp, st = llama_case
+    d = configs.to_device(inp)
+    S, D = inp["x"].shape
+    Q, K, V = _bf_dev((S, D)), _bf_dev((S, D)), _bf_dev((S, D))
+    groups.fused_llama_qkv_rope(d["x"], d["g1"], d["wq"], d["wk"], d["wv"], d["cos_t"],
+                                d["sin_t"], Q, K, V, LL_EPS)
+    torch.cuda.synchronize()
+    xn = refs.normed_bf16(inp["x"], inp["g1"], LL_EPS)
+    for name, t, wname, rope in (("Q", Q, "wq", True), ("K", K, "wk", True), ("V", V, "wv", False)):
+        mag = refs.mag_qkv(xn, inp[wname], inp["cos_t"], inp["sin_t"], rope)
+        check_bound(bf16(_host(t)), bf16(st[name]), mag, RTOL_BF16, what=name)
+    # position 0 is not rotated: Q row 0 equals the plain projection's rounding
+    q0 = bf16(_host(Q))[0]
+    plain0 = bf16(xn)[0] @ bf16(inp["wq"])
+    assert np.allclose(q0, plain0, rtol=1e-2, atol=1e-3)
+
+
+def test_c5_stage_attention(cuda, llama_case):
+    w, inp, st = llama_case
+    d = configs.to_device({k: st[k] for k in ("Q", "K", "V")})
+    A = _bf_dev(st["A"].shape)
+    groups.fused_llama_attention(d["Q"], d["K"], d["V"], A, LL_H, 0.125)
+    torch.cuda.synchronize()
+    mag = refs.mag_attention(st["Q"], st["K"], st["V"], LL_H)
+    check_bound(bf16(_host(A)), bf16(st["A"]), mag, RTOL_BF16, what="attention")
+    # causal: row 0 attends only to key 0, so it equals V's row 0 exactly
+    assert np.array_equal(_host(A)[0], st["V"][0])
+
+
+def test_c5_stage_oproj_residual(cuda, llama_case):
+    w, inp, st = llama_case
+    d = configs.to_device({"A": st["A"], "wo": inp["wo"], "x": inp["x"]})
+    h = _bf_dev(inp["x"].shape)
+    groups.fused_llama_matmul_residual(d["A"], d["wo"], d["x"], h)
+    torch.cuda.synchronize()
+    mag = refs.mag_residual(st["A"], inp["wo"], inp["x"])
+    check_bound(bf16(_host(h)), bf16(st["h"]), mag, RTOL_BF16, what="h")
+
+
+def test_c5_stage_swiglu(cuda, llama_case):
+    w, inp, st = llama_case
+    d = configs.to_device({"h": st["h"], "g2": inp["g2"], "wg": inp["wg"], "wu": inp["wu"]})
+    act = _bf_dev(st["act"].shape)
+    groups.fused_llama_rmsnorm_swiglu(d["h"], d["g2"], d["wg"], d["wu"], act, LL_EPS)
+    torch.cuda.synchronize()
+    hn = refs.normed_bf16(st["h"], inp["g2"], LL_EPS)
+    mag = refs.mag_swiglu(hn, inp["wg"], inp["wu"])
+    check_bound(bf16(_host(act)), bf16(st["act"]), mag, RTOL_BF16, what="act")
+
+
+def test_c5_stage_down_residual(cuda, llama_case):
+    w, inp, st = llama_case
+    d = configs.to_device({"act": st["act"], "wd": inp["wd"], "h": st["h"]})
+    out = _bf_dev(inp["x"].shape)
+    groups.fused_llama_matmul_residual(d["act"], d["wd"], d["h"], out)
+    torch.cuda.synchronize()
+    mag = refs.mag_residual(st["act"], inp["wd"], st["h"])
+    check_bound(bf16(_host(out)), bf16(st["out"]), mag, RTOL_BF16, what="out")
+
+
+def test_c5_layer_end_to_end(cuda, llama_case):
+    w, inp, st = llama_case
+    d = configs.to_device(inp)
+    o = w.make_outputs(d)
+    w.run(d, o, None)
+    torch.cuda.synchronize()
+    for name, (ref, mag) in refs.reference(w.name, inp).items():
+        check_bound(bf16(_host(o[name])), bf16(ref), mag, RTOL_BF16, what=f"layer {name}")
+
+
+@pytest.mark.parametrize("S,D,H,F", [(64, 128, 2, 192), (128, 64, 1, 64)])
+def test_c5_layer_small_shapes(cuda, S, D, H, F):
+    w = configs.llama_layer(S=S, D=D, H=H, F=F, seed=91 + S)
+    inp = w.make_inputs()
+    d = configs.to_device(inp)
+    o = w.make_outputs(d)
+    groups.llama_layer(d, o, H, LL_EPS)
+    torch.cuda.synchronize()
+    for name, (ref, mag) in refs.llama_reference(inp, H, LL_EPS).items():
+        check_bound(bf16(_host(o[name])), bf16(ref), mag, RTOL_BF16, what=f"layer {name}")
