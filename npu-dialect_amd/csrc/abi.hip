@@ -204,8 +204,11 @@ npu_status fused_conv2d_nhwc_bias_act(const npu_memref *x, const npu_memref *w,
                   (int)N, (int)H, (int)W, (int)C, (int)F, (int)KH, (int)KW, pad,
                   (int)Ho, (int)Wo, act};
   hipStream_t s = static_cast<hipStream_t>(stream);
-  hipError_t e = dt == NPU_F32 ? npu::launch_conv2d_nhwc_f32(a, s)
-                               : npu::launch_conv2d_nhwc_bf16(a, s);
+  hipError_t e;
+  if (npu::conv3x3_rows_supported(a, dt == NPU_F32 ? 4 : 2))
+    e = dt == NPU_F32 ? npu::launch_conv3x3_f32(a, s) : npu::launch_conv3x3_bf16(a, s);
+  else
+    e = dt == NPU_F32 ? npu::launch_conv2d_nhwc_f32(a, s) : npu::launch_conv2d_nhwc_bf16(a, s);
   return hip_status(e, "fused_conv2d_nhwc_bias_act launch");
 }
 
@@ -315,8 +318,8 @@ npu_status check_1d(const npu_memref *m, const char *name, int32_t dtype, int64_
 }
 
 npu_status check_gemm_dims(int64_t S, int64_t K, int64_t N) {
-  if (S % 64 != 0) return fail(NPU_ERR_UNSUPPORTED, "S = %lld must be a multiple of 64", (long long)S);
-  if (K % 32 != 0) return fail(NPU_ERR_UNSUPPORTED, "K = %lld must be a multiple of 32", (long long)K);
+  if (S % 32 != 0) return fail(NPU_ERR_UNSUPPORTED, "S = %lld must be a multiple of 32", (long long)S);
+  if (K % 64 != 0) return fail(NPU_ERR_UNSUPPORTED, "K = %lld must be a multiple of 64", (long long)K);
   if (N % 64 != 0) return fail(NPU_ERR_UNSUPPORTED, "N = %lld must be a multiple of 64", (long long)N);
   return NPU_OK;
 }

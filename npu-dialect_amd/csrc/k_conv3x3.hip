@@ -1,0 +1,172 @@
+// k_conv3x3.hip -- group `pad -> fill -> conv_2d_nhwc_fhwc(3x3, stride 1) ->
+// generic(bias, act)` for images up to 64 pixels wide: the shape of the
+// conv2d configurations (56x56x64 -> 64).
+//
+// A workgroup owns TR full image rows of one image and 64 (or 16) filters.
+// The reduction runs over channel chunks (16 f32 / 32 bf16 = one MFMA
+// operand run).  For each chunk the zero-padded (TR+2) x (W+2) input halo is
+// staged once into LDS and all nine taps read their A operands from it with
+// shifted addressing, so each input element leaves HBM/L2 once per chunk
+// instead of once per tap.  The next chunk's halo is fetched into registers
+// while the current one is multiplied (double-buffered LDS, one barrier per
+// chunk).  Filters are read straight from L2 as B operands (FHWC keeps each
+// lane's channel run contiguous); the pad of tensor.pad is the zero fill of
+// out-of-image halo records.
+//
+// LDS record: one pixel's 64 bytes of the chunk plus 16 bytes of padding, so
+// the 16 lanes that read 16 consecutive pixels hit distinct bank groups.
+#include "kernels.hpp"
+#include "npu_device.hpp"
+
+namespace npu {
+
+namespace {
+
+constexpr int kWMax = 64;      // widest image row this kernel stages
+constexpr int kRecBytes = 80;  // 64 data bytes + 16 pad
+
+template <class MM, typename T, int TR, int WF>
+__global__ __launch_bounds__(256) void conv3x3_rows_kernel(
+    const T *__restrict__ x, const T *__restrict__ w, const float *__restrict__ bias,
+    T *__restrict__ out, int H, int W, int C, int F, int act) {
+  constexpr int WP = 4 / WF;                 // waves along pixels
+  constexpr int KPL = MM::kPerLane;          // elements of one lane's 16-byte run
+  constexpr int KC = MM::kPerFrag;           // channels per chunk (64 bytes)
+  constexpr int REC = kRecBytes / sizeof(T); // LDS record stride in elements
+  constexpr int HR = TR + 2;
+  constexpr int PBMAX = (TR * kWMax + 15) / 16;
+  constexpr int PBW = (PBMAX + WP - 1) / WP; // pixel blocks per wave
+  constexpr int SEGS = (HR * (kWMax + 2) * 4 + 255) / 256;
+  static_assert(KC * sizeof(T) == 64, "a chunk is 64 bytes per pixel");
+  __shared__ __attribute__((aligned(16))) T halo[2][HR * (kWMax + 2) * REC];
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int r = lane & 15, q = lane >> 4;
+  const int tiles_h = (H + TR - 1) / TR;
+  const int n = blockIdx.x / tiles_h, h0 = (blockIdx.x - n * tiles_h) * TR;
+  const int f = (blockIdx.y * WF + (wave % WF)) * 16 + r;
+  const bool fok = f < F;
+  const int wp = wave / WF;
+  const int HC = W + 2, nseg = HR * HC * 4;
+  const int tile_px = TR * W;
+
+  // Per-lane pixel rows of the A operand (pixel = pb*16 + r within the tile).
+  int abase[PBW];
+  bool aok[PBW];
+#pragma unroll
+  for (int i = 0; i < PBW; ++i) {
+    const int p = (wp + i * WP) * 16 + r;
+    aok[i] = p < tile_px;
+    const int pr = aok[i] ? p / W : 0, pc = aok[i] ? p - pr * W : 0;
+    abase[i] = (pr * HC + pc) * REC + q * KPL;
+  }
+
+  u32x4 stage[SEGS];
+  auto fetch = [&](int c0) {
+#pragma unroll
+    for (int s = 0; s < SEGS; ++s) {
+      const int idx = tid + 256 * s;
+      stage[s] = u32x4{0u, 0u, 0u, 0u};
+      if (idx < nseg) {
+        const int rec = idx >> 2, seg = idx & 3;
+        const int hr = rec / HC, hc = rec - hr * HC;
+        const int ih = h0 + hr - 1, iw = hc - 1;
+        if (ih >= 0 && ih < H && iw >= 0 && iw < W)
+          stage[s] = *reinterpret_cast<const u32x4 *>(
+              x + ((size_t)(n * H + ih) * W + iw) * C + c0 + seg * (16 / sizeof(T)));
+      }
+    }
+  };
+  auto commit = [&](int buf) {
+#pragma unroll
+    for (int s = 0; s < SEGS; ++s) {
+      const int idx = tid + 256 * s;
+      if (idx < nseg)
+        *reinterpret_cast<u32x4 *>(&halo[buf][(idx >> 2) * REC + (idx & 3) * (16 / sizeof(T))]) =
+            stage[s];
+    }
+  };
+
+  typename MM::acc_t acc[PBW];
+#pragma unroll
+  for (int i = 0; i < PBW; ++i) acc[i] = typename MM::acc_t{0, 0, 0, 0};
+
+  fetch(0);
+  commit(0);
+  __syncthreads();
+  const int nchunks = C / KC;
+  const T *wrow = w + (size_t)(fok ? f : 0) * 9 * C + q * KPL;
+  for (int c = 0; c < nchunks; ++c) {
+    Frag16 b[9];
+#pragma unroll
+    for (int t = 0; t < 9; ++t) b[t] = fok ? load16(wrow + t * C + c * KC) : frag_zero();
+    if (c + 1 < nchunks) fetch((c + 1) * KC);
+    const T *hb = halo[c & 1];
+#pragma unroll
+    for (int t = 0; t < 9; ++t) {
+      const int toff = ((t / 3) * HC + (t % 3)) * REC;
+#pragma unroll
+      for (int i = 0; i < PBW; ++i) {
+        const Frag16 a = aok[i] ? load16(hb + abase[i] + toff) : frag_zero();
+        MM::mma(acc[i], a, b[t]);
+      }
+    }
+    if (c + 1 < nchunks) commit((c + 1) & 1);
+    __syncthreads();
+  }
+
+  if (!fok) return;
+  const float bv = bias ? bias[f] : 0.0f;
+#pragma unroll
+  for (int i = 0; i < PBW; ++i) {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int p = (wp + i * WP) * 16 + 4 * q + e;
+      if (p >= tile_px) continue;
+      const int pr = p / W, pc = p - pr * W;
+      if (h0 + pr >= H) continue;
+      const float v = act_apply(acc[i][e] + bv, act);
+      const size_t o = ((size_t)(n * H + h0 + pr) * W + pc) * F + f;
+      if constexpr (sizeof(T) == 4) {
+        out[o] = v;
+      } else {
+        out[o] = f32_to_bf16(v);
+      }
+    }
+  }
+}
+
+template <class MM, typename T, int TR, int WF>
+hipError_t launch_rows(const ConvArgs &a, hipStream_t s) {
+  const int tiles_h = (a.H + TR - 1) / TR;
+  dim3 grid(a.N * tiles_h, (a.F + 16 * WF - 1) / (16 * WF));
+  hipLaunchKernelGGL((conv3x3_rows_kernel<MM, T, TR, WF>), grid, dim3(256), 0, s,
+                     static_cast<const T *>(a.x), static_cast<const T *>(a.w), a.bias,
+                     static_cast<T *>(a.out), a.H, a.W, a.C, a.F, a.act);
+  return hipGetLastError();
+}
+
+// Two launch shapes: with many row tiles, each workgroup covers 2 rows x 64
+// filters (waves split the filters); with few (batch 1), 1 row x 16 filters
+// (waves split the row) so the grid still spreads over the CUs.
+template <class MM, typename T>
+hipError_t launch_conv3x3(const ConvArgs &a, hipStream_t s) {
+  if (a.N * ((a.H + 1) / 2) >= 512) return launch_rows<MM, T, 2, 4>(a, s);
+  return launch_rows<MM, T, 1, 1>(a, s);
+}
+
+}  // namespace
+
+bool conv3x3_rows_supported(const ConvArgs &a, int elem_bytes) {
+  const int kc = 64 / elem_bytes;
+  return a.KH == 3 && a.KW == 3 && a.pad == 1 && a.W <= kWMax && a.C % kc == 0 && a.F % 16 == 0;
+}
+
+hipError_t launch_conv3x3_f32(const ConvArgs &a, hipStream_t s) {
+  return launch_conv3x3<MfmaF32, float>(a, s);
+}
+hipError_t launch_conv3x3_bf16(const ConvArgs &a, hipStream_t s) {
+  return launch_conv3x3<MfmaBF16, uint16_t>(a, s);
+}
+
+}  // namespace npu

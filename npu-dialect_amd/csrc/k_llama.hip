@@ -9,16 +9,20 @@
 //   swiglu: hn = bf16(rmsnorm(h)*g2); act = bf16(silu(hn@Wg) * (hn@Wu))
 //   down  : out = bf16(h + act@Wd)
 //
-// The four matmul groups share one bf16 MFMA GEMM (v_mfma_f32_16x16x32_bf16)
-// with a 64x64 workgroup tile and K chunks of 32 staged through LDS.  The
-// weights are row-major [K][N] as linalg.matmul takes them, so each B chunk
-// is transposed on its way into LDS to give every lane a 16-byte k run.  The
-// RMSNorm is fused as a prologue (row inverse-RMS first, then the normalised
-// bf16 A chunk is produced while staging), RoPE / residual / SiLU-gating as
-// epilogues on the accumulators; nothing between the ops touches HBM.
+// GEMM groups: one bf16 MFMA kernel (v_mfma_f32_16x16x32_bf16), 32x64
+// workgroup tiles (the layer's M = 512 rows give 128-384 workgroups), K in
+// chunks of 64 staged through double-buffered LDS: the next chunk's global
+// loads are in flight while the current chunk is multiplied, one barrier per
+// chunk.  Weights are row-major [K][N] as linalg.matmul takes them; each B
+// chunk is transposed on its way into LDS, two k rows at a time, so that a
+// lane's MFMA operand is one 16-byte k run.  RMSNorm is a prologue (row
+// inverse-RMS, then the normalised bf16 A chunk is formed while staging);
+// RoPE, residual and SiLU-gating are epilogues on the accumulators.
 //
-// Attention is a causal flash kernel: one wave per 16 query rows of one head,
-// online softmax in f32, P rounded to bf16 for its MFMA with V.
+// Attention: causal flash attention, one workgroup per (head, 64 queries),
+// four waves of 16 query rows.  Key blocks of 64 (K rows and V transposed)
+// are staged once in LDS for the four waves, the next block prefetched into
+// registers; online softmax in f32; P rounded to bf16 for its MFMA with V.
 #include "kernels.hpp"
 #include "npu_device.hpp"
 
@@ -26,16 +30,26 @@ namespace npu {
 
 namespace {
 
-constexpr int TM = 64, TN = 64, TK = 32;
-constexpr int LDK = TK + 8;  // LDS row stride (elements) of the [row][k] staging tiles
+constexpr int TM = 32, TN = 64, TK = 64;
+constexpr int LDA = TK + 8;  // LDS row stride (elements) of the [row][k] tiles: 144 bytes
 
 __device__ __forceinline__ float silu(float g) { return g / (1.0f + expf(-g)); }
+
+__device__ __forceinline__ float bf_lo(uint32_t u) { return __uint_as_float(u << 16); }
+__device__ __forceinline__ float bf_hi(uint32_t u) { return __uint_as_float(u & 0xffff0000u); }
+
+// Pack element j (0..7) of two 8-element bf16 runs into one 32-bit word:
+// low half from run a, high half from run b.
+__device__ __forceinline__ uint32_t pair_word(const u32x4 &a, const u32x4 &b, int j) {
+  const uint32_t wa = a[j >> 1], wb = b[j >> 1];
+  return (j & 1) ? ((wa >> 16) | (wb & 0xffff0000u)) : ((wa & 0xffffu) | (wb << 16));
+}
 
 template <int PRO, int EPI>
 __global__ __launch_bounds__(256) void llama_gemm_kernel(const LlamaGemmArgs a) {
   constexpr int NB = (EPI == kEpiSwiglu) ? 2 : 1;
-  __shared__ __attribute__((aligned(16))) uint16_t As[TM * LDK];
-  __shared__ __attribute__((aligned(16))) uint16_t Bs[NB][TN * LDK];
+  __shared__ __attribute__((aligned(16))) uint16_t As[2][TM * LDA];
+  __shared__ __attribute__((aligned(16))) uint16_t Bs[2][NB][TN * LDA];
   __shared__ float inv_rms[TM];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -44,20 +58,19 @@ __global__ __launch_bounds__(256) void llama_gemm_kernel(const LlamaGemmArgs a) 
   const int tiles_per_part = a.Npart / TN;
   const int part = (EPI == kEpiQkvRope) ? blockIdx.x / tiles_per_part : 0;
   const int n0 = (blockIdx.x % tiles_per_part) * TN;
-  const uint16_t *B0 = a.B[part];
-  const uint16_t *B1 = a.B[NB - 1];
+  const uint16_t *Bp[2] = {a.B[part], a.B[NB - 1]};
 
   if (PRO == kProRmsnorm) {
-    // inverse RMS of the tile's rows: wave w reduces rows 16w .. 16w+15
-    for (int rr = 0; rr < 16; ++rr) {
-      const int row = m0 + wave * 16 + rr;
+    // inverse RMS of the tile's rows: wave w reduces rows 8w .. 8w+7
+    for (int rr = 0; rr < TM / 4; ++rr) {
+      const int row = m0 + wave * (TM / 4) + rr;
       float s = 0.0f;
       if (row < a.M) {
         for (int k = lane * 8; k < a.K; k += 512) {
           const Frag16 v = load16(a.A + (size_t)row * a.K + k);
 #pragma unroll
           for (int j = 0; j < 4; ++j) {
-            const float lo = __uint_as_float(v.u[j] << 16), hi = __uint_as_float(v.u[j] & 0xffff0000u);
+            const float lo = bf_lo(v.u[j]), hi = bf_hi(v.u[j]);
             s += lo * lo;
             s += hi * hi;
           }
@@ -65,111 +78,153 @@ __global__ __launch_bounds__(256) void llama_gemm_kernel(const LlamaGemmArgs a) 
       }
 #pragma unroll
       for (int off = 32; off >= 1; off >>= 1) s += __shfl_xor(s, off);
-      if (lane == 0) inv_rms[wave * 16 + rr] = 1.0f / sqrtf(s / (float)a.K + a.eps);
+      if (lane == 0) inv_rms[wave * (TM / 4) + rr] = 1.0f / sqrtf(s / (float)a.K + a.eps);
     }
     __syncthreads();
   }
 
-  f32x4 acc[NB][2][2];
-#pragma unroll
-  for (int b = 0; b < NB; ++b)
-#pragma unroll
-    for (int i = 0; i < 2; ++i)
-#pragma unroll
-      for (int j = 0; j < 2; ++j) acc[b][i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
-
-  const int wm = (wave & 1) * 32, wn = (wave >> 1) * 32;
-  const int arow = tid >> 2, akk = (tid & 3) * 8;  // A staging: 64 rows x 4 runs of 8
-  const int bk = tid >> 3, bnn = (tid & 7) * 8;    // B staging: 32 k-rows x 8 runs of 8
-  for (int k0 = 0; k0 < a.K; k0 += TK) {
-    {
-      Frag16 v = frag_zero();
-      const int row = m0 + arow;
-      if (row < a.M) v = load16(a.A + (size_t)row * a.K + k0 + akk);
-      if (PRO == kProRmsnorm) {
-        const float inv = inv_rms[arow];
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const float lo = __uint_as_float(v.u[j] << 16), hi = __uint_as_float(v.u[j] & 0xffff0000u);
-          const float ylo = (lo * inv) * a.gamma[k0 + akk + 2 * j];
-          const float yhi = (hi * inv) * a.gamma[k0 + akk + 2 * j + 1];
-          v.u[j] = (uint32_t)f32_to_bf16(ylo) | ((uint32_t)f32_to_bf16(yhi) << 16);
-        }
-      }
-      *reinterpret_cast<u32x4 *>(As + arow * LDK + akk) = v.u;
-    }
-#pragma unroll
-    for (int b = 0; b < NB; ++b) {
-      const uint16_t *Bp = b == 0 ? B0 : B1;
-      const Frag16 v = load16(Bp + (size_t)(k0 + bk) * a.Npart + n0 + bnn);
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        Bs[b][(bnn + 2 * j) * LDK + bk] = (uint16_t)(v.u[j] & 0xffffu);
-        Bs[b][(bnn + 2 * j + 1) * LDK + bk] = (uint16_t)(v.u[j] >> 16);
-      }
-    }
-    __syncthreads();
-    Frag16 af[2];
-#pragma unroll
-    for (int i = 0; i < 2; ++i) af[i] = load16(As + (wm + 16 * i + r) * LDK + 8 * q);
+  // staging assignment: A chunk [32 rows][64 k] = one 16-byte run per thread;
+  // B chunk [64 k][64 n] = two k rows x one 8-column run per thread.
+  const int arow = tid >> 3, akk = (tid & 7) * 8;
+  const int bkr = (tid >> 3) * 2, bng = (tid & 7) * 8;
+  u32x4 sa, sb[NB][2];
+  auto fetch = [&](int k0) {
+    const int row = m0 + arow;
+    sa = row < a.M ? load16(a.A + (size_t)row * a.K + k0 + akk).u : u32x4{0u, 0u, 0u, 0u};
 #pragma unroll
     for (int b = 0; b < NB; ++b)
 #pragma unroll
-      for (int j = 0; j < 2; ++j) {
-        const Frag16 bf = load16(Bs[b] + (wn + 16 * j + r) * LDK + 8 * q);
+      for (int h = 0; h < 2; ++h)
+        sb[b][h] = load16(Bp[b] + (size_t)(k0 + bkr + h) * a.Npart + n0 + bng).u;
+  };
+  auto commit = [&](int buf, int k0) {
+    u32x4 v = sa;
+    if (PRO == kProRmsnorm) {
+      const float inv = inv_rms[arow];
 #pragma unroll
-        for (int i = 0; i < 2; ++i) MfmaBF16::mma(acc[b][i][j], af[i], bf);
+      for (int j = 0; j < 4; ++j) {
+        const float ylo = (bf_lo(v[j]) * inv) * a.gamma[k0 + akk + 2 * j];
+        const float yhi = (bf_hi(v[j]) * inv) * a.gamma[k0 + akk + 2 * j + 1];
+        v[j] = (uint32_t)f32_to_bf16(ylo) | ((uint32_t)f32_to_bf16(yhi) << 16);
       }
+    }
+    *reinterpret_cast<u32x4 *>(&As[buf][arow * LDA + akk]) = v;
+#pragma unroll
+    for (int b = 0; b < NB; ++b)
+#pragma unroll
+      for (int j = 0; j < 8; ++j)
+        *reinterpret_cast<uint32_t *>(&Bs[buf][b][(bng + j) * LDA + bkr]) =
+            pair_word(sb[b][0], sb[b][1], j);
+  };
+
+  f32x4 acc[NB][2];
+#pragma unroll
+  for (int b = 0; b < NB; ++b)
+#pragma unroll
+    for (int j = 0; j < 2; ++j) acc[b][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  // wave (wm, wn): rows 16*wm.., columns 32*wn.. (two 16-column tiles)
+  const int wm = (wave & 1) * 16, wn = (wave >> 1) * 32;
+  const int nchunks = a.K / TK;
+  fetch(0);
+  commit(0, 0);
+  __syncthreads();
+  for (int c = 0; c < nchunks; ++c) {
+    if (c + 1 < nchunks) fetch((c + 1) * TK);
+    const int buf = c & 1;
+#pragma unroll
+    for (int ks = 0; ks < TK / 32; ++ks) {
+      const Frag16 af = load16(&As[buf][(wm + r) * LDA + 32 * ks + 8 * q]);
+#pragma unroll
+      for (int b = 0; b < NB; ++b)
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+          const Frag16 bf = load16(&Bs[buf][b][(wn + 16 * j + r) * LDA + 32 * ks + 8 * q]);
+          MfmaBF16::mma(acc[b][j], af, bf);
+        }
+    }
+    if (c + 1 < nchunks) commit(buf ^ 1, (c + 1) * TK);
     __syncthreads();
   }
 
-  // ---- epilogues: element (row m, column n) = acc[.][i][j][e]
+  // ---- epilogues: element (row m, column n) = acc[.][j][e]
 #pragma unroll
-  for (int i = 0; i < 2; ++i)
+  for (int j = 0; j < 2; ++j) {
+    const int n = n0 + wn + 16 * j + r;
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      const int n = n0 + wn + 16 * j + r;
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const int m = m0 + wm + 16 * i + 4 * q + e;
-        const float v = acc[0][i][j][e];
-        float y;
-        if (EPI == kEpiQkvRope) {
-          // RoPE pairs (2t, 2t+1) sit in adjacent lanes (columns r, r^1).
-          const float partner = __shfl_xor(v, 1);
-          y = v;
-          if (part < 2 && m < a.M) {
-            const int t = (n % a.Dh) >> 1;
-            const float c = a.cos_t[m * (a.Dh / 2) + t], s = a.sin_t[m * (a.Dh / 2) + t];
-            y = (n & 1) ? (partner * s + v * c) : (v * c - partner * s);
-          }
-        } else if (EPI == kEpiResidual) {
-          y = m < a.M ? bf16_to_f32(a.res[(size_t)m * a.Npart + n]) + v : 0.0f;
-        } else {
-          y = silu(v) * acc[NB - 1][i][j][e];
+    for (int e = 0; e < 4; ++e) {
+      const int m = m0 + wm + 4 * q + e;
+      const float v = acc[0][j][e];
+      float y;
+      if (EPI == kEpiQkvRope) {
+        // RoPE pairs (2t, 2t+1) sit in adjacent lanes (columns r, r^1).
+        const float partner = __shfl_xor(v, 1);
+        y = v;
+        if (part < 2 && m < a.M) {
+          const int t = (n % a.Dh) >> 1;
+          const float c = a.cos_t[m * (a.Dh / 2) + t], s = a.sin_t[m * (a.Dh / 2) + t];
+          y = (n & 1) ? (partner * s + v * c) : (v * c - partner * s);
         }
-        if (m < a.M) a.out[part][(size_t)m * a.Npart + n] = f32_to_bf16(y);
+      } else if (EPI == kEpiResidual) {
+        y = m < a.M ? bf16_to_f32(a.res[(size_t)m * a.Npart + n]) + v : 0.0f;
+      } else {
+        y = silu(v) * acc[NB - 1][j][e];
       }
+      if (m < a.M) a.out[part][(size_t)m * a.Npart + n] = f32_to_bf16(y);
     }
+  }
 }
 
-// Causal attention for head dimension 64: one wave owns 16 query rows of one
-// head and walks the key blocks of 32 up to its diagonal.
-__global__ __launch_bounds__(64) void llama_attention_kernel(const uint16_t *__restrict__ Q,
-                                                             const uint16_t *__restrict__ K,
-                                                             const uint16_t *__restrict__ V,
-                                                             uint16_t *__restrict__ O, int S,
-                                                             int H, float scale) {
+// Causal attention, head dimension 64.
+constexpr int AQ = 64;          // queries per workgroup (4 waves x 16)
+constexpr int AK = 64;          // keys per block
+constexpr int LDK = 64 + 8;     // LDS row stride of K rows, V^T rows, P rows (elements)
+
+__global__ __launch_bounds__(256) void llama_attention_kernel(const uint16_t *__restrict__ Q,
+                                                              const uint16_t *__restrict__ K,
+                                                              const uint16_t *__restrict__ V,
+                                                              uint16_t *__restrict__ O, int S,
+                                                              int H, float scale) {
   constexpr int DH = 64;
-  __shared__ __attribute__((aligned(16))) uint16_t Ps[16 * LDK];
-  const int lane = threadIdx.x, r = lane & 15, q = lane >> 4;
-  const int i0 = blockIdx.x * 16, h = blockIdx.y;
+  __shared__ __attribute__((aligned(16))) uint16_t Ks[2][AK * LDK];   // [key][d]
+  __shared__ __attribute__((aligned(16))) uint16_t Vt[2][DH * LDK];   // [d][key]
+  __shared__ __attribute__((aligned(16))) uint16_t Ps[4][16 * LDK];   // per wave [row][key]
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int r = lane & 15, q = lane >> 4;
+  const int q0 = blockIdx.x * AQ, h = blockIdx.y;
   const int D = H * DH;
+  const int i0 = q0 + wave * 16;  // this wave's first query row
 
   Frag16 qa[2];
 #pragma unroll
   for (int ks = 0; ks < 2; ++ks)
-    qa[ks] = (i0 + r < S) ? load16(Q + (size_t)(i0 + r) * D + h * DH + 32 * ks + 8 * q) : frag_zero();
+    qa[ks] = (i0 + r < S) ? load16(Q + (size_t)(i0 + r) * D + h * DH + 32 * ks + 8 * q)
+                          : frag_zero();
+
+  // staging: K block [64 keys][64 d] = 2 runs of 8 per thread; V block
+  // transposed: two keys x 8 d per thread.
+  const int kr = tid >> 2, kd = (tid & 3) * 16;       // K: key kr, d kd..kd+15
+  const int vk = (tid >> 3) * 2, vd = (tid & 7) * 8;  // V: keys vk, vk+1; d vd..vd+7
+  u32x4 sk[2], sv[2];
+  auto fetch = [&](int kb) {
+    const int key = kb + kr;
+#pragma unroll
+    for (int s2 = 0; s2 < 2; ++s2)
+      sk[s2] = key < S ? load16(K + (size_t)key * D + h * DH + kd + 8 * s2).u
+                       : u32x4{0u, 0u, 0u, 0u};
+#pragma unroll
+    for (int s2 = 0; s2 < 2; ++s2)
+      sv[s2] = (kb + vk + s2) < S ? load16(V + (size_t)(kb + vk + s2) * D + h * DH + vd).u
+                                  : u32x4{0u, 0u, 0u, 0u};
+  };
+  auto commit = [&](int buf) {
+#pragma unroll
+    for (int s2 = 0; s2 < 2; ++s2)
+      *reinterpret_cast<u32x4 *>(&Ks[buf][kr * LDK + kd + 8 * s2]) = sk[s2];
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+      *reinterpret_cast<uint32_t *>(&Vt[buf][(vd + j) * LDK + vk]) = pair_word(sv[0], sv[1], j);
+  };
 
   float mrow[4], lrow[4];
   f32x4 o[4];
@@ -181,81 +236,90 @@ __global__ __launch_bounds__(64) void llama_attention_kernel(const uint16_t *__r
 #pragma unroll
   for (int dt = 0; dt < 4; ++dt) o[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-  const int kend = min(i0 + 16, S);
-  for (int kb = 0; kb < kend; kb += 32) {
-    f32x4 s[2];
+  const int kend = min(q0 + AQ, S);  // keys beyond the block's last query are masked for all
+  const int nblocks = (kend + AK - 1) / AK;
+  fetch(0);
+  commit(0);
+  __syncthreads();
+  for (int blk = 0; blk < nblocks; ++blk) {
+    const int kb = blk * AK;
+    if (blk + 1 < nblocks) fetch(kb + AK);
+    const int buf = blk & 1;
+    const bool active = kb <= i0 + 15;  // some key of the block is visible to this wave
+    if (active) {
+      f32x4 s[4];
 #pragma unroll
-    for (int ct = 0; ct < 2; ++ct) {
-      s[ct] = f32x4{0.f, 0.f, 0.f, 0.f};
-      const int key = kb + 16 * ct + r;
+      for (int ct = 0; ct < 4; ++ct) {
+        s[ct] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int ks = 0; ks < 2; ++ks) {
+          const Frag16 kf = load16(&Ks[buf][(16 * ct + r) * LDK + 32 * ks + 8 * q]);
+          MfmaBF16::mma(s[ct], qa[ks], kf);
+        }
+      }
+      float mx[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int row = i0 + 4 * q + e;
+        mx[e] = -INFINITY;
+#pragma unroll
+        for (int ct = 0; ct < 4; ++ct) {
+          const int key = kb + 16 * ct + r;
+          const float v = (key <= row && key < S) ? s[ct][e] * scale : -INFINITY;
+          s[ct][e] = v;
+          mx[e] = fmaxf(mx[e], v);
+        }
+      }
+#pragma unroll
+      for (int off = 1; off < 16; off <<= 1)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) mx[e] = fmaxf(mx[e], __shfl_xor(mx[e], off));
+      float corr[4], sum[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const float mnew = fmaxf(mrow[e], mx[e]);
+        corr[e] = (mnew == -INFINITY) ? 1.0f : expf(mrow[e] - mnew);
+        sum[e] = 0.0f;
+#pragma unroll
+        for (int ct = 0; ct < 4; ++ct) {
+          const float p = (mnew == -INFINITY) ? 0.0f : expf(s[ct][e] - mnew);
+          s[ct][e] = p;
+          sum[e] += p;
+        }
+        mrow[e] = mnew;
+      }
+#pragma unroll
+      for (int off = 1; off < 16; off <<= 1)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) sum[e] += __shfl_xor(sum[e], off);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        lrow[e] = lrow[e] * corr[e] + sum[e];
+#pragma unroll
+        for (int dt = 0; dt < 4; ++dt) o[dt][e] *= corr[e];
+      }
+      // P (accumulator layout) -> this wave's LDS rows -> A-operand layout.
+      // Only this wave touches Ps[wave]; LDS operations of a wave complete in
+      // order, and the explicit wait makes the stores visible to the loads.
+#pragma unroll
+      for (int ct = 0; ct < 4; ++ct)
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          Ps[wave][(4 * q + e) * LDK + 16 * ct + r] = f32_to_bf16(s[ct][e]);
+      __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0)
+      __builtin_amdgcn_wave_barrier();
 #pragma unroll
       for (int ks = 0; ks < 2; ++ks) {
-        const Frag16 kf = key < S ? load16(K + (size_t)key * D + h * DH + 32 * ks + 8 * q) : frag_zero();
-        MfmaBF16::mma(s[ct], qa[ks], kf);
+        const Frag16 pa = load16(&Ps[wave][r * LDK + 32 * ks + 8 * q]);
+#pragma unroll
+        for (int dt = 0; dt < 4; ++dt) {
+          const Frag16 vf = load16(&Vt[buf][(16 * dt + r) * LDK + 32 * ks + 8 * q]);
+          MfmaBF16::mma(o[dt], pa, vf);
+        }
       }
     }
-    float mx[4];
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const int row = i0 + 4 * q + e;
-      mx[e] = -INFINITY;
-#pragma unroll
-      for (int ct = 0; ct < 2; ++ct) {
-        const int key = kb + 16 * ct + r;
-        const float v = (key <= row && key < S) ? s[ct][e] * scale : -INFINITY;
-        s[ct][e] = v;
-        mx[e] = fmaxf(mx[e], v);
-      }
-    }
-#pragma unroll
-    for (int off = 1; off < 16; off <<= 1)
-#pragma unroll
-      for (int e = 0; e < 4; ++e) mx[e] = fmaxf(mx[e], __shfl_xor(mx[e], off));
-    float corr[4], sum[4];
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const float mnew = fmaxf(mrow[e], mx[e]);
-      // rows past the end of the sequence see no key: keep them at zero
-      corr[e] = (mnew == -INFINITY) ? 1.0f : expf(mrow[e] - mnew);
-      sum[e] = 0.0f;
-#pragma unroll
-      for (int ct = 0; ct < 2; ++ct) {
-        const float p = (mnew == -INFINITY) ? 0.0f : expf(s[ct][e] - mnew);
-        s[ct][e] = p;
-        sum[e] += p;
-      }
-      mrow[e] = mnew;
-    }
-#pragma unroll
-    for (int off = 1; off < 16; off <<= 1)
-#pragma unroll
-      for (int e = 0; e < 4; ++e) sum[e] += __shfl_xor(sum[e], off);
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      lrow[e] = lrow[e] * corr[e] + sum[e];
-#pragma unroll
-      for (int dt = 0; dt < 4; ++dt) o[dt][e] *= corr[e];
-    }
-    // P (accumulator layout) -> LDS -> A-operand layout
-#pragma unroll
-    for (int ct = 0; ct < 2; ++ct)
-#pragma unroll
-      for (int e = 0; e < 4; ++e) Ps[(4 * q + e) * LDK + 16 * ct + r] = f32_to_bf16(s[ct][e]);
+    if (blk + 1 < nblocks) commit(buf ^ 1);
     __syncthreads();
-    const Frag16 pa = load16(Ps + r * LDK + 8 * q);
-    __syncthreads();
-#pragma unroll
-    for (int dt = 0; dt < 4; ++dt) {
-      Frag16 vf;
-#pragma unroll
-      for (int jj = 0; jj < 4; ++jj) {
-        const int k0 = kb + 8 * q + 2 * jj;
-        const uint32_t lo = k0 < S ? V[(size_t)k0 * D + h * DH + 16 * dt + r] : 0u;
-        const uint32_t hi = k0 + 1 < S ? V[(size_t)(k0 + 1) * D + h * DH + 16 * dt + r] : 0u;
-        vf.u[jj] = lo | (hi << 16);
-      }
-      MfmaBF16::mma(o[dt], pa, vf);
-    }
   }
 #pragma unroll
   for (int e = 0; e < 4; ++e) {
@@ -286,8 +350,8 @@ hipError_t launch_llama_gemm(const LlamaGemmArgs &a, int pro, int epi, hipStream
 
 hipError_t launch_llama_attention(const uint16_t *Q, const uint16_t *K, const uint16_t *V,
                                   uint16_t *O, int S, int H, float scale, hipStream_t s) {
-  dim3 grid((S + 15) / 16, H);
-  hipLaunchKernelGGL(llama_attention_kernel, grid, dim3(64), 0, s, Q, K, V, O, S, H, scale);
+  dim3 grid((S + AQ - 1) / AQ, H);
+  hipLaunchKernelGGL(llama_attention_kernel, grid, dim3(256), 0, s, Q, K, V, O, S, H, scale);
   return hipGetLastError();
 }
 

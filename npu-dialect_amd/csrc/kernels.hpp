@@ -23,6 +23,10 @@ struct ConvArgs {
 };
 hipError_t launch_conv2d_nhwc_f32(const ConvArgs &a, hipStream_t s);
 hipError_t launch_conv2d_nhwc_bf16(const ConvArgs &a, hipStream_t s);
+// 3x3 / stride 1 / pad 1 with rows of at most 64 pixels: LDS halo kernel.
+bool conv3x3_rows_supported(const ConvArgs &a, int elem_bytes);
+hipError_t launch_conv3x3_f32(const ConvArgs &a, hipStream_t s);
+hipError_t launch_conv3x3_bf16(const ConvArgs &a, hipStream_t s);
 
 struct QBottleneckArgs {
   const int8_t *x, *w1, *w2, *w3;

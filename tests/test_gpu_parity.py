@@ -118,6 +118,13 @@ def test_c2_conv_config_n32(cuda, dtype):
     (1, 6, 6, 16, 16, 3, 0, "relu", True, "f32"),    # valid (unpadded) conv
     (2, 5, 7, 32, 16, 3, 1, "relu", True, "bf16"),
     (1, 9, 6, 64, 80, 3, 1, "relu6", False, "bf16"),
+    # 3x3/pad-1 LDS-halo kernel: the 2-row x 64-filter shape needs >= 512 row
+    # pairs; an odd H leaves a half tile at the bottom of each image
+    (64, 17, 9, 16, 64, 3, 1, "relu", True, "f32"),
+    (64, 17, 9, 32, 80, 3, 1, "relu", True, "bf16"),
+    (1, 3, 64, 16, 32, 3, 1, "relu", True, "f32"),    # widest row the LDS tile holds
+    (1, 4, 70, 16, 16, 3, 1, "relu", True, "f32"),    # wider: general kernel
+    (2, 6, 66, 32, 16, 3, 1, "relu", True, "bf16"),
 ])
 def test_c2_conv_shapes(cuda, N, H, W, C, F, K, pad, act, bias, dtype):
     x = rng.uniform(12, 0, (N, H, W, C), 0, 1)
@@ -350,7 +357,7 @@ def test_c5_layer_end_to_end(cuda, llama_case):
         check_bound(bf16(_host(o[name])), bf16(ref), mag, RTOL_BF16, what=f"layer {name}")
 
 
-@pytest.mark.parametrize("S,D,H,F", [(64, 128, 2, 192), (128, 64, 1, 64)])
+@pytest.mark.parametrize("S,D,H,F", [(64, 128, 2, 192), (128, 64, 1, 64), (96, 128, 2, 128)])
 def test_c5_layer_small_shapes(cuda, S, D, H, F):
     w = configs.llama_layer(S=S, D=D, H=H, F=F, seed=91 + S)
     inp = w.make_inputs()
