@@ -51,30 +51,31 @@ __global__ __launch_bounds__(256) void conv3x3_rows_kernel(
   const int tile_px = TR * W;
 
   // Per-lane pixel rows of the A operand (pixel = pb*16 + r within the tile).
+  // Rows past the tile read a valid (clamped) record: they only feed output
+  // rows that are never stored, so they need no zeroing.
   int abase[PBW];
-  bool aok[PBW];
 #pragma unroll
   for (int i = 0; i < PBW; ++i) {
-    const int p = (wp + i * WP) * 16 + r;
-    aok[i] = p < tile_px;
-    const int pr = aok[i] ? p / W : 0, pc = aok[i] ? p - pr * W : 0;
+    const int p = min((wp + i * WP) * 16 + r, tile_px - 1);
+    const int pr = p / W, pc = p - pr * W;
     abase[i] = (pr * HC + pc) * REC + q * KPL;
   }
 
+  // Halo staging: 16-byte segments, loads from clamped addresses, the zero
+  // padding applied by a select.
   u32x4 stage[SEGS];
   auto fetch = [&](int c0) {
 #pragma unroll
     for (int s = 0; s < SEGS; ++s) {
-      const int idx = tid + 256 * s;
-      stage[s] = u32x4{0u, 0u, 0u, 0u};
-      if (idx < nseg) {
-        const int rec = idx >> 2, seg = idx & 3;
-        const int hr = rec / HC, hc = rec - hr * HC;
-        const int ih = h0 + hr - 1, iw = hc - 1;
-        if (ih >= 0 && ih < H && iw >= 0 && iw < W)
-          stage[s] = *reinterpret_cast<const u32x4 *>(
-              x + ((size_t)(n * H + ih) * W + iw) * C + c0 + seg * (16 / sizeof(T)));
-      }
+      const int idx = min(tid + 256 * s, nseg - 1);
+      const int rec = idx >> 2, seg = idx & 3;
+      const int hr = rec / HC, hc = rec - hr * HC;
+      const int ih = h0 + hr - 1, iw = hc - 1;
+      const bool inside = ih >= 0 && ih < H && iw >= 0 && iw < W;
+      const int ihc = min(max(ih, 0), H - 1), iwc = min(max(iw, 0), W - 1);
+      stage[s] = masked(*reinterpret_cast<const u32x4 *>(
+                            x + ((size_t)(n * H + ihc) * W + iwc) * C + c0 + seg * (16 / sizeof(T))),
+                        inside);
     }
   };
   auto commit = [&](int buf) {
@@ -95,21 +96,25 @@ __global__ __launch_bounds__(256) void conv3x3_rows_kernel(
   commit(0);
   __syncthreads();
   const int nchunks = C / KC;
-  const T *wrow = w + (size_t)(fok ? f : 0) * 9 * C + q * KPL;
+  // Filters past F read filter F-1: they only feed columns that are not stored.
+  const T *wrow = w + (size_t)min(f, F - 1) * 9 * C + q * KPL;
   for (int c = 0; c < nchunks; ++c) {
     Frag16 b[9];
 #pragma unroll
-    for (int t = 0; t < 9; ++t) b[t] = fok ? load16(wrow + t * C + c * KC) : frag_zero();
+    for (int t = 0; t < 9; ++t) b[t] = load16(wrow + t * C + c * KC);
     if (c + 1 < nchunks) fetch((c + 1) * KC);
     const T *hb = halo[c & 1];
 #pragma unroll
     for (int t = 0; t < 9; ++t) {
       const int toff = ((t / 3) * HC + (t % 3)) * REC;
+      Frag16 a[PBW];
 #pragma unroll
-      for (int i = 0; i < PBW; ++i) {
-        const Frag16 a = aok[i] ? load16(hb + abase[i] + toff) : frag_zero();
-        MM::mma(acc[i], a, b[t]);
-      }
+      for (int i = 0; i < PBW; ++i) a[i] = load16(hb + abase[i] + toff);
+      // independent accumulators between the dependent steps of one fragment
+#pragma unroll
+      for (int st = 0; st < MM::kSteps; ++st)
+#pragma unroll
+        for (int i = 0; i < PBW; ++i) MM::step(acc[i], a[i], b[t], st);
     }
     if (c + 1 < nchunks) commit((c + 1) & 1);
     __syncthreads();

@@ -11,7 +11,7 @@
 //
 // GEMM groups: one bf16 MFMA kernel (v_mfma_f32_16x16x32_bf16), 32x64
 // workgroup tiles (the layer's M = 512 rows give 128-384 workgroups), K in
-// chunks of 64 staged through double-buffered LDS: the next chunk's global
+// chunks of 128 staged through double-buffered LDS: the next chunk's global
 // loads are in flight while the current chunk is multiplied, one barrier per
 // chunk.  Weights are row-major [K][N] as linalg.matmul takes them; each B
 // chunk is transposed on its way into LDS, two k rows at a time, so that a
@@ -30,8 +30,8 @@ namespace npu {
 
 namespace {
 
-constexpr int TM = 32, TN = 64, TK = 64;
-constexpr int LDA = TK + 8;  // LDS row stride (elements) of the [row][k] tiles: 144 bytes
+constexpr int TM = 32, TN = 64, TK = 128;
+constexpr int LDA = TK + 8;  // LDS row stride (elements) of the [row][k] tiles: 272 bytes
 
 __device__ __forceinline__ float silu(float g) { return g / (1.0f + expf(-g)); }
 
@@ -45,9 +45,21 @@ __device__ __forceinline__ uint32_t pair_word(const u32x4 &a, const u32x4 &b, in
   return (j & 1) ? ((wa >> 16) | (wb & 0xffff0000u)) : ((wa & 0xffffu) | (wb << 16));
 }
 
+__device__ __forceinline__ float sumsq8(const u32x4 &v) {
+  float s = 0.0f;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const float lo = bf_lo(v[j]), hi = bf_hi(v[j]);
+    s += lo * lo;
+    s += hi * hi;
+  }
+  return s;
+}
+
 template <int PRO, int EPI>
 __global__ __launch_bounds__(256) void llama_gemm_kernel(const LlamaGemmArgs a) {
   constexpr int NB = (EPI == kEpiSwiglu) ? 2 : 1;
+  constexpr int RPW = TM / 4;  // RMSNorm rows per wave
   __shared__ __attribute__((aligned(16))) uint16_t As[2][TM * LDA];
   __shared__ __attribute__((aligned(16))) uint16_t Bs[2][NB][TN * LDA];
   __shared__ float inv_rms[TM];
@@ -61,60 +73,84 @@ __global__ __launch_bounds__(256) void llama_gemm_kernel(const LlamaGemmArgs a) 
   const uint16_t *Bp[2] = {a.B[part], a.B[NB - 1]};
 
   if (PRO == kProRmsnorm) {
-    // inverse RMS of the tile's rows: wave w reduces rows 8w .. 8w+7
-    for (int rr = 0; rr < TM / 4; ++rr) {
-      const int row = m0 + wave * (TM / 4) + rr;
-      float s = 0.0f;
-      if (row < a.M) {
-        for (int k = lane * 8; k < a.K; k += 512) {
-          const Frag16 v = load16(a.A + (size_t)row * a.K + k);
+    // inverse RMS of the tile's rows, wave w owning rows RPW*w ..: all of a
+    // wave's row loads are issued before any of them is reduced.
+    float s[RPW];
 #pragma unroll
-          for (int j = 0; j < 4; ++j) {
-            const float lo = bf_lo(v.u[j]), hi = bf_hi(v.u[j]);
-            s += lo * lo;
-            s += hi * hi;
-          }
-        }
+    for (int rr = 0; rr < RPW; ++rr) s[rr] = 0.0f;
+    for (int k = lane * 8; k < a.K; k += 512) {
+      u32x4 v[RPW];
+#pragma unroll
+      for (int rr = 0; rr < RPW; ++rr) {
+        const int row = m0 + wave * RPW + rr;
+        v[rr] = row < a.M ? load16(a.A + (size_t)row * a.K + k).u : u32x4{0u, 0u, 0u, 0u};
       }
 #pragma unroll
-      for (int off = 32; off >= 1; off >>= 1) s += __shfl_xor(s, off);
-      if (lane == 0) inv_rms[wave * (TM / 4) + rr] = 1.0f / sqrtf(s / (float)a.K + a.eps);
+      for (int rr = 0; rr < RPW; ++rr) s[rr] += sumsq8(v[rr]);
+    }
+#pragma unroll
+    for (int rr = 0; rr < RPW; ++rr) {
+#pragma unroll
+      for (int off = 32; off >= 1; off >>= 1) s[rr] += __shfl_xor(s[rr], off);
+    }
+    if (lane == 0) {
+#pragma unroll
+      for (int rr = 0; rr < RPW; ++rr)
+        inv_rms[wave * RPW + rr] = 1.0f / sqrtf(s[rr] / (float)a.K + a.eps);
     }
     __syncthreads();
   }
 
-  // staging assignment: A chunk [32 rows][64 k] = one 16-byte run per thread;
-  // B chunk [64 k][64 n] = two k rows x one 8-column run per thread.
+  // staging: A chunk [32 rows][128 k] = two 8-element runs per thread;
+  // B chunk [128 k][64 n] = four k rows (two pairs) x one 8-column run.
   const int arow = tid >> 3, akk = (tid & 7) * 8;
-  const int bkr = (tid >> 3) * 2, bng = (tid & 7) * 8;
-  u32x4 sa, sb[NB][2];
+  const int bkp = (tid >> 3) * 2, bng = (tid & 7) * 8;
+  u32x4 sa[2], sb[NB][4];
   auto fetch = [&](int k0) {
     const int row = m0 + arow;
-    sa = row < a.M ? load16(a.A + (size_t)row * a.K + k0 + akk).u : u32x4{0u, 0u, 0u, 0u};
+    // K is a multiple of 64: the last chunk may hold only its first half,
+    // the second half is zero-filled (and multiplies to zero).
+    // (loads from clamped addresses, masked by selects: see masked())
+    const int rowc = min(row, a.M - 1);
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const bool ok = row < a.M && k0 + 64 * h < a.K;
+      const int kc = min(k0 + 64 * h, a.K - 64);
+      sa[h] = masked(load16(a.A + (size_t)rowc * a.K + kc + akk).u, ok);
+    }
 #pragma unroll
     for (int b = 0; b < NB; ++b)
 #pragma unroll
-      for (int h = 0; h < 2; ++h)
-        sb[b][h] = load16(Bp[b] + (size_t)(k0 + bkr + h) * a.Npart + n0 + bng).u;
+      for (int h = 0; h < 4; ++h) {
+        const int k = k0 + bkp + (h & 1) + 64 * (h >> 1);
+        sb[b][h] = masked(load16(Bp[b] + (size_t)min(k, a.K - 1) * a.Npart + n0 + bng).u,
+                          k < a.K);
+      }
   };
   auto commit = [&](int buf, int k0) {
-    u32x4 v = sa;
-    if (PRO == kProRmsnorm) {
-      const float inv = inv_rms[arow];
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const float ylo = (bf_lo(v[j]) * inv) * a.gamma[k0 + akk + 2 * j];
-        const float yhi = (bf_hi(v[j]) * inv) * a.gamma[k0 + akk + 2 * j + 1];
-        v[j] = (uint32_t)f32_to_bf16(ylo) | ((uint32_t)f32_to_bf16(yhi) << 16);
+    for (int h = 0; h < 2; ++h) {
+      u32x4 v = sa[h];
+      const int kb = k0 + akk + 64 * h;
+      if (PRO == kProRmsnorm && kb < a.K) {
+        const float inv = inv_rms[arow];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const float ylo = (bf_lo(v[j]) * inv) * a.gamma[kb + 2 * j];
+          const float yhi = (bf_hi(v[j]) * inv) * a.gamma[kb + 2 * j + 1];
+          v[j] = (uint32_t)f32_to_bf16(ylo) | ((uint32_t)f32_to_bf16(yhi) << 16);
+        }
       }
+      *reinterpret_cast<u32x4 *>(&As[buf][arow * LDA + akk + 64 * h]) = v;
     }
-    *reinterpret_cast<u32x4 *>(&As[buf][arow * LDA + akk]) = v;
 #pragma unroll
     for (int b = 0; b < NB; ++b)
 #pragma unroll
-      for (int j = 0; j < 8; ++j)
-        *reinterpret_cast<uint32_t *>(&Bs[buf][b][(bng + j) * LDA + bkr]) =
-            pair_word(sb[b][0], sb[b][1], j);
+      for (int hp = 0; hp < 2; ++hp)
+#pragma unroll
+        for (int j = 0; j < 8; ++j)
+          *reinterpret_cast<uint32_t *>(&Bs[buf][b][(bng + j) * LDA + bkp + 64 * hp]) =
+              pair_word(sb[b][2 * hp], sb[b][2 * hp + 1], j);
   };
 
   f32x4 acc[NB][2];
@@ -125,7 +161,7 @@ __global__ __launch_bounds__(256) void llama_gemm_kernel(const LlamaGemmArgs a) 
 
   // wave (wm, wn): rows 16*wm.., columns 32*wn.. (two 16-column tiles)
   const int wm = (wave & 1) * 16, wn = (wave >> 1) * 32;
-  const int nchunks = a.K / TK;
+  const int nchunks = (a.K + TK - 1) / TK;
   fetch(0);
   commit(0, 0);
   __syncthreads();
@@ -178,7 +214,7 @@ __global__ __launch_bounds__(256) void llama_gemm_kernel(const LlamaGemmArgs a) 
 // Causal attention, head dimension 64.
 constexpr int AQ = 64;          // queries per workgroup (4 waves x 16)
 constexpr int AK = 64;          // keys per block
-constexpr int LDK = 64 + 8;     // LDS row stride of K rows, V^T rows, P rows (elements)
+constexpr int LDK = 64 + 8;  // LDS row stride of K rows, V^T rows, P rows (elements)
 
 __global__ __launch_bounds__(256) void llama_attention_kernel(const uint16_t *__restrict__ Q,
                                                               const uint16_t *__restrict__ K,
@@ -195,11 +231,11 @@ __global__ __launch_bounds__(256) void llama_attention_kernel(const uint16_t *__
   const int D = H * DH;
   const int i0 = q0 + wave * 16;  // this wave's first query row
 
+  // query rows past S read row S-1: their outputs are never stored
   Frag16 qa[2];
 #pragma unroll
   for (int ks = 0; ks < 2; ++ks)
-    qa[ks] = (i0 + r < S) ? load16(Q + (size_t)(i0 + r) * D + h * DH + 32 * ks + 8 * q)
-                          : frag_zero();
+    qa[ks] = load16(Q + (size_t)min(i0 + r, S - 1) * D + h * DH + 32 * ks + 8 * q);
 
   // staging: K block [64 keys][64 d] = 2 runs of 8 per thread; V block
   // transposed: two keys x 8 d per thread.
@@ -210,12 +246,12 @@ __global__ __launch_bounds__(256) void llama_attention_kernel(const uint16_t *__
     const int key = kb + kr;
 #pragma unroll
     for (int s2 = 0; s2 < 2; ++s2)
-      sk[s2] = key < S ? load16(K + (size_t)key * D + h * DH + kd + 8 * s2).u
-                       : u32x4{0u, 0u, 0u, 0u};
+      sk[s2] = masked(load16(K + (size_t)min(key, S - 1) * D + h * DH + kd + 8 * s2).u, key < S);
 #pragma unroll
-    for (int s2 = 0; s2 < 2; ++s2)
-      sv[s2] = (kb + vk + s2) < S ? load16(V + (size_t)(kb + vk + s2) * D + h * DH + vd).u
-                                  : u32x4{0u, 0u, 0u, 0u};
+    for (int s2 = 0; s2 < 2; ++s2) {
+      const int vkey = kb + vk + s2;
+      sv[s2] = masked(load16(V + (size_t)min(vkey, S - 1) * D + h * DH + vd).u, vkey < S);
+    }
   };
   auto commit = [&](int buf) {
 #pragma unroll

@@ -42,15 +42,19 @@ __device__ __forceinline__ Frag16 frag_zero() {
 }
 
 // acc += A_frag (16 rows x 16-byte k run) * B_frag, per element type.
+// A fragment pair is kSteps MFMA instructions; step(s) issues the s-th, so a
+// caller can interleave independent accumulators between dependent steps.
 struct MfmaF32 {
   using acc_t = f32x4;
   static constexpr int kPerFrag = 16;  // reduction indices covered per frag pair (4 lanes groups x 4)
   static constexpr int kPerLane = 4;   // consecutive elements per lane in 16 bytes
+  static constexpr int kSteps = 4;
+  __device__ __forceinline__ static void step(acc_t &acc, const Frag16 &a, const Frag16 &b, int s) {
+    acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a.f[s], b.f[s], acc, 0, 0, 0);
+  }
   __device__ __forceinline__ static void mma(acc_t &acc, const Frag16 &a, const Frag16 &b) {
-    acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a.f[0], b.f[0], acc, 0, 0, 0);
-    acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a.f[1], b.f[1], acc, 0, 0, 0);
-    acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a.f[2], b.f[2], acc, 0, 0, 0);
-    acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a.f[3], b.f[3], acc, 0, 0, 0);
+#pragma unroll
+    for (int s = 0; s < kSteps; ++s) step(acc, a, b, s);
   }
 };
 
@@ -58,8 +62,12 @@ struct MfmaBF16 {
   using acc_t = f32x4;
   static constexpr int kPerFrag = 32;
   static constexpr int kPerLane = 8;
-  __device__ __forceinline__ static void mma(acc_t &acc, const Frag16 &a, const Frag16 &b) {
+  static constexpr int kSteps = 1;
+  __device__ __forceinline__ static void step(acc_t &acc, const Frag16 &a, const Frag16 &b, int) {
     acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a.h, b.h, acc, 0, 0, 0);
+  }
+  __device__ __forceinline__ static void mma(acc_t &acc, const Frag16 &a, const Frag16 &b) {
+    step(acc, a, b, 0);
   }
 };
 
@@ -67,10 +75,23 @@ struct MfmaI8 {
   using acc_t = i32x4;
   static constexpr int kPerFrag = 64;
   static constexpr int kPerLane = 16;
-  __device__ __forceinline__ static void mma(acc_t &acc, const Frag16 &a, const Frag16 &b) {
+  static constexpr int kSteps = 1;
+  __device__ __forceinline__ static void step(acc_t &acc, const Frag16 &a, const Frag16 &b, int) {
     acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(a.i, b.i, acc, 0, 0, 0);
   }
+  __device__ __forceinline__ static void mma(acc_t &acc, const Frag16 &a, const Frag16 &b) {
+    step(acc, a, b, 0);
+  }
 };
+
+// Loads are issued unconditionally from an always-valid address and masked
+// afterwards with a select: a load under a divergent branch makes the
+// compiler wait for every outstanding load (vmcnt(0)) before its first use,
+// which defeats prefetching.
+__device__ __forceinline__ u32x4 masked(u32x4 v, bool keep) {
+  const uint32_t m = keep ? 0xffffffffu : 0u;
+  return u32x4{v[0] & m, v[1] & m, v[2] & m, v[3] & m};
+}
 
 // ---- bf16 <-> f32, round to nearest even (arith.truncf) -------------------
 __device__ __forceinline__ float bf16_to_f32(uint16_t h) {
