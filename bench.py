@@ -95,6 +95,18 @@ def cpu_sample(w, budget_s=30.0):
             "host": host_cpu()}
 
 
+def measured_traffic(workload_name):
+    """HBM bytes per launch from the committed counter summary, if there is one."""
+    path = os.path.join(ROOT, "profiles", f"{workload_name}_hbm_traffic.txt")
+    try:
+        for line in open(path):
+            if line.strip().startswith("#   traffic_bytes_per_launch"):
+                return int(line.split("=")[1])
+    except OSError:
+        pass
+    return None
+
+
 def host_cpu():
     try:
         for line in open("/proc/cpuinfo"):
@@ -139,7 +151,7 @@ def main():
                    "parallelism": "single GPU"},
         "throughput": {"value": w.units / sec, "unit": f"{w.unit_name}/s"},
         "wall_s_timed_region": wall,
-        "roofline": dict(w.roofline(sec), traffic=None,
+        "roofline": dict(w.roofline(sec), traffic=measured_traffic(w.name),
                          flops=w.flops, bytes=w.bytes, floor_us=w.floor_s() * 1e6),
     }
     if not args.no_cpu:

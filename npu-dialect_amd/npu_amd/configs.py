@@ -296,6 +296,27 @@ def llama_layer(S=512, D=512, H=8, F=1408, eps=1e-5, seed=rng.SEED_BASE + 5) -> 
         meta={"S": S, "D": D, "H": H, "F": F, "eps": eps})
 
 
+# ------------------------------------------------------------------ counter calibration
+def copy_calibration(nbytes=256 << 20) -> Workload:
+    """A plain device-to-device copy of known size (torch's copy kernel): the
+    reference point that scales the FETCH_SIZE / WRITE_SIZE counters to bytes."""
+    n = nbytes // 4
+
+    def make_inputs():
+        return {"src": np.zeros(n, np.float32)}
+
+    def make_outputs(d):
+        import torch
+        return {"dst": torch.empty(n, dtype=torch.float32, device="cuda")}
+
+    def run(d, o, stream):
+        o["dst"].copy_(d["src"])
+
+    return Workload(name="copy_calibration_256mib", config=0, dtype="f32", flops=0,
+                    bytes=2 * nbytes, make_inputs=make_inputs, make_outputs=make_outputs,
+                    run=run, desc=f"device copy of {nbytes} bytes", units=1, unit_name="copies")
+
+
 def all_workloads() -> list:
     """Every configuration this backend runs, in configuration order."""
     return [
@@ -312,7 +333,7 @@ HEADLINE = "conv3x3_bias_relu_f32_n32"
 
 
 def by_name(name: str) -> Workload:
-    for w in all_workloads():
+    for w in all_workloads() + [copy_calibration()]:
         if w.name == name:
             return w
     raise KeyError(name)
