@@ -1,0 +1,162 @@
+/*
+ * npu_cost.h -- C-ABI of the host-side compiler library (libnpu_host.so):
+ * the analytical cost model of lib/Analysis/CostModel.cpp, the per-op split
+ * rules of lib/Analysis/OperatorTilingSpec.cpp, and the MI355X target,
+ * restated without MLIR over a small SSA graph that the caller builds.
+ *
+ * A graph is one function body: values (tensor types) and ops in block
+ * order.  For linalg ops the operands are `ins` then `outs`, as
+ * Operation::getOperands() lists them.  Functions return -1 (and set
+ * npu_host_last_error()) on an invalid op or value id.
+ */
+#ifndef NPU_COST_H
+#define NPU_COST_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Op kinds (the reference's op vocabulary plus the ops authored here). */
+#define NPU_OP_MATMUL 0
+#define NPU_OP_BATCH_MATMUL 1
+#define NPU_OP_CONV2D_NCHW_FCHW 2
+#define NPU_OP_CONV2D_NHWC_FHWC 3
+#define NPU_OP_DEPTHWISE_NHWC_HWC 4
+#define NPU_OP_GENERIC 5
+#define NPU_OP_FILL 6
+#define NPU_OP_TRANSPOSE 7
+#define NPU_OP_PAD 8
+#define NPU_OP_EMPTY 9
+#define NPU_OP_CONSTANT 10
+#define NPU_OP_RETURN 11
+#define NPU_OP_COLLAPSE_SHAPE 12
+#define NPU_OP_EXPAND_SHAPE 13
+#define NPU_OP_CALL 14
+#define NPU_OP_OTHER 15
+
+/* Hardware target: the fields of the reference's HWTarget
+ * (include/npu/Analysis/CostModel.h:40-56) and of #npu.target
+ * (include/npu/Dialect/NPU/NPUDialect.td:100-113). */
+typedef struct npu_hw_target {
+  int64_t num_cores;
+  int64_t sram_per_core;      /* bytes */
+  int64_t dram_bandwidth;     /* GB/s */
+  int64_t sram_bandwidth;     /* GB/s */
+  int64_t matrix_throughput;  /* MAC / cycle */
+  int64_t dsp_throughput;     /* op / cycle */
+  int64_t dma_channels;
+  int64_t inter_core_sync_cost; /* cycles */
+  double clock_ghz;
+  int32_t interconnect;       /* 0 NoC, 1 SharedL1, 2 SharedSRAM, 3 DRAMOnly */
+  int32_t reserved;
+  int64_t noc_bandwidth;      /* GB/s */
+  int64_t noc_latency_cycles;
+  int64_t shared_l1_size;
+} npu_hw_target;
+
+/* The reference's defaults: 6 cores, 2 MiB, 32 GB/s, 4096 MAC/cycle, 1 GHz. */
+void npu_hw_target_default(npu_hw_target *t);
+/* MI355X per CU for one element width (32, 16 or 8 bits). */
+void npu_hw_target_mi355x(npu_hw_target *t, int32_t elem_bits);
+
+typedef struct npu_graph npu_graph;
+npu_graph *npu_graph_create(void);
+void npu_graph_destroy(npu_graph *g);
+/* shaped = 0 for scalars (e.g. the constant a linalg.fill reads). */
+int32_t npu_graph_add_value(npu_graph *g, const int64_t *shape, int32_t rank,
+                            int32_t bits, int32_t shaped);
+/* iters: generic iterator types (0 parallel, 1 reduction); perm: transpose. */
+int32_t npu_graph_add_op(npu_graph *g, int32_t kind, const int32_t *operands,
+                         int32_t n_operands, const int32_t *results,
+                         int32_t n_results, int32_t n_inputs,
+                         const int32_t *iters, int32_t n_iters,
+                         const int64_t *perm, int32_t n_perm);
+int32_t npu_graph_num_ops(const npu_graph *g);
+
+const char *npu_host_last_error(void);
+
+/* ---- level 0 (CostModel.cpp:46-113) ---- */
+int64_t npu_cm_op_macs(const npu_graph *g, const npu_hw_target *t, int32_t op);
+int64_t npu_cm_compute_cycles(const npu_graph *g, const npu_hw_target *t, int32_t op);
+int64_t npu_cm_dma_cycles(const npu_hw_target *t, int64_t bytes);
+int64_t npu_cm_tensor_bytes(const int64_t *shape, int32_t rank, int32_t bits);
+
+/* ---- roofline (CostModel.cpp:119-226) ---- */
+typedef struct npu_roofline {
+  double flops, mem_bytes, arithmetic_intensity, time_sec;
+  int32_t is_memory_bound, reserved;
+  double peak_attainable, efficiency;
+} npu_roofline;
+int32_t npu_cm_roofline_raw(const npu_hw_target *t, double flops, double mem_bytes,
+                            int32_t matrix, npu_roofline *out);
+/* One op (n = 1) or a fused group (external bytes only). */
+int32_t npu_cm_roofline(const npu_graph *g, const npu_hw_target *t, const int32_t *ops,
+                        int32_t n, npu_roofline *out);
+
+/* ---- level 1 (CostModel.cpp:232-340) ---- */
+typedef struct npu_schedule_cost {
+  int64_t compute_cycles, dma_cycles, total_cycles, sram_peak_bytes, num_tiles,
+      total_dma_bytes;
+  int32_t valid, n_tile_sizes;
+  int64_t tile_sizes[4];
+} npu_schedule_cost;
+int32_t npu_cm_matmul_tile(const npu_hw_target *t, int64_t tm, int64_t tn, int64_t tk,
+                           int64_t M, int64_t N, int64_t K, int64_t dtype_bytes,
+                           int64_t extra_bytes, npu_schedule_cost *out);
+int32_t npu_cm_conv2d_tile(const npu_hw_target *t, int64_t tn, int64_t tco, int64_t th,
+                           int64_t tw, int64_t N, int64_t Co, int64_t Ho, int64_t Wo,
+                           int64_t Ci, int64_t Kh, int64_t Kw, int64_t stride_h,
+                           int64_t stride_w, int64_t dtype_bytes,
+                           int64_t extra_output_shaped, npu_schedule_cost *out);
+/* Writes up to cap candidates, returns how many there are. */
+int32_t npu_cm_tile_candidates(int64_t dim, int64_t *out, int32_t cap);
+
+/* ---- level 2 (CostModel.cpp:346-823) ---- */
+int32_t npu_cm_best_tile_config(const npu_graph *g, const npu_hw_target *t, int32_t op,
+                                npu_schedule_cost *out);
+/* Returns 1 if fusing producer into consumer pays, 0 if not; *benefit in cycles. */
+int32_t npu_cm_fusion_profitable(const npu_graph *g, const npu_hw_target *t,
+                                 int32_t producer, int32_t consumer, int64_t *benefit);
+int32_t npu_cm_spatial_split(const npu_graph *g, const npu_hw_target *t, int32_t op,
+                             int32_t dim, int64_t chunks, npu_schedule_cost *out);
+typedef struct npu_spatial_split_cost {
+  int64_t per_core_dma_in_bytes, per_core_compute_cycles, shared_data_bytes,
+      split_data_bytes, halo_overhead_bytes;
+  int32_t needs_reduce, reserved;
+  int64_t total_cycles;
+} npu_spatial_split_cost;
+/* split_index selects one entry of the op's tiling spec (see npu_spec_*). */
+int32_t npu_cm_spatial_split_detailed(const npu_graph *g, const npu_hw_target *t,
+                                      int32_t op, int32_t split_index, int64_t chunks,
+                                      npu_spatial_split_cost *out);
+/* Returns 1 if aligned; *overhead_bytes as the reference computes it. */
+int32_t npu_cm_tile_alignment(const npu_graph *g, const npu_hw_target *t, const int32_t *ops,
+                              int32_t n, int64_t *overhead_bytes);
+/* 0 = retile, 1 = spill. */
+int32_t npu_cm_spill_strategy(const npu_hw_target *t, int64_t tile_working_set,
+                              int64_t intermediate_bytes);
+
+/* ---- level 3 (CostModel.cpp:829-951) ---- */
+typedef struct npu_subgraph_cost {
+  int64_t dma_in_cycles, matrix_cycles, dsp_cycles, dma_out_cycles, intermediate_dma,
+      pipelined_cycles, unpipelined_cycles, num_ops;
+} npu_subgraph_cost;
+int32_t npu_cm_subgraph(const npu_graph *g, const npu_hw_target *t, const int32_t *ops,
+                        int32_t n, npu_subgraph_cost *out);
+int32_t npu_cm_subgraph_fusion_profitable(const npu_graph *g, const npu_hw_target *t,
+                                          const int32_t *ops, int32_t n, int64_t *benefit);
+
+/* ---- tiling specs (OperatorTilingSpec.cpp:518-585) ---- */
+/* Number of split entries of op's spec (0 if it has none); with index >= 0,
+ * fills the entry: output dim (-1 for reduction), iteration dim, parallel. */
+int32_t npu_spec_num_splits(const npu_graph *g, int32_t op);
+int32_t npu_spec_split(const npu_graph *g, int32_t op, int32_t index, int32_t *output_dim,
+                       int32_t *iter_dim, int32_t *parallel);
+int32_t npu_spec_preferred_spatial_dim(const npu_graph *g, int32_t op);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* NPU_COST_H */

@@ -1,0 +1,312 @@
+// capi.cpp -- extern "C" boundary of libnpu_host.so (include/npu_cost.h).
+#include <algorithm>
+#include <cstdarg>
+#include <cstdio>
+#include <string>
+
+#include "../../include/npu_cost.h"
+#include "cost_model.hpp"
+
+struct npu_graph {
+  npu::ir::Graph g;
+};
+
+namespace {
+
+thread_local std::string g_err;
+
+int32_t fail(const char *fmt, ...) {
+  char buf[256];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof buf, fmt, ap);
+  va_end(ap);
+  g_err = buf;
+  return -1;
+}
+
+npu::HWTarget to_target(const npu_hw_target *t) {
+  npu::HWTarget h;
+  h.num_cores = t->num_cores;
+  h.sram_per_core = t->sram_per_core;
+  h.dram_bandwidth = t->dram_bandwidth;
+  h.sram_bandwidth = t->sram_bandwidth;
+  h.matrix_throughput = t->matrix_throughput;
+  h.dsp_throughput = t->dsp_throughput;
+  h.dma_channels = t->dma_channels;
+  h.inter_core_sync_cost = t->inter_core_sync_cost;
+  h.clock_ghz = t->clock_ghz;
+  h.interconnect = static_cast<npu::Interconnect>(t->interconnect);
+  h.noc_bandwidth = t->noc_bandwidth;
+  h.noc_latency_cycles = t->noc_latency_cycles;
+  h.shared_l1_size = t->shared_l1_size;
+  return h;
+}
+
+void from_target(const npu::HWTarget &h, npu_hw_target *t) {
+  t->num_cores = h.num_cores;
+  t->sram_per_core = h.sram_per_core;
+  t->dram_bandwidth = h.dram_bandwidth;
+  t->sram_bandwidth = h.sram_bandwidth;
+  t->matrix_throughput = h.matrix_throughput;
+  t->dsp_throughput = h.dsp_throughput;
+  t->dma_channels = h.dma_channels;
+  t->inter_core_sync_cost = h.inter_core_sync_cost;
+  t->clock_ghz = h.clock_ghz;
+  t->interconnect = static_cast<int32_t>(h.interconnect);
+  t->reserved = 0;
+  t->noc_bandwidth = h.noc_bandwidth;
+  t->noc_latency_cycles = h.noc_latency_cycles;
+  t->shared_l1_size = h.shared_l1_size;
+}
+
+bool bad_op(const npu_graph *g, int32_t op) {
+  return !g || op < 0 || op >= (int32_t)g->g.ops.size();
+}
+
+bool bad_ops(const npu_graph *g, const int32_t *ops, int32_t n) {
+  if (!g || (n > 0 && !ops) || n < 0) return true;
+  for (int32_t i = 0; i < n; ++i)
+    if (bad_op(g, ops[i])) return true;
+  return false;
+}
+
+void put_schedule(const npu::ScheduleCost &c, const std::vector<int64_t> &tiles,
+                  npu_schedule_cost *o) {
+  o->compute_cycles = c.compute_cycles;
+  o->dma_cycles = c.dma_cycles;
+  o->total_cycles = c.total_cycles;
+  o->sram_peak_bytes = c.sram_peak_bytes;
+  o->num_tiles = c.num_tiles;
+  o->total_dma_bytes = c.total_dma_bytes;
+  o->valid = c.valid() ? 1 : 0;
+  o->n_tile_sizes = (int32_t)std::min<size_t>(4, tiles.size());
+  for (int i = 0; i < 4; ++i) o->tile_sizes[i] = i < (int)tiles.size() ? tiles[i] : 0;
+}
+
+void put_roofline(const npu::RooflineCost &c, npu_roofline *o) {
+  o->flops = c.flops;
+  o->mem_bytes = c.mem_bytes;
+  o->arithmetic_intensity = c.arithmetic_intensity;
+  o->time_sec = c.time_sec;
+  o->is_memory_bound = c.memory_bound ? 1 : 0;
+  o->reserved = 0;
+  o->peak_attainable = c.peak_attainable;
+  o->efficiency = c.efficiency;
+}
+
+std::vector<int32_t> vec(const int32_t *p, int32_t n) { return std::vector<int32_t>(p, p + n); }
+
+}  // namespace
+
+extern "C" {
+
+void npu_hw_target_default(npu_hw_target *t) {
+  if (t) from_target(npu::HWTarget{}, t);
+}
+void npu_hw_target_mi355x(npu_hw_target *t, int32_t bits) {
+  if (t) from_target(npu::mi355x_target(bits), t);
+}
+
+npu_graph *npu_graph_create(void) { return new npu_graph(); }
+void npu_graph_destroy(npu_graph *g) { delete g; }
+
+int32_t npu_graph_add_value(npu_graph *g, const int64_t *shape, int32_t rank, int32_t bits,
+                            int32_t shaped) {
+  if (!g || rank < 0 || (rank > 0 && !shape) || bits <= 0) return fail("bad value");
+  npu::ir::Type t;
+  t.shape.assign(shape, shape + rank);
+  t.bits = bits;
+  t.shaped = shaped != 0;
+  return g->g.add_value(t);
+}
+
+int32_t npu_graph_add_op(npu_graph *g, int32_t kind, const int32_t *operands, int32_t n_operands,
+                         const int32_t *results, int32_t n_results, int32_t n_inputs,
+                         const int32_t *iters, int32_t n_iters, const int64_t *perm,
+                         int32_t n_perm) {
+  if (!g || kind < 0 || kind > NPU_OP_OTHER) return fail("bad op kind %d", kind);
+  const int32_t nv = (int32_t)g->g.values.size();
+  for (int32_t i = 0; i < n_operands; ++i)
+    if (operands[i] < 0 || operands[i] >= nv) return fail("operand %d: bad value id", i);
+  for (int32_t i = 0; i < n_results; ++i)
+    if (results[i] < 0 || results[i] >= nv || g->g.values[results[i]].def >= 0)
+      return fail("result %d: bad or already defined value", i);
+  npu::ir::Op op;
+  op.kind = static_cast<npu::ir::OpKind>(kind);
+  op.operands.assign(operands, operands + n_operands);
+  op.results.assign(results, results + n_results);
+  op.num_inputs = n_inputs;
+  if (iters) op.iters.assign(iters, iters + n_iters);
+  if (perm) op.perm.assign(perm, perm + n_perm);
+  return g->g.add_op(op);
+}
+
+int32_t npu_graph_num_ops(const npu_graph *g) { return g ? (int32_t)g->g.ops.size() : -1; }
+
+const char *npu_host_last_error(void) { return g_err.c_str(); }
+
+int64_t npu_cm_op_macs(const npu_graph *g, const npu_hw_target *t, int32_t op) {
+  if (bad_op(g, op) || !t) return fail("bad op");
+  return npu::CostModel(g->g, to_target(t)).op_macs(op);
+}
+int64_t npu_cm_compute_cycles(const npu_graph *g, const npu_hw_target *t, int32_t op) {
+  if (bad_op(g, op) || !t) return fail("bad op");
+  return npu::CostModel(g->g, to_target(t)).compute_cycles(op);
+}
+int64_t npu_cm_dma_cycles(const npu_hw_target *t, int64_t bytes) {
+  npu::ir::Graph empty;
+  return npu::CostModel(empty, to_target(t)).dma_cycles(bytes);
+}
+int64_t npu_cm_tensor_bytes(const int64_t *shape, int32_t rank, int32_t bits) {
+  npu::ir::Type ty;
+  ty.shape.assign(shape, shape + rank);
+  ty.bits = bits;
+  return npu::CostModel::tensor_bytes(ty);
+}
+
+int32_t npu_cm_roofline_raw(const npu_hw_target *t, double flops, double bytes, int32_t matrix,
+                            npu_roofline *out) {
+  if (!t || !out) return fail("null argument");
+  npu::ir::Graph empty;
+  put_roofline(npu::CostModel(empty, to_target(t)).roofline_raw(flops, bytes, matrix != 0), out);
+  return 0;
+}
+
+int32_t npu_cm_roofline(const npu_graph *g, const npu_hw_target *t, const int32_t *ops, int32_t n,
+                        npu_roofline *out) {
+  if (bad_ops(g, ops, n) || !t || !out) return fail("bad ops");
+  npu::CostModel cm(g->g, to_target(t));
+  put_roofline(n == 1 ? cm.roofline(ops[0]) : cm.roofline(vec(ops, n)), out);
+  return 0;
+}
+
+int32_t npu_cm_matmul_tile(const npu_hw_target *t, int64_t tm, int64_t tn, int64_t tk, int64_t M,
+                           int64_t N, int64_t K, int64_t dtb, int64_t extra,
+                           npu_schedule_cost *out) {
+  if (!t || !out || tm <= 0 || tn <= 0 || tk <= 0) return fail("bad tile");
+  npu::ir::Graph empty;
+  put_schedule(npu::CostModel(empty, to_target(t)).matmul_tile(tm, tn, tk, M, N, K, dtb, extra),
+               {tm, tn, tk}, out);
+  return 0;
+}
+
+int32_t npu_cm_conv2d_tile(const npu_hw_target *t, int64_t tn, int64_t tco, int64_t th, int64_t tw,
+                           int64_t N, int64_t Co, int64_t Ho, int64_t Wo, int64_t Ci, int64_t Kh,
+                           int64_t Kw, int64_t sh, int64_t sw, int64_t dtb, int64_t extra,
+                           npu_schedule_cost *out) {
+  if (!t || !out || tn <= 0 || tco <= 0 || th <= 0 || tw <= 0) return fail("bad tile");
+  npu::ir::Graph empty;
+  put_schedule(npu::CostModel(empty, to_target(t))
+                   .conv2d_tile(tn, tco, th, tw, N, Co, Ho, Wo, Ci, Kh, Kw, {sh, sw}, dtb, extra),
+               {tn, tco, th, tw}, out);
+  return 0;
+}
+
+int32_t npu_cm_tile_candidates(int64_t dim, int64_t *out, int32_t cap) {
+  const auto c = npu::CostModel::tile_candidates(dim);
+  for (int32_t i = 0; i < cap && i < (int32_t)c.size(); ++i) out[i] = c[i];
+  return (int32_t)c.size();
+}
+
+int32_t npu_cm_best_tile_config(const npu_graph *g, const npu_hw_target *t, int32_t op,
+                                npu_schedule_cost *out) {
+  if (bad_op(g, op) || !t || !out) return fail("bad op");
+  const npu::TileConfig c = npu::CostModel(g->g, to_target(t)).best_tile_config(op);
+  put_schedule(c.cost, c.tile_sizes, out);
+  return 0;
+}
+
+int32_t npu_cm_fusion_profitable(const npu_graph *g, const npu_hw_target *t, int32_t producer,
+                                 int32_t consumer, int64_t *benefit) {
+  if (bad_op(g, producer) || bad_op(g, consumer) || !t) return fail("bad op");
+  const auto d = npu::CostModel(g->g, to_target(t)).fusion_profitable(producer, consumer);
+  if (benefit) *benefit = d.benefit_cycles;
+  return d.fuse ? 1 : 0;
+}
+
+int32_t npu_cm_spatial_split(const npu_graph *g, const npu_hw_target *t, int32_t op, int32_t dim,
+                             int64_t chunks, npu_schedule_cost *out) {
+  if (bad_op(g, op) || !t || !out || dim < 0) return fail("bad op");
+  put_schedule(npu::CostModel(g->g, to_target(t)).spatial_split(op, (unsigned)dim, chunks), {}, out);
+  return 0;
+}
+
+int32_t npu_cm_spatial_split_detailed(const npu_graph *g, const npu_hw_target *t, int32_t op,
+                                      int32_t idx, int64_t chunks, npu_spatial_split_cost *out) {
+  if (bad_op(g, op) || !t || !out) return fail("bad op");
+  const npu::OperatorTilingSpec *spec = npu::get_tiling_spec(g->g, op);
+  if (!spec || idx < 0 || idx >= (int32_t)spec->split_dims.size()) return fail("bad split index");
+  const auto r = npu::CostModel(g->g, to_target(t)).spatial_split_detailed(op, spec->split_dims[idx], chunks);
+  out->per_core_dma_in_bytes = r.per_core_dma_in_bytes;
+  out->per_core_compute_cycles = r.per_core_compute_cycles;
+  out->shared_data_bytes = r.shared_data_bytes;
+  out->split_data_bytes = r.split_data_bytes;
+  out->halo_overhead_bytes = r.halo_overhead_bytes;
+  out->needs_reduce = r.needs_reduce ? 1 : 0;
+  out->reserved = 0;
+  out->total_cycles = r.total_cycles;
+  return 0;
+}
+
+int32_t npu_cm_tile_alignment(const npu_graph *g, const npu_hw_target *t, const int32_t *ops,
+                              int32_t n, int64_t *overhead) {
+  if (bad_ops(g, ops, n) || !t) return fail("bad ops");
+  const auto a = npu::CostModel(g->g, to_target(t)).tile_alignment(vec(ops, n));
+  if (overhead) *overhead = a.overhead_bytes;
+  return a.aligned ? 1 : 0;
+}
+
+int32_t npu_cm_spill_strategy(const npu_hw_target *t, int64_t ws, int64_t inter) {
+  npu::ir::Graph empty;
+  return (int32_t)npu::CostModel(empty, to_target(t)).spill_strategy(ws, inter);
+}
+
+int32_t npu_cm_subgraph(const npu_graph *g, const npu_hw_target *t, const int32_t *ops, int32_t n,
+                        npu_subgraph_cost *out) {
+  if (bad_ops(g, ops, n) || !t || !out) return fail("bad ops");
+  const auto c = npu::CostModel(g->g, to_target(t)).subgraph(vec(ops, n));
+  out->dma_in_cycles = c.dma_in_cycles;
+  out->matrix_cycles = c.matrix_cycles;
+  out->dsp_cycles = c.dsp_cycles;
+  out->dma_out_cycles = c.dma_out_cycles;
+  out->intermediate_dma = c.intermediate_dma;
+  out->pipelined_cycles = c.pipelined_cycles;
+  out->unpipelined_cycles = c.unpipelined_cycles;
+  out->num_ops = c.num_ops;
+  return 0;
+}
+
+int32_t npu_cm_subgraph_fusion_profitable(const npu_graph *g, const npu_hw_target *t,
+                                          const int32_t *ops, int32_t n, int64_t *benefit) {
+  if (bad_ops(g, ops, n) || !t) return fail("bad ops");
+  const auto d = npu::CostModel(g->g, to_target(t)).subgraph_fusion_profitable(vec(ops, n));
+  if (benefit) *benefit = d.benefit_cycles;
+  return d.fuse ? 1 : 0;
+}
+
+int32_t npu_spec_num_splits(const npu_graph *g, int32_t op) {
+  if (bad_op(g, op)) return fail("bad op");
+  const npu::OperatorTilingSpec *s = npu::get_tiling_spec(g->g, op);
+  return s ? (int32_t)s->split_dims.size() : 0;
+}
+
+int32_t npu_spec_split(const npu_graph *g, int32_t op, int32_t index, int32_t *output_dim,
+                       int32_t *iter_dim, int32_t *parallel) {
+  if (bad_op(g, op)) return fail("bad op");
+  const npu::OperatorTilingSpec *s = npu::get_tiling_spec(g->g, op);
+  if (!s || index < 0 || index >= (int32_t)s->split_dims.size()) return fail("bad split index");
+  const auto &d = s->split_dims[index];
+  if (output_dim) *output_dim = d.output_dim == npu::kNoOutputDim ? -1 : (int32_t)d.output_dim;
+  if (iter_dim) *iter_dim = (int32_t)d.iter_dim;
+  if (parallel) *parallel = d.parallel ? 1 : 0;
+  return 0;
+}
+
+int32_t npu_spec_preferred_spatial_dim(const npu_graph *g, int32_t op) {
+  if (bad_op(g, op)) return fail("bad op");
+  const npu::OperatorTilingSpec *s = npu::get_tiling_spec(g->g, op);
+  return s ? s->preferred_spatial_dim : -1;
+}
+
+}  // extern "C"

@@ -1,0 +1,300 @@
+"""ctypes binding of libnpu_host.so (include/npu_cost.h): the cost model, the
+split rules and the MI355X target, over graphs built from parsed functions."""
+from __future__ import annotations
+
+import ctypes as C
+import os
+
+from . import mlir
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+HOST_LIB_PATH = os.path.join(_HERE, "libnpu_host.so")
+
+OP_KINDS = {
+    "linalg.matmul": 0, "linalg.batch_matmul": 1, "linalg.conv_2d_nchw_fchw": 2,
+    "linalg.conv_2d_nhwc_fhwc": 3, "linalg.depthwise_conv_2d_nhwc_hwc": 4,
+    "linalg.generic": 5, "linalg.fill": 6, "linalg.transpose": 7, "tensor.pad": 8,
+    "tensor.empty": 9, "arith.constant": 10, "func.return": 11,
+    "tensor.collapse_shape": 12, "tensor.expand_shape": 13, "func.call": 14,
+}
+LINALG_KINDS = {0, 1, 2, 3, 4, 5, 6, 7}
+
+
+class HWTarget(C.Structure):
+    _fields_ = [
+        ("num_cores", C.c_int64), ("sram_per_core", C.c_int64), ("dram_bandwidth", C.c_int64),
+        ("sram_bandwidth", C.c_int64), ("matrix_throughput", C.c_int64),
+        ("dsp_throughput", C.c_int64), ("dma_channels", C.c_int64),
+        ("inter_core_sync_cost", C.c_int64), ("clock_ghz", C.c_double),
+        ("interconnect", C.c_int32), ("reserved", C.c_int32), ("noc_bandwidth", C.c_int64),
+        ("noc_latency_cycles", C.c_int64), ("shared_l1_size", C.c_int64),
+    ]
+
+    def as_dict(self):
+        return {k: getattr(self, k) for k, _ in self._fields_ if k != "reserved"}
+
+
+class Roofline(C.Structure):
+    _fields_ = [("flops", C.c_double), ("mem_bytes", C.c_double),
+                ("arithmetic_intensity", C.c_double), ("time_sec", C.c_double),
+                ("is_memory_bound", C.c_int32), ("reserved", C.c_int32),
+                ("peak_attainable", C.c_double), ("efficiency", C.c_double)]
+
+
+class ScheduleCost(C.Structure):
+    _fields_ = [("compute_cycles", C.c_int64), ("dma_cycles", C.c_int64),
+                ("total_cycles", C.c_int64), ("sram_peak_bytes", C.c_int64),
+                ("num_tiles", C.c_int64), ("total_dma_bytes", C.c_int64),
+                ("valid", C.c_int32), ("n_tile_sizes", C.c_int32), ("tile_sizes", C.c_int64 * 4)]
+
+    @property
+    def tiles(self):
+        return [self.tile_sizes[i] for i in range(self.n_tile_sizes)]
+
+
+class SpatialSplitCost(C.Structure):
+    _fields_ = [("per_core_dma_in_bytes", C.c_int64), ("per_core_compute_cycles", C.c_int64),
+                ("shared_data_bytes", C.c_int64), ("split_data_bytes", C.c_int64),
+                ("halo_overhead_bytes", C.c_int64), ("needs_reduce", C.c_int32),
+                ("reserved", C.c_int32), ("total_cycles", C.c_int64)]
+
+
+class SubgraphCost(C.Structure):
+    _fields_ = [(n, C.c_int64) for n in (
+        "dma_in_cycles", "matrix_cycles", "dsp_cycles", "dma_out_cycles", "intermediate_dma",
+        "pipelined_cycles", "unpipelined_cycles", "num_ops")]
+
+
+_I32, _I64, _P = C.c_int32, C.c_int64, C.c_void_p
+_PT = C.POINTER(HWTarget)
+_PI32 = C.POINTER(C.c_int32)
+_PI64 = C.POINTER(C.c_int64)
+
+SIGNATURES = {
+    "npu_hw_target_default": (None, [_PT]),
+    "npu_hw_target_mi355x": (None, [_PT, _I32]),
+    "npu_graph_create": (_P, []),
+    "npu_graph_destroy": (None, [_P]),
+    "npu_graph_add_value": (_I32, [_P, _PI64, _I32, _I32, _I32]),
+    "npu_graph_add_op": (_I32, [_P, _I32, _PI32, _I32, _PI32, _I32, _I32, _PI32, _I32, _PI64, _I32]),
+    "npu_graph_num_ops": (_I32, [_P]),
+    "npu_host_last_error": (C.c_char_p, []),
+    "npu_cm_op_macs": (_I64, [_P, _PT, _I32]),
+    "npu_cm_compute_cycles": (_I64, [_P, _PT, _I32]),
+    "npu_cm_dma_cycles": (_I64, [_PT, _I64]),
+    "npu_cm_tensor_bytes": (_I64, [_PI64, _I32, _I32]),
+    "npu_cm_roofline_raw": (_I32, [_PT, C.c_double, C.c_double, _I32, C.POINTER(Roofline)]),
+    "npu_cm_roofline": (_I32, [_P, _PT, _PI32, _I32, C.POINTER(Roofline)]),
+    "npu_cm_matmul_tile": (_I32, [_PT] + [_I64] * 8 + [C.POINTER(ScheduleCost)]),
+    "npu_cm_conv2d_tile": (_I32, [_PT] + [_I64] * 15 + [C.POINTER(ScheduleCost)]),
+    "npu_cm_tile_candidates": (_I32, [_I64, _PI64, _I32]),
+    "npu_cm_best_tile_config": (_I32, [_P, _PT, _I32, C.POINTER(ScheduleCost)]),
+    "npu_cm_fusion_profitable": (_I32, [_P, _PT, _I32, _I32, _PI64]),
+    "npu_cm_spatial_split": (_I32, [_P, _PT, _I32, _I32, _I64, C.POINTER(ScheduleCost)]),
+    "npu_cm_spatial_split_detailed": (_I32, [_P, _PT, _I32, _I32, _I64,
+                                             C.POINTER(SpatialSplitCost)]),
+    "npu_cm_tile_alignment": (_I32, [_P, _PT, _PI32, _I32, _PI64]),
+    "npu_cm_spill_strategy": (_I32, [_PT, _I64, _I64]),
+    "npu_cm_subgraph": (_I32, [_P, _PT, _PI32, _I32, C.POINTER(SubgraphCost)]),
+    "npu_cm_subgraph_fusion_profitable": (_I32, [_P, _PT, _PI32, _I32, _PI64]),
+    "npu_spec_num_splits": (_I32, [_P, _I32]),
+    "npu_spec_split": (_I32, [_P, _I32, _I32, _PI32, _PI32, _PI32]),
+    "npu_spec_preferred_spatial_dim": (_I32, [_P, _I32]),
+}
+
+_lib = None
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not os.path.exists(HOST_LIB_PATH):
+            raise RuntimeError(f"libnpu_host.so not found at {HOST_LIB_PATH}: build it with make")
+        h = C.CDLL(HOST_LIB_PATH)
+        for name, (res, args) in SIGNATURES.items():
+            fn = getattr(h, name)
+            fn.restype = res
+            fn.argtypes = args
+        _lib = h
+    return _lib
+
+
+def _check(rc):
+    if rc < 0:
+        raise ValueError(lib().npu_host_last_error().decode())
+    return rc
+
+
+def default_target() -> HWTarget:
+    t = HWTarget()
+    lib().npu_hw_target_default(C.byref(t))
+    return t
+
+
+def mi355x_target(elem_bits=32) -> HWTarget:
+    t = HWTarget()
+    lib().npu_hw_target_mi355x(C.byref(t), elem_bits)
+    return t
+
+
+def _arr(ctype, xs):
+    xs = list(xs)
+    return (ctype * max(1, len(xs)))(*xs), len(xs)
+
+
+class Graph:
+    """A function body in the host library.  ``op_id[i]`` is the graph op of
+    ``func.ops[i]``; ``value_id[name]`` the value of an SSA name."""
+
+    def __init__(self, func: mlir.MFunc):
+        self.func = func
+        self.h = lib().npu_graph_create()
+        self.value_id = {}
+        self.op_id = []
+        self.kinds = []
+        for name, t in func.args:
+            self._value(name, t)
+        for op in func.ops:
+            kind = OP_KINDS.get(op.name, 15)
+            operands = [self._ref(n) for n in op.all_operands]
+            results = [self._value(r, t) for r, t in zip(op.results, op.result_types)]
+            iters = [0 if it == "parallel" else 1 for it in op.iterators]
+            perm = op.attrs.get("permutation", [])
+            a_ops, n_ops = _arr(C.c_int32, operands)
+            a_res, n_res = _arr(C.c_int32, results)
+            a_it, n_it = _arr(C.c_int32, iters)
+            a_pm, n_pm = _arr(C.c_int64, perm)
+            oid = _check(lib().npu_graph_add_op(self.h, kind, a_ops, n_ops, a_res, n_res,
+                                                len(op.ins), a_it, n_it, a_pm, n_pm))
+            self.op_id.append(oid)
+            self.kinds.append(kind)
+
+    def _value(self, name, t: mlir.TType):
+        shape, rank = _arr(C.c_int64, t.shape)
+        vid = _check(lib().npu_graph_add_value(self.h, shape, rank, t.bits, 1 if t.shaped else 0))
+        self.value_id[name] = vid
+        return vid
+
+    def _ref(self, name):
+        if name not in self.value_id:
+            # an SSA name defined outside the subset (e.g. a block argument)
+            self._value(name, mlir.TType([], "f32", shaped=False))
+        return self.value_id[name]
+
+    def linalg_ops(self):
+        """Indices (into func.ops) of linalg ops, in block order."""
+        return [i for i, k in enumerate(self.kinds) if k in LINALG_KINDS]
+
+    def find(self, name_prefix, nth=0):
+        idx = [i for i, op in enumerate(self.func.ops) if op.name.startswith(name_prefix)]
+        return idx[nth]
+
+    def __del__(self):
+        try:
+            lib().npu_graph_destroy(self.h)
+        except Exception:
+            pass
+
+
+class CostModel:
+    """Cost model queries on a Graph (op arguments are indices into func.ops)."""
+
+    def __init__(self, graph: Graph, target: HWTarget):
+        self.g = graph
+        self.t = target
+
+    def _op(self, i):
+        return self.g.op_id[i]
+
+    def op_macs(self, i):
+        return _check(lib().npu_cm_op_macs(self.g.h, C.byref(self.t), self._op(i)))
+
+    def compute_cycles(self, i):
+        return _check(lib().npu_cm_compute_cycles(self.g.h, C.byref(self.t), self._op(i)))
+
+    def dma_cycles(self, nbytes):
+        return lib().npu_cm_dma_cycles(C.byref(self.t), nbytes)
+
+    def roofline(self, ops):
+        a, n = _arr(C.c_int32, [self._op(i) for i in ops])
+        r = Roofline()
+        _check(lib().npu_cm_roofline(self.g.h, C.byref(self.t), a, n, C.byref(r)))
+        return r
+
+    def best_tile_config(self, i):
+        s = ScheduleCost()
+        _check(lib().npu_cm_best_tile_config(self.g.h, C.byref(self.t), self._op(i), C.byref(s)))
+        return s
+
+    def fusion_profitable(self, producer, consumer):
+        b = C.c_int64()
+        f = _check(lib().npu_cm_fusion_profitable(self.g.h, C.byref(self.t), self._op(producer),
+                                                  self._op(consumer), C.byref(b)))
+        return bool(f), b.value
+
+    def spatial_split(self, i, dim, chunks):
+        s = ScheduleCost()
+        _check(lib().npu_cm_spatial_split(self.g.h, C.byref(self.t), self._op(i), dim, chunks,
+                                          C.byref(s)))
+        return s
+
+    def spatial_split_detailed(self, i, split_index, chunks):
+        s = SpatialSplitCost()
+        _check(lib().npu_cm_spatial_split_detailed(self.g.h, C.byref(self.t), self._op(i),
+                                                   split_index, chunks, C.byref(s)))
+        return s
+
+    def tile_alignment(self, ops):
+        a, n = _arr(C.c_int32, [self._op(i) for i in ops])
+        o = C.c_int64()
+        aligned = _check(lib().npu_cm_tile_alignment(self.g.h, C.byref(self.t), a, n, C.byref(o)))
+        return bool(aligned), o.value
+
+    def subgraph(self, ops):
+        a, n = _arr(C.c_int32, [self._op(i) for i in ops])
+        s = SubgraphCost()
+        _check(lib().npu_cm_subgraph(self.g.h, C.byref(self.t), a, n, C.byref(s)))
+        return s
+
+    def subgraph_fusion_profitable(self, ops):
+        a, n = _arr(C.c_int32, [self._op(i) for i in ops])
+        b = C.c_int64()
+        f = _check(lib().npu_cm_subgraph_fusion_profitable(self.g.h, C.byref(self.t), a, n,
+                                                           C.byref(b)))
+        return bool(f), b.value
+
+    def spec_splits(self, i):
+        n = _check(lib().npu_spec_num_splits(self.g.h, self._op(i)))
+        out = []
+        for k in range(n):
+            od, it, par = C.c_int32(), C.c_int32(), C.c_int32()
+            _check(lib().npu_spec_split(self.g.h, self._op(i), k, C.byref(od), C.byref(it),
+                                        C.byref(par)))
+            out.append((od.value, it.value, bool(par.value)))
+        return out
+
+
+def tile_candidates(dim):
+    buf = (C.c_int64 * 64)()
+    n = lib().npu_cm_tile_candidates(dim, buf, 64)
+    return [buf[i] for i in range(min(n, 64))]
+
+
+def matmul_tile(target, tm, tn, tk, M, N, K, dtype_bytes, extra=0):
+    s = ScheduleCost()
+    _check(lib().npu_cm_matmul_tile(C.byref(target), tm, tn, tk, M, N, K, dtype_bytes, extra,
+                                     C.byref(s)))
+    return s
+
+
+def conv2d_tile(target, tn, tco, th, tw, N, Co, Ho, Wo, Ci, Kh, Kw, dtype_bytes, stride=(1, 1),
+                extra=0):
+    s = ScheduleCost()
+    _check(lib().npu_cm_conv2d_tile(C.byref(target), tn, tco, th, tw, N, Co, Ho, Wo, Ci, Kh, Kw,
+                                    stride[0], stride[1], dtype_bytes, extra, C.byref(s)))
+    return s
+
+
+def spill_strategy(target, working_set, intermediate_bytes):
+    return "spill" if lib().npu_cm_spill_strategy(C.byref(target), working_set,
+                                                 intermediate_bytes) else "retile"

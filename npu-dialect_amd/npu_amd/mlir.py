@@ -1,0 +1,287 @@
+"""Reads the tensor-level linalg subset NPU-Dialect compiles into a flat op list.
+
+The reference's inputs are `func.func` bodies of `arith.constant`,
+`tensor.empty`, `tensor.pad`, `linalg.fill`, `linalg.matmul`,
+`linalg.batch_matmul`, `linalg.conv_2d_nchw_fchw`, `linalg.generic` (ReLU /
+add bodies) and `func.return` (SURVEY of test/**/*.mlir); the configurations
+here add `linalg.conv_2d_nhwc_fhwc`, `linalg.depthwise_conv_2d_nhwc_hwc` and
+`linalg.transpose`.  Like the reference's own harness, which reads MLIR text
+with regular expressions (tools/harness/verify_accuracy.py:298-359,
+tools/harness/e2e_verify.py:78-140), this is a reader for that pretty-printed
+subset, not a general MLIR parser: anything else is kept as an opaque op so
+that uses and users stay correct.
+"""
+from __future__ import annotations
+
+import re
+from dataclasses import dataclass, field
+
+TYPE_BITS = {"f16": 16, "bf16": 16, "f32": 32, "f64": 64, "i8": 8, "i16": 16, "i32": 32,
+             "i64": 64, "index": 64, "i1": 1}
+
+_STMT_START = re.compile(
+    r"^(%|return\b|func\.return\b|func\.call\b|linalg\.|tensor\.|arith\.|scf\.|memref\.|npu\.)")
+
+
+@dataclass
+class TType:
+    shape: list          # [] for scalars, -1 for dynamic dims
+    elem: str
+    shaped: bool = True
+
+    @property
+    def bits(self):
+        return TYPE_BITS.get(self.elem, 32)
+
+    def __str__(self):
+        if not self.shaped:
+            return self.elem
+        dims = "x".join("?" if d < 0 else str(d) for d in self.shape)
+        return f"tensor<{dims}x{self.elem}>" if dims else f"tensor<{self.elem}>"
+
+
+@dataclass
+class MOp:
+    name: str                          # e.g. "linalg.matmul"
+    results: list                      # SSA names
+    result_types: list
+    ins: list = field(default_factory=list)       # SSA names
+    outs: list = field(default_factory=list)
+    operands: list = field(default_factory=list)  # other operand names (pad source, return values)
+    iterators: list = field(default_factory=list)  # generic: "parallel" / "reduction"
+    body_ops: list = field(default_factory=list)   # generic region: arith op names
+    attrs: dict = field(default_factory=dict)
+    text: str = ""
+
+    @property
+    def all_operands(self):
+        return self.ins + self.outs + self.operands
+
+
+@dataclass
+class MFunc:
+    name: str
+    args: list          # [(name, TType)]
+    result_types: list
+    ops: list           # [MOp]
+    types: dict         # SSA name -> TType
+
+
+def parse_type(s: str) -> TType:
+    s = s.strip()
+    m = re.match(r"(tensor|memref)<([^>]*)>", s)
+    if not m:
+        return TType([], s, shaped=False)
+    parts = m.group(2).split(",")[0].strip().split("x")
+    elem = parts[-1]
+    shape = [-1 if p == "?" else int(p) for p in parts[:-1]]
+    return TType(shape, elem)
+
+
+def _split_top(s: str, sep=","):
+    out, depth, cur = [], 0, ""
+    for ch in s:
+        if ch in "([{<":
+            depth += 1
+        elif ch in ")]}>":
+            depth -= 1
+        if ch == sep and depth == 0:
+            out.append(cur)
+            cur = ""
+        else:
+            cur += ch
+    if cur.strip():
+        out.append(cur)
+    return [x.strip() for x in out]
+
+
+def _find_group(s: str, key: str):
+    """Text inside the parentheses of the first top-level `key(`."""
+    depth = 0
+    i = 0
+    while i < len(s):
+        ch = s[i]
+        if depth == 0 and s.startswith(key + "(", i) and (i == 0 or not s[i - 1].isalnum()):
+            j = i + len(key) + 1
+            d = 1
+            k = j
+            while k < len(s) and d:
+                if s[k] == "(":
+                    d += 1
+                elif s[k] == ")":
+                    d -= 1
+                k += 1
+            return s[j:k - 1]
+        if ch in "([{":
+            depth += 1
+        elif ch in ")]}":
+            depth -= 1
+        i += 1
+    return None
+
+
+def _operand_list(group: str):
+    """`%a, %b : t1, t2` -> ([names], [types])."""
+    if group is None:
+        return [], []
+    if ":" in group:
+        names, types = group.split(":", 1)
+        return ([n.strip() for n in names.split(",") if n.strip()],
+                [parse_type(t) for t in _split_top(types)])
+    return [n.strip() for n in group.split(",") if n.strip()], []
+
+
+def _strip_regions(s: str):
+    """The statement with every {...} region / attribute dict removed."""
+    out, depth = "", 0
+    for ch in s:
+        if ch == "{":
+            depth += 1
+            continue
+        if ch == "}":
+            depth -= 1
+            continue
+        if depth == 0:
+            out += ch
+    return out
+
+
+def _statements(body: str):
+    stmts, cur, depth = [], [], 0
+    for raw in body.split("\n"):
+        line = raw.split("//", 1)[0].rstrip()
+        if not line.strip():
+            continue
+        if depth == 0 and _STMT_START.match(line.strip()) and cur:
+            stmts.append("\n".join(cur))
+            cur = []
+        cur.append(line)
+        depth += sum(line.count(c) for c in "([{") - sum(line.count(c) for c in ")]}")
+    if cur:
+        stmts.append("\n".join(cur))
+    return stmts
+
+
+def parse_op(stmt: str) -> MOp:
+    s = stmt.strip()
+    results = []
+    m = re.match(r"^((?:%[\w]+(?::\d+)?\s*,\s*)*%[\w]+(?::\d+)?)\s*=\s*", s)
+    if m:
+        results = [r.strip() for r in m.group(1).split(",")]
+        s = s[m.end():]
+    name = re.match(r"[\w\.]+", s).group(0)
+    rest = s[len(name):]
+    op = MOp(name=name, results=results, result_types=[], text=stmt)
+    flat = _strip_regions(rest)
+    if name == "arith.constant":
+        ty = flat.rsplit(":", 1)[1].strip()
+        op.result_types = [parse_type(ty)]
+        op.attrs["value"] = flat.rsplit(":", 1)[0].strip()
+    elif name == "tensor.empty":
+        op.result_types = [parse_type(flat.rsplit(":", 1)[1])]
+    elif name == "tensor.pad":
+        src = re.match(r"\s*(%[\w]+)", flat).group(1)
+        op.operands = [src]
+        lo = re.search(r"low\[([^\]]*)\]", flat)
+        hi = re.search(r"high\[([^\]]*)\]", flat)
+        op.attrs["low"] = [int(x) for x in lo.group(1).split(",")] if lo else []
+        op.attrs["high"] = [int(x) for x in hi.group(1).split(",")] if hi else []
+        m2 = re.search(r":\s*(tensor<[^>]*>)\s*to\s*(tensor<[^>]*>)", flat)
+        op.result_types = [parse_type(m2.group(2))]
+        op.attrs["source_type"] = parse_type(m2.group(1))
+    elif name in ("return", "func.return"):
+        op.name = "func.return"
+        names = flat.split(":", 1)[0]
+        op.operands = [n.strip() for n in names.split(",") if n.strip().startswith("%")]
+    elif name in ("tensor.collapse_shape", "tensor.expand_shape"):
+        op.operands = [re.match(r"\s*(%[\w]+)", flat).group(1)]
+        op.result_types = [parse_type(flat.rsplit("into", 1)[1])]
+    elif name == "func.call":
+        m2 = re.match(r"\s*@([\w]+)\(([^)]*)\)\s*:\s*\(([^)]*)\)\s*->\s*(.*)$", flat.strip(), re.S)
+        op.attrs["callee"] = m2.group(1)
+        op.operands = [n.strip() for n in m2.group(2).split(",") if n.strip()]
+        rt = m2.group(4).strip()
+        if rt.startswith("("):
+            rt = rt[1:-1]
+        op.result_types = [parse_type(t) for t in _split_top(rt)] if rt else []
+    elif name.startswith("linalg."):
+        op.ins, in_types = _operand_list(_find_group(flat, "ins"))
+        op.outs, out_types = _operand_list(_find_group(flat, "outs"))
+        op.attrs["in_types"] = in_types
+        op.attrs["out_types"] = out_types
+        m2 = re.search(r"->\s*(.*)$", flat.strip(), re.S)
+        if m2:
+            rt = m2.group(1).strip()
+            if rt.startswith("("):
+                rt = rt[1:-1]
+            op.result_types = [parse_type(t) for t in _split_top(rt)]
+        elif results:
+            op.result_types = list(out_types)
+        if name == "linalg.generic":
+            it = re.search(r"iterator_types\s*=\s*\[([^\]]*)\]", rest)
+            op.iterators = re.findall(r'"(\w+)"', it.group(1)) if it else []
+            region = rest[rest.rfind("^bb"):] if "^bb" in rest else ""
+            op.body_ops = re.findall(r"\b(arith\.\w+|math\.\w+)", region)
+        if name == "linalg.transpose":
+            p = re.search(r"permutation\s*=\s*\[([^\]]*)\]", rest)
+            op.attrs["permutation"] = [int(x) for x in p.group(1).split(",")] if p else []
+        st = re.search(r"strides\s*=\s*dense<(\[[^\]]*\]|\d+)>", rest)
+        if st:
+            v = st.group(1)
+            op.attrs["strides"] = ([int(x) for x in v.strip("[]").split(",")] if v.startswith("[")
+                                   else [int(v)] * 2)
+    else:
+        op.operands = re.findall(r"%[\w]+", flat.split(":", 1)[0])
+    return op
+
+
+def parse_functions(text: str) -> list:
+    """Every func.func with a body in the text."""
+    funcs = []
+    for m in re.finditer(r"func\.func\s+(?:private\s+)?@([\w]+)\s*\(", text):
+        i = m.end()
+        depth, j = 1, i
+        while depth:
+            if text[j] == "(":
+                depth += 1
+            elif text[j] == ")":
+                depth -= 1
+            j += 1
+        args_txt = text[i:j - 1]
+        k = text.index("{", j)
+        header = text[j:k]
+        if "attributes" in header and header.strip().startswith("->") is False and "->" not in header:
+            pass
+        depth, e = 1, k + 1
+        while depth:
+            if text[e] == "{":
+                depth += 1
+            elif text[e] == "}":
+                depth -= 1
+            e += 1
+        body = text[k + 1:e - 1]
+        args = []
+        for a in _split_top(args_txt):
+            if not a:
+                continue
+            n, t = a.split(":", 1)
+            args.append((n.strip(), parse_type(t.split("{")[0])))
+        rtypes = []
+        rm = re.search(r"->\s*(.*?)(?:attributes|$)", header, re.S)
+        if rm and rm.group(1).strip():
+            rt = rm.group(1).strip()
+            if rt.startswith("("):
+                rt = rt[1:-1]
+            rtypes = [parse_type(t) for t in _split_top(rt)]
+        ops = [parse_op(s) for s in _statements(body)]
+        types = {n: t for n, t in args}
+        for op in ops:
+            for r, t in zip(op.results, op.result_types):
+                types[r] = t
+        funcs.append(MFunc(m.group(1), args, rtypes, ops, types))
+    return funcs
+
+
+def parse_file(path: str) -> list:
+    with open(path) as f:
+        return parse_functions(f.read())

@@ -15,27 +15,39 @@ from npu_amd.memref import BF16, F32, I8
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 
 
-def declared_functions():
+def declared_functions(header):
     names = set()
-    for h in glob.glob(os.path.join(ROOT, "include", "*.h")):
-        text = open(h).read()
-        text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
-        for m in re.finditer(r"^\s*[A-Za-z_][\w\s\*]*?\b([a-z_][a-z0-9_]*)\s*\(", text, re.M):
-            if m.group(1) not in ("if", "return", "sizeof"):
-                names.add(m.group(1))
+    text = open(os.path.join(ROOT, "include", header)).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    for m in re.finditer(r"^\s*[A-Za-z_][\w\s\*]*?\b([a-z_][a-z0-9_]*)\s*\(", text, re.M):
+        if m.group(1) not in ("if", "return", "sizeof"):
+            names.add(m.group(1))
     return names
 
 
+def test_headers_cover_every_library():
+    assert sorted(os.path.basename(h) for h in glob.glob(os.path.join(ROOT, "include", "*.h"))) \
+        == ["npu_amd.h", "npu_cost.h"]
+
+
 def test_header_declares_entry_points():
-    names = declared_functions()
+    names = declared_functions("npu_amd.h")
     assert {"fused_matmul_bias_act", "fused_conv2d_nhwc_bias_act", "npu_last_error"} <= names
 
 
 def test_library_exports_every_declared_symbol():
     lib = npu_amd.lib()
-    missing = [n for n in sorted(declared_functions()) if not hasattr(lib, n)]
-    assert not missing, f"declared in include/ but not exported: {missing}"
-    assert set(_lib.SIGNATURES) == declared_functions()
+    missing = [n for n in sorted(declared_functions("npu_amd.h")) if not hasattr(lib, n)]
+    assert not missing, f"declared in npu_amd.h but not exported: {missing}"
+    assert set(_lib.SIGNATURES) == declared_functions("npu_amd.h")
+
+
+def test_host_library_exports_every_declared_symbol():
+    from npu_amd import host
+    h = host.lib()
+    missing = [n for n in sorted(declared_functions("npu_cost.h")) if not hasattr(h, n)]
+    assert not missing, f"declared in npu_cost.h but not exported: {missing}"
+    assert set(host.SIGNATURES) == declared_functions("npu_cost.h")
 
 
 def test_version_and_status_strings():
