@@ -156,6 +156,45 @@ int32_t npu_spec_split(const npu_graph *g, int32_t op, int32_t index, int32_t *o
                        int32_t *iter_dim, int32_t *parallel);
 int32_t npu_spec_preferred_spatial_dim(const npu_graph *g, int32_t op);
 
+/* ---- pass decisions (lib/Transforms) ---- */
+/* npu-fusion's greedy groups (FusionPass.cpp:147-298; anchors by descending
+ * compute cycles, ties in block order).  Op ids group after group into
+ * ops_out, group sizes into sizes_out; returns the number of groups. */
+int32_t npu_pass_fusion_groups(const npu_graph *g, const npu_hw_target *t, int32_t *ops_out,
+                               int32_t cap_ops, int32_t *sizes_out, int32_t cap_groups);
+/* Tile-and-fuse of a (matrix op -> generic) pair (FusionPass.cpp:306-359):
+ * 1 and the consumer's tile config if it is tiled, 0 if not. */
+int32_t npu_pass_tile_and_fuse(const npu_graph *g, const npu_hw_target *t, int32_t consumer,
+                               npu_schedule_cost *out);
+/* npu-outline-fused-groups (OutlineFusedGroupsPass.cpp:123-321) over every
+ * linalg op; groups numbered by their first op.  Same output convention as
+ * npu_pass_fusion_groups. */
+int32_t npu_pass_outline_groups(const npu_graph *g, const npu_hw_target *t, int32_t *ops_out,
+                                int32_t cap_ops, int32_t *sizes_out, int32_t cap_groups);
+/* Name (fused_<ops>_<idx>) and signature of outlined group `index`:
+ * external inputs in first-use order, outputs used outside then the last
+ * op's results (value ids). */
+int32_t npu_pass_outline_group_info(const npu_graph *g, const npu_hw_target *t, int32_t index,
+                                    char *name, int32_t name_cap, int32_t *inputs,
+                                    int32_t *n_inputs, int32_t *outputs, int32_t *n_outputs,
+                                    int32_t cap);
+typedef struct npu_spatial_decision {
+  int32_t iter_dim, out_dim;
+  int64_t dim_size, tile_size, full_iters, peel_size, cost;
+  int32_t n_candidates, reserved;
+  int32_t cand_iter_dims[8];
+  int64_t cand_costs[8];
+} npu_spatial_decision;
+/* npu-spatial-tiling for one top-level op (SpatialTilingPass.cpp:38-168):
+ * 1 if the op is tiled (decision in *out), 0 if it is not a candidate. */
+int32_t npu_pass_spatial(const npu_graph *g, const npu_hw_target *t, int32_t op, int64_t cores,
+                         npu_spatial_decision *out);
+/* npu-temporal-tiling (TemporalTilingPass.cpp:76-336): the number of loops
+ * (tile sizes in iteration-domain coordinates, 0 = untiled dim) or 0 if the
+ * op stays untiled. */
+int32_t npu_pass_temporal(const npu_graph *g, const npu_hw_target *t, int32_t op,
+                          npu_schedule_cost *cost, int64_t *tile_sizes, int32_t cap);
+
 #ifdef __cplusplus
 }
 #endif

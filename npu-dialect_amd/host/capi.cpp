@@ -6,6 +6,7 @@
 
 #include "../../include/npu_cost.h"
 #include "cost_model.hpp"
+#include "passes.hpp"
 
 struct npu_graph {
   npu::ir::Graph g;
@@ -307,6 +308,109 @@ int32_t npu_spec_preferred_spatial_dim(const npu_graph *g, int32_t op) {
   if (bad_op(g, op)) return fail("bad op");
   const npu::OperatorTilingSpec *s = npu::get_tiling_spec(g->g, op);
   return s ? s->preferred_spatial_dim : -1;
+}
+
+static int32_t put_groups(const std::vector<std::vector<int32_t>> &groups, int32_t *ops_out,
+                          int32_t cap_ops, int32_t *sizes_out, int32_t cap_groups) {
+  int32_t k = 0;
+  for (size_t i = 0; i < groups.size(); ++i) {
+    if ((int32_t)i < cap_groups && sizes_out) sizes_out[i] = (int32_t)groups[i].size();
+    for (int32_t op : groups[i]) {
+      if (k < cap_ops && ops_out) ops_out[k] = op;
+      ++k;
+    }
+  }
+  return (int32_t)groups.size();
+}
+
+int32_t npu_pass_fusion_groups(const npu_graph *g, const npu_hw_target *t, int32_t *ops_out,
+                               int32_t cap_ops, int32_t *sizes_out, int32_t cap_groups) {
+  if (!g || !t) return fail("null argument");
+  npu::CostModel cm(g->g, to_target(t));
+  return put_groups(npu::fusion_groups(g->g, cm), ops_out, cap_ops, sizes_out, cap_groups);
+}
+
+int32_t npu_pass_tile_and_fuse(const npu_graph *g, const npu_hw_target *t, int32_t consumer,
+                               npu_schedule_cost *out) {
+  if (bad_op(g, consumer) || !t || !out) return fail("bad op");
+  npu::CostModel cm(g->g, to_target(t));
+  npu::TileConfig c;
+  const bool tiled = npu::tile_and_fuse_decision(g->g, cm, consumer, &c);
+  put_schedule(c.cost, c.tile_sizes, out);
+  return tiled ? 1 : 0;
+}
+
+static std::vector<npu::OutlinedGroup> outline_all(const npu_graph *g, const npu::CostModel &cm) {
+  std::vector<int32_t> scope(g->g.ops.size());
+  for (size_t i = 0; i < scope.size(); ++i) scope[i] = (int32_t)i;
+  return npu::outline_groups(g->g, cm, scope);
+}
+
+int32_t npu_pass_outline_groups(const npu_graph *g, const npu_hw_target *t, int32_t *ops_out,
+                                int32_t cap_ops, int32_t *sizes_out, int32_t cap_groups) {
+  if (!g || !t) return fail("null argument");
+  npu::CostModel cm(g->g, to_target(t));
+  std::vector<std::vector<int32_t>> groups;
+  for (const auto &grp : outline_all(g, cm)) groups.push_back(grp.ops);
+  return put_groups(groups, ops_out, cap_ops, sizes_out, cap_groups);
+}
+
+int32_t npu_pass_outline_group_info(const npu_graph *g, const npu_hw_target *t, int32_t index,
+                                    char *name, int32_t name_cap, int32_t *inputs,
+                                    int32_t *n_inputs, int32_t *outputs, int32_t *n_outputs,
+                                    int32_t cap) {
+  if (!g || !t) return fail("null argument");
+  npu::CostModel cm(g->g, to_target(t));
+  const auto groups = outline_all(g, cm);
+  if (index < 0 || index >= (int32_t)groups.size()) return fail("bad group index %d", index);
+  const auto &grp = groups[index];
+  if (name && name_cap > 0) {
+    const size_t n = std::min<size_t>(grp.name.size(), (size_t)name_cap - 1);
+    std::copy(grp.name.begin(), grp.name.begin() + n, name);
+    name[n] = '\0';
+  }
+  if (n_inputs) *n_inputs = (int32_t)grp.inputs.size();
+  if (n_outputs) *n_outputs = (int32_t)grp.outputs.size();
+  for (int32_t i = 0; i < cap && i < (int32_t)grp.inputs.size(); ++i)
+    if (inputs) inputs[i] = grp.inputs[i];
+  for (int32_t i = 0; i < cap && i < (int32_t)grp.outputs.size(); ++i)
+    if (outputs) outputs[i] = grp.outputs[i];
+  return 0;
+}
+
+int32_t npu_pass_spatial(const npu_graph *g, const npu_hw_target *t, int32_t op, int64_t cores,
+                         npu_spatial_decision *out) {
+  if (bad_op(g, op) || !t || !out || cores <= 0) return fail("bad argument");
+  npu::CostModel cm(g->g, to_target(t));
+  npu::SpatialDecision d;
+  const bool tiled = npu::spatial_decision(g->g, cm, op, cores, &d);
+  *out = npu_spatial_decision{};
+  if (!tiled) return 0;
+  out->iter_dim = d.iter_dim;
+  out->out_dim = d.out_dim;
+  out->dim_size = d.dim_size;
+  out->tile_size = d.tile_size;
+  out->full_iters = d.full_iters;
+  out->peel_size = d.peel_size;
+  out->cost = d.cost;
+  out->n_candidates = (int32_t)std::min<size_t>(8, d.candidates.size());
+  for (int32_t i = 0; i < out->n_candidates; ++i) {
+    out->cand_iter_dims[i] = d.candidates[i].first;
+    out->cand_costs[i] = d.candidates[i].second;
+  }
+  return 1;
+}
+
+int32_t npu_pass_temporal(const npu_graph *g, const npu_hw_target *t, int32_t op,
+                          npu_schedule_cost *cost, int64_t *tile_sizes, int32_t cap) {
+  if (bad_op(g, op) || !t) return fail("bad argument");
+  npu::CostModel cm(g->g, to_target(t));
+  npu::TileConfig c;
+  if (!npu::temporal_decision(g->g, cm, op, &c)) return 0;
+  if (cost) put_schedule(c.cost, c.tile_sizes, cost);
+  for (int32_t i = 0; i < cap && i < (int32_t)c.tile_sizes.size(); ++i)
+    if (tile_sizes) tile_sizes[i] = c.tile_sizes[i];
+  return (int32_t)c.tile_sizes.size();
 }
 
 }  // extern "C"

@@ -298,3 +298,79 @@ def conv2d_tile(target, tn, tco, th, tw, N, Co, Ho, Wo, Ci, Kh, Kw, dtype_bytes,
 def spill_strategy(target, working_set, intermediate_bytes):
     return "spill" if lib().npu_cm_spill_strategy(C.byref(target), working_set,
                                                  intermediate_bytes) else "retile"
+
+
+# ---------------------------------------------------------------- pass decisions
+class SpatialDecision(C.Structure):
+    _fields_ = [("iter_dim", C.c_int32), ("out_dim", C.c_int32), ("dim_size", C.c_int64),
+                ("tile_size", C.c_int64), ("full_iters", C.c_int64), ("peel_size", C.c_int64),
+                ("cost", C.c_int64), ("n_candidates", C.c_int32), ("reserved", C.c_int32),
+                ("cand_iter_dims", C.c_int32 * 8), ("cand_costs", C.c_int64 * 8)]
+
+    @property
+    def candidates(self):
+        return [(self.cand_iter_dims[i], self.cand_costs[i]) for i in range(self.n_candidates)]
+
+
+SIGNATURES.update({
+    "npu_pass_fusion_groups": (_I32, [_P, _PT, _PI32, _I32, _PI32, _I32]),
+    "npu_pass_tile_and_fuse": (_I32, [_P, _PT, _I32, C.POINTER(ScheduleCost)]),
+    "npu_pass_outline_groups": (_I32, [_P, _PT, _PI32, _I32, _PI32, _I32]),
+    "npu_pass_outline_group_info": (_I32, [_P, _PT, _I32, C.c_char_p, _I32, _PI32, _PI32, _PI32,
+                                           _PI32, _I32]),
+    "npu_pass_spatial": (_I32, [_P, _PT, _I32, _I64, C.POINTER(SpatialDecision)]),
+    "npu_pass_temporal": (_I32, [_P, _PT, _I32, C.POINTER(ScheduleCost), _PI64, _I32]),
+})
+
+
+def _groups(fn, g: Graph, t: HWTarget):
+    ops = (C.c_int32 * 4096)()
+    sizes = (C.c_int32 * 1024)()
+    n = _check(fn(g.h, C.byref(t), ops, 4096, sizes, 1024))
+    inv = {oid: i for i, oid in enumerate(g.op_id)}
+    out, k = [], 0
+    for i in range(n):
+        out.append([inv[ops[k + j]] for j in range(sizes[i])])
+        k += sizes[i]
+    return out
+
+
+def fusion_groups(g: Graph, t: HWTarget):
+    """npu-fusion groups, as lists of indices into func.ops."""
+    return _groups(lib().npu_pass_fusion_groups, g, t)
+
+
+def tile_and_fuse(g: Graph, t: HWTarget, consumer):
+    s = ScheduleCost()
+    tiled = _check(lib().npu_pass_tile_and_fuse(g.h, C.byref(t), g.op_id[consumer], C.byref(s)))
+    return bool(tiled), s
+
+
+def outline_groups(g: Graph, t: HWTarget):
+    """npu-outline-fused-groups: [{ops, name, inputs, outputs}] with SSA names."""
+    groups = _groups(lib().npu_pass_outline_groups, g, t)
+    names = {v: k for k, v in g.value_id.items()}
+    out = []
+    for i, ops in enumerate(groups):
+        buf = C.create_string_buffer(512)
+        ins, outs = (C.c_int32 * 64)(), (C.c_int32 * 64)()
+        ni, no = C.c_int32(), C.c_int32()
+        _check(lib().npu_pass_outline_group_info(g.h, C.byref(t), i, buf, 512, ins, C.byref(ni),
+                                                 outs, C.byref(no), 64))
+        out.append({"ops": ops, "name": buf.value.decode(),
+                    "inputs": [names[ins[j]] for j in range(ni.value)],
+                    "outputs": [names[outs[j]] for j in range(no.value)]})
+    return out
+
+
+def spatial(g: Graph, t: HWTarget, op, cores):
+    d = SpatialDecision()
+    tiled = _check(lib().npu_pass_spatial(g.h, C.byref(t), g.op_id[op], cores, C.byref(d)))
+    return d if tiled else None
+
+
+def temporal(g: Graph, t: HWTarget, op):
+    s = ScheduleCost()
+    ts = (C.c_int64 * 16)()
+    n = _check(lib().npu_pass_temporal(g.h, C.byref(t), g.op_id[op], C.byref(s), ts, 16))
+    return (list(ts[:n]), s) if n else (None, None)
