@@ -39,50 +39,103 @@ __global__ __launch_bounds__(256) void irb_kernel(const float *__restrict__ x,
   constexpr int XS = KC1 * 16 + 4;    // LDS row strides in floats (+4 against bank conflicts)
   constexpr int ES = E + 4;
   constexpr int FB1 = E / 16;         // expand filter blocks
+  constexpr int FBW = (FB1 + 3) / 4;  // ... per wave (wave w owns w, w+4, ...)
   constexpr int KC2 = E / 16;         // project reduction chunks
   constexpr int FB2 = (C + 15) / 16;  // project filter blocks
+  constexpr int XV = KC1 * 4;         // float4 columns per staged x row
+  constexpr int XSEG = HPB * 16 * XV;
+  constexpr int XSEGS = (XSEG + 255) / 256;
   __shared__ __attribute__((aligned(16))) float xs[HPB * 16 * XS];
   __shared__ __attribute__((aligned(16))) float es[HP * ES];
+  __shared__ __attribute__((aligned(16))) float wds[9 * E];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int r = lane & 15, q = lane >> 4;
   const int n = blockIdx.y;
   const int ty0 = (blockIdx.x / tiles_w) * TH, tx0 = (blockIdx.x % tiles_w) * TW;
 
-  // ---- x halo tile, zero-padded to KC1*16 channels and 112 rows.
-  constexpr int XV = KC1 * 4;  // float4 columns per row
-  for (int idx = tid; idx < HPB * 16 * XV; idx += 256) {
+  // ---- every global load up front: the x halo (zero-padded to KC1*16
+  //      channels and 112 rows; clamped addresses, zero fill by select), this
+  //      wave's expand filter blocks and the depthwise taps.
+  f32x4 st[XSEGS];
+#pragma unroll
+  for (int s = 0; s < XSEGS; ++s) {
+    const int idx = min(tid + 256 * s, XSEG - 1);
     const int hp = idx / XV, c = (idx - hp * XV) * 4;
     const int iy = ty0 + hp / HW - 1, ix = tx0 + hp % HW - 1;
-    f32x4 v = {0.f, 0.f, 0.f, 0.f};
-    if (hp < HP && c < C && iy >= 0 && iy < H && ix >= 0 && ix < W)
-      v = *reinterpret_cast<const f32x4 *>(x + ((size_t)(n * H + iy) * W + ix) * C + c);
-    *reinterpret_cast<f32x4 *>(xs + hp * XS + c) = v;
+    const bool inside = hp < HP && c < C && iy >= 0 && iy < H && ix >= 0 && ix < W;
+    const int iyc = min(max(iy, 0), H - 1), ixc = min(max(ix, 0), W - 1);
+    const f32x4 v = *reinterpret_cast<const f32x4 *>(
+        x + ((size_t)(n * H + iyc) * W + ixc) * C + min(c, C - 4));
+    st[s] = inside ? v : f32x4{0.f, 0.f, 0.f, 0.f};
+  }
+  Frag16 be[FBW][KC1];
+#pragma unroll
+  for (int j = 0; j < FBW; ++j)
+#pragma unroll
+    for (int kc = 0; kc < KC1; ++kc) {
+      const int f = min(wave + 4 * j, FB1 - 1) * 16 + r;
+      const int k = kc * 16 + 4 * q;
+      Frag16 b = load16(we + f * C + min(k, C - 4));
+      b.u = masked(b.u, k < C);
+      be[j][kc] = b;
+    }
+  for (int i = tid; i < 9 * E / 4; i += 256)
+    reinterpret_cast<f32x4 *>(wds)[i] = reinterpret_cast<const f32x4 *>(wdw)[i];
+#pragma unroll
+  for (int s = 0; s < XSEGS; ++s) {
+    const int idx = tid + 256 * s;
+    if (idx < XSEG) {
+      const int hp = idx / XV, c = (idx - hp * XV) * 4;
+      *reinterpret_cast<f32x4 *>(xs + hp * XS + c) = st[s];
+    }
   }
   __syncthreads();
 
-  // ---- expand on the halo: 7 pixel blocks x FB1 filter blocks, round-robin.
-  for (int t = wave; t < HPB * FB1; t += 4) {
-    const int pb = t / FB1, fb = t - pb * FB1;
+  // ---- expand on the halo: wave w computes its filter blocks for all 7
+  //      pixel blocks; the four MFMA steps of a fragment are interleaved
+  //      across the pixel blocks.
+#pragma unroll
+  for (int j = 0; j < FBW; ++j) {
+    const int fb = wave + 4 * j;
+    if (fb >= FB1) break;
     const int f = fb * 16 + r;
-    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+    f32x4 acc[HPB];
+#pragma unroll
+    for (int pb = 0; pb < HPB; ++pb) acc[pb] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int kc = 0; kc < KC1; ++kc) {
-      const int k = kc * 16 + 4 * q;
-      const Frag16 a = load16(xs + (pb * 16 + r) * XS + k);
-      const Frag16 b = k < C ? load16(we + f * C + k) : frag_zero();
-      MfmaF32::mma(acc, a, b);
+      Frag16 a[HPB];
+#pragma unroll
+      for (int pb = 0; pb < HPB; ++pb) a[pb] = load16(xs + (pb * 16 + r) * XS + kc * 16 + 4 * q);
+#pragma unroll
+      for (int st2 = 0; st2 < 4; ++st2)
+#pragma unroll
+        for (int pb = 0; pb < HPB; ++pb) MfmaF32::step(acc[pb], a[pb], be[j][kc], st2);
     }
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const int hp = pb * 16 + 4 * q + e;
-      if (hp < HP) {
-        const int iy = ty0 + hp / HW - 1, ix = tx0 + hp % HW - 1;
-        const bool inside = iy >= 0 && iy < H && ix >= 0 && ix < W;
-        es[hp * ES + f] = inside ? relu6(acc[e]) : 0.0f;
+    for (int pb = 0; pb < HPB; ++pb)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int hp = pb * 16 + 4 * q + e;
+        if (hp < HP) {
+          const int iy = ty0 + hp / HW - 1, ix = tx0 + hp % HW - 1;
+          const bool inside = iy >= 0 && iy < H && ix >= 0 && ix < W;
+          es[hp * ES + f] = inside ? relu6(acc[pb][e]) : 0.0f;
+        }
       }
-    }
   }
+  // the project filters are fetched while the other waves finish expanding
+  Frag16 bp[KC2][FB2];
+#pragma unroll
+  for (int kc = 0; kc < KC2; ++kc)
+#pragma unroll
+    for (int fb = 0; fb < FB2; ++fb) {
+      const int c = fb * 16 + r;
+      Frag16 b = load16(wp + min(c, C - 1) * E + kc * 16 + 4 * q);
+      b.u = masked(b.u, c < C);
+      bp[kc][fb] = b;
+    }
   __syncthreads();
 
   // ---- depthwise (in registers, A-operand layout) + project + residual.
@@ -92,24 +145,20 @@ __global__ __launch_bounds__(256) void irb_kernel(const float *__restrict__ x,
   f32x4 acc2[FB2];
 #pragma unroll
   for (int fb = 0; fb < FB2; ++fb) acc2[fb] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
   for (int kc = 0; kc < KC2; ++kc) {
     const int e0 = kc * 16 + 4 * q;
     f32x4 d = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int t = 0; t < 9; ++t) {
-      const int hidx = hbase + (t / 3) * HW + (t % 3);
-      const f32x4 ev = *reinterpret_cast<const f32x4 *>(es + hidx * ES + e0);
-      const f32x4 wv = *reinterpret_cast<const f32x4 *>(wdw + t * E + e0);
+      const f32x4 ev = *reinterpret_cast<const f32x4 *>(es + (hbase + (t / 3) * HW + (t % 3)) * ES + e0);
+      const f32x4 wv = *reinterpret_cast<const f32x4 *>(wds + t * E + e0);
       d += ev * wv;
     }
     Frag16 a;
     a.f = f32x4{relu6(d[0]), relu6(d[1]), relu6(d[2]), relu6(d[3])};
 #pragma unroll
-    for (int fb = 0; fb < FB2; ++fb) {
-      const int c = fb * 16 + r;
-      const Frag16 b = c < C ? load16(wp + c * E + e0) : frag_zero();
-      MfmaF32::mma(acc2[fb], a, b);
-    }
+    for (int fb = 0; fb < FB2; ++fb) MfmaF32::mma(acc2[fb], a, bp[kc][fb]);
   }
 #pragma unroll
   for (int fb = 0; fb < FB2; ++fb) {

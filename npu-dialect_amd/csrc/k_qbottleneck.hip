@@ -43,9 +43,13 @@ __global__ __launch_bounds__(256) void qbottleneck_kernel(
     const int32_t *__restrict__ m2, const int32_t *__restrict__ s2,
     const int32_t *__restrict__ m3, const int32_t *__restrict__ s3, int8_t *__restrict__ out,
     int H, int W, int tiles_w) {
-  static_assert(C % 64 == 0 && M1 % 64 == 0, "channel counts must be multiples of 64");
+  static_assert(C % 64 == 0 && M1 == 64, "C must be a multiple of 64 and M1 = 64");
   constexpr int XS = C + 16;    // LDS row strides (16-byte pad against bank conflicts)
   constexpr int YS = M1 + 16;
+  constexpr int XCH = C / 16;   // 16-byte runs per pixel
+  constexpr int NSEG = HPB * 16 * XCH;
+  constexpr int SEGS = (NSEG + 255) / 256;
+  constexpr int FB3 = C / 16 / 4;  // conv3 filter blocks per wave
   __shared__ __attribute__((aligned(16))) int8_t xs[HPB * 16 * XS];
   __shared__ __attribute__((aligned(16))) int8_t y1[HPB * 16 * YS];
   __shared__ __attribute__((aligned(16))) int8_t y2[OP * YS];
@@ -55,74 +59,85 @@ __global__ __launch_bounds__(256) void qbottleneck_kernel(
   const int n = blockIdx.y;
   const int ty0 = (blockIdx.x / tiles_w) * TH, tx0 = (blockIdx.x % tiles_w) * TW;
 
-  // ---- stage the x halo tile (zero outside the image: the pad of conv2
-  //      is applied to y1 below; x's own halo values only feed conv1).
-  constexpr int XCH = C / 16;
-  for (int idx = tid; idx < HPB * 16 * XCH; idx += 256) {
+  // ---- issue every global load the first two stages need at once: the x
+  //      halo (clamped addresses, zero fill by select), and this wave's
+  //      filter block of w1 and w2 (wave w owns filters 16w..16w+15 of conv1
+  //      and conv2).
+  u32x4 st[SEGS];
+#pragma unroll
+  for (int s = 0; s < SEGS; ++s) {
+    const int idx = min(tid + 256 * s, NSEG - 1);
     const int hp = idx / XCH, ch = idx - hp * XCH;
     const int iy = ty0 + hp / HW - 1, ix = tx0 + hp % HW - 1;
-    u32x4 v = {0u, 0u, 0u, 0u};
-    if (hp < HP && iy >= 0 && iy < H && ix >= 0 && ix < W)
-      v = *reinterpret_cast<const u32x4 *>(x + ((size_t)(n * H + iy) * W + ix) * C + ch * 16);
-    *reinterpret_cast<u32x4 *>(xs + hp * XS + ch * 16) = v;
+    const bool inside = hp < HP && iy >= 0 && iy < H && ix >= 0 && ix < W;
+    const int iyc = min(max(iy, 0), H - 1), ixc = min(max(ix, 0), W - 1);
+    st[s] = masked(*reinterpret_cast<const u32x4 *>(
+                       x + ((size_t)(n * H + iyc) * W + ixc) * C + ch * 16),
+                   inside);
+  }
+  const int f12 = wave * 16 + r;
+  Frag16 b1[C / 64], b2[9];
+#pragma unroll
+  for (int kc = 0; kc < C / 64; ++kc) b1[kc] = load16(w1 + f12 * C + kc * 64 + 16 * q);
+#pragma unroll
+  for (int t = 0; t < 9; ++t) b2[t] = load16(w2 + (f12 * 9 + t) * M1 + 16 * q);
+  const int mul1 = m1[f12], sh1 = s1[f12], mul2 = m2[f12], sh2 = s2[f12];
+#pragma unroll
+  for (int s = 0; s < SEGS; ++s) {
+    const int idx = tid + 256 * s;
+    if (idx < NSEG) {
+      const int hp = idx / XCH, ch = idx - hp * XCH;
+      *reinterpret_cast<u32x4 *>(xs + hp * XS + ch * 16) = st[s];
+    }
   }
   __syncthreads();
 
+  // conv3's weights are fetched while conv1 and conv2 run.
+  Frag16 b3[FB3];
+  int mul3[FB3], sh3[FB3];
+#pragma unroll
+  for (int j = 0; j < FB3; ++j) {
+    const int f = (wave + 4 * j) * 16 + r;
+    b3[j] = load16(w3 + f * M1 + 16 * q);
+    mul3[j] = m3[f];
+    sh3[j] = s3[f];
+  }
+
   // ---- conv1 (1x1, C -> M1) on all halo pixels, requant + ReLU into y1.
-  for (int fb = wave; fb < M1 / 16; fb += 4) {
-    const int f = fb * 16 + r;
-    Frag16 b[C / 64];
 #pragma unroll
-    for (int kc = 0; kc < C / 64; ++kc) b[kc] = load16(w1 + f * C + kc * 64 + 16 * q);
-    const int mul = m1[f], sh = s1[f];
+  for (int pb = 0; pb < HPB; ++pb) {
+    i32x4 acc = {0, 0, 0, 0};
 #pragma unroll
-    for (int pb = 0; pb < HPB; ++pb) {
-      i32x4 acc = {0, 0, 0, 0};
+    for (int kc = 0; kc < C / 64; ++kc) {
+      const Frag16 a = load16(xs + (pb * 16 + r) * XS + kc * 64 + 16 * q);
+      MfmaI8::mma(acc, a, b1[kc]);
+    }
 #pragma unroll
-      for (int kc = 0; kc < C / 64; ++kc) {
-        const Frag16 a = load16(xs + (pb * 16 + r) * XS + kc * 64 + 16 * q);
-        MfmaI8::mma(acc, a, b[kc]);
-      }
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const int hp = pb * 16 + 4 * q + e;
-        const int iy = ty0 + hp / HW - 1, ix = tx0 + hp % HW - 1;
-        const bool inside = hp < HP && iy >= 0 && iy < H && ix >= 0 && ix < W;
-        const int v = inside ? clamp_i(requant(acc[e], mul, sh), 0, 127) : 0;
-        y1[hp * YS + f] = (int8_t)v;
-      }
+    for (int e = 0; e < 4; ++e) {
+      const int hp = pb * 16 + 4 * q + e;
+      const int iy = ty0 + hp / HW - 1, ix = tx0 + hp % HW - 1;
+      const bool inside = hp < HP && iy >= 0 && iy < H && ix >= 0 && ix < W;
+      const int v = inside ? clamp_i(requant(acc[e], mul1, sh1), 0, 127) : 0;
+      y1[hp * YS + f12] = (int8_t)v;
     }
   }
   __syncthreads();
 
   // ---- conv2 (3x3, M1 -> M1) over the 8x8 tile from the y1 halo.
-  for (int fb = wave; fb < M1 / 16; fb += 4) {
-    const int f = fb * 16 + r;
-    Frag16 b[9][M1 / 64];
 #pragma unroll
-    for (int t = 0; t < 9; ++t)
+  for (int pb = 0; pb < OP / 16; ++pb) {
+    const int p = pb * 16 + r;
+    const int hbase = (p / TW) * HW + (p % TW);
+    i32x4 acc = {0, 0, 0, 0};
 #pragma unroll
-      for (int kc = 0; kc < M1 / 64; ++kc) b[t][kc] = load16(w2 + (f * 9 + t) * M1 + kc * 64 + 16 * q);
-    const int mul = m2[f], sh = s2[f];
+    for (int t = 0; t < 9; ++t) {
+      const Frag16 a = load16(y1 + (hbase + (t / 3) * HW + (t % 3)) * YS + 16 * q);
+      MfmaI8::mma(acc, a, b2[t]);
+    }
 #pragma unroll
-    for (int pb = 0; pb < OP / 16; ++pb) {
-      const int p = pb * 16 + r;
-      const int hbase = (p / TW) * HW + (p % TW);
-      i32x4 acc = {0, 0, 0, 0};
-#pragma unroll
-      for (int t = 0; t < 9; ++t) {
-        const int hidx = hbase + (t / 3) * HW + (t % 3);
-#pragma unroll
-        for (int kc = 0; kc < M1 / 64; ++kc) {
-          const Frag16 a = load16(y1 + hidx * YS + kc * 64 + 16 * q);
-          MfmaI8::mma(acc, a, b[t][kc]);
-        }
-      }
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const int pe = pb * 16 + 4 * q + e;
-        y2[pe * YS + f] = (int8_t)clamp_i(requant(acc[e], mul, sh), 0, 127);
-      }
+    for (int e = 0; e < 4; ++e) {
+      const int pe = pb * 16 + 4 * q + e;
+      y2[pe * YS + f12] = (int8_t)clamp_i(requant(acc[e], mul2, sh2), 0, 127);
     }
   }
   __syncthreads();
@@ -130,25 +145,21 @@ __global__ __launch_bounds__(256) void qbottleneck_kernel(
   // ---- conv3 (1x1, M1 -> C), requant + residual + ReLU.  The result
   //      overwrites the residual's own slot in the x tile (each element is
   //      read and written by the same lane).
-  for (int fb = wave; fb < C / 16; fb += 4) {
-    const int f = fb * 16 + r;
-    Frag16 b[M1 / 64];
+  Frag16 a3[OP / 16];
 #pragma unroll
-    for (int kc = 0; kc < M1 / 64; ++kc) b[kc] = load16(w3 + f * M1 + kc * 64 + 16 * q);
-    const int mul = m3[f], sh = s3[f];
+  for (int pb = 0; pb < OP / 16; ++pb) a3[pb] = load16(y2 + (pb * 16 + r) * YS + 16 * q);
+#pragma unroll
+  for (int j = 0; j < FB3; ++j) {
+    const int f = (wave + 4 * j) * 16 + r;
 #pragma unroll
     for (int pb = 0; pb < OP / 16; ++pb) {
       i32x4 acc = {0, 0, 0, 0};
-#pragma unroll
-      for (int kc = 0; kc < M1 / 64; ++kc) {
-        const Frag16 a = load16(y2 + (pb * 16 + r) * YS + kc * 64 + 16 * q);
-        MfmaI8::mma(acc, a, b[kc]);
-      }
+      MfmaI8::mma(acc, a3[pb], b3[j]);
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         const int pe = pb * 16 + 4 * q + e;
         const int hp = (pe / TW + 1) * HW + (pe % TW) + 1;
-        const int v = requant(acc[e], mul, sh) + (int)xs[hp * XS + f];
+        const int v = requant(acc[e], mul3[j], sh3[j]) + (int)xs[hp * XS + f];
         xs[hp * XS + f] = (int8_t)clamp_i(v, 0, 127);
       }
     }
