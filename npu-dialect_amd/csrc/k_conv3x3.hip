@@ -3,18 +3,28 @@
 // conv2d configurations (56x56x64 -> 64).
 //
 // A workgroup owns TR full image rows of one image and 64 (or 16) filters.
-// The reduction runs over channel chunks (16 f32 / 32 bf16 = one MFMA
-// operand run).  For each chunk the zero-padded (TR+2) x (W+2) input halo is
-// staged once into LDS and all nine taps read their A operands from it with
-// shifted addressing, so each input element leaves HBM/L2 once per chunk
-// instead of once per tap.  The next chunk's halo is fetched into registers
+// The reduction runs over stages of NCH channel chunks (a chunk is one MFMA
+// operand run: 16 f32 or 32 bf16 channels).  For each stage the zero-padded
+// (TR+2) x (W+2) input halo is staged once into LDS and all nine taps read
+// their A operands from it with shifted addressing, so each input element
+// leaves HBM/L2 once per stage instead of once per tap.  With several stages
+// the next stage's halo and filter fragments are fetched into registers
 // while the current one is multiplied (double-buffered LDS, one barrier per
-// chunk).  Filters are read straight from L2 as B operands (FHWC keeps each
-// lane's channel run contiguous); the pad of tensor.pad is the zero fill of
-// out-of-image halo records.
+// stage); when one stage covers every channel (bf16, C = 64) the whole
+// reduction runs after a single barrier.  Filters are read straight from L2
+// as B operands (FHWC keeps each lane's channel run contiguous); the pad of
+// tensor.pad is the zero fill of out-of-image halo records.
 //
-// LDS record: one pixel's 64 bytes of the chunk plus 16 bytes of padding, so
-// the 16 lanes that read 16 consecutive pixels hit distinct bank groups.
+// Summation order is fixed (chunk by chunk, tap by tap within a chunk)
+// whatever NCH is, so every variant returns the same bits.
+//
+// LDS record: one pixel's NCH*64 bytes of the stage plus 16 bytes of padding,
+// so the 16 lanes that read 16 consecutive pixels hit distinct bank groups.
+//
+// Workgroups are dispatched round-robin over the 8 XCDs, each with its own
+// L2.  Consecutive block indices are remapped so that each XCD gets a
+// contiguous range of row tiles: neighbouring tiles share two halo rows, and
+// on one XCD the second read of those rows hits L2 instead of HBM.
 #include "kernels.hpp"
 #include "npu_device.hpp"
 
@@ -22,32 +32,35 @@ namespace npu {
 
 namespace {
 
-constexpr int kWMax = 64;      // widest image row this kernel stages
-constexpr int kRecBytes = 80;  // 64 data bytes + 16 pad
+constexpr int kXcds = 8;
 
-template <class MM, typename T, int TR, int WF>
+template <class MM, typename T, int TR, int WF, int WMAX, int NCH, int NBUF>
 __global__ __launch_bounds__(256) void conv3x3_rows_kernel(
     const T *__restrict__ x, const T *__restrict__ w, const float *__restrict__ bias,
     T *__restrict__ out, int H, int W, int C, int F, int act) {
-  constexpr int WP = 4 / WF;                 // waves along pixels
-  constexpr int KPL = MM::kPerLane;          // elements of one lane's 16-byte run
-  constexpr int KC = MM::kPerFrag;           // channels per chunk (64 bytes)
-  constexpr int REC = kRecBytes / sizeof(T); // LDS record stride in elements
+  constexpr int WP = 4 / WF;                  // waves along pixels
+  constexpr int KPL = MM::kPerLane;           // elements of one lane's 16-byte run
+  constexpr int KC = MM::kPerFrag;            // channels per chunk (64 bytes)
+  constexpr int SEGP = NCH * 4;               // 16-byte segments per pixel and stage
+  constexpr int REC = (NCH * 64 + 16) / sizeof(T);  // LDS record stride in elements
   constexpr int HR = TR + 2;
-  constexpr int PBMAX = (TR * kWMax + 15) / 16;
-  constexpr int PBW = (PBMAX + WP - 1) / WP; // pixel blocks per wave
-  constexpr int SEGS = (HR * (kWMax + 2) * 4 + 255) / 256;
+  constexpr int PBMAX = (TR * WMAX + 15) / 16;
+  constexpr int PBW = (PBMAX + WP - 1) / WP;  // pixel blocks per wave
+  constexpr int SEGS = (HR * (WMAX + 2) * SEGP + 255) / 256;
   static_assert(KC * sizeof(T) == 64, "a chunk is 64 bytes per pixel");
-  __shared__ __attribute__((aligned(16))) T halo[2][HR * (kWMax + 2) * REC];
+  static_assert(NBUF == 1 || NBUF == 2, "single or double buffered");
+  __shared__ __attribute__((aligned(16))) T halo[NBUF][HR * (WMAX + 2) * REC];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int r = lane & 15, q = lane >> 4;
   const int tiles_h = (H + TR - 1) / TR;
-  const int n = blockIdx.x / tiles_h, h0 = (blockIdx.x - n * tiles_h) * TR;
+  int tile = blockIdx.x;
+  if (gridDim.x % kXcds == 0) tile = (tile % kXcds) * (gridDim.x / kXcds) + tile / kXcds;
+  const int n = tile / tiles_h, h0 = (tile - n * tiles_h) * TR;
   const int f = (blockIdx.y * WF + (wave % WF)) * 16 + r;
   const bool fok = f < F;
   const int wp = wave / WF;
-  const int HC = W + 2, nseg = HR * HC * 4;
+  const int HC = W + 2, nseg = HR * HC * SEGP;
   const int tile_px = TR * W;
 
   // Per-lane pixel rows of the A operand (pixel = pb*16 + r within the tile).
@@ -68,7 +81,7 @@ __global__ __launch_bounds__(256) void conv3x3_rows_kernel(
 #pragma unroll
     for (int s = 0; s < SEGS; ++s) {
       const int idx = min(tid + 256 * s, nseg - 1);
-      const int rec = idx >> 2, seg = idx & 3;
+      const int rec = idx / SEGP, seg = idx % SEGP;
       const int hr = rec / HC, hc = rec - hr * HC;
       const int ih = h0 + hr - 1, iw = hc - 1;
       const bool inside = ih >= 0 && ih < H && iw >= 0 && iw < W;
@@ -83,9 +96,18 @@ __global__ __launch_bounds__(256) void conv3x3_rows_kernel(
     for (int s = 0; s < SEGS; ++s) {
       const int idx = tid + 256 * s;
       if (idx < nseg)
-        *reinterpret_cast<u32x4 *>(&halo[buf][(idx >> 2) * REC + (idx & 3) * (16 / sizeof(T))]) =
+        *reinterpret_cast<u32x4 *>(&halo[buf][(idx / SEGP) * REC + (idx % SEGP) * (16 / sizeof(T))]) =
             stage[s];
     }
+  };
+  // Filters past F read filter F-1: they only feed columns that are not stored.
+  const T *wrow = w + (size_t)min(f, F - 1) * 9 * C + q * KPL;
+  Frag16 b[NCH][9];
+  auto fetch_b = [&](Frag16 (&dst)[NCH][9], int c0) {
+#pragma unroll
+    for (int ch = 0; ch < NCH; ++ch)
+#pragma unroll
+      for (int t = 0; t < 9; ++t) dst[ch][t] = load16(wrow + t * C + c0 + ch * KC);
   };
 
   typename MM::acc_t acc[PBW];
@@ -93,31 +115,48 @@ __global__ __launch_bounds__(256) void conv3x3_rows_kernel(
   for (int i = 0; i < PBW; ++i) acc[i] = typename MM::acc_t{0, 0, 0, 0};
 
   fetch(0);
+  fetch_b(b, 0);
   commit(0);
   __syncthreads();
-  const int nchunks = C / KC;
-  // Filters past F read filter F-1: they only feed columns that are not stored.
-  const T *wrow = w + (size_t)min(f, F - 1) * 9 * C + q * KPL;
-  for (int c = 0; c < nchunks; ++c) {
-    Frag16 b[9];
+  const int nstages = C / (KC * NCH);  // 1 when NBUF == 1 (checked by the launcher)
+  for (int st = 0; st < nstages; ++st) {
+    const bool more = NBUF == 2 && st + 1 < nstages;
+    Frag16 bn[NCH][9];
+    if (more) {
+      fetch((st + 1) * NCH * KC);
+      fetch_b(bn, (st + 1) * NCH * KC);
+    }
+    const T *hb = halo[NBUF == 2 ? (st & 1) : 0];
+    // Two-deep pipeline over (chunk, tap): the A fragments of the next tap
+    // are read from LDS while this tap's MFMAs run.  The scheduling barrier
+    // keeps the compiler from hoisting every tap's reads (which would need
+    // NCH*9*PBW fragments live at once).
+    auto load_a = [&](Frag16 (&dst)[PBW], int j) {
+      const int ch = j / 9, t = j % 9;
+      const int toff = ((t / 3) * HC + (t % 3)) * REC + ch * KC;
 #pragma unroll
-    for (int t = 0; t < 9; ++t) b[t] = load16(wrow + t * C + c * KC);
-    if (c + 1 < nchunks) fetch((c + 1) * KC);
-    const T *hb = halo[c & 1];
+      for (int i = 0; i < PBW; ++i) dst[i] = load16(hb + abase[i] + toff);
+    };
+    Frag16 a[2][PBW];
+    load_a(a[0], 0);
 #pragma unroll
-    for (int t = 0; t < 9; ++t) {
-      const int toff = ((t / 3) * HC + (t % 3)) * REC;
-      Frag16 a[PBW];
-#pragma unroll
-      for (int i = 0; i < PBW; ++i) a[i] = load16(hb + abase[i] + toff);
+    for (int j = 0; j < NCH * 9; ++j) {
+      if (j + 1 < NCH * 9) load_a(a[(j + 1) & 1], j + 1);
       // independent accumulators between the dependent steps of one fragment
 #pragma unroll
-      for (int st = 0; st < MM::kSteps; ++st)
+      for (int s = 0; s < MM::kSteps; ++s)
 #pragma unroll
-        for (int i = 0; i < PBW; ++i) MM::step(acc[i], a[i], b[t], st);
+        for (int i = 0; i < PBW; ++i) MM::step(acc[i], a[j & 1][i], b[j / 9][j % 9], s);
+      __builtin_amdgcn_sched_barrier(0);
     }
-    if (c + 1 < nchunks) commit((c + 1) & 1);
-    __syncthreads();
+    if (more) {
+      commit((st + 1) & 1);
+#pragma unroll
+      for (int ch = 0; ch < NCH; ++ch)
+#pragma unroll
+        for (int t = 0; t < 9; ++t) b[ch][t] = bn[ch][t];
+    }
+    if (NBUF == 2) __syncthreads();
   }
 
   if (!fok) return;
@@ -141,30 +180,43 @@ __global__ __launch_bounds__(256) void conv3x3_rows_kernel(
   }
 }
 
-template <class MM, typename T, int TR, int WF>
+template <class MM, typename T, int TR, int WF, int WMAX, int NCH, int NBUF>
 hipError_t launch_rows(const ConvArgs &a, hipStream_t s) {
+  if (a.W > WMAX || a.C % (MM::kPerFrag * NCH) != 0 ||
+      (NBUF == 1 && a.C != MM::kPerFrag * NCH))
+    return hipErrorInvalidValue;
   const int tiles_h = (a.H + TR - 1) / TR;
   dim3 grid(a.N * tiles_h, (a.F + 16 * WF - 1) / (16 * WF));
-  hipLaunchKernelGGL((conv3x3_rows_kernel<MM, T, TR, WF>), grid, dim3(256), 0, s,
+  hipLaunchKernelGGL((conv3x3_rows_kernel<MM, T, TR, WF, WMAX, NCH, NBUF>), grid, dim3(256), 0, s,
                      static_cast<const T *>(a.x), static_cast<const T *>(a.w), a.bias,
                      static_cast<T *>(a.out), a.H, a.W, a.C, a.F, a.act);
   return hipGetLastError();
 }
 
-// Two launch shapes: with many row tiles, each workgroup covers 2 rows x 64
+// Launch shapes: with many row tiles, each workgroup covers 2 rows x 64
 // filters (waves split the filters); with few (batch 1), 1 row x 16 filters
-// (waves split the row) so the grid still spreads over the CUs.
+// (waves split the row) so the grid still spreads over the CUs.  Rows of up
+// to 56 pixels use tiles sized for 56 (7 pixel blocks for 2 rows, none
+// wasted).  One 64-byte chunk per stage when C spans several; all of C in
+// one stage when it is two chunks.
+template <class MM, typename T, int WMAX>
+hipError_t launch_w(const ConvArgs &a, hipStream_t s) {
+  const bool big = a.N * ((a.H + 1) / 2) >= 512;
+  if (a.C == 2 * MM::kPerFrag)
+    return big ? launch_rows<MM, T, 2, 4, WMAX, 2, 1>(a, s) : launch_rows<MM, T, 1, 1, WMAX, 2, 1>(a, s);
+  return big ? launch_rows<MM, T, 2, 4, WMAX, 1, 2>(a, s) : launch_rows<MM, T, 1, 1, WMAX, 1, 2>(a, s);
+}
+
 template <class MM, typename T>
 hipError_t launch_conv3x3(const ConvArgs &a, hipStream_t s) {
-  if (a.N * ((a.H + 1) / 2) >= 512) return launch_rows<MM, T, 2, 4>(a, s);
-  return launch_rows<MM, T, 1, 1>(a, s);
+  return a.W <= 56 ? launch_w<MM, T, 56>(a, s) : launch_w<MM, T, 64>(a, s);
 }
 
 }  // namespace
 
 bool conv3x3_rows_supported(const ConvArgs &a, int elem_bytes) {
   const int kc = 64 / elem_bytes;
-  return a.KH == 3 && a.KW == 3 && a.pad == 1 && a.W <= kWMax && a.C % kc == 0 && a.F % 16 == 0;
+  return a.KH == 3 && a.KW == 3 && a.pad == 1 && a.W <= 64 && a.C % kc == 0 && a.F % 16 == 0;
 }
 
 hipError_t launch_conv3x3_f32(const ConvArgs &a, hipStream_t s) {
