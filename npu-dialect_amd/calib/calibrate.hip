@@ -1,0 +1,220 @@
+// calibrate.hip -- measures the machine constants the MI355X launch model
+// needs and that no data sheet gives: the cost of one launch in a stream of
+// back-to-back launches, the latency of a dependent global load (idle and
+// with every CU loading), the bandwidth of a plain HBM copy, the rate at
+// which one CU reads L2-resident data, and the shader clock.
+//
+// Every kernel here is bounded: the pointer chases follow a single cycle over
+// an index array whose entries are all in range, with a fixed hop count; the
+// copies and reads use grid-stride loops over their own buffers.
+//
+// Output: one JSON line on stdout.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cstdint>
+#include <cstdio>
+#include <numeric>
+#include <random>
+#include <vector>
+
+#define CK(x)                                                                          \
+  do {                                                                                 \
+    hipError_t e_ = (x);                                                               \
+    if (e_ != hipSuccess) {                                                            \
+      fprintf(stderr, "HIP error %s at %s:%d\n", hipGetErrorString(e_), __FILE__, __LINE__); \
+      return 1;                                                                        \
+    }                                                                                  \
+  } while (0)
+
+namespace {
+
+constexpr int kStride = 64;  // int32 slots between chased entries (256 bytes)
+
+__global__ void empty_kernel(int *p) {
+  if (p && threadIdx.x == 1024) p[0] = 0;  // never taken: keeps the argument live
+}
+
+// Every lane follows the cycle `hops` times from its own entry (so the loads
+// are per-lane vector loads); entry i of the cycle lives at next[i * kStride].
+__global__ void chase_kernel(const int *__restrict__ next, int hops, int n, int *out) {
+  const unsigned g = blockIdx.x * blockDim.x + threadIdx.x;
+  int j = (int)((g * 2654435761u) % (unsigned)n);
+  for (int h = 0; h < hops; ++h) j = next[(size_t)j * kStride];
+  if (j == -1) out[g] = j;  // never true: keeps the chase live
+}
+
+// Grid-stride copy, four independent 16-byte loads per lane per step; n is a
+// multiple of 4 x the grid's lane count.
+__global__ void copy_kernel(const float4 *__restrict__ src, float4 *__restrict__ dst, size_t n) {
+  const size_t lanes = (size_t)gridDim.x * blockDim.x;
+  for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < n; i += 4 * lanes) {
+    float4 v[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) v[u] = src[i + u * lanes];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) dst[i + u * lanes] = v[u];
+  }
+}
+
+// Each workgroup reads the same L2-resident buffer `reps` times, eight
+// independent 16-byte loads in flight per lane.  n is a multiple of 8 x blockDim.
+__global__ void l2_read_kernel(const float4 *__restrict__ src, size_t n, int reps, float *out) {
+  float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  for (int r = 0; r < reps; ++r)
+    for (size_t i = threadIdx.x; i < n; i += 8 * blockDim.x) {
+      float4 v[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) v[u] = src[i + u * blockDim.x];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) acc[u] += v[u].x + v[u].y + v[u].z + v[u].w;
+    }
+  float t = 0.f;
+#pragma unroll
+  for (int u = 0; u < 8; ++u) t += acc[u];
+  if (t == 12345.f) out[blockIdx.x] = t;
+}
+
+// Shader clock over the 100 MHz constant clock.
+__global__ void clock_kernel(long long *out, int spins) {
+  if (threadIdx.x != 0) return;
+  const long long c0 = clock64(), w0 = wall_clock64();
+  volatile float x = 1.0f;
+  for (int i = 0; i < spins; ++i) x = x * 1.0000001f;
+  const long long c1 = clock64(), w1 = wall_clock64();
+  out[0] = c1 - c0;
+  out[1] = w1 - w0;
+}
+
+template <class F>
+int time_us(F launch, int reps, double *us) {
+  hipEvent_t a, b;
+  CK(hipEventCreate(&a));
+  CK(hipEventCreate(&b));
+  for (int i = 0; i < 3; ++i) launch();
+  CK(hipDeviceSynchronize());
+  CK(hipEventRecord(a, 0));
+  for (int i = 0; i < reps; ++i) launch();
+  CK(hipEventRecord(b, 0));
+  CK(hipEventSynchronize(b));
+  float ms = 0;
+  CK(hipEventElapsedTime(&ms, a, b));
+  *us = 1000.0 * ms / reps;
+  CK(hipGetLastError());
+  CK(hipEventDestroy(a));
+  CK(hipEventDestroy(b));
+  return 0;
+}
+
+// A single random cycle through n entries (Sattolo), laid out kStride apart.
+std::vector<int> make_cycle(int n, uint64_t seed) {
+  std::vector<int> perm(n);
+  std::iota(perm.begin(), perm.end(), 0);
+  std::mt19937_64 g(seed);
+  for (int i = n - 1; i > 0; --i) {
+    std::uniform_int_distribution<int> d(0, i - 1);
+    std::swap(perm[i], perm[d(g)]);
+  }
+  std::vector<int> next((size_t)n * kStride, 0);
+  for (int i = 0; i < n; ++i) next[(size_t)i * kStride] = perm[i];
+  return next;
+}
+
+}  // namespace
+
+int main() {
+  hipDeviceProp_t prop;
+  CK(hipGetDeviceProperties(&prop, 0));
+  const int cus = prop.multiProcessorCount;
+
+  // shader clock
+  long long *dclk;
+  CK(hipMalloc(&dclk, 2 * sizeof(long long)));
+  hipLaunchKernelGGL(clock_kernel, dim3(1), dim3(64), 0, 0, dclk, 2000000);
+  CK(hipDeviceSynchronize());
+  long long clk[2];
+  CK(hipMemcpy(clk, dclk, sizeof(clk), hipMemcpyDeviceToHost));
+  const double ghz = (double)clk[0] / (double)clk[1] * 0.1;
+
+  // launch cost in a back-to-back stream
+  double t_launch;
+  if (time_us([&] { hipLaunchKernelGGL(empty_kernel, dim3(1), dim3(64), 0, 0, nullptr); }, 2000,
+              &t_launch))
+    return 1;
+  double t_launch_full;  // a grid that covers every CU
+  if (time_us([&] { hipLaunchKernelGGL(empty_kernel, dim3(4 * cus), dim3(256), 0, 0, nullptr); },
+              2000, &t_launch_full))
+    return 1;
+
+  // dependent-load latency: HBM (1 GiB span), L2 (1 MiB span)
+  int *dout;
+  CK(hipMalloc(&dout, 4 * cus * 64 * sizeof(int)));
+  const int n_hbm = (1 << 30) / (kStride * 4), n_l2 = (1 << 20) / (kStride * 4);
+  const int hops = 4000;
+  double lat_hbm, lat_l2, lat_loaded;
+  {
+    std::vector<int> next = make_cycle(n_hbm, 1);
+    int *d;
+    CK(hipMalloc(&d, next.size() * sizeof(int)));
+    CK(hipMemcpy(d, next.data(), next.size() * sizeof(int), hipMemcpyHostToDevice));
+    double us;
+    if (time_us([&] { hipLaunchKernelGGL(chase_kernel, dim3(1), dim3(64), 0, 0, d, hops, n_hbm, dout); },
+                3, &us))
+      return 1;
+    lat_hbm = us / hops;
+    // every CU chasing at once, 4 waves each
+    if (time_us([&] { hipLaunchKernelGGL(chase_kernel, dim3(4 * cus), dim3(64), 0, 0, d, hops, n_hbm, dout); },
+                3, &us))
+      return 1;
+    lat_loaded = us / hops;
+    CK(hipFree(d));
+  }
+  {
+    std::vector<int> next = make_cycle(n_l2, 2);
+    int *d;
+    CK(hipMalloc(&d, next.size() * sizeof(int)));
+    CK(hipMemcpy(d, next.data(), next.size() * sizeof(int), hipMemcpyHostToDevice));
+    double us;
+    if (time_us([&] { hipLaunchKernelGGL(chase_kernel, dim3(1), dim3(64), 0, 0, d, hops, n_l2, dout); },
+                3, &us))
+      return 1;
+    lat_l2 = us / hops;
+    CK(hipFree(d));
+  }
+
+  // HBM copy bandwidth, 1 GiB each way
+  const size_t bytes = (size_t)1 << 30;
+  float4 *src, *dst;
+  CK(hipMalloc(&src, bytes));
+  CK(hipMalloc(&dst, bytes));
+  CK(hipMemset(src, 0, bytes));
+  double t_copy;
+  if (time_us([&] { hipLaunchKernelGGL(copy_kernel, dim3(8 * cus), dim3(256), 0, 0, src, dst, bytes / 16); },
+              10, &t_copy))
+    return 1;
+  const double copy_gbs = 2.0 * bytes / (t_copy * 1e3);
+
+  // per-CU read rate from L2: one 1024-lane workgroup per CU, 256 KiB buffer
+  // read 64 times (l2n is a multiple of 8 x 1024)
+  const size_t l2n = (256 << 10) / 16;
+  const int reps = 64;
+  float *dsink;
+  CK(hipMalloc(&dsink, cus * 4 * sizeof(float)));
+  double t_l2;
+  if (time_us([&] { hipLaunchKernelGGL(l2_read_kernel, dim3(cus), dim3(1024), 0, 0, src, l2n, reps, dsink); },
+              5, &t_l2))
+    return 1;
+  const double l2_bytes_per_clk_cu = (double)l2n * 16 * reps / (t_l2 * 1e3 * ghz);
+
+  printf("{\"device\": \"%s\", \"cus\": %d, \"shader_clock_ghz\": %.3f, \"launch_us\": %.3f, "
+         "\"launch_full_grid_us\": %.3f, \"hbm_latency_us\": %.3f, \"hbm_latency_loaded_us\": %.3f, "
+         "\"l2_latency_us\": %.3f, \"hbm_copy_gbs\": %.1f, \"l2_read_bytes_per_clk_cu\": %.2f}\n",
+         prop.gcnArchName, cus, ghz, t_launch, t_launch_full, lat_hbm, lat_loaded, lat_l2, copy_gbs,
+         l2_bytes_per_clk_cu);
+  CK(hipFree(src));
+  CK(hipFree(dst));
+  CK(hipFree(dsink));
+  CK(hipFree(dout));
+  CK(hipFree(dclk));
+  return 0;
+}

@@ -18,8 +18,11 @@
 // Summation order is fixed (chunk by chunk, tap by tap within a chunk)
 // whatever NCH is, so every variant returns the same bits.
 //
-// LDS record: one pixel's NCH*64 bytes of the stage plus 16 bytes of padding,
-// so the 16 lanes that read 16 consecutive pixels hit distinct bank groups.
+// LDS record: one pixel's NCH*64 bytes of the stage plus 32 bytes of padding.
+// On gfx950 a ds_read_b128 in which 16 lanes read 16 consecutive records runs
+// conflict-free when the record stride is 32 mod 64 bytes (measured: 22
+// cycles per wave instruction with four waves reading, against 32 for a
+// stride of 16 mod 64 and 64 for an unpadded 128-byte stride).
 //
 // Workgroups are dispatched round-robin over the 8 XCDs, each with its own
 // L2.  Consecutive block indices are remapped so that each XCD gets a
@@ -27,12 +30,11 @@
 // on one XCD the second read of those rows hits L2 instead of HBM.
 #include "kernels.hpp"
 #include "npu_device.hpp"
+#include "persistent.hpp"
 
 namespace npu {
 
 namespace {
-
-constexpr int kXcds = 8;
 
 template <class MM, typename T, int TR, int WF, int WMAX, int NCH, int NBUF>
 __global__ __launch_bounds__(256) void conv3x3_rows_kernel(
@@ -42,7 +44,7 @@ __global__ __launch_bounds__(256) void conv3x3_rows_kernel(
   constexpr int KPL = MM::kPerLane;           // elements of one lane's 16-byte run
   constexpr int KC = MM::kPerFrag;            // channels per chunk (64 bytes)
   constexpr int SEGP = NCH * 4;               // 16-byte segments per pixel and stage
-  constexpr int REC = (NCH * 64 + 16) / sizeof(T);  // LDS record stride in elements
+  constexpr int REC = (NCH * 64 + 32) / sizeof(T);  // LDS record stride in elements
   constexpr int HR = TR + 2;
   constexpr int PBMAX = (TR * WMAX + 15) / 16;
   constexpr int PBW = (PBMAX + WP - 1) / WP;  // pixel blocks per wave
@@ -161,6 +163,7 @@ __global__ __launch_bounds__(256) void conv3x3_rows_kernel(
 
   if (!fok) return;
   const float bv = bias ? bias[f] : 0.0f;
+  const ActBounds ab = act_bounds(act);
 #pragma unroll
   for (int i = 0; i < PBW; ++i) {
 #pragma unroll
@@ -169,7 +172,7 @@ __global__ __launch_bounds__(256) void conv3x3_rows_kernel(
       if (p >= tile_px) continue;
       const int pr = p / W, pc = p - pr * W;
       if (h0 + pr >= H) continue;
-      const float v = act_apply(acc[i][e] + bv, act);
+      const float v = act_clamp(acc[i][e] + bv, ab);
       const size_t o = ((size_t)(n * H + h0 + pr) * W + pc) * F + f;
       if constexpr (sizeof(T) == 4) {
         out[o] = v;
@@ -178,6 +181,169 @@ __global__ __launch_bounds__(256) void conv3x3_rows_kernel(
       }
     }
   }
+}
+
+// Persistent variant for reductions that fit one stage (C = NCH chunks):
+// each workgroup loads its 64 filters' fragments into registers once, then
+// walks a strided set of 2-row tiles, fetching the next tile's halo into
+// registers while the current tile is multiplied, so loads, MFMAs and stores
+// of different tiles overlap instead of every workgroup of a round waiting
+// on its loads at the same time.  The tiles of one XCD are a contiguous
+// range, so the halo rows two neighbouring tiles share are read from HBM once.
+template <class MM, typename T, int WMAX, int NCH, int WFIX>
+__global__ __launch_bounds__(256, NCH <= 2 ? 2 : 1) void conv3x3_stream_kernel(
+    const T *__restrict__ x, const T *__restrict__ w, const float *__restrict__ bias,
+    T *__restrict__ out, int H, int w_rt, int F, int act, int ntiles) {
+  // A compile-time width (WFIX > 0) and channel count turn the index
+  // arithmetic below (divisions by the row width, address products) into
+  // shifts and constant multiplies; it is most of the kernel's VALU work.
+  const int W = WFIX > 0 ? WFIX : w_rt;
+  constexpr int C = NCH * MM::kPerFrag;
+  constexpr int TR = 2;
+  constexpr int KPL = MM::kPerLane;
+  constexpr int KC = MM::kPerFrag;
+  constexpr int SEGP = NCH * 4;
+  constexpr int REC = (NCH * 64 + 32) / sizeof(T);
+  constexpr int HR = TR + 2;
+  constexpr int PBW = (TR * WMAX + 15) / 16;
+  constexpr int SEGS = (HR * (WMAX + 2) * SEGP + 255) / 256;
+  static_assert(KC * sizeof(T) == 64, "a chunk is 64 bytes per pixel");
+  // Output tile staged in LDS (64 filters per pixel plus 32 bytes of
+  // padding) so that it leaves in whole 16-byte runs per lane.
+  constexpr int OREC = (64 * sizeof(T) + 32) / sizeof(T);
+  constexpr int OSEGP = 64 * sizeof(T) / 16;  // 16-byte runs per pixel
+  __shared__ __attribute__((aligned(16))) T halo[HR * (WMAX + 2) * REC];
+  __shared__ __attribute__((aligned(16))) T ostage[TR * WMAX * OREC];
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int r = lane & 15, q = lane >> 4;
+  const int tiles_h = (H + TR - 1) / TR;
+  const TileWalk walk = tile_walk(ntiles);
+  const int t_first = walk.first, t_end = walk.end, step = walk.step;
+  const int f = (blockIdx.y * 4 + wave) * 16 + r;  // F is a multiple of 64
+  const int HC = W + 2, nseg = HR * HC * SEGP;
+  const int tile_px = TR * W;
+
+  int abase[PBW];
+#pragma unroll
+  for (int i = 0; i < PBW; ++i) {
+    const int p = min(i * 16 + r, tile_px - 1);
+    const int pr = p / W, pc = p - pr * W;
+    abase[i] = (pr * HC + pc) * REC + q * KPL;
+  }
+
+  u32x4 stage[SEGS];
+  auto fetch = [&](int t) {
+    const int n = t / tiles_h, h0 = (t - n * tiles_h) * TR;
+    const int lt = opaque(tid);
+#pragma unroll
+    for (int s = 0; s < SEGS; ++s) {
+      const int idx = min(lt + 256 * s, nseg - 1);
+      const int rec = idx / SEGP, seg = idx % SEGP;
+      const int hr = rec / HC, hc = rec - hr * HC;
+      const int ih = h0 + hr - 1, iw = hc - 1;
+      const bool inside = ih >= 0 && ih < H && iw >= 0 && iw < W;
+      const int ihc = min(max(ih, 0), H - 1), iwc = min(max(iw, 0), W - 1);
+      stage[s] = masked(*reinterpret_cast<const u32x4 *>(
+                            x + ((size_t)(n * H + ihc) * W + iwc) * C + seg * (16 / sizeof(T))),
+                        inside);
+    }
+  };
+  auto commit = [&]() {
+#pragma unroll
+    for (int s = 0; s < SEGS; ++s) {
+      const int idx = tid + 256 * s;
+      if (idx < nseg)
+        *reinterpret_cast<u32x4 *>(&halo[(idx / SEGP) * REC + (idx % SEGP) * (16 / sizeof(T))]) =
+            stage[s];
+    }
+  };
+
+  if (t_first >= t_end) return;  // uniform over the workgroup
+  fetch(t_first);
+  const T *wrow = w + (size_t)f * 9 * C + q * KPL;
+  Frag16 b[NCH][9];
+#pragma unroll
+  for (int ch = 0; ch < NCH; ++ch)
+#pragma unroll
+    for (int t = 0; t < 9; ++t) b[ch][t] = load16(wrow + t * C + ch * KC);
+  const float bv = bias ? bias[f] : 0.0f;
+  const ActBounds ab = act_bounds(act);
+  commit();
+  __syncthreads();
+
+  // One halo buffer: the next tile's halo waits in registers until every
+  // wave has finished reading the current one.
+  for (int t = t_first; t < t_end; t += step) {
+    const bool more = t + step < t_end;
+    if (more) fetch(t + step);
+    const T *hb = halo;
+    typename MM::acc_t acc[PBW];
+#pragma unroll
+    for (int i = 0; i < PBW; ++i) acc[i] = typename MM::acc_t{0, 0, 0, 0};
+    // Two-deep pipeline over taps: the next tap's A fragments are read from
+    // LDS while this tap's MFMAs run; the scheduling barrier keeps each
+    // tap's reads and MFMAs in their own region.
+    auto load_a = [&](Frag16 (&dst)[PBW], int j) {
+      const int toff = ((j % 9 / 3) * HC + (j % 3)) * REC + (j / 9) * KC;
+#pragma unroll
+      for (int i = 0; i < PBW; ++i) dst[i] = load16(hb + abase[i] + toff);
+    };
+    Frag16 a[2][PBW];
+    load_a(a[0], 0);
+#pragma unroll
+    for (int j = 0; j < NCH * 9; ++j) {
+      if (j + 1 < NCH * 9) load_a(a[(j + 1) & 1], j + 1);
+#pragma unroll
+      for (int s = 0; s < MM::kSteps; ++s)
+#pragma unroll
+        for (int i = 0; i < PBW; ++i) MM::step(acc[i], a[j & 1][i], b[j / 9][j % 9], s);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    {
+      const int lq = opaque(q);
+#pragma unroll
+      for (int i = 0; i < PBW; ++i)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int p = i * 16 + 4 * lq + e;
+          if (p >= tile_px) continue;
+          const float v = act_clamp(acc[i][e] + bv, ab);
+          if constexpr (sizeof(T) == 4) {
+            ostage[p * OREC + wave * 16 + r] = v;
+          } else {
+            ostage[p * OREC + wave * 16 + r] = f32_to_bf16(v);
+          }
+        }
+    }
+    __syncthreads();
+    {
+      const int n = t / tiles_h, h0 = (t - n * tiles_h) * TR;
+      const int rows = min(TR, H - h0);
+      for (int idx = opaque(tid); idx < rows * W * OSEGP; idx += 256) {
+        const int p = idx / OSEGP, sg = idx - p * OSEGP;
+        const int pr = p / W, pc = p - pr * W;
+        *reinterpret_cast<u32x4 *>(out + ((size_t)(n * H + h0 + pr) * W + pc) * F +
+                                   blockIdx.y * 64 + sg * (16 / sizeof(T))) =
+            *reinterpret_cast<const u32x4 *>(ostage + p * OREC + sg * (16 / sizeof(T)));
+      }
+    }
+    if (more) commit();
+    __syncthreads();
+  }
+}
+
+template <class MM, typename T, int WMAX, int NCH, int WFIX>
+hipError_t launch_stream(const ConvArgs &a, int wgs, hipStream_t s) {
+  if (a.W > WMAX || (WFIX > 0 && a.W != WFIX) || a.C != MM::kPerFrag * NCH || a.F % 64 != 0 ||
+      wgs % kXcds != 0)
+    return hipErrorInvalidValue;
+  const int ntiles = a.N * ((a.H + 1) / 2);
+  dim3 grid(wgs, (a.F + 63) / 64);
+  hipLaunchKernelGGL((conv3x3_stream_kernel<MM, T, WMAX, NCH, WFIX>), grid, dim3(256), 0, s,
+                     static_cast<const T *>(a.x), static_cast<const T *>(a.w), a.bias,
+                     static_cast<T *>(a.out), a.H, a.W, a.F, a.act, ntiles);
+  return hipGetLastError();
 }
 
 template <class MM, typename T, int TR, int WF, int WMAX, int NCH, int NBUF>
@@ -193,15 +359,27 @@ hipError_t launch_rows(const ConvArgs &a, hipStream_t s) {
   return hipGetLastError();
 }
 
-// Launch shapes: with many row tiles, each workgroup covers 2 rows x 64
-// filters (waves split the filters); with few (batch 1), 1 row x 16 filters
-// (waves split the row) so the grid still spreads over the CUs.  Rows of up
-// to 56 pixels use tiles sized for 56 (7 pixel blocks for 2 rows, none
-// wasted).  One 64-byte chunk per stage when C spans several; all of C in
-// one stage when it is two chunks.
-template <class MM, typename T, int WMAX>
+template <class MM, typename T, int WMAX, int NCH, int WFIX>
+hipError_t launch_persistent(const ConvArgs &a, hipStream_t s) {
+  const int g = persistent_grid(conv3x3_stream_kernel<MM, T, WMAX, NCH, WFIX>);
+  if (g == 0) return hipErrorInvalidDeviceFunction;
+  return launch_stream<MM, T, WMAX, NCH, WFIX>(a, g, s);
+}
+
+// Launch shapes.  With many row tiles (batched images) and C of two or four
+// chunks, the persistent kernel (filter fragments held in registers); else
+// one workgroup per tile: 2 rows x 64 filters (waves split the filters) when
+// tiles are many, 1 row x 16 filters (waves split the row) when few (batch
+// 1), so the grid still spreads over the CUs.  Rows of up to 56 pixels use
+// tiles sized for 56 (7 pixel blocks for 2 rows, none wasted); a row width
+// of exactly 56 is also compiled in, so index arithmetic folds.
+template <class MM, typename T, int WMAX, int WFIX>
 hipError_t launch_w(const ConvArgs &a, hipStream_t s) {
   const bool big = a.N * ((a.H + 1) / 2) >= 512;
+  if (big && a.F % 64 == 0) {
+    if (a.C == 2 * MM::kPerFrag) return launch_persistent<MM, T, WMAX, 2, WFIX>(a, s);
+    if (a.C == 4 * MM::kPerFrag) return launch_persistent<MM, T, WMAX, 4, WFIX>(a, s);
+  }
   if (a.C == 2 * MM::kPerFrag)
     return big ? launch_rows<MM, T, 2, 4, WMAX, 2, 1>(a, s) : launch_rows<MM, T, 1, 1, WMAX, 2, 1>(a, s);
   return big ? launch_rows<MM, T, 2, 4, WMAX, 1, 2>(a, s) : launch_rows<MM, T, 1, 1, WMAX, 1, 2>(a, s);
@@ -209,7 +387,8 @@ hipError_t launch_w(const ConvArgs &a, hipStream_t s) {
 
 template <class MM, typename T>
 hipError_t launch_conv3x3(const ConvArgs &a, hipStream_t s) {
-  return a.W <= 56 ? launch_w<MM, T, 56>(a, s) : launch_w<MM, T, 64>(a, s);
+  if (a.W == 56) return launch_w<MM, T, 56, 56>(a, s);
+  return a.W < 56 ? launch_w<MM, T, 56, 0>(a, s) : launch_w<MM, T, 64, 0>(a, s);
 }
 
 }  // namespace

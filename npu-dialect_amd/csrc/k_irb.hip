@@ -5,8 +5,10 @@
 // (NHWC restatement of test/mobilenet_block.mlir:8-94, with a true depthwise
 // stage where the reference models it as a full conv, :45-53).
 //
-// Vertical fusion with the intermediates in LDS: a workgroup owns an 8x8
-// output tile, stages the 10x10 x halo, recomputes the expand conv on the
+// Vertical fusion with the intermediates in LDS: a workgroup computes 8x8
+// output tiles one at a time (persistent: filters loaded once, the next
+// tile's x halo fetched while the current one is computed), stages the 10x10
+// x halo, recomputes the expand conv on the
 // halo (the tensor.pad before the depthwise conv becomes zeros written for
 // out-of-image halo pixels), and keeps the E-channel tile in LDS.  The
 // depthwise result is computed directly in the A-operand layout of the
@@ -15,6 +17,7 @@
 // E-channel intermediates (6x the block's own bytes) never reach it.
 #include "kernels.hpp"
 #include "npu_device.hpp"
+#include "persistent.hpp"
 
 namespace npu {
 
@@ -28,47 +31,71 @@ constexpr int HPB = (HP + 15) / 16;  // 7 blocks of 16 rows
 __device__ __forceinline__ float relu6(float v) { return act_apply(v, 2); }
 
 template <int C, int E>
-__global__ __launch_bounds__(256) void irb_kernel(const float *__restrict__ x,
+__global__ __launch_bounds__(256, E >= 192 ? 1 : 2) void irb_kernel(const float *__restrict__ x,
                                                   const float *__restrict__ we,
                                                   const float *__restrict__ wdw,
                                                   const float *__restrict__ wp,
                                                   float *__restrict__ out, int H, int W,
-                                                  int tiles_w) {
+                                                  int tiles_w, int tiles_per_image, int ntiles) {
   static_assert(C % 4 == 0 && E % 16 == 0, "C must be a multiple of 4, E of 16");
   constexpr int KC1 = (C + 15) / 16;  // expand reduction chunks (C padded to 16)
-  constexpr int XS = KC1 * 16 + 4;    // LDS row strides in floats (+4 against bank conflicts)
-  constexpr int ES = E + 4;
+  // LDS row strides in floats.  A stride of 32 mod 64 bytes keeps the 16-lane
+  // 16-byte row reads conflict-free; the E-channel rows (read nine times per
+  // pixel by the depthwise stage) always get it, the x rows only if two
+  // workgroups still fit in one CU's LDS.
+  constexpr int ES = E + 8;
+  constexpr int XS8 = KC1 * 16 + 8;
+  constexpr int XS = (HP * XS8 + HP * ES + 9 * E) * 4 <= 81920 ? XS8 : KC1 * 16 + 4;
   constexpr int FB1 = E / 16;         // expand filter blocks
   constexpr int FBW = (FB1 + 3) / 4;  // ... per wave (wave w owns w, w+4, ...)
   constexpr int KC2 = E / 16;         // project reduction chunks
   constexpr int FB2 = (C + 15) / 16;  // project filter blocks
   constexpr int XV = KC1 * 4;         // float4 columns per staged x row
-  constexpr int XSEG = HPB * 16 * XV;
+  constexpr int XSEG = HP * XV;
   constexpr int XSEGS = (XSEG + 255) / 256;
-  __shared__ __attribute__((aligned(16))) float xs[HPB * 16 * XS];
+  __shared__ __attribute__((aligned(16))) float xs[HP * XS];
   __shared__ __attribute__((aligned(16))) float es[HP * ES];
   __shared__ __attribute__((aligned(16))) float wds[9 * E];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int r = lane & 15, q = lane >> 4;
-  const int n = blockIdx.y;
-  const int ty0 = (blockIdx.x / tiles_w) * TH, tx0 = (blockIdx.x % tiles_w) * TW;
+  const TileWalk walk = tile_walk(ntiles);
+  if (walk.first >= walk.end) return;  // uniform over the workgroup
 
-  // ---- every global load up front: the x halo (zero-padded to KC1*16
-  //      channels and 112 rows; clamped addresses, zero fill by select), this
-  //      wave's expand filter blocks and the depthwise taps.
+  // x halo of tile t into registers (zero-padded to KC1*16 channels; clamped
+  // addresses, zero fill by select).
   f32x4 st[XSEGS];
+  auto fetch = [&](int t) {
+    const int n = t / tiles_per_image, tt = t - n * tiles_per_image;
+    const int ty0 = (tt / tiles_w) * TH, tx0 = (tt % tiles_w) * TW;
+    const int lt = opaque(tid);
 #pragma unroll
-  for (int s = 0; s < XSEGS; ++s) {
-    const int idx = min(tid + 256 * s, XSEG - 1);
-    const int hp = idx / XV, c = (idx - hp * XV) * 4;
-    const int iy = ty0 + hp / HW - 1, ix = tx0 + hp % HW - 1;
-    const bool inside = hp < HP && c < C && iy >= 0 && iy < H && ix >= 0 && ix < W;
-    const int iyc = min(max(iy, 0), H - 1), ixc = min(max(ix, 0), W - 1);
-    const f32x4 v = *reinterpret_cast<const f32x4 *>(
-        x + ((size_t)(n * H + iyc) * W + ixc) * C + min(c, C - 4));
-    st[s] = inside ? v : f32x4{0.f, 0.f, 0.f, 0.f};
-  }
+    for (int s = 0; s < XSEGS; ++s) {
+      const int idx = min(lt + 256 * s, XSEG - 1);
+      const int hp = idx / XV, c = (idx - hp * XV) * 4;
+      const int iy = ty0 + hp / HW - 1, ix = tx0 + hp % HW - 1;
+      const bool inside = c < C && iy >= 0 && iy < H && ix >= 0 && ix < W;
+      const int iyc = min(max(iy, 0), H - 1), ixc = min(max(ix, 0), W - 1);
+      const f32x4 v = *reinterpret_cast<const f32x4 *>(
+          x + ((size_t)(n * H + iyc) * W + ixc) * C + min(c, C - 4));
+      st[s] = inside ? v : f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+  };
+  auto commit = [&]() {
+    const int lt = opaque(tid);
+#pragma unroll
+    for (int s = 0; s < XSEGS; ++s) {
+      const int idx = lt + 256 * s;
+      if (idx < XSEG) {
+        const int hp = idx / XV, c = (idx - hp * XV) * 4;
+        *reinterpret_cast<f32x4 *>(xs + hp * XS + c) = st[s];
+      }
+    }
+  };
+
+  // ---- once per workgroup: the first halo, this wave's expand filter
+  //      blocks, every project filter fragment, the depthwise taps (LDS).
+  fetch(walk.first);
   Frag16 be[FBW][KC1];
 #pragma unroll
   for (int j = 0; j < FBW; ++j)
@@ -80,52 +107,6 @@ __global__ __launch_bounds__(256) void irb_kernel(const float *__restrict__ x,
       b.u = masked(b.u, k < C);
       be[j][kc] = b;
     }
-  for (int i = tid; i < 9 * E / 4; i += 256)
-    reinterpret_cast<f32x4 *>(wds)[i] = reinterpret_cast<const f32x4 *>(wdw)[i];
-#pragma unroll
-  for (int s = 0; s < XSEGS; ++s) {
-    const int idx = tid + 256 * s;
-    if (idx < XSEG) {
-      const int hp = idx / XV, c = (idx - hp * XV) * 4;
-      *reinterpret_cast<f32x4 *>(xs + hp * XS + c) = st[s];
-    }
-  }
-  __syncthreads();
-
-  // ---- expand on the halo: wave w computes its filter blocks for all 7
-  //      pixel blocks; the four MFMA steps of a fragment are interleaved
-  //      across the pixel blocks.
-#pragma unroll
-  for (int j = 0; j < FBW; ++j) {
-    const int fb = wave + 4 * j;
-    if (fb >= FB1) break;
-    const int f = fb * 16 + r;
-    f32x4 acc[HPB];
-#pragma unroll
-    for (int pb = 0; pb < HPB; ++pb) acc[pb] = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int kc = 0; kc < KC1; ++kc) {
-      Frag16 a[HPB];
-#pragma unroll
-      for (int pb = 0; pb < HPB; ++pb) a[pb] = load16(xs + (pb * 16 + r) * XS + kc * 16 + 4 * q);
-#pragma unroll
-      for (int st2 = 0; st2 < 4; ++st2)
-#pragma unroll
-        for (int pb = 0; pb < HPB; ++pb) MfmaF32::step(acc[pb], a[pb], be[j][kc], st2);
-    }
-#pragma unroll
-    for (int pb = 0; pb < HPB; ++pb)
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const int hp = pb * 16 + 4 * q + e;
-        if (hp < HP) {
-          const int iy = ty0 + hp / HW - 1, ix = tx0 + hp % HW - 1;
-          const bool inside = iy >= 0 && iy < H && ix >= 0 && ix < W;
-          es[hp * ES + f] = inside ? relu6(acc[pb][e]) : 0.0f;
-        }
-      }
-  }
-  // the project filters are fetched while the other waves finish expanding
   Frag16 bp[KC2][FB2];
 #pragma unroll
   for (int kc = 0; kc < KC2; ++kc)
@@ -136,52 +117,109 @@ __global__ __launch_bounds__(256) void irb_kernel(const float *__restrict__ x,
       b.u = masked(b.u, c < C);
       bp[kc][fb] = b;
     }
+  for (int i = tid; i < 9 * E / 4; i += 256)
+    reinterpret_cast<f32x4 *>(wds)[i] = reinterpret_cast<const f32x4 *>(wdw)[i];
+  commit();
   __syncthreads();
 
-  // ---- depthwise (in registers, A-operand layout) + project + residual.
-  // Wave w owns output pixels 16w .. 16w+15.
-  const int p = wave * 16 + r;
-  const int hbase = (p / TW) * HW + (p % TW);
-  f32x4 acc2[FB2];
+  for (int t = walk.first; t < walk.end; t += walk.step) {
+    const bool more = t + walk.step < walk.end;
+    if (more) fetch(t + walk.step);
+    const int n = t / tiles_per_image, tt = t - n * tiles_per_image;
+    const int ty0 = (tt / tiles_w) * TH, tx0 = (tt % tiles_w) * TW;
+
+    // ---- expand on the halo: wave w computes its filter blocks for all 7
+    //      pixel blocks; the four MFMA steps of a fragment are interleaved
+    //      across the pixel blocks.  Rows past the halo (the last block's 12
+    //      spare rows) read row HP-1: their outputs are never stored.
 #pragma unroll
-  for (int fb = 0; fb < FB2; ++fb) acc2[fb] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int j = 0; j < FBW; ++j) {
+      const int fb = wave + 4 * j;
+      if (fb >= FB1) break;
+      const int f = fb * 16 + r;
+      f32x4 acc[HPB];
 #pragma unroll
-  for (int kc = 0; kc < KC2; ++kc) {
-    const int e0 = kc * 16 + 4 * q;
-    f32x4 d = {0.f, 0.f, 0.f, 0.f};
+      for (int pb = 0; pb < HPB; ++pb) acc[pb] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int t = 0; t < 9; ++t) {
-      const f32x4 ev = *reinterpret_cast<const f32x4 *>(es + (hbase + (t / 3) * HW + (t % 3)) * ES + e0);
-      const f32x4 wv = *reinterpret_cast<const f32x4 *>(wds + t * E + e0);
-      d += ev * wv;
+      for (int kc = 0; kc < KC1; ++kc) {
+        Frag16 a[HPB];
+#pragma unroll
+        for (int pb = 0; pb < HPB; ++pb)
+          a[pb] = load16(xs + min(pb * 16 + r, HP - 1) * XS + kc * 16 + 4 * q);
+#pragma unroll
+        for (int s2 = 0; s2 < 4; ++s2)
+#pragma unroll
+          for (int pb = 0; pb < HPB; ++pb) MfmaF32::step(acc[pb], a[pb], be[j][kc], s2);
+      }
+      const int lq = opaque(q);
+#pragma unroll
+      for (int pb = 0; pb < HPB; ++pb)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int hp = pb * 16 + 4 * lq + e;
+          if (hp < HP) {
+            const int iy = ty0 + hp / HW - 1, ix = tx0 + hp % HW - 1;
+            const bool inside = iy >= 0 && iy < H && ix >= 0 && ix < W;
+            es[hp * ES + f] = inside ? relu6(acc[pb][e]) : 0.0f;
+          }
+        }
     }
-    Frag16 a;
-    a.f = f32x4{relu6(d[0]), relu6(d[1]), relu6(d[2]), relu6(d[3])};
+    __syncthreads();
+
+    // ---- depthwise (in registers, A-operand layout) + project + residual.
+    // Wave w owns output pixels 16w .. 16w+15.
+    const int p = wave * 16 + r;
+    const int hbase = (p / TW) * HW + (p % TW);
+    f32x4 acc2[FB2];
 #pragma unroll
-    for (int fb = 0; fb < FB2; ++fb) MfmaF32::mma(acc2[fb], a, bp[kc][fb]);
-  }
+    for (int fb = 0; fb < FB2; ++fb) acc2[fb] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-  for (int fb = 0; fb < FB2; ++fb) {
-    const int c = fb * 16 + r;
-    if (c >= C) continue;
+    for (int kc = 0; kc < KC2; ++kc) {
+      const int e0 = kc * 16 + 4 * q;
+      f32x4 d = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const int pe = wave * 16 + 4 * q + e;
-      const int oy = ty0 + pe / TW, ox = tx0 + pe % TW;
-      if (oy < H && ox < W) {
-        const float res = xs[((pe / TW + 1) * HW + (pe % TW) + 1) * XS + c];
-        out[((size_t)(n * H + oy) * W + ox) * C + c] = acc2[fb][e] + res;
+      for (int tap = 0; tap < 9; ++tap) {
+        const f32x4 ev =
+            *reinterpret_cast<const f32x4 *>(es + (hbase + (tap / 3) * HW + (tap % 3)) * ES + e0);
+        const f32x4 wv = *reinterpret_cast<const f32x4 *>(wds + tap * E + e0);
+        d += ev * wv;
+      }
+      Frag16 a;
+      a.f = f32x4{relu6(d[0]), relu6(d[1]), relu6(d[2]), relu6(d[3])};
+#pragma unroll
+      for (int fb = 0; fb < FB2; ++fb) MfmaF32::mma(acc2[fb], a, bp[kc][fb]);
+    }
+    const int lq = opaque(q);
+#pragma unroll
+    for (int fb = 0; fb < FB2; ++fb) {
+      const int c = fb * 16 + r;
+      if (c >= C) continue;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int pe = wave * 16 + 4 * lq + e;
+        const int oy = ty0 + pe / TW, ox = tx0 + pe % TW;
+        if (oy < H && ox < W) {
+          const float res = xs[((pe / TW + 1) * HW + (pe % TW) + 1) * XS + c];
+          out[((size_t)(n * H + oy) * W + ox) * C + c] = acc2[fb][e] + res;
+        }
       }
     }
+    if (more) {
+      __syncthreads();  // every wave is done with xs and es of this tile
+      commit();
+    }
+    __syncthreads();
   }
 }
 
 template <int C, int E>
 hipError_t launch_irb_t(const IrbArgs &a, hipStream_t s) {
   const int tiles_w = (a.W + TW - 1) / TW, tiles_h = (a.H + TH - 1) / TH;
-  dim3 grid(tiles_w * tiles_h, a.N);
-  hipLaunchKernelGGL((irb_kernel<C, E>), grid, dim3(256), 0, s, a.x, a.we, a.wdw, a.wp, a.out,
-                     a.H, a.W, tiles_w);
+  const int per_image = tiles_w * tiles_h, ntiles = a.N * per_image;
+  const int g = persistent_grid(irb_kernel<C, E>);
+  if (g == 0) return hipErrorInvalidDeviceFunction;
+  hipLaunchKernelGGL((irb_kernel<C, E>), dim3(g), dim3(256), 0, s, a.x, a.we, a.wdw, a.wp, a.out,
+                     a.H, a.W, tiles_w, per_image, ntiles);
   return hipGetLastError();
 }
 

@@ -31,7 +31,7 @@ namespace npu {
 namespace {
 
 constexpr int TM = 32, TN = 64, TK = 128;
-constexpr int LDA = TK + 8;  // LDS row stride (elements) of the [row][k] tiles: 272 bytes
+constexpr int LDA = TK + 16;  // LDS row stride (elements) of the [row][k] tiles: 288 bytes (32 mod 64)
 
 __device__ __forceinline__ float silu(float g) { return g / (1.0f + expf(-g)); }
 
@@ -214,7 +214,7 @@ __global__ __launch_bounds__(256) void llama_gemm_kernel(const LlamaGemmArgs a) 
 // Causal attention, head dimension 64.
 constexpr int AQ = 64;          // queries per workgroup (4 waves x 16)
 constexpr int AK = 64;          // keys per block
-constexpr int LDK = 64 + 8;  // LDS row stride of K rows, V^T rows, P rows (elements)
+constexpr int LDK = 64 + 16;  // LDS row stride of K rows, V^T rows, P rows (elements): 160 bytes
 
 __global__ __launch_bounds__(256) void llama_attention_kernel(const uint16_t *__restrict__ Q,
                                                               const uint16_t *__restrict__ K,

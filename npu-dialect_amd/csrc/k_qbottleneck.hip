@@ -44,8 +44,8 @@ __global__ __launch_bounds__(256) void qbottleneck_kernel(
     const int32_t *__restrict__ m3, const int32_t *__restrict__ s3, int8_t *__restrict__ out,
     int H, int W, int tiles_w) {
   static_assert(C % 64 == 0 && M1 == 64, "C must be a multiple of 64 and M1 = 64");
-  constexpr int XS = C + 16;    // LDS row strides (16-byte pad against bank conflicts)
-  constexpr int YS = M1 + 16;
+  constexpr int XS = C + 32;    // LDS row strides: 32 mod 64 bytes keeps 16-lane
+  constexpr int YS = M1 + 32;   // 16-byte row reads free of bank conflicts
   constexpr int XCH = C / 16;   // 16-byte runs per pixel
   constexpr int NSEG = HPB * 16 * XCH;
   constexpr int SEGS = (NSEG + 255) / 256;

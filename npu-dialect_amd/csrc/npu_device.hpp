@@ -97,12 +97,11 @@ __device__ __forceinline__ u32x4 masked(u32x4 v, bool keep) {
 __device__ __forceinline__ float bf16_to_f32(uint16_t h) {
   return __uint_as_float(((uint32_t)h) << 16);
 }
+// gfx950 converts in hardware (v_cvt_pk_bf16_f32): round to nearest even,
+// NaN stays NaN.
 __device__ __forceinline__ uint16_t f32_to_bf16(float f) {
-  uint32_t u = __float_as_uint(f);
-  if ((u & 0x7f800000u) == 0x7f800000u && (u & 0x007fffffu))
-    return (uint16_t)((u >> 16) | 0x0040u);
-  u += 0x7fffu + ((u >> 16) & 1u);
-  return (uint16_t)(u >> 16);
+  const __bf16 h = (__bf16)f;
+  return __builtin_bit_cast(uint16_t, h);
 }
 
 // arith.maximumf / minimumf semantics (NaN propagates).
@@ -114,6 +113,21 @@ __device__ __forceinline__ float act_apply(float v, int act) {
     return v < 6.0f ? v : 6.0f;
   }
   return v;
+}
+
+// The same activations without a branch per element: the activation is
+// resolved once into clamp bounds (none: [-inf, inf], ReLU: [0, inf],
+// ReLU6: [0, 6]) and a NaN passes through the select.
+struct ActBounds {
+  float lo, hi;
+};
+__device__ __forceinline__ ActBounds act_bounds(int act) {
+  const float inf = __builtin_inff();
+  return ActBounds{act == 0 ? -inf : 0.0f, act == 2 ? 6.0f : inf};
+}
+__device__ __forceinline__ float act_clamp(float v, ActBounds b) {
+  const float c = fminf(fmaxf(v, b.lo), b.hi);
+  return v != v ? v : c;
 }
 
 __device__ __forceinline__ Frag16 load16(const void *p) {

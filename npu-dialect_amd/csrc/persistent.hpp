@@ -1,0 +1,59 @@
+// persistent.hpp -- shared pieces of the persistent (tile-walking) kernels.
+//
+// A persistent kernel launches as many workgroups as the CUs can hold at
+// once; each loads what every tile needs (filter fragments, requant
+// parameters) once, then walks its share of the tiles, fetching the next
+// tile's inputs into registers while the current tile is computed.
+//
+// Workgroups are dispatched round-robin over the 8 XCDs (blockIdx.x % 8), and
+// each XCD has its own L2.  The tiles are split into 8 contiguous ranges, one
+// per XCD, so tiles that share input rows (halos) run on the same L2.
+#pragma once
+#include <hip/hip_runtime.h>
+
+namespace npu {
+
+constexpr int kXcds = 8;
+
+struct TileWalk {
+  int first, end, step;
+};
+
+// Tiles of this workgroup: first, first + step, ... below end.  gridDim.x must
+// be a multiple of kXcds.
+__device__ __forceinline__ TileWalk tile_walk(int ntiles) {
+  const int xcd = blockIdx.x % kXcds;
+  TileWalk w;
+  w.step = gridDim.x / kXcds;
+  w.end = (int)((long long)(xcd + 1) * ntiles / kXcds);
+  w.first = (int)((long long)xcd * ntiles / kXcds) + blockIdx.x / kXcds;
+  return w;
+}
+
+// Index arithmetic that does not depend on the tile would be hoisted out of
+// a tile loop by the compiler and pinned in registers for its whole length;
+// passing a value through an empty asm makes it be recomputed per tile
+// instead (a few VALU operations against tens of VGPRs).
+__device__ __forceinline__ int opaque(int v) {
+  asm volatile("" : "+v"(v));
+  return v;
+}
+
+// Resident workgroups per CU for `kernel` (256 threads), times the CU count,
+// rounded down to whole XCD rounds: the persistent grid.  Queried once per
+// kernel from the runtime (register and LDS use decide it); 0 on failure.
+template <class K>
+int persistent_grid(K kernel) {
+  static int grid = 0;
+  if (grid == 0) {
+    int dev = 0, cus = 0, per_cu = 0;
+    if (hipGetDevice(&dev) != hipSuccess ||
+        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+        hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, 256, 0) != hipSuccess)
+      return 0;
+    grid = (per_cu > 0 ? per_cu : 1) * cus / kXcds * kXcds;
+  }
+  return grid;
+}
+
+}  // namespace npu
