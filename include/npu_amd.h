@@ -182,6 +182,40 @@ npu_status fused_llama_rmsnorm_swiglu(const npu_memref *h, const npu_memref *g2,
                                       const npu_memref *act, float eps,
                                       npu_stream stream);
 
+/* ---- launch plans ------------------------------------------------------
+ * What each kernel launch of the calling thread's most recent entry-point
+ * call does per work tile: the input of the MI355X launch model in
+ * npu_cost.h (npu_cm_predict_launch).  This is the GPU counterpart of the
+ * per-tile DMA and compute figures the reference's cost model derives from
+ * a tile configuration (evaluateConv2dTile / evaluateMatmulTile,
+ * lib/Analysis/CostModel.cpp:232-324): a work tile is what one workgroup
+ * computes between two loads of fresh input; a persistent workgroup walks
+ * several.  Filled by every fused_* entry point; the most recent call's
+ * plans replace the previous ones.  Byte and operation counts are of the
+ * work as issued (padding, halo re-reads and recompute included). */
+typedef struct npu_launch_plan {
+  char kernel[48];          /* kernel family                                   */
+  int32_t grid;             /* workgroups launched (256 lanes each)            */
+  int32_t wg_per_cu;        /* resident workgroups per CU (runtime occupancy)  */
+  int32_t tiles;            /* work tiles of the launch                        */
+  int32_t load_phases;      /* dependent global-load round trips per tile that
+                               no prefetch hides                               */
+  int32_t mfma_bits;        /* MFMA operand width: 32 (f32), 16 (bf16), 8 (i8) */
+  int32_t reserved;
+  double tile_macs;         /* MFMA multiply-adds per tile                     */
+  double tile_valu;         /* vector-ALU lane operations per tile besides the
+                               MFMAs (depthwise taps, norms, softmax, requant) */
+  double tile_lds_bytes;    /* LDS bytes read and written per tile             */
+  double tile_load_bytes;   /* global bytes loaded per tile                    */
+  double tile_store_bytes;  /* global bytes stored per tile                    */
+  double wg_setup_bytes;    /* global bytes a persistent workgroup loads once  */
+  double hbm_bytes;         /* compulsory HBM bytes of the launch              */
+} npu_launch_plan;
+
+/* Copies up to max_plans plans of the calling thread's most recent fused_*
+ * call and returns how many that call recorded. */
+int32_t npu_last_launch_plans(npu_launch_plan *plans, int32_t max_plans);
+
 #ifdef __cplusplus
 }
 #endif

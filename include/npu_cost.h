@@ -14,6 +14,8 @@
 
 #include <stdint.h>
 
+#include "npu_amd.h" /* npu_launch_plan */
+
 #ifdef __cplusplus
 extern "C" {
 #endif
@@ -194,6 +196,56 @@ int32_t npu_pass_spatial(const npu_graph *g, const npu_hw_target *t, int32_t op,
  * op stays untiled. */
 int32_t npu_pass_temporal(const npu_graph *g, const npu_hw_target *t, int32_t op,
                           npu_schedule_cost *cost, int64_t *tile_sizes, int32_t cap);
+
+/* ---- MI355X launch model ------------------------------------------------
+ * Time of one kernel launch from its launch plan (npu_last_launch_plans,
+ * npu_amd.h).  The reference's tile pipeline (evaluateConv2dTile /
+ * evaluateMatmulTile, CostModel.cpp:232-324: dmaIn + (tiles-1) *
+ * max(dmaIn, compute) + compute + dmaOut on one core) is applied per CU, a
+ * CU's "tiles" being the work tiles its resident workgroups run.  What a GPU
+ * adds to that model: several workgroups per CU overlap one another's load
+ * latency; compute is the slowest of the MFMA, LDS and vector-ALU streams;
+ * every CU shares one HBM.  Per CU with n tiles, k resident workgroups:
+ *   compute = max(macs / MFMA rate, LDS bytes / LDS rate, valu / VALU rate)
+ *   xfer    = (load + store bytes) / per-CU L2 rate
+ *   serial  = load_phases * latency + xfer + compute         (one tile alone)
+ *   cu      = setup + max(n * max(compute, xfer), n * serial / k)
+ *   time    = max(cu, HBM bytes / HBM bandwidth)
+ * The machine constants come from the MI355X data sheet (CUs, clock, MFMA
+ * rates) and from npu_calibrate (latency, copy bandwidth, L2 and LDS rates,
+ * launch cost). */
+typedef struct npu_gpu_params {
+  int32_t cus;
+  int32_t reserved;
+  double clock_ghz;
+  double hbm_gbs;               /* achievable HBM bandwidth (device copy)      */
+  double l2_bytes_per_clk_cu;   /* L2 -> CU read rate                          */
+  double lds_bytes_per_clk_cu;  /* conflict-free 16-byte LDS reads             */
+  double valu_lanes_per_clk_cu; /* 4 SIMDs x 16 lanes                          */
+  double mfma_macs_per_clk_cu[3]; /* f32, bf16, i8 (dense)                    */
+  double mem_latency_us;        /* dependent global load with every CU loading */
+  double launch_us;             /* per kernel in a captured graph of launches  */
+} npu_gpu_params;
+void npu_gpu_params_mi355x(npu_gpu_params *p);
+
+#define NPU_BOUND_HBM 0
+#define NPU_BOUND_MFMA 1
+#define NPU_BOUND_LDS 2
+#define NPU_BOUND_VALU 3
+#define NPU_BOUND_L2 4
+#define NPU_BOUND_LATENCY 5
+typedef struct npu_launch_cost {
+  double time_us;      /* predicted kernel duration                          */
+  double hbm_us;       /* HBM bytes at the achievable bandwidth               */
+  double cu_us;        /* per-CU pipeline time                                */
+  double tile_compute_us, tile_xfer_us, tile_serial_us; /* one tile           */
+  double tiles_per_cu;
+  int32_t bound;       /* NPU_BOUND_*                                         */
+  int32_t reserved;
+} npu_launch_cost;
+/* 0 on success, -1 on an invalid plan (message in npu_host_last_error). */
+int32_t npu_cm_predict_launch(const npu_launch_plan *plan, const npu_gpu_params *gpu,
+                              npu_launch_cost *out);
 
 #ifdef __cplusplus
 }

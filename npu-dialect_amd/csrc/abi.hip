@@ -13,6 +13,20 @@
 
 #include "../../include/npu_amd.h"
 #include "kernels.hpp"
+#include "plans.hpp"
+
+#include <vector>
+
+namespace npu {
+
+namespace {
+thread_local std::vector<npu_launch_plan> g_plans;
+}
+
+void plans_reset() { g_plans.clear(); }
+void plans_add(const npu_launch_plan &p) { g_plans.push_back(p); }
+
+}  // namespace npu
 
 namespace {
 
@@ -127,6 +141,12 @@ const char *npu_status_string(npu_status s) {
   }
 }
 
+int32_t npu_last_launch_plans(npu_launch_plan *plans, int32_t max_plans) {
+  const int32_t n = (int32_t)npu::g_plans.size();
+  for (int32_t i = 0; i < n && i < max_plans && plans; ++i) plans[i] = npu::g_plans[i];
+  return n;
+}
+
 int32_t npu_device_count(void) {
   int n = 0;
   if (hipGetDeviceCount(&n) != hipSuccess) return -1;
@@ -136,6 +156,7 @@ int32_t npu_device_count(void) {
 npu_status fused_matmul_bias_act(const npu_memref *A, const npu_memref *B,
                                  const npu_memref *bias, const npu_memref *out, int32_t act,
                                  npu_stream stream) {
+  npu::plans_reset();
   const void *pa, *pb, *pbias = nullptr, *po;
   NPU_TRY(check_memref(A, "A", 2, NPU_F32, &pa));
   NPU_TRY(check_memref(B, "B", 2, NPU_F32, &pb));
@@ -165,6 +186,7 @@ npu_status fused_matmul_bias_act(const npu_memref *A, const npu_memref *B,
 npu_status fused_conv2d_nhwc_bias_act(const npu_memref *x, const npu_memref *w,
                                       const npu_memref *bias, const npu_memref *out,
                                       int32_t pad, int32_t act, npu_stream stream) {
+  npu::plans_reset();
   if (!x) return fail(NPU_ERR_INVALID_ARG, "x: null descriptor");
   const int32_t dt = x->dtype;
   if (dt != NPU_F32 && dt != NPU_BF16)
@@ -218,6 +240,7 @@ npu_status fused_qbottleneck_i8(const npu_memref *x, const npu_memref *w1,
                                 const npu_memref *m2, const npu_memref *s2,
                                 const npu_memref *m3, const npu_memref *s3,
                                 const npu_memref *out, npu_stream stream) {
+  npu::plans_reset();
   const void *px, *pw1, *pw2, *pw3, *pm1, *ps1, *pm2, *ps2, *pm3, *ps3, *po;
   NPU_TRY(check_memref(x, "x", 4, NPU_I8, &px));
   const int64_t N = x->sizes[0], H = x->sizes[1], W = x->sizes[2], C = x->sizes[3];
@@ -264,6 +287,7 @@ npu_status fused_qbottleneck_i8(const npu_memref *x, const npu_memref *w1,
 
 npu_status fused_irb_f32(const npu_memref *x, const npu_memref *we, const npu_memref *wdw,
                          const npu_memref *wp, const npu_memref *out, npu_stream stream) {
+  npu::plans_reset();
   const void *px, *pwe, *pwdw, *pwp, *po;
   NPU_TRY(check_memref(x, "x", 4, NPU_F32, &px));
   const int64_t N = x->sizes[0], H = x->sizes[1], W = x->sizes[2], C = x->sizes[3];
@@ -341,6 +365,7 @@ npu_status fused_llama_qkv_rope(const npu_memref *x, const npu_memref *g1, const
                                 const npu_memref *cos_t, const npu_memref *sin_t,
                                 const npu_memref *Q, const npu_memref *K, const npu_memref *V,
                                 float eps, npu_stream stream) {
+  npu::plans_reset();
   const void *px, *pg, *pq, *pk, *pv, *pc, *ps, *oq, *ok, *ov;
   NPU_TRY(check_memref(x, "x", 2, NPU_BF16, &px));
   const int64_t S = x->sizes[0], D = x->sizes[1];
@@ -374,6 +399,7 @@ npu_status fused_llama_qkv_rope(const npu_memref *x, const npu_memref *g1, const
 npu_status fused_llama_attention(const npu_memref *Q, const npu_memref *K, const npu_memref *V,
                                  const npu_memref *A, int32_t n_heads, float scale,
                                  npu_stream stream) {
+  npu::plans_reset();
   const void *pq, *pk, *pv, *pa;
   NPU_TRY(check_memref(Q, "Q", 2, NPU_BF16, &pq));
   const int64_t S = Q->sizes[0], D = Q->sizes[1];
@@ -392,6 +418,7 @@ npu_status fused_llama_attention(const npu_memref *Q, const npu_memref *K, const
 npu_status fused_llama_matmul_residual(const npu_memref *am, const npu_memref *w,
                                        const npu_memref *res, const npu_memref *out,
                                        npu_stream stream) {
+  npu::plans_reset();
   const void *pa, *pw, *pr, *po;
   NPU_TRY(check_memref(am, "a", 2, NPU_BF16, &pa));
   const int64_t S = am->sizes[0], Kd = am->sizes[1];
@@ -418,6 +445,7 @@ npu_status fused_llama_matmul_residual(const npu_memref *am, const npu_memref *w
 npu_status fused_llama_rmsnorm_swiglu(const npu_memref *h, const npu_memref *g2,
                                       const npu_memref *wg, const npu_memref *wu,
                                       const npu_memref *act, float eps, npu_stream stream) {
+  npu::plans_reset();
   const void *ph, *pg, *pwg, *pwu, *po;
   NPU_TRY(check_memref(h, "h", 2, NPU_BF16, &ph));
   const int64_t S = h->sizes[0], D = h->sizes[1];

@@ -14,6 +14,7 @@
 // bf16 rounding of the bf16 variant) runs on the accumulators.
 #include "kernels.hpp"
 #include "npu_device.hpp"
+#include "plans.hpp"
 
 namespace npu {
 
@@ -112,6 +113,17 @@ template <class MM, typename T>
 hipError_t launch_conv(const ConvArgs &a, hipStream_t s) {
   const int P = a.N * a.Ho * a.Wo;
   dim3 grid((P + 63) / 64, (a.F + 63) / 64);
+  const int iters = a.KH * a.KW * ((a.C + MM::kPerFrag - 1) / MM::kPerFrag);
+  npu_launch_plan p = make_plan("conv2d_nhwc", grid.x * grid.y, wg_per_cu(conv2d_nhwc_kernel<MM, T>),
+                                grid.x * grid.y, 8 * sizeof(T));
+  p.load_phases = iters;  // each (tap, channel chunk) step loads, then multiplies
+  p.tile_macs = 64.0 * 64 * iters * MM::kPerFrag;
+  p.tile_valu = 64.0 * 64 * 4;
+  p.tile_load_bytes = iters * 4.0 * 4 * 1024;  // per wave 2 A and 2 B fragments of 1 KB
+  p.tile_store_bytes = 64.0 * 64 * sizeof(T);
+  p.hbm_bytes = (double)sizeof(T) * ((double)a.N * a.H * a.W * a.C + (double)a.F * a.KH * a.KW * a.C +
+                                     (double)P * a.F) + (a.bias ? 4.0 * a.F : 0.0);
+  plans_add(p);
   hipLaunchKernelGGL((conv2d_nhwc_kernel<MM, T>), grid, dim3(256), 0, s,
                      static_cast<const T *>(a.x), static_cast<const T *>(a.w), a.bias,
                      static_cast<T *>(a.out), a.N, a.H, a.W, a.C, a.F, a.KH, a.KW, a.pad,

@@ -31,6 +31,7 @@
 #include "kernels.hpp"
 #include "npu_device.hpp"
 #include "persistent.hpp"
+#include "plans.hpp"
 
 namespace npu {
 
@@ -78,8 +79,14 @@ __global__ __launch_bounds__(256) void conv3x3_rows_kernel(
 
   // Halo staging: 16-byte segments, loads from clamped addresses, the zero
   // padding applied by a select.
+  // The zero fill is applied when the segments are written to LDS, not when
+  // they are loaded: a select on a loaded value right after the load would
+  // make the wave wait for it, and the next stage's loads must stay in
+  // flight while the current stage is multiplied.
   u32x4 stage[SEGS];
+  uint32_t inside_bits = 0;
   auto fetch = [&](int c0) {
+    inside_bits = 0;
 #pragma unroll
     for (int s = 0; s < SEGS; ++s) {
       const int idx = min(tid + 256 * s, nseg - 1);
@@ -88,9 +95,9 @@ __global__ __launch_bounds__(256) void conv3x3_rows_kernel(
       const int ih = h0 + hr - 1, iw = hc - 1;
       const bool inside = ih >= 0 && ih < H && iw >= 0 && iw < W;
       const int ihc = min(max(ih, 0), H - 1), iwc = min(max(iw, 0), W - 1);
-      stage[s] = masked(*reinterpret_cast<const u32x4 *>(
-                            x + ((size_t)(n * H + ihc) * W + iwc) * C + c0 + seg * (16 / sizeof(T))),
-                        inside);
+      stage[s] = *reinterpret_cast<const u32x4 *>(
+          x + ((size_t)(n * H + ihc) * W + iwc) * C + c0 + seg * (16 / sizeof(T)));
+      inside_bits |= (uint32_t)inside << s;
     }
   };
   auto commit = [&](int buf) {
@@ -99,7 +106,7 @@ __global__ __launch_bounds__(256) void conv3x3_rows_kernel(
       const int idx = tid + 256 * s;
       if (idx < nseg)
         *reinterpret_cast<u32x4 *>(&halo[buf][(idx / SEGP) * REC + (idx % SEGP) * (16 / sizeof(T))]) =
-            stage[s];
+            masked(stage[s], (inside_bits >> s) & 1u);
     }
   };
   // Filters past F read filter F-1: they only feed columns that are not stored.
@@ -232,10 +239,14 @@ __global__ __launch_bounds__(256, NCH <= 2 ? 2 : 1) void conv3x3_stream_kernel(
     abase[i] = (pr * HC + pc) * REC + q * KPL;
   }
 
+  // Raw loads now, zero fill when written to LDS (a select right after a
+  // load would make the wave wait for it, serialising the prefetch).
   u32x4 stage[SEGS];
+  uint32_t inside_bits = 0;
   auto fetch = [&](int t) {
     const int n = t / tiles_h, h0 = (t - n * tiles_h) * TR;
     const int lt = opaque(tid);
+    inside_bits = 0;
 #pragma unroll
     for (int s = 0; s < SEGS; ++s) {
       const int idx = min(lt + 256 * s, nseg - 1);
@@ -244,9 +255,9 @@ __global__ __launch_bounds__(256, NCH <= 2 ? 2 : 1) void conv3x3_stream_kernel(
       const int ih = h0 + hr - 1, iw = hc - 1;
       const bool inside = ih >= 0 && ih < H && iw >= 0 && iw < W;
       const int ihc = min(max(ih, 0), H - 1), iwc = min(max(iw, 0), W - 1);
-      stage[s] = masked(*reinterpret_cast<const u32x4 *>(
-                            x + ((size_t)(n * H + ihc) * W + iwc) * C + seg * (16 / sizeof(T))),
-                        inside);
+      stage[s] = *reinterpret_cast<const u32x4 *>(
+          x + ((size_t)(n * H + ihc) * W + iwc) * C + seg * (16 / sizeof(T)));
+      inside_bits |= (uint32_t)inside << s;
     }
   };
   auto commit = [&]() {
@@ -255,7 +266,7 @@ __global__ __launch_bounds__(256, NCH <= 2 ? 2 : 1) void conv3x3_stream_kernel(
       const int idx = tid + 256 * s;
       if (idx < nseg)
         *reinterpret_cast<u32x4 *>(&halo[(idx / SEGP) * REC + (idx % SEGP) * (16 / sizeof(T))]) =
-            stage[s];
+            masked(stage[s], (inside_bits >> s) & 1u);
     }
   };
 
@@ -267,16 +278,38 @@ __global__ __launch_bounds__(256, NCH <= 2 ? 2 : 1) void conv3x3_stream_kernel(
   for (int ch = 0; ch < NCH; ++ch)
 #pragma unroll
     for (int t = 0; t < 9; ++t) b[ch][t] = load16(wrow + t * C + ch * KC);
-  const float bv = bias ? bias[f] : 0.0f;
+  // The filters are the MFMA's A operand and the pixels its B operand, so
+  // a lane's accumulator holds filters 4q..4q+3 (of its wave's 16) of one
+  // pixel: the epilogue writes them to the output stage as one 8-byte (bf16)
+  // or 16-byte (f32) LDS store.
+  const int fq = (blockIdx.y * 4 + wave) * 16 + 4 * q;
+  float bv[4];
+#pragma unroll
+  for (int e = 0; e < 4; ++e) bv[e] = bias ? bias[fq + e] : 0.0f;
   const ActBounds ab = act_bounds(act);
   commit();
+#pragma unroll
+  for (int ch = 0; ch < NCH; ++ch)
+#pragma unroll
+    for (int t = 0; t < 9; ++t) settle(b[ch][t].u);
+#pragma unroll
+  for (int e = 0; e < 4; ++e) settle(bv[e]);
   __syncthreads();
 
   // One halo buffer: the next tile's halo waits in registers until every
   // wave has finished reading the current one.
+  // Pipeline: the halo of tile t+step is in registers while tile t is
+  // multiplied; after the epilogue it goes to LDS and the fetch of tile
+  // t+2*step is issued before tile t's output stores, so no register that
+  // feeds a pending store is a load destination (the in-order memory
+  // counter would otherwise make the next fetch wait for those stores).
+  // Fetch and commit are unconditional (past the end the walk refetches a
+  // tile whose copy is never read): with a condition on either, the
+  // compiler's wait analysis assumes a fetch can be pending at the loop head
+  // and drains every outstanding load there.
+  auto next_of = [&](int t) { return t + step < t_end ? t + step : t; };
+  fetch(next_of(t_first));
   for (int t = t_first; t < t_end; t += step) {
-    const bool more = t + step < t_end;
-    if (more) fetch(t + step);
     const T *hb = halo;
     typename MM::acc_t acc[PBW];
 #pragma unroll
@@ -297,26 +330,31 @@ __global__ __launch_bounds__(256, NCH <= 2 ? 2 : 1) void conv3x3_stream_kernel(
 #pragma unroll
       for (int s = 0; s < MM::kSteps; ++s)
 #pragma unroll
-        for (int i = 0; i < PBW; ++i) MM::step(acc[i], a[j & 1][i], b[j / 9][j % 9], s);
+        for (int i = 0; i < PBW; ++i) MM::step(acc[i], b[j / 9][j % 9], a[j & 1][i], s);
       __builtin_amdgcn_sched_barrier(0);
     }
     {
-      const int lq = opaque(q);
+      const int lr = opaque(r);
 #pragma unroll
-      for (int i = 0; i < PBW; ++i)
+      for (int i = 0; i < PBW; ++i) {
+        const int p = i * 16 + lr;
+        if (p >= tile_px) continue;
+        float v[4];
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const int p = i * 16 + 4 * lq + e;
-          if (p >= tile_px) continue;
-          const float v = act_clamp(acc[i][e] + bv, ab);
-          if constexpr (sizeof(T) == 4) {
-            ostage[p * OREC + wave * 16 + r] = v;
-          } else {
-            ostage[p * OREC + wave * 16 + r] = f32_to_bf16(v);
-          }
+        for (int e = 0; e < 4; ++e) v[e] = act_clamp(acc[i][e] + bv[e], ab);
+        T *dst = ostage + p * OREC + wave * 16 + 4 * q;
+        if constexpr (sizeof(T) == 4) {
+          *reinterpret_cast<f32x4 *>(dst) = f32x4{v[0], v[1], v[2], v[3]};
+        } else {
+          const uint32_t lo = f32_to_bf16(v[0]) | ((uint32_t)f32_to_bf16(v[1]) << 16);
+          const uint32_t hi = f32_to_bf16(v[2]) | ((uint32_t)f32_to_bf16(v[3]) << 16);
+          *reinterpret_cast<uint2 *>(dst) = make_uint2(lo, hi);
         }
+      }
     }
     __syncthreads();
+    commit();
+    fetch(next_of(next_of(t)));
     {
       const int n = t / tiles_h, h0 = (t - n * tiles_h) * TR;
       const int rows = min(TR, H - h0);
@@ -328,7 +366,6 @@ __global__ __launch_bounds__(256, NCH <= 2 ? 2 : 1) void conv3x3_stream_kernel(
             *reinterpret_cast<const u32x4 *>(ostage + p * OREC + sg * (16 / sizeof(T)));
       }
     }
-    if (more) commit();
     __syncthreads();
   }
 }
@@ -340,6 +377,25 @@ hipError_t launch_stream(const ConvArgs &a, int wgs, hipStream_t s) {
     return hipErrorInvalidValue;
   const int ntiles = a.N * ((a.H + 1) / 2);
   dim3 grid(wgs, (a.F + 63) / 64);
+  {
+    constexpr int TR = 2, PBW = (TR * WMAX + 15) / 16, REC = NCH * 64 + 32;
+    const double es = sizeof(T), halo = 4.0 * (a.W + 2) * a.C * es;
+    npu_launch_plan p =
+        make_plan("conv3x3_persistent", wgs * grid.y,
+                  wg_per_cu(conv3x3_stream_kernel<MM, T, WMAX, NCH, WFIX>), ntiles * grid.y, 8 * sizeof(T));
+    p.load_phases = 0;  // the next tile's halo is fetched during this tile
+    p.tile_macs = 4.0 * PBW * 256 * 9 * a.C;
+    p.tile_valu = 4.0 * 64 * (PBW * 4 * 4 + 40);
+    p.tile_lds_bytes = 4.0 * (a.W + 2) * REC +                  // halo written
+                       4.0 * PBW * 9 * NCH * 1024 +             // A fragments read
+                       2.0 * TR * a.W * (64 * es + 32);         // output staged and read
+    p.tile_load_bytes = halo;
+    p.tile_store_bytes = TR * a.W * 64 * es;
+    p.wg_setup_bytes = 4.0 * 16 * 9 * a.C * es;
+    p.hbm_bytes = es * ((double)a.N * a.H * a.W * a.C + 9.0 * a.F * a.C + (double)a.N * a.H * a.W * a.F) +
+                  (a.bias ? 4.0 * a.F : 0.0);
+    plans_add(p);
+  }
   hipLaunchKernelGGL((conv3x3_stream_kernel<MM, T, WMAX, NCH, WFIX>), grid, dim3(256), 0, s,
                      static_cast<const T *>(a.x), static_cast<const T *>(a.w), a.bias,
                      static_cast<T *>(a.out), a.H, a.W, a.F, a.act, ntiles);
@@ -353,6 +409,24 @@ hipError_t launch_rows(const ConvArgs &a, hipStream_t s) {
     return hipErrorInvalidValue;
   const int tiles_h = (a.H + TR - 1) / TR;
   dim3 grid(a.N * tiles_h, (a.F + 16 * WF - 1) / (16 * WF));
+  {
+    constexpr int WP = 4 / WF, PBW = ((TR * WMAX + 15) / 16 + WP - 1) / WP;
+    constexpr int REC = NCH * 64 + 32;
+    const int nstages = a.C / (MM::kPerFrag * NCH);
+    const double es = sizeof(T);
+    npu_launch_plan p = make_plan("conv3x3_rows", grid.x * grid.y,
+                                  wg_per_cu(conv3x3_rows_kernel<MM, T, TR, WF, WMAX, NCH, NBUF>),
+                                  grid.x * grid.y, 8 * sizeof(T));
+    p.load_phases = 1;  // later stages are fetched while the previous one computes
+    p.tile_macs = 4.0 * PBW * 256 * 9 * a.C;
+    p.tile_valu = 4.0 * 64 * (PBW * 4 * 4 + 40 * nstages);
+    p.tile_lds_bytes = (TR + 2.0) * (a.W + 2) * REC * nstages + 4.0 * PBW * 9 * NCH * 1024 * nstages;
+    p.tile_load_bytes = (TR + 2.0) * (a.W + 2) * a.C * es + 4.0 * 16 * 9 * a.C * es;
+    p.tile_store_bytes = (double)TR * a.W * 16 * WF * es;
+    p.hbm_bytes = es * ((double)a.N * a.H * a.W * a.C + 9.0 * a.F * a.C + (double)a.N * a.H * a.W * a.F) +
+                  (a.bias ? 4.0 * a.F : 0.0);
+    plans_add(p);
+  }
   hipLaunchKernelGGL((conv3x3_rows_kernel<MM, T, TR, WF, WMAX, NCH, NBUF>), grid, dim3(256), 0, s,
                      static_cast<const T *>(a.x), static_cast<const T *>(a.w), a.bias,
                      static_cast<T *>(a.out), a.H, a.W, a.C, a.F, a.act);

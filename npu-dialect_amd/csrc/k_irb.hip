@@ -18,6 +18,7 @@
 #include "kernels.hpp"
 #include "npu_device.hpp"
 #include "persistent.hpp"
+#include "plans.hpp"
 
 namespace npu {
 
@@ -27,6 +28,7 @@ constexpr int TH = 8, TW = 8;        // output tile
 constexpr int HW = TW + 2;           // halo tile width (and height)
 constexpr int HP = HW * (TH + 2);    // 100 halo pixels
 constexpr int HPB = (HP + 15) / 16;  // 7 blocks of 16 rows
+constexpr int OP = TH * TW;          // 64 output pixels
 
 __device__ __forceinline__ float relu6(float v) { return act_apply(v, 2); }
 
@@ -64,11 +66,15 @@ __global__ __launch_bounds__(256, E >= 192 ? 1 : 2) void irb_kernel(const float 
 
   // x halo of tile t into registers (zero-padded to KC1*16 channels; clamped
   // addresses, zero fill by select).
-  f32x4 st[XSEGS];
+  // Raw loads now, zero fill when written to LDS (a select right after a
+  // load would make the wave wait for it, serialising the prefetch).
+  u32x4 st[XSEGS];
+  uint32_t inside_bits = 0;
   auto fetch = [&](int t) {
     const int n = t / tiles_per_image, tt = t - n * tiles_per_image;
     const int ty0 = (tt / tiles_w) * TH, tx0 = (tt % tiles_w) * TW;
     const int lt = opaque(tid);
+    inside_bits = 0;
 #pragma unroll
     for (int s = 0; s < XSEGS; ++s) {
       const int idx = min(lt + 256 * s, XSEG - 1);
@@ -76,9 +82,9 @@ __global__ __launch_bounds__(256, E >= 192 ? 1 : 2) void irb_kernel(const float 
       const int iy = ty0 + hp / HW - 1, ix = tx0 + hp % HW - 1;
       const bool inside = c < C && iy >= 0 && iy < H && ix >= 0 && ix < W;
       const int iyc = min(max(iy, 0), H - 1), ixc = min(max(ix, 0), W - 1);
-      const f32x4 v = *reinterpret_cast<const f32x4 *>(
+      st[s] = *reinterpret_cast<const u32x4 *>(
           x + ((size_t)(n * H + iyc) * W + ixc) * C + min(c, C - 4));
-      st[s] = inside ? v : f32x4{0.f, 0.f, 0.f, 0.f};
+      inside_bits |= (uint32_t)inside << s;
     }
   };
   auto commit = [&]() {
@@ -88,7 +94,7 @@ __global__ __launch_bounds__(256, E >= 192 ? 1 : 2) void irb_kernel(const float 
       const int idx = lt + 256 * s;
       if (idx < XSEG) {
         const int hp = idx / XV, c = (idx - hp * XV) * 4;
-        *reinterpret_cast<f32x4 *>(xs + hp * XS + c) = st[s];
+        *reinterpret_cast<u32x4 *>(xs + hp * XS + c) = masked(st[s], (inside_bits >> s) & 1u);
       }
     }
   };
@@ -120,11 +126,25 @@ __global__ __launch_bounds__(256, E >= 192 ? 1 : 2) void irb_kernel(const float 
   for (int i = tid; i < 9 * E / 4; i += 256)
     reinterpret_cast<f32x4 *>(wds)[i] = reinterpret_cast<const f32x4 *>(wdw)[i];
   commit();
+#pragma unroll
+  for (int j = 0; j < FBW; ++j)
+#pragma unroll
+    for (int kc = 0; kc < KC1; ++kc) settle(be[j][kc].u);
+#pragma unroll
+  for (int kc = 0; kc < KC2; ++kc)
+#pragma unroll
+    for (int fb = 0; fb < FB2; ++fb) settle(bp[kc][fb].u);
   __syncthreads();
 
+  // Pipeline: the halo of tile t+step is in registers while tile t is
+  // computed; once every wave is done with xs it goes to LDS and the fetch
+  // of tile t+2*step is issued.  Fetch and commit are unconditional (past the
+  // end the walk refetches a tile whose copy is never read): with a
+  // condition on either, the compiler's wait analysis assumes a fetch can be
+  // pending at the loop head and drains every outstanding load there.
+  auto next_of = [&](int t) { return t + walk.step < walk.end ? t + walk.step : t; };
+  fetch(next_of(walk.first));
   for (int t = walk.first; t < walk.end; t += walk.step) {
-    const bool more = t + walk.step < walk.end;
-    if (more) fetch(t + walk.step);
     const int n = t / tiles_per_image, tt = t - n * tiles_per_image;
     const int ty0 = (tt / tiles_w) * TH, tx0 = (tt % tiles_w) * TW;
 
@@ -189,7 +209,22 @@ __global__ __launch_bounds__(256, E >= 192 ? 1 : 2) void irb_kernel(const float 
 #pragma unroll
       for (int fb = 0; fb < FB2; ++fb) MfmaF32::mma(acc2[fb], a, bp[kc][fb]);
     }
+    // residual added while x is still in LDS; the stores go out after the
+    // next halo is committed and the one after it is fetched, so they are
+    // the newest memory operations when the loop comes round
     const int lq = opaque(q);
+#pragma unroll
+    for (int fb = 0; fb < FB2; ++fb) {
+      const int c = min(fb * 16 + r, C - 1);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int pe = wave * 16 + 4 * lq + e;
+        acc2[fb][e] += xs[((pe / TW + 1) * HW + (pe % TW) + 1) * XS + c];
+      }
+    }
+    __syncthreads();  // every wave is done with xs and es of this tile
+    commit();
+    fetch(next_of(next_of(t)));
 #pragma unroll
     for (int fb = 0; fb < FB2; ++fb) {
       const int c = fb * 16 + r;
@@ -198,15 +233,8 @@ __global__ __launch_bounds__(256, E >= 192 ? 1 : 2) void irb_kernel(const float 
       for (int e = 0; e < 4; ++e) {
         const int pe = wave * 16 + 4 * lq + e;
         const int oy = ty0 + pe / TW, ox = tx0 + pe % TW;
-        if (oy < H && ox < W) {
-          const float res = xs[((pe / TW + 1) * HW + (pe % TW) + 1) * XS + c];
-          out[((size_t)(n * H + oy) * W + ox) * C + c] = acc2[fb][e] + res;
-        }
+        if (oy < H && ox < W) out[((size_t)(n * H + oy) * W + ox) * C + c] = acc2[fb][e];
       }
-    }
-    if (more) {
-      __syncthreads();  // every wave is done with xs and es of this tile
-      commit();
     }
     __syncthreads();
   }
@@ -218,6 +246,23 @@ hipError_t launch_irb_t(const IrbArgs &a, hipStream_t s) {
   const int per_image = tiles_w * tiles_h, ntiles = a.N * per_image;
   const int g = persistent_grid(irb_kernel<C, E>);
   if (g == 0) return hipErrorInvalidDeviceFunction;
+  {
+    constexpr int KC1 = (C + 15) / 16, FB2 = (C + 15) / 16;
+    npu_launch_plan p = make_plan("mbv2_inverted_residual", g, wg_per_cu(irb_kernel<C, E>), ntiles, 32);
+    p.load_phases = 0;  // the next tile's halo is fetched during this tile
+    p.tile_macs = (double)E * HPB * 16 * KC1 * 16 + (double)OP * FB2 * 16 * E;
+    p.tile_valu = (double)OP * E * 9 + 3.0 * (HP + OP) * E;      // depthwise taps, ReLU6
+    p.tile_lds_bytes = HP * (KC1 * 16 + 8) * 4.0 +                // halo written
+                       (E / 16.0) * KC1 * HPB * 1024 +            // expand A read
+                       HP * E * 4.0 +                             // expanded tile written
+                       2.0 * 4 * (E / 16) * 9 * 1024 +            // depthwise taps and weights read
+                       OP * C * 4.0;                              // residual
+    p.tile_load_bytes = HP * C * 4.0;
+    p.tile_store_bytes = OP * C * 4.0;
+    p.wg_setup_bytes = 4.0 * 1024 * ((E / 64.0) * KC1 + (E / 16.0) * FB2) + 9.0 * E * 4;
+    p.hbm_bytes = 4.0 * (2.0 * a.N * a.H * a.W * C + 2.0 * C * E + 9.0 * E);
+    plans_add(p);
+  }
   hipLaunchKernelGGL((irb_kernel<C, E>), dim3(g), dim3(256), 0, s, a.x, a.we, a.wdw, a.wp, a.out,
                      a.H, a.W, tiles_w, per_image, ntiles);
   return hipGetLastError();

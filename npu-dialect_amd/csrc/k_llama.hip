@@ -25,6 +25,7 @@
 // registers; online softmax in f32; P rounded to bf16 for its MFMA with V.
 #include "kernels.hpp"
 #include "npu_device.hpp"
+#include "plans.hpp"
 
 namespace npu {
 
@@ -370,23 +371,71 @@ __global__ __launch_bounds__(256) void llama_attention_kernel(const uint16_t *__
 
 }  // namespace
 
+namespace {
+
+// Launch plan of one GEMM variant: a TM x (NB*TN) output tile walks K in
+// TK chunks (double-buffered: each chunk's loads overlap the previous
+// chunk's MFMAs, so one exposed load phase plus the prologue's row loads).
+template <class Kern>
+void plan_gemm(const char *name, Kern kern, const LlamaGemmArgs &a, int grid, int nb, bool norm,
+               int epi) {
+  const int kchunks = (a.K + TK - 1) / TK;
+  npu_launch_plan p = make_plan(name, grid, wg_per_cu(kern), grid, 16);
+  p.load_phases = norm ? 2 : 1;
+  p.tile_macs = (double)TM * TN * nb * kchunks * TK;
+  p.tile_valu = (norm ? 3.0 * TM * a.K : 0.0) + (double)TM * TN * nb * (epi == kEpiResidual ? 3 : 8);
+  p.tile_lds_bytes = 2.0 * ((double)TM + nb * TN) * kchunks * TK * 2;   // written once, read once
+  p.tile_load_bytes = ((double)TM + nb * TN) * kchunks * TK * 2 + (norm ? 4.0 * a.K : 0.0);
+  p.tile_store_bytes = (double)TM * TN * 2;
+  const double parts = epi == kEpiQkvRope ? a.nparts : (epi == kEpiSwiglu ? 2 : 1);
+  p.hbm_bytes = 2.0 * ((double)a.M * a.K + parts * a.K * a.Npart +
+                       (double)a.M * a.Npart * (epi == kEpiQkvRope ? a.nparts : 1) +
+                       (epi == kEpiResidual ? (double)a.M * a.Npart : 0.0)) +
+                (norm ? 4.0 * a.K : 0.0) + (epi == kEpiQkvRope ? 2.0 * 4 * a.M * a.Dh / 2 : 0.0);
+  plans_add(p);
+}
+
+}  // namespace
+
 hipError_t launch_llama_gemm(const LlamaGemmArgs &a, int pro, int epi, hipStream_t s) {
   const int tiles_n = (a.Npart / TN) * (epi == kEpiQkvRope ? a.nparts : 1);
   dim3 grid(tiles_n, (a.M + TM - 1) / TM);
-  if (pro == kProRmsnorm && epi == kEpiQkvRope)
+  const int g = grid.x * grid.y;
+  if (pro == kProRmsnorm && epi == kEpiQkvRope) {
+    plan_gemm("llama_rmsnorm_qkv_rope", llama_gemm_kernel<kProRmsnorm, kEpiQkvRope>, a, g, 1, true, epi);
     hipLaunchKernelGGL((llama_gemm_kernel<kProRmsnorm, kEpiQkvRope>), grid, dim3(256), 0, s, a);
-  else if (pro == kProPlain && epi == kEpiResidual)
+  } else if (pro == kProPlain && epi == kEpiResidual) {
+    plan_gemm("llama_matmul_residual", llama_gemm_kernel<kProPlain, kEpiResidual>, a, g, 1, false, epi);
     hipLaunchKernelGGL((llama_gemm_kernel<kProPlain, kEpiResidual>), grid, dim3(256), 0, s, a);
-  else if (pro == kProRmsnorm && epi == kEpiSwiglu)
+  } else if (pro == kProRmsnorm && epi == kEpiSwiglu) {
+    plan_gemm("llama_rmsnorm_swiglu", llama_gemm_kernel<kProRmsnorm, kEpiSwiglu>, a, g, 2, true, epi);
     hipLaunchKernelGGL((llama_gemm_kernel<kProRmsnorm, kEpiSwiglu>), grid, dim3(256), 0, s, a);
-  else
+  } else {
     return hipErrorInvalidValue;
+  }
   return hipGetLastError();
 }
 
 hipError_t launch_llama_attention(const uint16_t *Q, const uint16_t *K, const uint16_t *V,
                                   uint16_t *O, int S, int H, float scale, hipStream_t s) {
   dim3 grid((S + AQ - 1) / AQ, H);
+  {
+    // Causal: query block b sees key blocks 0..b, so the average tile walks
+    // (nqb + 1) / 2 key blocks; every key block costs QK^T and PV MFMAs, the
+    // online-softmax update, and one staged K and V^T block.
+    const int nqb = grid.x;
+    const double kblocks = (nqb + 1) / 2.0;
+    npu_launch_plan p = make_plan("llama_causal_attention", grid.x * grid.y,
+                                  wg_per_cu(llama_attention_kernel), grid.x * grid.y, 16);
+    p.load_phases = 1;
+    p.tile_macs = kblocks * 2.0 * AQ * AK * 64;
+    p.tile_valu = kblocks * (double)AQ * AK * 12;
+    p.tile_lds_bytes = kblocks * (2.0 * 2 * AK * 64 * 2 + 2.0 * AQ * AK * 2 + 4.0 * AQ * 64 * 2);
+    p.tile_load_bytes = kblocks * 2.0 * AK * 64 * 2 + AQ * 64 * 2.0;
+    p.tile_store_bytes = AQ * 64 * 2.0;
+    p.hbm_bytes = 4.0 * S * H * 64 * 2;  // Q, K, V in, O out
+    plans_add(p);
+  }
   hipLaunchKernelGGL(llama_attention_kernel, grid, dim3(256), 0, s, Q, K, V, O, S, H, scale);
   return hipGetLastError();
 }

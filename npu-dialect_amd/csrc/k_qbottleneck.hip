@@ -17,6 +17,7 @@
 // summation order gives the oracle's result bit for bit.
 #include "kernels.hpp"
 #include "npu_device.hpp"
+#include "plans.hpp"
 
 namespace npu {
 
@@ -182,6 +183,20 @@ template <int C, int M1>
 hipError_t launch_qb(const QBottleneckArgs &a, hipStream_t s) {
   const int tiles_w = (a.W + TW - 1) / TW, tiles_h = (a.H + TH - 1) / TH;
   dim3 grid(tiles_w * tiles_h, a.N);
+  {
+    constexpr int FB3 = C / 64;
+    npu_launch_plan p = make_plan("int8_bottleneck", grid.x * grid.y,
+                                  wg_per_cu(qbottleneck_kernel<C, M1>), grid.x * grid.y, 8);
+    p.load_phases = 1;  // halo and conv1/conv2 filters together; conv3's during conv1
+    p.tile_macs = (double)HPB * 16 * M1 * C + (double)OP * M1 * 9 * M1 + (double)OP * C * M1;
+    p.tile_valu = 6.0 * (HPB * 16.0 * M1 + OP * M1 + OP * C);     // requant, clamp, pack
+    p.tile_lds_bytes = HP * (C + 32.0) + 4.0 * HPB * (C / 64) * 1024 + HPB * 16.0 * M1 +
+                       4.0 * 4 * 9 * 1024 + OP * M1 + 4.0 * 4 * 1024 + 3.0 * OP * C;
+    p.tile_load_bytes = HP * (double)C + 4.0 * 1024 * (C / 64 + 9 + FB3) + 4.0 * 4 * (2 + 2 * FB3) * 64;
+    p.tile_store_bytes = OP * (double)C;
+    p.hbm_bytes = 2.0 * a.N * a.H * a.W * C + (double)M1 * C * 2 + 9.0 * M1 * M1 + 4.0 * 2 * (2 * M1 + C);
+    plans_add(p);
+  }
   hipLaunchKernelGGL((qbottleneck_kernel<C, M1>), grid, dim3(256), 0, s, a.x, a.w1, a.w2, a.w3,
                      a.m1, a.s1, a.m2, a.s2, a.m3, a.s3, a.out, a.H, a.W, tiles_w);
   return hipGetLastError();

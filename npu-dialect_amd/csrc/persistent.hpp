@@ -39,6 +39,17 @@ __device__ __forceinline__ int opaque(int v) {
   return v;
 }
 
+// Marks a loaded value as used, so the wave waits for its load here.  A
+// persistent kernel calls this on everything it loads once (filter
+// fragments, bias) before entering its tile loop: the counter of
+// outstanding vector-memory operations is in order, so if such a load could
+// still be pending inside the loop, the waits the compiler places there for
+// it would also drain the next tile's prefetch.
+template <class V>
+__device__ __forceinline__ void settle(const V &v) {
+  asm volatile("" ::"v"(v));
+}
+
 // Resident workgroups per CU for `kernel` (256 threads), times the CU count,
 // rounded down to whole XCD rounds: the persistent grid.  Queried once per
 // kernel from the runtime (register and LDS use decide it); 0 on failure.

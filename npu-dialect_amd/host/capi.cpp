@@ -8,6 +8,11 @@
 #include "cost_model.hpp"
 #include "passes.hpp"
 
+namespace npu {
+void gpu_params_mi355x(npu_gpu_params *p);
+bool predict_launch(const npu_launch_plan &pl, const npu_gpu_params &g, npu_launch_cost *out);
+}  // namespace npu
+
 struct npu_graph {
   npu::ir::Graph g;
 };
@@ -146,6 +151,19 @@ int32_t npu_graph_add_op(npu_graph *g, int32_t kind, const int32_t *operands, in
 int32_t npu_graph_num_ops(const npu_graph *g) { return g ? (int32_t)g->g.ops.size() : -1; }
 
 const char *npu_host_last_error(void) { return g_err.c_str(); }
+
+void npu_gpu_params_mi355x(npu_gpu_params *p) {
+  if (p) npu::gpu_params_mi355x(p);
+}
+
+int32_t npu_cm_predict_launch(const npu_launch_plan *plan, const npu_gpu_params *gpu,
+                              npu_launch_cost *out) {
+  if (!plan || !gpu || !out) return fail("null argument");
+  if (!npu::predict_launch(*plan, *gpu, out))
+    return fail("invalid launch plan '%.48s' (grid %d, tiles %d)", plan->kernel, plan->grid,
+                plan->tiles);
+  return 0;
+}
 
 int64_t npu_cm_op_macs(const npu_graph *g, const npu_hw_target *t, int32_t op) {
   if (bad_op(g, op) || !t) return fail("bad op");

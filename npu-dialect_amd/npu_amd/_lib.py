@@ -35,6 +35,27 @@ class NpuMemref(C.Structure):
 
 _MR = C.POINTER(NpuMemref)
 
+
+class NpuLaunchPlan(C.Structure):
+    """npu_launch_plan: per-tile work of one kernel launch (launch-model input)."""
+
+    _fields_ = [
+        ("kernel", C.c_char * 48),
+        ("grid", C.c_int32),
+        ("wg_per_cu", C.c_int32),
+        ("tiles", C.c_int32),
+        ("load_phases", C.c_int32),
+        ("mfma_bits", C.c_int32),
+        ("reserved", C.c_int32),
+        ("tile_macs", C.c_double),
+        ("tile_valu", C.c_double),
+        ("tile_lds_bytes", C.c_double),
+        ("tile_load_bytes", C.c_double),
+        ("tile_store_bytes", C.c_double),
+        ("wg_setup_bytes", C.c_double),
+        ("hbm_bytes", C.c_double),
+    ]
+
 SIGNATURES = {
     "npu_version": (C.c_char_p, []),
     "npu_last_error": (C.c_char_p, []),
@@ -48,6 +69,7 @@ SIGNATURES = {
     "fused_llama_attention": (_I32, [_MR] * 4 + [_I32, C.c_float, _P]),
     "fused_llama_matmul_residual": (_I32, [_MR] * 4 + [_P]),
     "fused_llama_rmsnorm_swiglu": (_I32, [_MR] * 5 + [C.c_float, _P]),
+    "npu_last_launch_plans": (_I32, [C.POINTER(NpuLaunchPlan), _I32]),
 }
 
 _lib = None
@@ -72,3 +94,11 @@ def lib():
             fn.argtypes = args
         _lib = handle
     return _lib
+
+
+def last_launch_plans():
+    """Launch plans of this thread's most recent fused_* call (a list of NpuLaunchPlan)."""
+    n = lib().npu_last_launch_plans(None, 0)
+    arr = (NpuLaunchPlan * max(n, 1))()
+    lib().npu_last_launch_plans(arr, n)
+    return [arr[i] for i in range(n)]

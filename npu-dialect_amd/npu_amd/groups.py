@@ -44,9 +44,30 @@ def _stream(stream):
     return getattr(stream, "cuda_stream", stream)
 
 
+_plan_log = None
+
+
+class collect_plans:
+    """Context manager: gathers the launch plans of every entry-point call made
+    inside it (in call order) into ``.plans``."""
+
+    def __enter__(self):
+        global _plan_log
+        self.plans = []
+        self._prev, _plan_log = _plan_log, self.plans
+        return self
+
+    def __exit__(self, *exc):
+        global _plan_log
+        _plan_log = self._prev
+        return False
+
+
 def _check(status, where):
     if status != 0:
         raise NpuError(status, where)
+    if _plan_log is not None:
+        _plan_log.extend(_lib.last_launch_plans())
 
 
 def _opt(t):

@@ -6,6 +6,7 @@ import ctypes as C
 import os
 
 from . import mlir
+from ._lib import NpuLaunchPlan  # the struct only: does not load libnpu_amd.so
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
 HOST_LIB_PATH = os.path.join(_HERE, "libnpu_host.so")
@@ -65,6 +66,29 @@ class SubgraphCost(C.Structure):
         "pipelined_cycles", "unpipelined_cycles", "num_ops")]
 
 
+class GpuParams(C.Structure):
+    """npu_gpu_params: machine constants of the MI355X launch model."""
+
+    _fields_ = [
+        ("cus", C.c_int32), ("reserved", C.c_int32), ("clock_ghz", C.c_double),
+        ("hbm_gbs", C.c_double), ("l2_bytes_per_clk_cu", C.c_double),
+        ("lds_bytes_per_clk_cu", C.c_double), ("valu_lanes_per_clk_cu", C.c_double),
+        ("mfma_macs_per_clk_cu", C.c_double * 3), ("mem_latency_us", C.c_double),
+        ("launch_us", C.c_double),
+    ]
+
+
+class LaunchCost(C.Structure):
+    _fields_ = [
+        ("time_us", C.c_double), ("hbm_us", C.c_double), ("cu_us", C.c_double),
+        ("tile_compute_us", C.c_double), ("tile_xfer_us", C.c_double),
+        ("tile_serial_us", C.c_double), ("tiles_per_cu", C.c_double),
+        ("bound", C.c_int32), ("reserved", C.c_int32),
+    ]
+
+
+BOUNDS = ("hbm", "mfma", "lds", "valu", "l2", "latency")
+
 _I32, _I64, _P = C.c_int32, C.c_int64, C.c_void_p
 _PT = C.POINTER(HWTarget)
 _PI32 = C.POINTER(C.c_int32)
@@ -100,6 +124,9 @@ SIGNATURES = {
     "npu_spec_num_splits": (_I32, [_P, _I32]),
     "npu_spec_split": (_I32, [_P, _I32, _I32, _PI32, _PI32, _PI32]),
     "npu_spec_preferred_spatial_dim": (_I32, [_P, _I32]),
+    "npu_gpu_params_mi355x": (None, [C.POINTER(GpuParams)]),
+    "npu_cm_predict_launch": (_I32, [C.POINTER(NpuLaunchPlan), C.POINTER(GpuParams),
+                                     C.POINTER(LaunchCost)]),
 }
 
 _lib = None
@@ -374,3 +401,26 @@ def temporal(g: Graph, t: HWTarget, op):
     ts = (C.c_int64 * 16)()
     n = _check(lib().npu_pass_temporal(g.h, C.byref(t), g.op_id[op], C.byref(s), ts, 16))
     return (list(ts[:n]), s) if n else (None, None)
+
+
+def mi355x_gpu() -> GpuParams:
+    """The calibrated MI355X constants of the launch model."""
+    g = GpuParams()
+    lib().npu_gpu_params_mi355x(C.byref(g))
+    return g
+
+
+def predict_launch(plan: NpuLaunchPlan, gpu: GpuParams = None) -> LaunchCost:
+    """Launch-model time of one kernel launch (npu_cm_predict_launch)."""
+    out = LaunchCost()
+    _check(lib().npu_cm_predict_launch(C.byref(plan), C.byref(gpu or mi355x_gpu()), C.byref(out)))
+    return out
+
+
+def predict_block(plans, gpu: GpuParams = None):
+    """Predicted time of a fused block: its launches back to back in a captured
+    graph (each kernel's duration plus the per-launch cost).  Returns
+    (total_us, [(kernel, LaunchCost), ...])."""
+    gpu = gpu or mi355x_gpu()
+    parts = [(p.kernel.decode(), predict_launch(p, gpu)) for p in plans]
+    return sum(c.time_us + gpu.launch_us for _, c in parts), parts
