@@ -12,7 +12,10 @@ microseconds (lower is better).
 
 ``roofline`` relates the algorithmic work of one launch (compulsory HBM
 bytes, or MFMA FLOPs, of the fused block) to the measured launch duration and
-the MI355X published peak.  ``cpu_baseline`` times the CPU restatement of the
+the MI355X published peak.  ``graph_us`` is the same step's device time with
+the host's per-launch cost removed (20 steps captured in one HIP graph,
+replayed); ``cost_model`` compares it with the MI355X launch model's
+prediction from the launch plans the entry points record.  ``cpu_baseline`` times the CPU restatement of the
 reference's execution path (the oracle: unfused scalar loop nests, one
 thread) on a bounded sample of the same workload on this host.  ``blocks``
 repeats the GPU measurement for every other configuration.
@@ -61,6 +64,53 @@ def time_gpu(w, steps, warmup):
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
     return start.elapsed_time(end) * 1e-3 / steps, wall, o
+
+
+def time_graph(w, steps, reps=10):
+    """Device time per step with host launch overhead removed: `steps` steps
+    captured in one HIP graph, replayed `reps` times between HIP events.
+    Also checks that the graph's outputs equal an eager run's, bit for bit.
+    Returns (seconds per step, outputs match)."""
+    import torch
+
+    from npu_amd import configs
+    d = configs.to_device(w.make_inputs())
+    o = w.make_outputs(d)
+    w.run(d, o, torch.cuda.current_stream())  # eager run: initialises lazy launch state
+    torch.cuda.synchronize()
+    eager = [t.clone() for t in o.values()]
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        cs = torch.cuda.current_stream()
+        for _ in range(steps):
+            w.run(d, o, cs)
+    stream = torch.cuda.current_stream()
+    g.replay()
+    torch.cuda.synchronize()
+    same = all(torch.equal(a, b) for a, b in zip(eager, o.values()))
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record(stream)
+    for _ in range(reps):
+        g.replay()
+    end.record(stream)
+    torch.cuda.synchronize()
+    return start.elapsed_time(end) * 1e-3 / (reps * steps), same
+
+
+def model_prediction(w):
+    """Launch-model prediction for one step: the launch plans the entry points
+    record, through the MI355X model of libnpu_host.so."""
+    import torch
+
+    from npu_amd import configs, groups, host
+    d = configs.to_device(w.make_inputs())
+    o = w.make_outputs(d)
+    with groups.collect_plans() as cp:
+        w.run(d, o, torch.cuda.current_stream())
+    torch.cuda.synchronize()
+    total, parts = host.predict_block(cp.plans)
+    return total, [{"kernel": k, "us": round(c.time_us, 3), "bound": host.BOUNDS[c.bound]}
+                   for k, c in parts]
 
 
 def cpu_sample(w, budget_s=30.0):
@@ -134,6 +184,8 @@ def main():
     name = args.workload or configs.HEADLINE
     w = configs.by_name(name)
     sec, wall, _ = time_gpu(w, args.steps, args.warmup)
+    gsec, gsame = time_graph(w, 20)
+    pred, parts = model_prediction(w)
     line = {
         "metric": "fused-block latency",
         "value": round(sec * 1e6, 3),
@@ -153,6 +205,10 @@ def main():
         "wall_s_timed_region": wall,
         "roofline": dict(w.roofline(sec), traffic=measured_traffic(w.name),
                          flops=w.flops, bytes=w.bytes, floor_us=w.floor_s() * 1e6),
+        "graph_us": round(gsec * 1e6, 3),
+        "graph_matches_eager": gsame,
+        "cost_model": {"predicted_us": round(pred, 3), "measured_us": round(gsec * 1e6, 3),
+                       "error": round(pred / (gsec * 1e6) - 1, 3), "kernels": parts},
     }
     if not args.no_cpu:
         line["cpu_baseline"] = cpu_sample(w)
@@ -162,11 +218,19 @@ def main():
             if other.name == w.name:
                 continue
             s, _, _ = time_gpu(other, max(20, args.steps // 2), max(5, args.warmup // 2))
+            gs, same = time_graph(other, 20)
+            p, pk = model_prediction(other)
             rl = other.roofline(s)
             blocks.append({"workload": other.name, "latency_us": round(s * 1e6, 3),
+                           "graph_us": round(gs * 1e6, 3), "graph_matches_eager": same,
                            "bound": rl["bound"], "frac": round(rl["frac"], 4),
-                           "floor_us": round(other.floor_s() * 1e6, 3)})
+                           "graph_frac": round(other.roofline(gs)["frac"], 4),
+                           "floor_us": round(other.floor_s() * 1e6, 3),
+                           "model_us": round(p, 3), "model_error": round(p / (gs * 1e6) - 1, 3),
+                           "model_kernels": pk})
         line["blocks"] = blocks
+        errs = [abs(line["cost_model"]["error"])] + [abs(b["model_error"]) for b in blocks]
+        line["cost_model"]["within_25pct"] = f"{sum(e <= 0.25 for e in errs)}/{len(errs)}"
     print(json.dumps(line), flush=True)
 
 

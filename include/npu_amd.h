@@ -203,8 +203,12 @@ typedef struct npu_launch_plan {
   int32_t mfma_bits;        /* MFMA operand width: 32 (f32), 16 (bf16), 8 (i8) */
   int32_t reserved;
   double tile_macs;         /* MFMA multiply-adds per tile                     */
-  double tile_valu;         /* vector-ALU lane operations per tile besides the
-                               MFMAs (depthwise taps, norms, softmax, requant) */
+  double tile_valu;         /* vector-ALU instructions per tile besides the
+                               MFMAs, summed over the workgroup's waves
+                               (index arithmetic, epilogues, depthwise taps,
+                               norms, softmax, requant): the instruction budget
+                               of the code as written, counted with the
+                               SQ_INSTS_VALU counter                           */
   double tile_lds_bytes;    /* LDS bytes read and written per tile             */
   double tile_load_bytes;   /* global bytes loaded per tile                    */
   double tile_store_bytes;  /* global bytes stored per tile                    */

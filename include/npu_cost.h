@@ -206,7 +206,9 @@ int32_t npu_pass_temporal(const npu_graph *g, const npu_hw_target *t, int32_t op
  * adds to that model: several workgroups per CU overlap one another's load
  * latency; compute is the slowest of the MFMA, LDS and vector-ALU streams;
  * every CU shares one HBM.  Per CU with n tiles, k resident workgroups:
- *   compute = max(macs / MFMA rate, LDS bytes / LDS rate, valu / VALU rate)
+ *   compute = max(LDS bytes / LDS rate, macs / MFMA rate + valu / VALU rate)
+ *             (a SIMD issues its waves' vector instructions one at a time,
+ *             so the MFMA and vector-ALU streams are charged in sequence)
  *   xfer    = (load + store bytes) / per-CU L2 rate
  *   serial  = load_phases * latency + xfer + compute         (one tile alone)
  *   cu      = setup + max(n * max(compute, xfer), n * serial / k)
@@ -221,10 +223,11 @@ typedef struct npu_gpu_params {
   double hbm_gbs;               /* achievable HBM bandwidth (device copy)      */
   double l2_bytes_per_clk_cu;   /* L2 -> CU read rate                          */
   double lds_bytes_per_clk_cu;  /* conflict-free 16-byte LDS reads             */
-  double valu_lanes_per_clk_cu; /* 4 SIMDs x 16 lanes                          */
+  double valu_instr_per_clk_cu; /* wave instructions: 4 SIMDs, 4 clocks each   */
   double mfma_macs_per_clk_cu[3]; /* f32, bf16, i8 (dense)                    */
   double mem_latency_us;        /* dependent global load with every CU loading */
-  double launch_us;             /* per kernel in a captured graph of launches  */
+  double launch_us;             /* per kernel in a captured graph of launches
+                                   (an empty kernel's cost, npu_calibrate)    */
 } npu_gpu_params;
 void npu_gpu_params_mi355x(npu_gpu_params *p);
 

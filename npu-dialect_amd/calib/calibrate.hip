@@ -146,12 +146,42 @@ int main() {
               2000, &t_launch_full))
     return 1;
 
+  // per-kernel cost inside a captured graph: 200 launches of an empty
+  // single-workgroup kernel, and of a full-grid one, replayed
+  double t_graph = 0, t_graph_full = 0;
+  for (int full = 0; full < 2; ++full) {
+    hipStream_t st;
+    CK(hipStreamCreate(&st));
+    hipGraph_t graph;
+    hipGraphExec_t exec;
+    CK(hipStreamBeginCapture(st, hipStreamCaptureModeGlobal));
+    for (int i = 0; i < 200; ++i)
+      hipLaunchKernelGGL(empty_kernel, dim3(full ? 4 * cus : 1), dim3(full ? 256 : 64), 0, st, nullptr);
+    CK(hipStreamEndCapture(st, &graph));
+    CK(hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0));
+    CK(hipGraphLaunch(exec, st));
+    CK(hipStreamSynchronize(st));
+    hipEvent_t a, b;
+    CK(hipEventCreate(&a));
+    CK(hipEventCreate(&b));
+    CK(hipEventRecord(a, st));
+    for (int r = 0; r < 10; ++r) CK(hipGraphLaunch(exec, st));
+    CK(hipEventRecord(b, st));
+    CK(hipEventSynchronize(b));
+    float ms = 0;
+    CK(hipEventElapsedTime(&ms, a, b));
+    (full ? t_graph_full : t_graph) = 1000.0 * ms / (10 * 200);
+    CK(hipGraphExecDestroy(exec));
+    CK(hipGraphDestroy(graph));
+    CK(hipStreamDestroy(st));
+  }
+
   // dependent-load latency: HBM (1 GiB span), L2 (1 MiB span)
   int *dout;
   CK(hipMalloc(&dout, 4 * cus * 64 * sizeof(int)));
   const int n_hbm = (1 << 30) / (kStride * 4), n_l2 = (1 << 20) / (kStride * 4);
   const int hops = 4000;
-  double lat_hbm, lat_l2, lat_loaded;
+  double lat_hbm, lat_l2, lat_loaded, lat_l2_loaded;
   {
     std::vector<int> next = make_cycle(n_hbm, 1);
     int *d;
@@ -179,6 +209,11 @@ int main() {
                 3, &us))
       return 1;
     lat_l2 = us / hops;
+    // every CU chasing at once through the same L2-resident span
+    if (time_us([&] { hipLaunchKernelGGL(chase_kernel, dim3(4 * cus), dim3(64), 0, 0, d, hops, n_l2, dout); },
+                3, &us))
+      return 1;
+    lat_l2_loaded = us / hops;
     CK(hipFree(d));
   }
 
@@ -207,9 +242,9 @@ int main() {
   const double l2_bytes_per_clk_cu = (double)l2n * 16 * reps / (t_l2 * 1e3 * ghz);
 
   printf("{\"device\": \"%s\", \"cus\": %d, \"shader_clock_ghz\": %.3f, \"launch_us\": %.3f, "
-         "\"launch_full_grid_us\": %.3f, \"hbm_latency_us\": %.3f, \"hbm_latency_loaded_us\": %.3f, "
-         "\"l2_latency_us\": %.3f, \"hbm_copy_gbs\": %.1f, \"l2_read_bytes_per_clk_cu\": %.2f}\n",
-         prop.gcnArchName, cus, ghz, t_launch, t_launch_full, lat_hbm, lat_loaded, lat_l2, copy_gbs,
+         "\"launch_full_grid_us\": %.3f, \"graph_launch_us\": %.3f, \"graph_launch_full_grid_us\": %.3f, \"hbm_latency_us\": %.3f, \"hbm_latency_loaded_us\": %.3f, "
+         "\"l2_latency_us\": %.3f, \"l2_latency_loaded_us\": %.3f, \"hbm_copy_gbs\": %.1f, \"l2_read_bytes_per_clk_cu\": %.2f}\n",
+         prop.gcnArchName, cus, ghz, t_launch, t_launch_full, t_graph, t_graph_full, lat_hbm, lat_loaded, lat_l2, lat_l2_loaded, copy_gbs,
          l2_bytes_per_clk_cu);
   CK(hipFree(src));
   CK(hipFree(dst));

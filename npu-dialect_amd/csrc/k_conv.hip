@@ -118,7 +118,7 @@ hipError_t launch_conv(const ConvArgs &a, hipStream_t s) {
                                 grid.x * grid.y, 8 * sizeof(T));
   p.load_phases = iters;  // each (tap, channel chunk) step loads, then multiplies
   p.tile_macs = 64.0 * 64 * iters * MM::kPerFrag;
-  p.tile_valu = 64.0 * 64 * 4;
+  p.tile_valu = 4.0 * (40.0 * iters + 150);  // per wave: addressing per step, epilogue
   p.tile_load_bytes = iters * 4.0 * 4 * 1024;  // per wave 2 A and 2 B fragments of 1 KB
   p.tile_store_bytes = 64.0 * 64 * sizeof(T);
   p.hbm_bytes = (double)sizeof(T) * ((double)a.N * a.H * a.W * a.C + (double)a.F * a.KH * a.KW * a.C +

@@ -385,7 +385,8 @@ hipError_t launch_stream(const ConvArgs &a, int wgs, hipStream_t s) {
                   wg_per_cu(conv3x3_stream_kernel<MM, T, WMAX, NCH, WFIX>), ntiles * grid.y, 8 * sizeof(T));
     p.load_phases = 0;  // the next tile's halo is fetched during this tile
     p.tile_macs = 4.0 * PBW * 256 * 9 * a.C;
-    p.tile_valu = 4.0 * 64 * (PBW * 4 * 4 + 40);
+    // counted per wave and tile: 950 (bf16, two chunks), 1292 (f32, four chunks)
+    p.tile_valu = 4.0 * (600.0 + 175.0 * NCH);
     p.tile_lds_bytes = 4.0 * (a.W + 2) * REC +                  // halo written
                        4.0 * PBW * 9 * NCH * 1024 +             // A fragments read
                        2.0 * TR * a.W * (64 * es + 32);         // output staged and read
@@ -419,7 +420,8 @@ hipError_t launch_rows(const ConvArgs &a, hipStream_t s) {
                                   grid.x * grid.y, 8 * sizeof(T));
     p.load_phases = 1;  // later stages are fetched while the previous one computes
     p.tile_macs = 4.0 * PBW * 256 * 9 * a.C;
-    p.tile_valu = 4.0 * 64 * (PBW * 4 * 4 + 40 * nstages);
+    // counted per wave: 570 (f32, one chunk per stage, four stages), 554 (bf16, one stage)
+    p.tile_valu = 4.0 * (540.0 + 8.0 * nstages * PBW);
     p.tile_lds_bytes = (TR + 2.0) * (a.W + 2) * REC * nstages + 4.0 * PBW * 9 * NCH * 1024 * nstages;
     p.tile_load_bytes = (TR + 2.0) * (a.W + 2) * a.C * es + 4.0 * 16 * 9 * a.C * es;
     p.tile_store_bytes = (double)TR * a.W * 16 * WF * es;

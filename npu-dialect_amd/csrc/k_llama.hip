@@ -23,6 +23,8 @@
 // four waves of 16 query rows.  Key blocks of 64 (K rows and V transposed)
 // are staged once in LDS for the four waves, the next block prefetched into
 // registers; online softmax in f32; P rounded to bf16 for its MFMA with V.
+#include <type_traits>
+
 #include "kernels.hpp"
 #include "npu_device.hpp"
 #include "plans.hpp"
@@ -57,6 +59,9 @@ __device__ __forceinline__ float sumsq8(const u32x4 &v) {
   return s;
 }
 
+template <int N>
+using Slot = std::integral_constant<int, N>;
+
 template <int PRO, int EPI>
 __global__ __launch_bounds__(256) void llama_gemm_kernel(const LlamaGemmArgs a) {
   constexpr int NB = (EPI == kEpiSwiglu) ? 2 : 1;
@@ -72,20 +77,120 @@ __global__ __launch_bounds__(256) void llama_gemm_kernel(const LlamaGemmArgs a) 
   const int part = (EPI == kEpiQkvRope) ? blockIdx.x / tiles_per_part : 0;
   const int n0 = (blockIdx.x % tiles_per_part) * TN;
   const uint16_t *Bp[2] = {a.B[part], a.B[NB - 1]};
+  // wave (wm, wn): rows 16*wm.., columns 32*wn.. (two 16-column tiles)
+  const int wm = (wave & 1) * 16, wn = (wave >> 1) * 32;
+  const int nchunks = (a.K + TK - 1) / TK;
+
+  // Latency, not arithmetic, bounds these small GEMMs: every dependent
+  // memory round trip of a workgroup is on the critical path.  So the
+  // epilogue's inputs are loaded first, the first two K chunks are in flight
+  // together with the RMSNorm row loads, and the K loop keeps two chunks in
+  // flight (register slots 0 and 1; chunk j lives in slot j % 2).
+  //
+  // staging: A chunk [32 rows][128 k] = two 8-element runs per thread;
+  // B chunk [128 k][64 n] = four k rows (two pairs) x one 8-column run.
+  // fetch() only issues loads (raw, from clamped addresses); the zero fill,
+  // the RMSNorm scaling and the B transpose happen in commit().
+  // B lanes: 32 consecutive lanes take 32 consecutive k pairs of one 8-column
+  // group, so each transposed 4-byte LDS write of a wave covers consecutive
+  // words (with the column group varying fastest, the rows 8 apart would all
+  // fall in one bank: an 8-way conflict on every write).
+  const int arow = tid >> 3, akk = (tid & 7) * 8;
+  const int bkp = (tid & 31) * 2, bng = (tid >> 5) * 8;
+  u32x4 sa[2][2], sb[2][NB][4];
+  f32x4 sg[2][2][2];  // gamma of this thread's two A runs (RMSNorm prologue)
+  uint32_t okbits[2] = {0u, 0u};
+  auto fetch = [&](auto slot, int chunk) {
+    constexpr int S = decltype(slot)::value;
+    const int k0 = min(chunk, nchunks - 1) * TK;
+    const int row = m0 + arow;
+    // K is a multiple of 64: the last chunk may hold only its first half,
+    // the second half is zero-filled (and multiplies to zero).
+    const int rowc = min(row, a.M - 1);
+    uint32_t ok = 0;
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const int kc = min(k0 + 64 * h, a.K - 64);
+      sa[S][h] = load16(a.A + (size_t)rowc * a.K + kc + akk).u;
+      if (PRO == kProRmsnorm) {
+        sg[S][h][0] = *reinterpret_cast<const f32x4 *>(a.gamma + kc + akk);
+        sg[S][h][1] = *reinterpret_cast<const f32x4 *>(a.gamma + kc + akk + 4);
+      }
+      ok |= (uint32_t)(row < a.M && k0 + 64 * h < a.K) << h;
+    }
+#pragma unroll
+    for (int b = 0; b < NB; ++b)
+#pragma unroll
+      for (int h = 0; h < 4; ++h) {
+        const int k = k0 + bkp + (h & 1) + 64 * (h >> 1);
+        sb[S][b][h] = load16(Bp[b] + (size_t)min(k, a.K - 1) * a.Npart + n0 + bng).u;
+        ok |= (uint32_t)(k < a.K) << (2 + 4 * b + h);
+      }
+    okbits[S] = ok;
+  };
+  auto commit = [&](auto slot, int buf) {
+    constexpr int S = decltype(slot)::value;
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      u32x4 v = masked(sa[S][h], (okbits[S] >> h) & 1u);
+      if (PRO == kProRmsnorm) {
+        const float inv = inv_rms[arow];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const float ylo = (bf_lo(v[j]) * inv) * sg[S][h][j >> 1][(2 * j) & 3];
+          const float yhi = (bf_hi(v[j]) * inv) * sg[S][h][j >> 1][(2 * j + 1) & 3];
+          v[j] = (uint32_t)f32_to_bf16(ylo) | ((uint32_t)f32_to_bf16(yhi) << 16);
+        }
+      }
+      *reinterpret_cast<u32x4 *>(&As[buf][arow * LDA + akk + 64 * h]) = v;
+    }
+#pragma unroll
+    for (int b = 0; b < NB; ++b) {
+      u32x4 m[4];
+#pragma unroll
+      for (int h = 0; h < 4; ++h) m[h] = masked(sb[S][b][h], (okbits[S] >> (2 + 4 * b + h)) & 1u);
+#pragma unroll
+      for (int hp = 0; hp < 2; ++hp)
+#pragma unroll
+        for (int j = 0; j < 8; ++j)
+          *reinterpret_cast<uint32_t *>(&Bs[buf][b][(bng + j) * LDA + bkp + 64 * hp]) =
+              pair_word(m[2 * hp], m[2 * hp + 1], j);
+    }
+  };
+
+  // ---- epilogue inputs (cos/sin or the residual), from clamped addresses
+  float ex0[2][4], ex1[2][4];
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const int n = n0 + wn + 16 * j + r;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int mc = min(m0 + wm + 4 * q + e, a.M - 1);
+      ex0[j][e] = ex1[j][e] = 0.0f;
+      if (EPI == kEpiQkvRope) {
+        const int t = (n % a.Dh) >> 1;
+        ex0[j][e] = a.cos_t[mc * (a.Dh / 2) + t];
+        ex1[j][e] = a.sin_t[mc * (a.Dh / 2) + t];
+      } else if (EPI == kEpiResidual) {
+        ex0[j][e] = bf16_to_f32(a.res[(size_t)mc * a.Npart + n]);
+      }
+    }
+  }
+  fetch(Slot<0>{}, 0);
+  fetch(Slot<1>{}, 1);
 
   if (PRO == kProRmsnorm) {
     // inverse RMS of the tile's rows, wave w owning rows RPW*w ..: all of a
-    // wave's row loads are issued before any of them is reduced.
+    // wave's row loads are issued before any of them is reduced; rows past M
+    // read row M-1 (their outputs are never stored).
     float s[RPW];
 #pragma unroll
     for (int rr = 0; rr < RPW; ++rr) s[rr] = 0.0f;
     for (int k = lane * 8; k < a.K; k += 512) {
       u32x4 v[RPW];
 #pragma unroll
-      for (int rr = 0; rr < RPW; ++rr) {
-        const int row = m0 + wave * RPW + rr;
-        v[rr] = row < a.M ? load16(a.A + (size_t)row * a.K + k).u : u32x4{0u, 0u, 0u, 0u};
-      }
+      for (int rr = 0; rr < RPW; ++rr)
+        v[rr] = load16(a.A + (size_t)min(m0 + wave * RPW + rr, a.M - 1) * a.K + k).u;
 #pragma unroll
       for (int rr = 0; rr < RPW; ++rr) s[rr] += sumsq8(v[rr]);
     }
@@ -102,86 +207,43 @@ __global__ __launch_bounds__(256) void llama_gemm_kernel(const LlamaGemmArgs a) 
     __syncthreads();
   }
 
-  // staging: A chunk [32 rows][128 k] = two 8-element runs per thread;
-  // B chunk [128 k][64 n] = four k rows (two pairs) x one 8-column run.
-  const int arow = tid >> 3, akk = (tid & 7) * 8;
-  const int bkp = (tid >> 3) * 2, bng = (tid & 7) * 8;
-  u32x4 sa[2], sb[NB][4];
-  auto fetch = [&](int k0) {
-    const int row = m0 + arow;
-    // K is a multiple of 64: the last chunk may hold only its first half,
-    // the second half is zero-filled (and multiplies to zero).
-    // (loads from clamped addresses, masked by selects: see masked())
-    const int rowc = min(row, a.M - 1);
-#pragma unroll
-    for (int h = 0; h < 2; ++h) {
-      const bool ok = row < a.M && k0 + 64 * h < a.K;
-      const int kc = min(k0 + 64 * h, a.K - 64);
-      sa[h] = masked(load16(a.A + (size_t)rowc * a.K + kc + akk).u, ok);
-    }
-#pragma unroll
-    for (int b = 0; b < NB; ++b)
-#pragma unroll
-      for (int h = 0; h < 4; ++h) {
-        const int k = k0 + bkp + (h & 1) + 64 * (h >> 1);
-        sb[b][h] = masked(load16(Bp[b] + (size_t)min(k, a.K - 1) * a.Npart + n0 + bng).u,
-                          k < a.K);
-      }
-  };
-  auto commit = [&](int buf, int k0) {
-#pragma unroll
-    for (int h = 0; h < 2; ++h) {
-      u32x4 v = sa[h];
-      const int kb = k0 + akk + 64 * h;
-      if (PRO == kProRmsnorm && kb < a.K) {
-        const float inv = inv_rms[arow];
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const float ylo = (bf_lo(v[j]) * inv) * a.gamma[kb + 2 * j];
-          const float yhi = (bf_hi(v[j]) * inv) * a.gamma[kb + 2 * j + 1];
-          v[j] = (uint32_t)f32_to_bf16(ylo) | ((uint32_t)f32_to_bf16(yhi) << 16);
-        }
-      }
-      *reinterpret_cast<u32x4 *>(&As[buf][arow * LDA + akk + 64 * h]) = v;
-    }
-#pragma unroll
-    for (int b = 0; b < NB; ++b)
-#pragma unroll
-      for (int hp = 0; hp < 2; ++hp)
-#pragma unroll
-        for (int j = 0; j < 8; ++j)
-          *reinterpret_cast<uint32_t *>(&Bs[buf][b][(bng + j) * LDA + bkp + 64 * hp]) =
-              pair_word(sb[b][2 * hp], sb[b][2 * hp + 1], j);
-  };
-
   f32x4 acc[NB][2];
 #pragma unroll
   for (int b = 0; b < NB; ++b)
 #pragma unroll
     for (int j = 0; j < 2; ++j) acc[b][j] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-  // wave (wm, wn): rows 16*wm.., columns 32*wn.. (two 16-column tiles)
-  const int wm = (wave & 1) * 16, wn = (wave >> 1) * 32;
-  const int nchunks = (a.K + TK - 1) / TK;
-  fetch(0);
-  commit(0, 0);
+  commit(Slot<0>{}, 0);
   __syncthreads();
-  for (int c = 0; c < nchunks; ++c) {
-    if (c + 1 < nchunks) fetch((c + 1) * TK);
-    const int buf = c & 1;
+  // Iteration c: chunk c is in LDS buffer c % 2 and chunk c+1 in register
+  // slot (c+1) % 2.  Fetch chunk c+2 into slot c % 2, multiply chunk c,
+  // commit chunk c+1, barrier.  Fetch and commit are unconditional (past the
+  // end they repeat the last chunk into the idle buffer, which is never
+  // read): with a condition on either, the compiler's wait analysis would
+  // drain every outstanding load at the loop head.  Unrolled by two so that
+  // the register slots are compile-time.
+  auto iteration = [&](auto slot, int c) {
+    constexpr int S = decltype(slot)::value;  // = c % 2
+    fetch(slot, c + 2);
+    if (c < nchunks) {
 #pragma unroll
-    for (int ks = 0; ks < TK / 32; ++ks) {
-      const Frag16 af = load16(&As[buf][(wm + r) * LDA + 32 * ks + 8 * q]);
+      for (int ks = 0; ks < TK / 32; ++ks) {
+        const Frag16 af = load16(&As[S][(wm + r) * LDA + 32 * ks + 8 * q]);
 #pragma unroll
-      for (int b = 0; b < NB; ++b)
+        for (int b = 0; b < NB; ++b)
 #pragma unroll
-        for (int j = 0; j < 2; ++j) {
-          const Frag16 bf = load16(&Bs[buf][b][(wn + 16 * j + r) * LDA + 32 * ks + 8 * q]);
-          MfmaBF16::mma(acc[b][j], af, bf);
-        }
+          for (int j = 0; j < 2; ++j) {
+            const Frag16 bf = load16(&Bs[S][b][(wn + 16 * j + r) * LDA + 32 * ks + 8 * q]);
+            MfmaBF16::mma(acc[b][j], af, bf);
+          }
+      }
     }
-    if (c + 1 < nchunks) commit(buf ^ 1, (c + 1) * TK);
+    commit(Slot<1 - S>{}, 1 - S);
     __syncthreads();
+  };
+  for (int c = 0; c < nchunks; c += 2) {
+    iteration(Slot<0>{}, c);
+    iteration(Slot<1>{}, c + 1);
   }
 
   // ---- epilogues: element (row m, column n) = acc[.][j][e]
@@ -194,16 +256,14 @@ __global__ __launch_bounds__(256) void llama_gemm_kernel(const LlamaGemmArgs a) 
       const float v = acc[0][j][e];
       float y;
       if (EPI == kEpiQkvRope) {
-        // RoPE pairs (2t, 2t+1) sit in adjacent lanes (columns r, r^1).
+        // RoPE pairs (2t, 2t+1) sit in adjacent lanes (columns r, r^1); the
+        // V part (part 2) is not rotated.
         const float partner = __shfl_xor(v, 1);
-        y = v;
-        if (part < 2 && m < a.M) {
-          const int t = (n % a.Dh) >> 1;
-          const float c = a.cos_t[m * (a.Dh / 2) + t], s = a.sin_t[m * (a.Dh / 2) + t];
-          y = (n & 1) ? (partner * s + v * c) : (v * c - partner * s);
-        }
+        const float c = ex0[j][e], s = ex1[j][e];
+        const float rot = (n & 1) ? (partner * s + v * c) : (v * c - partner * s);
+        y = part < 2 ? rot : v;
       } else if (EPI == kEpiResidual) {
-        y = m < a.M ? bf16_to_f32(a.res[(size_t)m * a.Npart + n]) + v : 0.0f;
+        y = ex0[j][e] + v;
       } else {
         y = silu(v) * acc[NB - 1][j][e];
       }
@@ -213,9 +273,20 @@ __global__ __launch_bounds__(256) void llama_gemm_kernel(const LlamaGemmArgs a) 
 }
 
 // Causal attention, head dimension 64.
+//
+// Layout.  A wave owns 16 queries.  Scores are computed transposed,
+// S^T = K Q^T (the K block is the MFMA's A operand, the queries its B
+// operand), so lane (r, q) holds query r's scores for keys 4q..4q+3 of each
+// 16-key column block: the online-softmax row statistics of query r live in
+// lanes r, r+16, r+32, r+48 (two cross-lane steps), and the probabilities
+// are already in the B-operand layout of O^T = V^T P^T.  An MFMA pairs the
+// k slots of its two operands by position, and any assignment of keys to
+// slots gives the same sum, so lane (r, q)'s eight slots of a 32-key step
+// are its own keys {4q..4q+3, 16+4q..16+4q+3}, and the V^T operand is read
+// in that same key order (two 8-byte LDS reads).  P never goes through LDS.
 constexpr int AQ = 64;          // queries per workgroup (4 waves x 16)
 constexpr int AK = 64;          // keys per block
-constexpr int LDK = 64 + 16;  // LDS row stride of K rows, V^T rows, P rows (elements): 160 bytes
+constexpr int LDK = 64 + 16;  // LDS row stride of K rows and V^T rows (elements): 160 bytes
 
 __global__ __launch_bounds__(256) void llama_attention_kernel(const uint16_t *__restrict__ Q,
                                                               const uint16_t *__restrict__ K,
@@ -223,149 +294,150 @@ __global__ __launch_bounds__(256) void llama_attention_kernel(const uint16_t *__
                                                               uint16_t *__restrict__ O, int S,
                                                               int H, float scale) {
   constexpr int DH = 64;
+  constexpr float kLog2e = 1.4426950408889634f;
   __shared__ __attribute__((aligned(16))) uint16_t Ks[2][AK * LDK];   // [key][d]
   __shared__ __attribute__((aligned(16))) uint16_t Vt[2][DH * LDK];   // [d][key]
-  __shared__ __attribute__((aligned(16))) uint16_t Ps[4][16 * LDK];   // per wave [row][key]
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int r = lane & 15, q = lane >> 4;
   const int q0 = blockIdx.x * AQ, h = blockIdx.y;
   const int D = H * DH;
   const int i0 = q0 + wave * 16;  // this wave's first query row
+  const int row = i0 + r;         // this lane's query
 
   // query rows past S read row S-1: their outputs are never stored
-  Frag16 qa[2];
+  Frag16 qb[2];
 #pragma unroll
   for (int ks = 0; ks < 2; ++ks)
-    qa[ks] = load16(Q + (size_t)min(i0 + r, S - 1) * D + h * DH + 32 * ks + 8 * q);
+    qb[ks] = load16(Q + (size_t)min(row, S - 1) * D + h * DH + 32 * ks + 8 * q);
 
   // staging: K block [64 keys][64 d] = 2 runs of 8 per thread; V block
-  // transposed: two keys x 8 d per thread.
-  const int kr = tid >> 2, kd = (tid & 3) * 16;       // K: key kr, d kd..kd+15
-  const int vk = (tid >> 3) * 2, vd = (tid & 7) * 8;  // V: keys vk, vk+1; d vd..vd+7
+  // transposed: two keys x 8 d per thread.  Raw loads in fetch(), the zero
+  // fill of keys past S in commit(), so the loads overlap the block's MFMAs.
+  // V lanes: 32 consecutive lanes take 32 consecutive key pairs of one
+  // 8-wide d group, so the transposed 4-byte LDS writes of a wave hit
+  // consecutive words instead of one bank.
+  const int kr = tid >> 2, kd = (tid & 3) * 16;        // K: key kr, d kd..kd+15
+  const int vk = (tid & 31) * 2, vd = (tid >> 5) * 8;  // V: keys vk, vk+1; d vd..vd+7
   u32x4 sk[2], sv[2];
+  uint32_t okbits = 0;
   auto fetch = [&](int kb) {
     const int key = kb + kr;
 #pragma unroll
     for (int s2 = 0; s2 < 2; ++s2)
-      sk[s2] = masked(load16(K + (size_t)min(key, S - 1) * D + h * DH + kd + 8 * s2).u, key < S);
+      sk[s2] = load16(K + (size_t)min(key, S - 1) * D + h * DH + kd + 8 * s2).u;
+    okbits = (uint32_t)(key < S);
 #pragma unroll
     for (int s2 = 0; s2 < 2; ++s2) {
       const int vkey = kb + vk + s2;
-      sv[s2] = masked(load16(V + (size_t)min(vkey, S - 1) * D + h * DH + vd).u, vkey < S);
+      sv[s2] = load16(V + (size_t)min(vkey, S - 1) * D + h * DH + vd).u;
+      okbits |= (uint32_t)(vkey < S) << (1 + s2);
     }
   };
   auto commit = [&](int buf) {
 #pragma unroll
     for (int s2 = 0; s2 < 2; ++s2)
-      *reinterpret_cast<u32x4 *>(&Ks[buf][kr * LDK + kd + 8 * s2]) = sk[s2];
+      *reinterpret_cast<u32x4 *>(&Ks[buf][kr * LDK + kd + 8 * s2]) = masked(sk[s2], okbits & 1u);
+    const u32x4 v0 = masked(sv[0], (okbits >> 1) & 1u), v1 = masked(sv[1], (okbits >> 2) & 1u);
 #pragma unroll
     for (int j = 0; j < 8; ++j)
-      *reinterpret_cast<uint32_t *>(&Vt[buf][(vd + j) * LDK + vk]) = pair_word(sv[0], sv[1], j);
+      *reinterpret_cast<uint32_t *>(&Vt[buf][(vd + j) * LDK + vk]) = pair_word(v0, v1, j);
   };
 
-  float mrow[4], lrow[4];
-  f32x4 o[4];
-#pragma unroll
-  for (int e = 0; e < 4; ++e) {
-    mrow[e] = -INFINITY;
-    lrow[e] = 0.0f;
-  }
+  // online softmax state of query `row`, in the log2 domain
+  float m2 = -INFINITY, l = 0.0f;
+  f32x4 o[4];  // o[dt][e] = O[row][16*dt + 4q + e] (unnormalised)
 #pragma unroll
   for (int dt = 0; dt < 4; ++dt) o[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
+  const float sc2 = scale * kLog2e;
 
   const int kend = min(q0 + AQ, S);  // keys beyond the block's last query are masked for all
   const int nblocks = (kend + AK - 1) / AK;
   fetch(0);
   commit(0);
   __syncthreads();
+  // fetch and commit are unconditional (the last round refetches the last
+  // block into the idle buffer): with a condition on either, the compiler's
+  // wait analysis drains every outstanding load at the loop head.
   for (int blk = 0; blk < nblocks; ++blk) {
     const int kb = blk * AK;
-    if (blk + 1 < nblocks) fetch(kb + AK);
+    fetch(min(blk + 1, nblocks - 1) * AK);
     const int buf = blk & 1;
-    const bool active = kb <= i0 + 15;  // some key of the block is visible to this wave
-    if (active) {
-      f32x4 s[4];
+    if (kb <= i0 + 15) {  // some key of the block is visible to this wave (uniform)
+      f32x4 s[4];         // s[ct][e]: score of key kb + 16ct + 4q + e
 #pragma unroll
       for (int ct = 0; ct < 4; ++ct) {
         s[ct] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int ks = 0; ks < 2; ++ks) {
           const Frag16 kf = load16(&Ks[buf][(16 * ct + r) * LDK + 32 * ks + 8 * q]);
-          MfmaBF16::mma(s[ct], qa[ks], kf);
+          MfmaBF16::mma(s[ct], kf, qb[ks]);
         }
       }
-      float mx[4];
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const int row = i0 + 4 * q + e;
-        mx[e] = -INFINITY;
-#pragma unroll
-        for (int ct = 0; ct < 4; ++ct) {
-          const int key = kb + 16 * ct + r;
-          const float v = (key <= row && key < S) ? s[ct][e] * scale : -INFINITY;
-          s[ct][e] = v;
-          mx[e] = fmaxf(mx[e], v);
-        }
-      }
-#pragma unroll
-      for (int off = 1; off < 16; off <<= 1)
-#pragma unroll
-        for (int e = 0; e < 4; ++e) mx[e] = fmaxf(mx[e], __shfl_xor(mx[e], off));
-      float corr[4], sum[4];
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const float mnew = fmaxf(mrow[e], mx[e]);
-        corr[e] = (mnew == -INFINITY) ? 1.0f : expf(mrow[e] - mnew);
-        sum[e] = 0.0f;
-#pragma unroll
-        for (int ct = 0; ct < 4; ++ct) {
-          const float p = (mnew == -INFINITY) ? 0.0f : expf(s[ct][e] - mnew);
-          s[ct][e] = p;
-          sum[e] += p;
-        }
-        mrow[e] = mnew;
-      }
-#pragma unroll
-      for (int off = 1; off < 16; off <<= 1)
-#pragma unroll
-        for (int e = 0; e < 4; ++e) sum[e] += __shfl_xor(sum[e], off);
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        lrow[e] = lrow[e] * corr[e] + sum[e];
-#pragma unroll
-        for (int dt = 0; dt < 4; ++dt) o[dt][e] *= corr[e];
-      }
-      // P (accumulator layout) -> this wave's LDS rows -> A-operand layout.
-      // Only this wave touches Ps[wave]; LDS operations of a wave complete in
-      // order, and the explicit wait makes the stores visible to the loads.
+      float mx = -INFINITY;
 #pragma unroll
       for (int ct = 0; ct < 4; ++ct)
 #pragma unroll
-        for (int e = 0; e < 4; ++e)
-          Ps[wave][(4 * q + e) * LDK + 16 * ct + r] = f32_to_bf16(s[ct][e]);
-      __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0)
-      __builtin_amdgcn_wave_barrier();
+        for (int e = 0; e < 4; ++e) {
+          const int key = kb + 16 * ct + 4 * q + e;
+          const float v = (key <= row && key < S) ? s[ct][e] * sc2 : -INFINITY;
+          s[ct][e] = v;
+          mx = fmaxf(mx, v);
+        }
+      mx = fmaxf(mx, __shfl_xor(mx, 16));
+      mx = fmaxf(mx, __shfl_xor(mx, 32));
+      const float mnew = fmaxf(m2, mx);
+      const float corr = (mnew == -INFINITY) ? 1.0f : __builtin_amdgcn_exp2f(m2 - mnew);
+      float sum = 0.0f;
+#pragma unroll
+      for (int ct = 0; ct < 4; ++ct)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const float p = (mnew == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(s[ct][e] - mnew);
+          s[ct][e] = p;
+          sum += p;
+        }
+      sum += __shfl_xor(sum, 16);
+      sum += __shfl_xor(sum, 32);
+      l = l * corr + sum;
+      m2 = mnew;
+#pragma unroll
+      for (int dt = 0; dt < 4; ++dt) o[dt] *= corr;
 #pragma unroll
       for (int ks = 0; ks < 2; ++ks) {
-        const Frag16 pa = load16(&Ps[wave][r * LDK + 32 * ks + 8 * q]);
+        // B operand: P^T, slots 0-3 = keys 32ks + 4q + e, slots 4-7 = 32ks + 16 + 4q + e
+        Frag16 pb;
+#pragma unroll
+        for (int e2 = 0; e2 < 2; ++e2) {
+          pb.u[e2] = (uint32_t)f32_to_bf16(s[2 * ks][2 * e2]) |
+                     ((uint32_t)f32_to_bf16(s[2 * ks][2 * e2 + 1]) << 16);
+          pb.u[2 + e2] = (uint32_t)f32_to_bf16(s[2 * ks + 1][2 * e2]) |
+                         ((uint32_t)f32_to_bf16(s[2 * ks + 1][2 * e2 + 1]) << 16);
+        }
 #pragma unroll
         for (int dt = 0; dt < 4; ++dt) {
-          const Frag16 vf = load16(&Vt[buf][(16 * dt + r) * LDK + 32 * ks + 8 * q]);
-          MfmaBF16::mma(o[dt], pa, vf);
+          // A operand: V^T rows d = 16dt + r, the same keys in the same slots
+          const uint16_t *vrow = &Vt[buf][(16 * dt + r) * LDK + 32 * ks + 4 * q];
+          const uint2 lo = *reinterpret_cast<const uint2 *>(vrow);
+          const uint2 hi = *reinterpret_cast<const uint2 *>(vrow + 16);
+          Frag16 va;
+          va.u = u32x4{lo.x, lo.y, hi.x, hi.y};
+          MfmaBF16::mma(o[dt], va, pb);
         }
       }
     }
-    if (blk + 1 < nblocks) commit(buf ^ 1);
+    commit(buf ^ 1);
     __syncthreads();
   }
+  if (row < S) {
+    const float inv = 1.0f / l;
 #pragma unroll
-  for (int e = 0; e < 4; ++e) {
-    const int row = i0 + 4 * q + e;
-    if (row >= S) continue;
-    const float inv = 1.0f / lrow[e];
-#pragma unroll
-    for (int dt = 0; dt < 4; ++dt)
-      O[(size_t)row * D + h * DH + 16 * dt + r] = f32_to_bf16(o[dt][e] * inv);
+    for (int dt = 0; dt < 4; ++dt) {
+      const uint32_t lo = (uint32_t)f32_to_bf16(o[dt][0] * inv) |
+                          ((uint32_t)f32_to_bf16(o[dt][1] * inv) << 16);
+      const uint32_t hi = (uint32_t)f32_to_bf16(o[dt][2] * inv) |
+                          ((uint32_t)f32_to_bf16(o[dt][3] * inv) << 16);
+      *reinterpret_cast<uint2 *>(O + (size_t)row * D + h * DH + 16 * dt + 4 * q) = make_uint2(lo, hi);
+    }
   }
 }
 
@@ -383,7 +455,11 @@ void plan_gemm(const char *name, Kern kern, const LlamaGemmArgs &a, int grid, in
   npu_launch_plan p = make_plan(name, grid, wg_per_cu(kern), grid, 16);
   p.load_phases = norm ? 2 : 1;
   p.tile_macs = (double)TM * TN * nb * kchunks * TK;
-  p.tile_valu = (norm ? 3.0 * TM * a.K : 0.0) + (double)TM * TN * nb * (epi == kEpiResidual ? 3 : 8);
+  // counted per wave: 225 + 98 per chunk (residual), 1050 + 160 per chunk
+  // (RMSNorm + RoPE), 1100 + 260 per chunk (RMSNorm + SwiGLU, two B operands)
+  const double fixed = epi == kEpiResidual ? 225 : (epi == kEpiQkvRope ? 1050 : 1100);
+  const double per = epi == kEpiResidual ? 98 : (epi == kEpiQkvRope ? 160 : 260);
+  p.tile_valu = 4.0 * (fixed + per * kchunks);
   p.tile_lds_bytes = 2.0 * ((double)TM + nb * TN) * kchunks * TK * 2;   // written once, read once
   p.tile_load_bytes = ((double)TM + nb * TN) * kchunks * TK * 2 + (norm ? 4.0 * a.K : 0.0);
   p.tile_store_bytes = (double)TM * TN * 2;
@@ -429,8 +505,8 @@ hipError_t launch_llama_attention(const uint16_t *Q, const uint16_t *K, const ui
                                   wg_per_cu(llama_attention_kernel), grid.x * grid.y, 16);
     p.load_phases = 1;
     p.tile_macs = kblocks * 2.0 * AQ * AK * 64;
-    p.tile_valu = kblocks * (double)AQ * AK * 12;
-    p.tile_lds_bytes = kblocks * (2.0 * 2 * AK * 64 * 2 + 2.0 * AQ * AK * 2 + 4.0 * AQ * 64 * 2);
+    p.tile_valu = 4.0 * (150.0 + 335.0 * kblocks);  // counted: 1659 per wave at 4.5 blocks
+    p.tile_lds_bytes = kblocks * (2.0 * 2 * AK * 64 * 2 + 4.0 * 2 * AK * 64 * 2);
     p.tile_load_bytes = kblocks * 2.0 * AK * 64 * 2 + AQ * 64 * 2.0;
     p.tile_store_bytes = AQ * 64 * 2.0;
     p.hbm_bytes = 4.0 * S * H * 64 * 2;  // Q, K, V in, O out

@@ -189,7 +189,7 @@ hipError_t launch_qb(const QBottleneckArgs &a, hipStream_t s) {
                                   wg_per_cu(qbottleneck_kernel<C, M1>), grid.x * grid.y, 8);
     p.load_phases = 1;  // halo and conv1/conv2 filters together; conv3's during conv1
     p.tile_macs = (double)HPB * 16 * M1 * C + (double)OP * M1 * 9 * M1 + (double)OP * C * M1;
-    p.tile_valu = 6.0 * (HPB * 16.0 * M1 + OP * M1 + OP * C);     // requant, clamp, pack
+    p.tile_valu = 4.0 * (1280.0 * (0.25 + 0.75 * C / 256.0));  // counted per wave: 1280 at C = 256
     p.tile_lds_bytes = HP * (C + 32.0) + 4.0 * HPB * (C / 64) * 1024 + HPB * 16.0 * M1 +
                        4.0 * 4 * 9 * 1024 + OP * M1 + 4.0 * 4 * 1024 + 3.0 * OP * C;
     p.tile_load_bytes = HP * (double)C + 4.0 * 1024 * (C / 64 + 9 + FB3) + 4.0 * 4 * (2 + 2 * FB3) * 64;

@@ -12,11 +12,14 @@ namespace npu {
 
 // Machine constants.  Data sheet: 256 CUs at 2.4 GHz; dense MFMA per CU per
 // clock 128 f32, 2048 bf16 and 4096 i8 multiply-adds (157.3 / 2516.6 /
-// 5033.2 T op/s); 4 SIMDs x 16 lanes of VALU.  Measured on an MI355X with
-// npu_calibrate (calib/calibrate.hip) and the LDS read probe: 4.31 TB/s for
-// a 1 GiB device copy, 51 bytes/clock/CU read from L2, 1.2 us dependent-load
-// latency with every CU loading (0.33 us idle), 186 bytes/clock/CU of
-// conflict-free ds_read_b128 (four waves, 22 clocks per wave instruction).
+// 5033.2 T op/s); 4 SIMDs of 16 lanes, so a wave64 vector instruction takes
+// 4 clocks and a CU issues one per clock.  Measured on an MI355X with
+// npu_calibrate (calib/calibrate.hip) and an LDS read probe: 4.3 TB/s for a
+// 1 GiB device copy, 51 bytes/clock/CU read from L2, 1.2 us dependent-load
+// latency with every CU loading (0.31 us idle; 0.13 us from L2), 186
+// bytes/clock/CU of conflict-free ds_read_b128 (four waves, 22 clocks per
+// wave instruction), 1.58 us per kernel in a captured graph of empty
+// kernels.
 void gpu_params_mi355x(npu_gpu_params *p) {
   p->cus = 256;
   p->reserved = 0;
@@ -24,12 +27,12 @@ void gpu_params_mi355x(npu_gpu_params *p) {
   p->hbm_gbs = 4312.0;
   p->l2_bytes_per_clk_cu = 51.0;
   p->lds_bytes_per_clk_cu = 186.0;
-  p->valu_lanes_per_clk_cu = 64.0;
+  p->valu_instr_per_clk_cu = 1.0;
   p->mfma_macs_per_clk_cu[0] = 128.0;
   p->mfma_macs_per_clk_cu[1] = 2048.0;
   p->mfma_macs_per_clk_cu[2] = 4096.0;
   p->mem_latency_us = 1.2;
-  p->launch_us = 1.0;
+  p->launch_us = 1.58;
 }
 
 bool predict_launch(const npu_launch_plan &pl, const npu_gpu_params &g, npu_launch_cost *out) {
@@ -39,8 +42,8 @@ bool predict_launch(const npu_launch_plan &pl, const npu_gpu_params &g, npu_laun
   // compute streams of one tile, in clocks of one CU
   const double c_mfma = pl.tile_macs / g.mfma_macs_per_clk_cu[mi];
   const double c_lds = pl.tile_lds_bytes / g.lds_bytes_per_clk_cu;
-  const double c_valu = pl.tile_valu / g.valu_lanes_per_clk_cu;
-  const double c_comp = std::max(c_mfma, std::max(c_lds, c_valu));
+  const double c_valu = pl.tile_valu / g.valu_instr_per_clk_cu;
+  const double c_comp = std::max(c_lds, c_mfma + c_valu);
   const double c_xfer = (pl.tile_load_bytes + pl.tile_store_bytes) / g.l2_bytes_per_clk_cu;
   const double c_lat = pl.load_phases * g.mem_latency_us * clk_per_us;
   const double c_serial = c_lat + c_xfer + c_comp;
@@ -66,10 +69,10 @@ bool predict_launch(const npu_launch_plan &pl, const npu_gpu_params &g, npu_laun
     out->bound = NPU_BOUND_LATENCY;
   else if (c_xfer >= c_comp)
     out->bound = NPU_BOUND_L2;
-  else if (c_comp == c_mfma)
-    out->bound = NPU_BOUND_MFMA;
-  else if (c_comp == c_lds)
+  else if (c_lds >= c_mfma + c_valu)
     out->bound = NPU_BOUND_LDS;
+  else if (c_mfma >= c_valu)
+    out->bound = NPU_BOUND_MFMA;
   else
     out->bound = NPU_BOUND_VALU;
   out->reserved = 0;

@@ -72,7 +72,7 @@ class GpuParams(C.Structure):
     _fields_ = [
         ("cus", C.c_int32), ("reserved", C.c_int32), ("clock_ghz", C.c_double),
         ("hbm_gbs", C.c_double), ("l2_bytes_per_clk_cu", C.c_double),
-        ("lds_bytes_per_clk_cu", C.c_double), ("valu_lanes_per_clk_cu", C.c_double),
+        ("lds_bytes_per_clk_cu", C.c_double), ("valu_instr_per_clk_cu", C.c_double),
         ("mfma_macs_per_clk_cu", C.c_double * 3), ("mem_latency_us", C.c_double),
         ("launch_us", C.c_double),
     ]
