@@ -205,3 +205,66 @@ def test_bad_ids_raise():
     cm.g.op_id.append(999)
     with pytest.raises(ValueError):
         cm.op_macs(len(cm.g.op_id) - 1)
+
+
+# ---- MI355X launch model (npu_cm_predict_launch) -------------------------
+def _plan(**kw):
+    from npu_amd._lib import NpuLaunchPlan
+    p = NpuLaunchPlan()
+    p.kernel = b"test"
+    p.grid, p.wg_per_cu, p.tiles, p.load_phases, p.mfma_bits = 256, 1, 256, 0, 16
+    for k, v in kw.items():
+        setattr(p, k, v)
+    return p
+
+
+def test_launch_model_hbm_bound():
+    """A plan whose only cost is HBM bytes takes bytes / copy bandwidth."""
+    g = host.mi355x_gpu()
+    c = host.predict_launch(_plan(hbm_bytes=4.3e9), g)
+    assert host.BOUNDS[c.bound] == "hbm"
+    assert c.time_us == pytest.approx(4.3e9 / (g.hbm_gbs * 1e3))
+
+
+def test_launch_model_compute_streams():
+    """MFMA and vector-ALU issue add up on a SIMD; LDS is the other stream."""
+    g = host.mi355x_gpu()
+    clk = g.clock_ghz * 1e3
+    # 2048 bf16 MAC/clk/CU: 2048*1000 MACs = 1000 clocks of MFMA, plus 500 VALU instructions
+    c = host.predict_launch(_plan(tile_macs=2048.0 * 1000, tile_valu=500.0), g)
+    assert c.tile_compute_us == pytest.approx(1500 / clk)
+    assert host.BOUNDS[c.bound] == "mfma"
+    # LDS-bound: 186 B/clk/CU
+    c = host.predict_launch(_plan(tile_macs=2048.0 * 10, tile_lds_bytes=186.0 * 4000), g)
+    assert c.tile_compute_us == pytest.approx(4000 / clk) and host.BOUNDS[c.bound] == "lds"
+    # f32 is 16x slower per MAC than bf16
+    c32 = host.predict_launch(_plan(tile_macs=128.0 * 1000, mfma_bits=32), g)
+    assert c32.tile_compute_us == pytest.approx(1000 / clk)
+
+
+def test_launch_model_pipeline_and_occupancy():
+    """n tiles per CU: one dependent load per tile is hidden by a second
+    resident workgroup (the reference's pipelined tile formula per CU)."""
+    g = host.mi355x_gpu()
+    clk = g.clock_ghz * 1e3
+    base = dict(tiles=256 * 8, grid=256, tile_macs=2048.0 * 3000, load_phases=1)
+    one = host.predict_launch(_plan(wg_per_cu=1, **base), g)
+    two = host.predict_launch(_plan(wg_per_cu=2, grid=512, **{k: v for k, v in base.items() if k != "grid"}), g)
+    serial = g.mem_latency_us + 3000 / clk
+    assert one.tiles_per_cu == 8
+    assert one.cu_us == pytest.approx(g.mem_latency_us + 8 * serial)       # setup + 8 serial tiles
+    # two overlap their loads; then the MFMA stream itself (8 x 3000 clocks) binds
+    assert two.cu_us == pytest.approx(g.mem_latency_us + max(8 * 3000 / clk, 8 * serial / 2))
+    assert host.BOUNDS[one.bound] == "latency" and host.BOUNDS[two.bound] == "mfma"
+
+
+def test_launch_model_rejects_empty_plan():
+    with pytest.raises(ValueError):
+        host.predict_launch(_plan(grid=0))
+
+
+def test_block_prediction_adds_launch_cost():
+    g = host.mi355x_gpu()
+    plans = [_plan(hbm_bytes=1e6), _plan(hbm_bytes=2e6)]
+    total, parts = host.predict_block(plans, g)
+    assert total == pytest.approx(sum(c.time_us for _, c in parts) + 2 * g.launch_us)
