@@ -222,6 +222,7 @@ def main():
             p, pk = model_prediction(other)
             rl = other.roofline(s)
             blocks.append({"workload": other.name, "latency_us": round(s * 1e6, 3),
+                           "traffic": measured_traffic(other.name),
                            "graph_us": round(gs * 1e6, 3), "graph_matches_eager": same,
                            "bound": rl["bound"], "frac": round(rl["frac"], 4),
                            "graph_frac": round(other.roofline(gs)["frac"], 4),

@@ -1,8 +1,10 @@
 // calibrate.hip -- measures the machine constants the MI355X launch model
 // needs and that no data sheet gives: the cost of one launch in a stream of
-// back-to-back launches, the latency of a dependent global load (idle and
-// with every CU loading), the bandwidth of a plain HBM copy, the rate at
-// which one CU reads L2-resident data, and the shader clock.
+// back-to-back launches and inside a captured graph, the latency of a
+// dependent global load (idle and with every CU loading, from HBM and from
+// L2), the bandwidth of a plain HBM copy, the rate at which one CU reads
+// L2-resident data, the LDS read rate for the record strides the kernels
+// use, and the shader clock.
 //
 // Every kernel here is bounded: the pointer chases follow a single cycle over
 // an index array whose entries are all in range, with a fixed hop count; the
@@ -28,6 +30,8 @@
   } while (0)
 
 namespace {
+
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 
 constexpr int kStride = 64;  // int32 slots between chased entries (256 bytes)
 
@@ -73,6 +77,32 @@ __global__ void l2_read_kernel(const float4 *__restrict__ src, size_t n, int rep
 #pragma unroll
   for (int u = 0; u < 8; ++u) t += acc[u];
   if (t == 12345.f) out[blockIdx.x] = t;
+}
+
+// LDS read rate: 4 waves each issue `iters` x 8 ds_read_b128 in which lane
+// l reads 16 bytes at (l % 16) * rs + (l / 16) * 16 (16 consecutive records
+// of stride rs, one 16-byte column per lane group: the A-operand read of the
+// kernels).  Offsets vary with the iteration in steps of 8 KiB, which keeps
+// the bank mapping; all addresses stay below 64 KiB.
+__global__ void lds_read_kernel(int rs, int iters, unsigned long long *cyc) {
+  __shared__ __attribute__((aligned(16))) unsigned char lds[65536];
+  for (int i = threadIdx.x; i < 65536 / 16; i += blockDim.x)
+    reinterpret_cast<u32x4 *>(lds)[i] = u32x4{(unsigned)i, 1u, 2u, 3u};
+  __syncthreads();
+  const int l = threadIdx.x & 63;
+  const unsigned addr = (l % 16) * rs + (l / 16) * 16;  // <= 15 * 272 + 48
+  __syncthreads();
+  const unsigned long long t0 = clock64();
+  for (int it = 0; it < iters; ++it) {
+    u32x4 v[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u)
+      v[u] = *reinterpret_cast<const u32x4 *>(lds + addr + (it & 3) * 8192 + u * 2048);
+#pragma unroll
+    for (int u = 0; u < 8; ++u) asm volatile("" ::"v"(v[u]));
+  }
+  const unsigned long long t1 = clock64();
+  if (threadIdx.x == 0) cyc[0] = t1 - t0;
 }
 
 // Shader clock over the 100 MHz constant clock.
@@ -217,6 +247,22 @@ int main() {
     CK(hipFree(d));
   }
 
+  // LDS: clocks per ds_read_b128 wave instruction, four waves reading, for
+  // record strides of 16 mod 64 bytes (80, 144), 32 mod 64 (96, 160) and 128
+  const int strides[5] = {80, 96, 128, 144, 160};
+  double lds_clk[5];
+  unsigned long long *dcyc;
+  CK(hipMalloc(&dcyc, sizeof(unsigned long long)));
+  for (int i = 0; i < 5; ++i) {
+    const int iters = 200;
+    hipLaunchKernelGGL(lds_read_kernel, dim3(1), dim3(256), 0, 0, strides[i], iters, dcyc);
+    CK(hipDeviceSynchronize());
+    unsigned long long c = 0;
+    CK(hipMemcpy(&c, dcyc, sizeof c, hipMemcpyDeviceToHost));
+    lds_clk[i] = (double)c / (iters * 8);
+  }
+  CK(hipFree(dcyc));
+
   // HBM copy bandwidth, 1 GiB each way
   const size_t bytes = (size_t)1 << 30;
   float4 *src, *dst;
@@ -243,9 +289,12 @@ int main() {
 
   printf("{\"device\": \"%s\", \"cus\": %d, \"shader_clock_ghz\": %.3f, \"launch_us\": %.3f, "
          "\"launch_full_grid_us\": %.3f, \"graph_launch_us\": %.3f, \"graph_launch_full_grid_us\": %.3f, \"hbm_latency_us\": %.3f, \"hbm_latency_loaded_us\": %.3f, "
-         "\"l2_latency_us\": %.3f, \"l2_latency_loaded_us\": %.3f, \"hbm_copy_gbs\": %.1f, \"l2_read_bytes_per_clk_cu\": %.2f}\n",
+         "\"l2_latency_us\": %.3f, \"l2_latency_loaded_us\": %.3f, \"hbm_copy_gbs\": %.1f, \"l2_read_bytes_per_clk_cu\": %.2f, "
+         "\"lds_b128_clk_per_wave_instr\": {\"80\": %.1f, \"96\": %.1f, \"128\": %.1f, \"144\": %.1f, \"160\": %.1f}, "
+         "\"lds_bytes_per_clk_cu\": %.1f}\n",
          prop.gcnArchName, cus, ghz, t_launch, t_launch_full, t_graph, t_graph_full, lat_hbm, lat_loaded, lat_l2, lat_l2_loaded, copy_gbs,
-         l2_bytes_per_clk_cu);
+         l2_bytes_per_clk_cu, lds_clk[0], lds_clk[1], lds_clk[2], lds_clk[3], lds_clk[4],
+         4.0 * 1024 / lds_clk[4]);
   CK(hipFree(src));
   CK(hipFree(dst));
   CK(hipFree(dsink));
