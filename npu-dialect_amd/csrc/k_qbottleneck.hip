@@ -17,6 +17,7 @@
 // summation order gives the oracle's result bit for bit.
 #include "kernels.hpp"
 #include "npu_device.hpp"
+#include "persistent.hpp"
 #include "plans.hpp"
 
 namespace npu {
@@ -57,8 +58,14 @@ __global__ __launch_bounds__(256) void qbottleneck_kernel(
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int r = lane & 15, q = lane >> 4;
-  const int n = blockIdx.y;
-  const int ty0 = (blockIdx.x / tiles_w) * TH, tx0 = (blockIdx.x % tiles_w) * TW;
+  // Workgroups go round-robin to the 8 XCDs (linear id % 8), each with its
+  // own L2; remapping the linear id gives every XCD a contiguous range of
+  // tiles, so the halo rows neighbouring tiles share are fetched from HBM
+  // once instead of once per XCD.
+  const int nblk = gridDim.x * gridDim.y, lin = blockIdx.y * gridDim.x + blockIdx.x;
+  const int tile = nblk % kXcds == 0 ? (lin % kXcds) * (nblk / kXcds) + lin / kXcds : lin;
+  const int n = tile / gridDim.x, tt = tile - n * gridDim.x;
+  const int ty0 = (tt / tiles_w) * TH, tx0 = (tt % tiles_w) * TW;
 
   // ---- issue every global load the first two stages need at once: the x
   //      halo (clamped addresses, zero fill by select), and this wave's
