@@ -197,6 +197,51 @@ int32_t npu_pass_spatial(const npu_graph *g, const npu_hw_target *t, int32_t op,
 int32_t npu_pass_temporal(const npu_graph *g, const npu_hw_target *t, int32_t op,
                           npu_schedule_cost *cost, int64_t *tile_sizes, int32_t cap);
 
+/* ---- buffers after tiling: bufferize, SRAM plan, cost record -------------
+ * NPUBufferizePass's DMA insertion for one tile loop (BufferizePass.cpp:97-222),
+ * NPUSRAMAllocationPass's dual-end plan (SRAMAllocationPass.cpp:127-342) and
+ * NPUCostEvaluatePass's per-function record (CostEvaluatePass.cpp:57-168).
+ * On MI355X the SRAM is a CU's LDS and the plan a workgroup's LDS layout. */
+#define NPU_BUF_INPUT 0        /* copied in, read                          */
+#define NPU_BUF_OUTPUT 1       /* copied in, written, copied back          */
+#define NPU_BUF_INTERMEDIATE 2 /* lives only in SRAM                       */
+typedef struct npu_sram_buffer {
+  int32_t value;               /* graph value held, -1 for none           */
+  int32_t role;                /* NPU_BUF_*                               */
+  int64_t bytes;
+  int64_t first_use, last_use; /* program steps                           */
+  int32_t in_loop;             /* inside a tile loop: inputs get ping/pong */
+  int32_t double_buffered;     /* plan: ping/pong pair                    */
+  int64_t addr, addr_pong, prefetch_addr; /* plan: byte offsets, -1 none  */
+  int32_t spilled;             /* plan: did not fit, stays in DRAM        */
+  int32_t reserved;
+} npu_sram_buffer;
+typedef struct npu_sram_summary {
+  int64_t spilled, prefetched, prefetch_bytes, peak_bytes, free_after;
+} npu_sram_summary;
+/* Tile loop whose body holds ops[0..n_ops) (block order): one buffer per
+ * shaped operand defined outside the body, first-use order; bytes[v] (if
+ * bytes and v < n_bytes and bytes[v] > 0) replaces value v's tensor size.
+ * Returns the number of buffers (all written to out when cap allows). */
+int32_t npu_pass_bufferize(const npu_graph *g, const int32_t *ops, int32_t n_ops,
+                           const int64_t *bytes, int32_t n_bytes, npu_sram_buffer *out,
+                           int32_t cap);
+/* Plans bufs in place for an SRAM of sram_size bytes (summary may be NULL).
+ * Buffers are taken in first-use order, ties in array order. */
+int32_t npu_pass_sram_allocation(npu_sram_buffer *bufs, int32_t n, int64_t sram_size,
+                                 npu_sram_summary *summary);
+typedef struct npu_kernel_cost {
+  double flops, mem_bytes, arithmetic_intensity, time_sec, efficiency;
+  int32_t memory_bound, reserved;
+  int64_t dma_in_bytes, dma_out_bytes, matrix_cycles, dsp_cycles;
+  int64_t peak_sram_bytes, num_tile_iterations, num_linalg_ops, sram_budget;
+} npu_kernel_cost;
+/* The COST_JSON record of a function whose body is ops, its SRAM plan bufs,
+ * its tile loops running tile_iterations times. */
+int32_t npu_pass_cost_evaluate(const npu_graph *g, const npu_hw_target *t, const int32_t *ops,
+                               int32_t n_ops, const npu_sram_buffer *bufs, int32_t n_bufs,
+                               int64_t tile_iterations, npu_kernel_cost *out);
+
 /* ---- MI355X launch model ------------------------------------------------
  * Time of one kernel launch from its launch plan (npu_last_launch_plans,
  * npu_amd.h).  The reference's tile pipeline (evaluateConv2dTile /

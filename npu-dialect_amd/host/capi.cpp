@@ -6,6 +6,7 @@
 
 #include "../../include/npu_cost.h"
 #include "cost_model.hpp"
+#include "memory_plan.hpp"
 #include "passes.hpp"
 
 namespace npu {
@@ -151,6 +152,106 @@ int32_t npu_graph_add_op(npu_graph *g, int32_t kind, const int32_t *operands, in
 int32_t npu_graph_num_ops(const npu_graph *g) { return g ? (int32_t)g->g.ops.size() : -1; }
 
 const char *npu_host_last_error(void) { return g_err.c_str(); }
+
+namespace {
+npu::SramBuffer from_c(const npu_sram_buffer &c) {
+  npu::SramBuffer b;
+  b.value = c.value;
+  b.bytes = c.bytes;
+  b.role = (npu::BufRole)c.role;
+  b.first_use = c.first_use;
+  b.last_use = c.last_use;
+  b.in_loop = c.in_loop != 0;
+  b.addr = c.addr;
+  b.addr_pong = c.addr_pong;
+  b.prefetch_addr = c.prefetch_addr;
+  b.double_buffered = c.double_buffered != 0;
+  b.spilled = c.spilled != 0;
+  return b;
+}
+npu_sram_buffer to_c(const npu::SramBuffer &b) {
+  npu_sram_buffer c;
+  c.value = b.value;
+  c.role = (int32_t)b.role;
+  c.bytes = b.bytes;
+  c.first_use = b.first_use;
+  c.last_use = b.last_use;
+  c.in_loop = b.in_loop;
+  c.double_buffered = b.double_buffered;
+  c.addr = b.addr;
+  c.addr_pong = b.addr_pong;
+  c.prefetch_addr = b.prefetch_addr;
+  c.spilled = b.spilled;
+  c.reserved = 0;
+  return c;
+}
+}  // namespace
+
+int32_t npu_pass_bufferize(const npu_graph *g, const int32_t *ops, int32_t n_ops,
+                           const int64_t *bytes, int32_t n_bytes, npu_sram_buffer *out,
+                           int32_t cap) {
+  if (!g || (!ops && n_ops > 0) || n_ops < 0) return fail("bad arguments");
+  std::vector<int32_t> v(ops, ops + n_ops);
+  for (int32_t o : v)
+    if (bad_op(g, o)) return fail("bad op %d", o);
+  std::vector<int64_t> by;
+  if (bytes && n_bytes > 0) by.assign(bytes, bytes + n_bytes);
+  const auto bufs = npu::bufferize_loop(g->g, v, by.empty() ? nullptr : &by);
+  for (size_t i = 0; i < bufs.size() && (int32_t)i < cap && out; ++i) out[i] = to_c(bufs[i]);
+  return (int32_t)bufs.size();
+}
+
+int32_t npu_pass_sram_allocation(npu_sram_buffer *bufs, int32_t n, int64_t sram_size,
+                                 npu_sram_summary *summary) {
+  if ((!bufs && n > 0) || n < 0 || sram_size <= 0) return fail("bad arguments");
+  std::vector<npu::SramBuffer> v;
+  for (int32_t i = 0; i < n; ++i) {
+    if (bufs[i].role < 0 || bufs[i].role > 2 || bufs[i].bytes < 0) return fail("bad buffer %d", i);
+    npu::SramBuffer b = from_c(bufs[i]);
+    b.addr = b.addr_pong = b.prefetch_addr = -1;
+    b.double_buffered = b.spilled = false;
+    v.push_back(b);
+  }
+  const npu::SramPlanSummary s = npu::plan_sram(v, sram_size);
+  for (int32_t i = 0; i < n; ++i) bufs[i] = to_c(v[i]);
+  if (summary) {
+    summary->spilled = s.spilled;
+    summary->prefetched = s.prefetched;
+    summary->prefetch_bytes = s.prefetch_bytes;
+    summary->peak_bytes = s.peak_bytes;
+    summary->free_after = s.free_after;
+  }
+  return 0;
+}
+
+int32_t npu_pass_cost_evaluate(const npu_graph *g, const npu_hw_target *t, const int32_t *ops,
+                               int32_t n_ops, const npu_sram_buffer *bufs, int32_t n_bufs,
+                               int64_t tile_iterations, npu_kernel_cost *out) {
+  if (!g || !t || !out || (!ops && n_ops > 0) || (!bufs && n_bufs > 0)) return fail("bad arguments");
+  std::vector<int32_t> v(ops, ops + n_ops);
+  for (int32_t o : v)
+    if (bad_op(g, o)) return fail("bad op %d", o);
+  std::vector<npu::SramBuffer> b;
+  for (int32_t i = 0; i < n_bufs; ++i) b.push_back(from_c(bufs[i]));
+  const npu::CostModel cm(g->g, to_target(t));
+  const npu::KernelCost k = npu::cost_evaluate(g->g, cm, v, b, tile_iterations);
+  out->flops = k.flops;
+  out->mem_bytes = k.mem_bytes;
+  out->arithmetic_intensity = k.arithmetic_intensity;
+  out->time_sec = k.time_sec;
+  out->efficiency = k.efficiency;
+  out->memory_bound = k.memory_bound;
+  out->reserved = 0;
+  out->dma_in_bytes = k.dma_in_bytes;
+  out->dma_out_bytes = k.dma_out_bytes;
+  out->matrix_cycles = k.matrix_cycles;
+  out->dsp_cycles = k.dsp_cycles;
+  out->peak_sram_bytes = k.peak_sram_bytes;
+  out->num_tile_iterations = k.num_tile_iterations;
+  out->num_linalg_ops = k.num_linalg_ops;
+  out->sram_budget = k.sram_budget;
+  return 0;
+}
 
 void npu_gpu_params_mi355x(npu_gpu_params *p) {
   if (p) npu::gpu_params_mi355x(p);

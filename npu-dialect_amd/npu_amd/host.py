@@ -403,6 +403,96 @@ def temporal(g: Graph, t: HWTarget, op):
     return (list(ts[:n]), s) if n else (None, None)
 
 
+# ---------------------------------------------------------------- buffers after tiling
+ROLES = ("input", "output", "intermediate")
+
+
+class SramBuffer(C.Structure):
+    _fields_ = [("value", C.c_int32), ("role", C.c_int32), ("bytes", C.c_int64),
+                ("first_use", C.c_int64), ("last_use", C.c_int64), ("in_loop", C.c_int32),
+                ("double_buffered", C.c_int32), ("addr", C.c_int64), ("addr_pong", C.c_int64),
+                ("prefetch_addr", C.c_int64), ("spilled", C.c_int32), ("reserved", C.c_int32)]
+
+
+class SramSummary(C.Structure):
+    _fields_ = [("spilled", C.c_int64), ("prefetched", C.c_int64), ("prefetch_bytes", C.c_int64),
+                ("peak_bytes", C.c_int64), ("free_after", C.c_int64)]
+
+
+class KernelCost(C.Structure):
+    _fields_ = [("flops", C.c_double), ("mem_bytes", C.c_double),
+                ("arithmetic_intensity", C.c_double), ("time_sec", C.c_double),
+                ("efficiency", C.c_double), ("memory_bound", C.c_int32), ("reserved", C.c_int32),
+                ("dma_in_bytes", C.c_int64), ("dma_out_bytes", C.c_int64),
+                ("matrix_cycles", C.c_int64), ("dsp_cycles", C.c_int64),
+                ("peak_sram_bytes", C.c_int64), ("num_tile_iterations", C.c_int64),
+                ("num_linalg_ops", C.c_int64), ("sram_budget", C.c_int64)]
+
+
+SIGNATURES.update({
+    "npu_pass_bufferize": (_I32, [_P, _PI32, _I32, _PI64, _I32, C.POINTER(SramBuffer), _I32]),
+    "npu_pass_sram_allocation": (_I32, [C.POINTER(SramBuffer), _I32, _I64, C.POINTER(SramSummary)]),
+    "npu_pass_cost_evaluate": (_I32, [_P, _PT, _PI32, _I32, C.POINTER(SramBuffer), _I32, _I64,
+                                      C.POINTER(KernelCost)]),
+})
+
+
+def bufferize(g: Graph, ops, tile_bytes=None):
+    """npu-bufferize's DMA insertion for the tile loop whose body is `ops`
+    (indices into func.ops): one SRAM buffer per shaped operand defined
+    outside, with its role and liveness.  `tile_bytes` maps SSA names to the
+    bytes of their tile slice (else the full tensor)."""
+    a_ops, n_ops = _arr(C.c_int32, [g.op_id[i] for i in ops])
+    by = None
+    nb = 0
+    if tile_bytes:
+        nb = max(g.value_id.values()) + 1
+        by = (C.c_int64 * nb)()
+        for name, b in tile_bytes.items():
+            by[g.value_id[name]] = b
+    n = _check(lib().npu_pass_bufferize(g.h, a_ops, n_ops, by, nb, None, 0))
+    out = (SramBuffer * max(n, 1))()
+    lib().npu_pass_bufferize(g.h, a_ops, n_ops, by, nb, out, n)
+    return list(out[:n])
+
+
+def sram_allocation(buffers, sram_size):
+    """npu-sram-allocation's dual-end plan of `buffers` (SramBuffer list, planned
+    in place) for an SRAM of `sram_size` bytes; returns the summary."""
+    arr = (SramBuffer * max(len(buffers), 1))(*buffers)
+    summ = SramSummary()
+    _check(lib().npu_pass_sram_allocation(arr, len(buffers), sram_size, C.byref(summ)))
+    for i in range(len(buffers)):
+        buffers[i] = arr[i]
+    return summ
+
+
+def cost_evaluate(g: Graph, t: HWTarget, ops, buffers, tile_iterations=1) -> KernelCost:
+    a_ops, n_ops = _arr(C.c_int32, [g.op_id[i] for i in ops])
+    arr = (SramBuffer * max(len(buffers), 1))(*buffers)
+    kc = KernelCost()
+    _check(lib().npu_pass_cost_evaluate(g.h, C.byref(t), a_ops, n_ops, arr, len(buffers),
+                                        tile_iterations, C.byref(kc)))
+    return kc
+
+
+def cost_json(name, kc: KernelCost, extra=None) -> str:
+    """The COST_JSON line of CostEvaluatePass.cpp:135-158 (same keys, same
+    order), optionally followed by extra keys (the MI355X prediction)."""
+    import json
+    rec = {"name": name, "flops": kc.flops, "mem_bytes": kc.mem_bytes,
+           "arithmetic_intensity": kc.arithmetic_intensity, "time_sec": kc.time_sec,
+           "is_memory_bound": bool(kc.memory_bound), "efficiency": kc.efficiency,
+           "dma_in_bytes": kc.dma_in_bytes, "dma_out_bytes": kc.dma_out_bytes,
+           "matrix_cycles": kc.matrix_cycles, "dsp_cycles": kc.dsp_cycles,
+           "peak_sram_bytes": kc.peak_sram_bytes, "num_tile_iterations": kc.num_tile_iterations,
+           "num_linalg_ops": kc.num_linalg_ops, "sram_budget": kc.sram_budget,
+           "bottleneck": "memory" if kc.memory_bound else "compute"}
+    if extra:
+        rec.update(extra)
+    return "COST_JSON: " + json.dumps(rec)
+
+
 def mi355x_gpu() -> GpuParams:
     """The calibrated MI355X constants of the launch model."""
     g = GpuParams()
