@@ -192,206 +192,293 @@ __global__ __launch_bounds__(256) void conv3x3_rows_kernel(
 
 // Persistent variant for reductions that fit one stage (C = NCH chunks):
 // each workgroup loads its 64 filters' fragments into registers once, then
-// walks a strided set of 2-row tiles, fetching the next tile's halo into
-// registers while the current tile is multiplied, so loads, MFMAs and stores
-// of different tiles overlap instead of every workgroup of a round waiting
-// on its loads at the same time.  The tiles of one XCD are a contiguous
-// range, so the halo rows two neighbouring tiles share are read from HBM once.
+// walks a contiguous range of output rows in 2-row tiles (a 1-row tile where
+// the range or an image ends), fetching the next tile's halo into registers
+// while the current tile is multiplied, so loads, MFMAs and stores of
+// different tiles overlap instead of every workgroup of a round waiting on
+// its loads at the same time.  The ranges are balanced to within one row and
+// those of one XCD are neighbours, so the halo rows two tiles share are read
+// from HBM once.
+//
+// Per tile, only the tile's base addresses change: the rows of the halo and
+// of the output are wave-uniform (scalar registers), and each lane's offset
+// within a row is fixed for the whole walk.  So every global load and store
+// is a scalar base plus one loop-invariant lane offset, and the LDS addresses
+// are loop-invariant plus immediates: the per-tile vector-ALU work is the
+// epilogue's clamp and conversion, not index arithmetic.
 template <class MM, typename T, int WMAX, int NCH, int WFIX>
 __global__ __launch_bounds__(256, NCH <= 2 ? 2 : 1) void conv3x3_stream_kernel(
     const T *__restrict__ x, const T *__restrict__ w, const float *__restrict__ bias,
-    T *__restrict__ out, int H, int w_rt, int F, int act, int ntiles) {
-  // A compile-time width (WFIX > 0) and channel count turn the index
-  // arithmetic below (divisions by the row width, address products) into
-  // shifts and constant multiplies; it is most of the kernel's VALU work.
+    T *__restrict__ out, int H, int w_rt, int F, int act, int nrows) {
   const int W = WFIX > 0 ? WFIX : w_rt;
+  constexpr int ES = sizeof(T);
   constexpr int C = NCH * MM::kPerFrag;
-  constexpr int TR = 2;
+  constexpr int TR = 2, HR = TR + 2;
   constexpr int KPL = MM::kPerLane;
   constexpr int KC = MM::kPerFrag;
-  constexpr int SEGP = NCH * 4;
-  constexpr int REC = (NCH * 64 + 32) / sizeof(T);
-  constexpr int HR = TR + 2;
-  constexpr int PBW = (TR * WMAX + 15) / 16;
-  constexpr int SEGS = (HR * (WMAX + 2) * SEGP + 255) / 256;
-  static_assert(KC * sizeof(T) == 64, "a chunk is 64 bytes per pixel");
+  constexpr int SEGP = C * ES / 16;                  // 16-byte runs per input pixel
+  constexpr int REC = (NCH * 64 + 32) / ES;          // LDS halo record stride (elements)
+  constexpr int HCMAX = WMAX + 2;
+  constexpr int LPR = (HCMAX * SEGP + 255) / 256;    // loads per halo row
+  constexpr int PBW = (TR * WMAX + 15) / 16;         // 16-pixel blocks of a 2-row tile
+  constexpr int PB1 = (WMAX + 15) / 16;              // ... of a 1-row tile
   // Output tile staged in LDS (64 filters per pixel plus 32 bytes of
   // padding) so that it leaves in whole 16-byte runs per lane.
-  constexpr int OREC = (64 * sizeof(T) + 32) / sizeof(T);
-  constexpr int OSEGP = 64 * sizeof(T) / 16;  // 16-byte runs per pixel
-  __shared__ __attribute__((aligned(16))) T halo[HR * (WMAX + 2) * REC];
-  __shared__ __attribute__((aligned(16))) T ostage[TR * WMAX * OREC];
+  constexpr int OREC = (64 * ES + 32) / ES;
+  constexpr int OSEGP = 64 * ES / 16;                // 16-byte runs per output pixel
+  constexpr int OPIX = 256 / OSEGP;                  // output pixels per store instruction
+  constexpr int NST = (TR * WMAX + OPIX - 1) / OPIX; // store instructions per tile
+  // Filter staging: a wave's 16 runs of one tap (C elements each), padded to
+  // a stride of 32 mod 64 bytes so the fragment reads are conflict-free.
+  constexpr int WRS = C * ES + 32;
+  constexpr int FPI = 64 / SEGP;                     // filter runs per load instruction
+  constexpr int NWI = 16 / FPI;                      // load instructions per tap
+  static_assert(KC * ES == 64, "a chunk is 64 bytes per pixel");
+  static_assert(4 * 16 * WRS <= HR * HCMAX * REC * ES, "filter staging fits the halo buffer");
+  // halo rows, then one 16-byte slot per lane that takes the writes of lanes
+  // with no halo record (past the row end, or a zero-padding column)
+  constexpr int HALO = HR * HCMAX * REC;
+  __shared__ __attribute__((aligned(16))) T halo[HALO + 64 * 16 / ES];
+  __shared__ __attribute__((aligned(16))) T ostage[PBW * 16 * OREC];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int r = lane & 15, q = lane >> 4;
-  const int tiles_h = (H + TR - 1) / TR;
-  const TileWalk walk = tile_walk(ntiles);
-  const int t_first = walk.first, t_end = walk.end, step = walk.step;
-  const int f = (blockIdx.y * 4 + wave) * 16 + r;  // F is a multiple of 64
-  const int HC = W + 2, nseg = HR * HC * SEGP;
-  const int tile_px = TR * W;
+  const RowRange range = row_range(nrows);
+  const int HC = W + 2;
+  const size_t row_bytes = (size_t)W * C * ES, orow_bytes = (size_t)W * F * ES;
+  // rows of the tile that starts at row `g` (global over the batch)
+  auto tile_rows = [&](int g) { return min(min(TR, range.end - g), H - g % H); };
 
+  // B-operand (pixel) fragment addresses of the tile's 16-pixel blocks
   int abase[PBW];
 #pragma unroll
   for (int i = 0; i < PBW; ++i) {
-    const int p = min(i * 16 + r, tile_px - 1);
+    const int p = min(i * 16 + r, TR * W - 1);
     const int pr = p / W, pc = p - pr * W;
     abase[i] = (pr * HC + pc) * REC + q * KPL;
   }
-
-  // Raw loads now, zero fill when written to LDS (a select right after a
-  // load would make the wave wait for it, serialising the prefetch).
-  u32x4 stage[SEGS];
-  uint32_t inside_bits = 0;
-  auto fetch = [&](int t) {
-    const int n = t / tiles_h, h0 = (t - n * tiles_h) * TR;
-    const int lt = opaque(tid);
-    inside_bits = 0;
+  // Halo fetch: load j of every halo row covers the row's 16-byte runs
+  // tid + 256 j.  goff: byte offset in the input row (the column clamped
+  // into the image); loff: byte address in the LDS halo, or the lane's slot
+  // past the halo when the run has no record to fill (the zero-padding
+  // columns are cleared once, before the walk, and never written again).
+  uint32_t goff[LPR], loff[HR][LPR];
 #pragma unroll
-    for (int s = 0; s < SEGS; ++s) {
-      const int idx = min(lt + 256 * s, nseg - 1);
-      const int rec = idx / SEGP, seg = idx % SEGP;
-      const int hr = rec / HC, hc = rec - hr * HC;
-      const int ih = h0 + hr - 1, iw = hc - 1;
-      const bool inside = ih >= 0 && ih < H && iw >= 0 && iw < W;
-      const int ihc = min(max(ih, 0), H - 1), iwc = min(max(iw, 0), W - 1);
-      stage[s] = *reinterpret_cast<const u32x4 *>(
-          x + ((size_t)(n * H + ihc) * W + iwc) * C + seg * (16 / sizeof(T)));
-      inside_bits |= (uint32_t)inside << s;
+  for (int j = 0; j < LPR; ++j) {
+    const int idx = tid + 256 * j, idxc = min(idx, HC * SEGP - 1);
+    const int hc = idxc / SEGP, seg = idxc - hc * SEGP;
+    const int iw = min(max(hc - 1, 0), W - 1);
+    goff[j] = (uint32_t)(iw * C * ES + seg * 16);
+    const bool rec = idx < HC * SEGP && hc >= 1 && hc <= W;
+#pragma unroll
+    for (int hr = 0; hr < HR; ++hr)
+      loff[hr][j] = rec ? (uint32_t)((hr * HC + hc) * REC * ES + seg * 16)
+                        : (uint32_t)(HALO * ES + lane * 16);
+  }
+  // Output stores: store s moves pixels s*OPIX + tid/OSEGP of the tile
+  const int op = tid / OSEGP, osg = tid - op * OSEGP;
+  const uint32_t ooff = (uint32_t)(op * F * ES + osg * 16);
+  const uint32_t oloff = (uint32_t)(op * OREC * ES + osg * 16);
+
+  // Raw loads now, zero rows chosen when written to LDS (a select right
+  // after a load would make the wave wait for it, serialising the prefetch).
+  u32x4 stage[HR][LPR];
+  uint32_t rowok = 0;
+  auto fetch = [&](int g) {
+    const int n = g / H, h0 = g - n * H;
+    rowok = 0;
+#pragma unroll
+    for (int hr = 0; hr < HR; ++hr) {
+      const int ih = h0 + hr - 1;
+      rowok |= (uint32_t)(ih >= 0 && ih < H) << hr;
+      const char *rb = reinterpret_cast<const char *>(x) +
+                       (size_t)(n * H + min(max(ih, 0), H - 1)) * row_bytes;
+#pragma unroll
+      for (int j = 0; j < LPR; ++j)
+        stage[hr][j] = *reinterpret_cast<const u32x4 *>(rb + goff[j]);
     }
   };
+  char *const hbytes = reinterpret_cast<char *>(halo);
   auto commit = [&]() {
+    const u32x4 zero{0u, 0u, 0u, 0u};
 #pragma unroll
-    for (int s = 0; s < SEGS; ++s) {
-      const int idx = tid + 256 * s;
-      if (idx < nseg)
-        *reinterpret_cast<u32x4 *>(&halo[(idx / SEGP) * REC + (idx % SEGP) * (16 / sizeof(T))]) =
-            masked(stage[s], (inside_bits >> s) & 1u);
+    for (int hr = 0; hr < HR; ++hr) {
+      if ((rowok >> hr) & 1u) {
+#pragma unroll
+        for (int j = 0; j < LPR; ++j) *reinterpret_cast<u32x4 *>(hbytes + loff[hr][j]) = stage[hr][j];
+      } else {
+#pragma unroll
+        for (int j = 0; j < LPR; ++j) *reinterpret_cast<u32x4 *>(hbytes + loff[hr][j]) = zero;
+      }
     }
   };
 
-  if (t_first >= t_end) return;  // uniform over the workgroup
-  fetch(t_first);
-  const T *wrow = w + (size_t)f * 9 * C + q * KPL;
-  Frag16 b[NCH][9];
+  if (range.first >= range.end) return;  // uniform over the workgroup
+  fetch(range.first);
+  // Filter fragments.  A fragment (filter r, 16-byte run q of a chunk) read
+  // straight from global memory would touch 16 filters' 64-byte pieces per
+  // instruction; instead each tap's 16 runs are loaded whole (SEGP lanes
+  // per run, full cache lines) and turned into fragments through this
+  // wave's slot of the halo buffer, before the first halo is written there.
+  u32x4 wraw[9][NWI];
+  {
+    const char *wb = reinterpret_cast<const char *>(w) +
+                     (size_t)(blockIdx.y * 4 + wave) * 16 * 9 * C * ES;
+    const int fl = lane / SEGP, pc = lane - fl * SEGP;
 #pragma unroll
-  for (int ch = 0; ch < NCH; ++ch)
+    for (int t = 0; t < 9; ++t)
 #pragma unroll
-    for (int t = 0; t < 9; ++t) b[ch][t] = load16(wrow + t * C + ch * KC);
+      for (int i = 0; i < NWI; ++i)
+        wraw[t][i] = *reinterpret_cast<const u32x4 *>(
+            wb + ((size_t)(fl + FPI * i) * 9 + t) * C * ES + pc * 16);
+  }
   // The filters are the MFMA's A operand and the pixels its B operand, so
   // a lane's accumulator holds filters 4q..4q+3 (of its wave's 16) of one
   // pixel: the epilogue writes them to the output stage as one 8-byte (bf16)
-  // or 16-byte (f32) LDS store.
+  // or 16-byte (f32) LDS store.  The accumulators start at the bias.
   const int fq = (blockIdx.y * 4 + wave) * 16 + 4 * q;
   float bv[4];
 #pragma unroll
   for (int e = 0; e < 4; ++e) bv[e] = bias ? bias[fq + e] : 0.0f;
   const ActBounds ab = act_bounds(act);
+  Frag16 b[NCH][9];
+  {
+    char *ws = reinterpret_cast<char *>(halo) + wave * 16 * WRS;
+    const int fl = lane / SEGP, pc = lane - fl * SEGP;
+#pragma unroll
+    for (int t = 0; t < 9; ++t) {
+#pragma unroll
+      for (int i = 0; i < NWI; ++i)
+        *reinterpret_cast<u32x4 *>(ws + (fl + FPI * i) * WRS + pc * 16) = wraw[t][i];
+#pragma unroll
+      for (int ch = 0; ch < NCH; ++ch)
+        b[ch][t].u = *reinterpret_cast<const u32x4 *>(ws + r * WRS + ch * KC * ES + q * 16);
+    }
+  }
+  __syncthreads();  // every wave's staging is read before the halo is written
+  // zero-padding columns 0 and W+1 of the halo rows
+  for (int i = tid; i < HR * 2 * SEGP; i += 256) {
+    const int hr = i / (2 * SEGP), k = i - hr * 2 * SEGP, side = k / SEGP, seg = k - side * SEGP;
+    *reinterpret_cast<u32x4 *>(hbytes + (hr * HC + side * (W + 1)) * REC * ES + seg * 16) =
+        u32x4{0u, 0u, 0u, 0u};
+  }
   commit();
-#pragma unroll
-  for (int ch = 0; ch < NCH; ++ch)
-#pragma unroll
-    for (int t = 0; t < 9; ++t) settle(b[ch][t].u);
 #pragma unroll
   for (int e = 0; e < 4; ++e) settle(bv[e]);
   __syncthreads();
 
   // One halo buffer: the next tile's halo waits in registers until every
   // wave has finished reading the current one.
-  // Pipeline: the halo of tile t+step is in registers while tile t is
-  // multiplied; after the epilogue it goes to LDS and the fetch of tile
-  // t+2*step is issued before tile t's output stores, so no register that
+  // Pipeline: the halo of the next tile is in registers while this tile is
+  // multiplied; after the epilogue it goes to LDS and the fetch of the tile
+  // after it is issued before this tile's output stores, so no register that
   // feeds a pending store is a load destination (the in-order memory
   // counter would otherwise make the next fetch wait for those stores).
   // Fetch and commit are unconditional (past the end the walk refetches a
   // tile whose copy is never read): with a condition on either, the
   // compiler's wait analysis assumes a fetch can be pending at the loop head
   // and drains every outstanding load there.
-  auto next_of = [&](int t) { return t + step < t_end ? t + step : t; };
-  fetch(next_of(t_first));
-  for (int t = t_first; t < t_end; t += step) {
+  auto next_of = [&](int g) {
+    const int n = g + tile_rows(g);
+    return n < range.end ? n : g;
+  };
+  fetch(next_of(range.first));
+  for (int g = range.first; g < range.end; g += tile_rows(g)) {
+    const int rows = tile_rows(g);
     const T *hb = halo;
     typename MM::acc_t acc[PBW];
 #pragma unroll
-    for (int i = 0; i < PBW; ++i) acc[i] = typename MM::acc_t{0, 0, 0, 0};
-    // Two-deep pipeline over taps: the next tap's A fragments are read from
+    for (int i = 0; i < PBW; ++i) acc[i] = typename MM::acc_t{bv[0], bv[1], bv[2], bv[3]};
+    // Two-deep pipeline over taps: the next tap's B fragments are read from
     // LDS while this tap's MFMAs run; the scheduling barrier keeps each
-    // tap's reads and MFMAs in their own region.
-    auto load_a = [&](Frag16 (&dst)[PBW], int j) {
-      const int toff = ((j % 9 / 3) * HC + (j % 3)) * REC + (j / 9) * KC;
+    // tap's reads and MFMAs in their own region.  A 1-row tile multiplies
+    // only its own pixel blocks.
+    auto multiply = [&](auto nblk) {
+      constexpr int NB = decltype(nblk)::value;
+      auto load_a = [&](Frag16 (&dst)[PBW], int j) {
+        const int toff = ((j % 9 / 3) * HC + (j % 3)) * REC + (j / 9) * KC;
 #pragma unroll
-      for (int i = 0; i < PBW; ++i) dst[i] = load16(hb + abase[i] + toff);
+        for (int i = 0; i < NB; ++i) dst[i] = load16(hb + abase[i] + toff);
+      };
+      Frag16 a[2][PBW];
+      load_a(a[0], 0);
+#pragma unroll
+      for (int j = 0; j < NCH * 9; ++j) {
+        if (j + 1 < NCH * 9) load_a(a[(j + 1) & 1], j + 1);
+#pragma unroll
+        for (int s = 0; s < MM::kSteps; ++s)
+#pragma unroll
+          for (int i = 0; i < NB; ++i) MM::step(acc[i], b[j / 9][j % 9], a[j & 1][i], s);
+        __builtin_amdgcn_sched_barrier(0);
+      }
     };
-    Frag16 a[2][PBW];
-    load_a(a[0], 0);
+    if (rows == TR)
+      multiply(std::integral_constant<int, PBW>{});
+    else
+      multiply(std::integral_constant<int, PB1>{});
+    // Every 16-pixel block is staged (the stage has room for PBW*16 pixels);
+    // the stores below move only the tile's pixels.
 #pragma unroll
-    for (int j = 0; j < NCH * 9; ++j) {
-      if (j + 1 < NCH * 9) load_a(a[(j + 1) & 1], j + 1);
+    for (int i = 0; i < PBW; ++i) {
+      float v[4];
 #pragma unroll
-      for (int s = 0; s < MM::kSteps; ++s)
-#pragma unroll
-        for (int i = 0; i < PBW; ++i) MM::step(acc[i], b[j / 9][j % 9], a[j & 1][i], s);
-      __builtin_amdgcn_sched_barrier(0);
-    }
-    {
-      const int lr = opaque(r);
-#pragma unroll
-      for (int i = 0; i < PBW; ++i) {
-        const int p = i * 16 + lr;
-        if (p >= tile_px) continue;
-        float v[4];
-#pragma unroll
-        for (int e = 0; e < 4; ++e) v[e] = act_clamp(acc[i][e] + bv[e], ab);
-        T *dst = ostage + p * OREC + wave * 16 + 4 * q;
-        if constexpr (sizeof(T) == 4) {
-          *reinterpret_cast<f32x4 *>(dst) = f32x4{v[0], v[1], v[2], v[3]};
-        } else {
-          const uint32_t lo = f32_to_bf16(v[0]) | ((uint32_t)f32_to_bf16(v[1]) << 16);
-          const uint32_t hi = f32_to_bf16(v[2]) | ((uint32_t)f32_to_bf16(v[3]) << 16);
-          *reinterpret_cast<uint2 *>(dst) = make_uint2(lo, hi);
-        }
+      for (int e = 0; e < 4; ++e) v[e] = act_clamp(acc[i][e], ab);
+      T *dst = ostage + (i * 16 + r) * OREC + wave * 16 + 4 * q;
+      if constexpr (sizeof(T) == 4) {
+        *reinterpret_cast<f32x4 *>(dst) = f32x4{v[0], v[1], v[2], v[3]};
+      } else {
+        const uint32_t lo = f32_to_bf16(v[0]) | ((uint32_t)f32_to_bf16(v[1]) << 16);
+        const uint32_t hi = f32_to_bf16(v[2]) | ((uint32_t)f32_to_bf16(v[3]) << 16);
+        *reinterpret_cast<uint2 *>(dst) = make_uint2(lo, hi);
       }
     }
     __syncthreads();
     commit();
-    fetch(next_of(next_of(t)));
+    fetch(next_of(next_of(g)));
     {
-      const int n = t / tiles_h, h0 = (t - n * tiles_h) * TR;
-      const int rows = min(TR, H - h0);
-      for (int idx = opaque(tid); idx < rows * W * OSEGP; idx += 256) {
-        const int p = idx / OSEGP, sg = idx - p * OSEGP;
-        const int pr = p / W, pc = p - pr * W;
-        *reinterpret_cast<u32x4 *>(out + ((size_t)(n * H + h0 + pr) * W + pc) * F +
-                                   blockIdx.y * 64 + sg * (16 / sizeof(T))) =
-            *reinterpret_cast<const u32x4 *>(ostage + p * OREC + sg * (16 / sizeof(T)));
-      }
+      const int npx = rows * W;
+      char *ob = reinterpret_cast<char *>(out) + (size_t)g * orow_bytes + blockIdx.y * 64 * ES;
+      const char *ol = reinterpret_cast<const char *>(ostage) + oloff;
+#pragma unroll
+      for (int s = 0; s < NST; ++s)
+        if (op + s * OPIX < npx)
+          *reinterpret_cast<u32x4 *>(ob + (size_t)s * OPIX * F * ES + ooff) =
+              *reinterpret_cast<const u32x4 *>(ol + s * OPIX * OREC * ES);
     }
     __syncthreads();
   }
 }
+
+// Vector-ALU instructions per wave and output row of the persistent kernel
+// (counted with SQ_INSTS_VALU less SQ_INSTS_MFMA): a fixed part (epilogue,
+// loop control) and a part per 64-byte input chunk (halo commit, fetch).
+constexpr double STREAM_VALU_ROW_FIXED = 60.0;
+constexpr double STREAM_VALU_ROW_PER_CHUNK = 10.0;
 
 template <class MM, typename T, int WMAX, int NCH, int WFIX>
 hipError_t launch_stream(const ConvArgs &a, int wgs, hipStream_t s) {
   if (a.W > WMAX || (WFIX > 0 && a.W != WFIX) || a.C != MM::kPerFrag * NCH || a.F % 64 != 0 ||
       wgs % kXcds != 0)
     return hipErrorInvalidValue;
-  const int ntiles = a.N * ((a.H + 1) / 2);
+  const int nrows = a.N * a.H;
   dim3 grid(wgs, (a.F + 63) / 64);
   {
+    // The plan's work unit is one output row (half a 2-row tile): the walk
+    // gives each workgroup a contiguous range of rows.
     constexpr int TR = 2, PBW = (TR * WMAX + 15) / 16, REC = NCH * 64 + 32;
-    const double es = sizeof(T), halo = 4.0 * (a.W + 2) * a.C * es;
+    const double es = sizeof(T);
     npu_launch_plan p =
         make_plan("conv3x3_persistent", wgs * grid.y,
-                  wg_per_cu(conv3x3_stream_kernel<MM, T, WMAX, NCH, WFIX>), ntiles * grid.y, 8 * sizeof(T));
+                  wg_per_cu(conv3x3_stream_kernel<MM, T, WMAX, NCH, WFIX>), nrows * grid.y, 8 * sizeof(T));
     p.load_phases = 0;  // the next tile's halo is fetched during this tile
-    p.tile_macs = 4.0 * PBW * 256 * 9 * a.C;
-    // counted per wave and tile: 950 (bf16, two chunks), 1292 (f32, four chunks)
-    p.tile_valu = 4.0 * (600.0 + 175.0 * NCH);
-    p.tile_lds_bytes = 4.0 * (a.W + 2) * REC +                  // halo written
-                       4.0 * PBW * 9 * NCH * 1024 +             // A fragments read
-                       2.0 * TR * a.W * (64 * es + 32);         // output staged and read
-    p.tile_load_bytes = halo;
-    p.tile_store_bytes = TR * a.W * 64 * es;
+    p.tile_macs = 4.0 * (PBW / 2.0) * 256 * 9 * a.C;
+    // vector-ALU instructions per row, summed over the four waves
+    p.tile_valu = 4.0 * (STREAM_VALU_ROW_FIXED + STREAM_VALU_ROW_PER_CHUNK * NCH);
+    p.tile_lds_bytes = 2.0 * (a.W + 2) * REC +                  // halo written
+                       2.0 * PBW * 9 * NCH * 1024 +             // B fragments read
+                       2.0 * a.W * (64 * es + 32);              // output staged and read
+    p.tile_load_bytes = 2.0 * (a.W + 2) * a.C * es;
+    p.tile_store_bytes = a.W * 64 * es;
     p.wg_setup_bytes = 4.0 * 16 * 9 * a.C * es;
     p.hbm_bytes = es * ((double)a.N * a.H * a.W * a.C + 9.0 * a.F * a.C + (double)a.N * a.H * a.W * a.F) +
                   (a.bias ? 4.0 * a.F : 0.0);
@@ -399,7 +486,7 @@ hipError_t launch_stream(const ConvArgs &a, int wgs, hipStream_t s) {
   }
   hipLaunchKernelGGL((conv3x3_stream_kernel<MM, T, WMAX, NCH, WFIX>), grid, dim3(256), 0, s,
                      static_cast<const T *>(a.x), static_cast<const T *>(a.w), a.bias,
-                     static_cast<T *>(a.out), a.H, a.W, a.F, a.act, ntiles);
+                     static_cast<T *>(a.out), a.H, a.W, a.F, a.act, nrows);
   return hipGetLastError();
 }
 

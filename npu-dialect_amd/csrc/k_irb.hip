@@ -30,7 +30,7 @@ constexpr int HP = HW * (TH + 2);    // 100 halo pixels
 constexpr int HPB = (HP + 15) / 16;  // 7 blocks of 16 rows
 constexpr int OP = TH * TW;          // 64 output pixels
 
-__device__ __forceinline__ float relu6(float v) { return act_apply(v, 2); }
+__device__ __forceinline__ float relu6(float v) { return act_clamp(v, ActBounds{0.0f, 6.0f}); }
 
 template <int C, int E>
 __global__ __launch_bounds__(256, E >= 192 ? 1 : 2) void irb_kernel(const float *__restrict__ x,

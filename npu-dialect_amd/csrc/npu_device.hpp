@@ -125,9 +125,10 @@ __device__ __forceinline__ ActBounds act_bounds(int act) {
   const float inf = __builtin_inff();
   return ActBounds{act == 0 ? -inf : 0.0f, act == 2 ? 6.0f : inf};
 }
+// IEEE maximum/minimum (NaN in, NaN out; -0 < +0): gfx950's v_maximum3_f32
+// and v_minimum3_f32, one instruction each.
 __device__ __forceinline__ float act_clamp(float v, ActBounds b) {
-  const float c = fminf(fmaxf(v, b.lo), b.hi);
-  return v != v ? v : c;
+  return __builtin_elementwise_minimum(__builtin_elementwise_maximum(v, b.lo), b.hi);
 }
 
 __device__ __forceinline__ Frag16 load16(const void *p) {

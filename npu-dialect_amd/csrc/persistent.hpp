@@ -30,6 +30,22 @@ __device__ __forceinline__ TileWalk tile_walk(int ntiles) {
   return w;
 }
 
+// Balanced contiguous share of `nrows` work rows for this workgroup: the
+// workgroups of one XCD take neighbouring ranges (so rows that two ranges
+// share are read through the same L2), and range sizes differ by at most
+// one row, so no CU carries a whole extra tile.  gridDim.x must be a
+// multiple of kXcds.
+struct RowRange {
+  int first, end;
+};
+__device__ __forceinline__ RowRange row_range(int nrows) {
+  const int g = (blockIdx.x % kXcds) * (gridDim.x / kXcds) + blockIdx.x / kXcds;
+  RowRange r;
+  r.first = (int)((long long)nrows * g / gridDim.x);
+  r.end = (int)((long long)nrows * (g + 1) / gridDim.x);
+  return r;
+}
+
 // Index arithmetic that does not depend on the tile would be hoisted out of
 // a tile loop by the compiler and pinned in registers for its whole length;
 // passing a value through an empty asm makes it be recomputed per tile

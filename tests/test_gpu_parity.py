@@ -122,6 +122,13 @@ def test_c2_conv_config_n32(cuda, dtype):
     # pairs; an odd H leaves a half tile at the bottom of each image
     (64, 17, 9, 16, 64, 3, 1, "relu", True, "f32"),
     (64, 17, 9, 32, 80, 3, 1, "relu", True, "bf16"),
+    # the persistent kernel (>= 512 row pairs, F a multiple of 64, C two or
+    # four 64-byte chunks) at a run-time width, an odd H, two 64-filter
+    # blocks, a 64-wide row and four bf16 chunks
+    (64, 17, 9, 32, 128, 3, 1, "relu", True, "f32"),
+    (32, 32, 64, 64, 64, 3, 1, "relu", True, "f32"),
+    (40, 26, 60, 64, 64, 3, 1, "relu6", False, "bf16"),
+    (64, 16, 20, 128, 64, 3, 1, "none", True, "bf16"),
     (1, 3, 64, 16, 32, 3, 1, "relu", True, "f32"),    # widest row the LDS tile holds
     (1, 4, 70, 16, 16, 3, 1, "relu", True, "f32"),    # wider: general kernel
     (2, 6, 66, 32, 16, 3, 1, "relu", True, "bf16"),
@@ -143,6 +150,36 @@ def test_c2_conv_shapes(cuda, N, H, W, C, F, K, pad, act, bias, dtype):
         check_bound(_host(out), ref, mag, RTOL_F32, what="conv")
     else:
         check_bound(bf16(_host(out)), bf16(ref), mag, RTOL_BF16, what="conv")
+
+
+@pytest.mark.parametrize("N,H,W,C,F", [(2, 5, 7, 16, 16), (64, 17, 9, 32, 128)])
+def test_c2_nan_propagates(cuda, N, H, W, C, F):
+    """arith.maximumf propagates NaN: a NaN input pixel makes every output
+    of its 3x3 neighbourhood NaN through the ReLU, in the oracle and here
+    (rows kernel and persistent kernel)."""
+    x = rng.uniform(13, 0, (N, H, W, C), 0, 1)
+    x[N - 1, H // 2, W // 2, C - 1] = np.nan
+    w = rng.normal(13, 1, (F, 3, 3, C), 0, math.sqrt(2 / (9 * C)))
+    b = rng.uniform(13, 2, (F,), -0.1, 0.1)
+    out = torch.empty(N, H, W, F, device="cuda", dtype=torch.float32)
+    groups.fused_conv2d_nhwc_bias_act(_dev(x), _dev(w), _dev(b), out, 1, "relu")
+    torch.cuda.synchronize()
+    got = _host(out)
+    ref, mag = refs.conv_bias_act(x, w, b, 1, "relu")
+    assert np.array_equal(np.isnan(got), np.isnan(ref)) and np.isnan(ref).sum() == 9 * F
+    ok = ~np.isnan(ref)
+    check_bound(got[ok], ref[ok], mag[ok], RTOL_F32, what="conv with NaN")
+
+
+def test_c1_nan_propagates(cuda):
+    A = rng.uniform(14, 0, (64, 128), -1, 1)
+    A[5, 17] = np.nan
+    B = rng.uniform(14, 1, (128, 64), -1, 1)
+    out = torch.empty(64, 64, device="cuda", dtype=torch.float32)
+    groups.fused_matmul_bias_act(_dev(A), _dev(B), None, out, "relu")
+    torch.cuda.synchronize()
+    got = _host(out)
+    assert np.isnan(got[5]).all() and not np.isnan(np.delete(got, 5, axis=0)).any()
 
 
 def test_c2_reference_kat_fills(cuda):
