@@ -15,6 +15,8 @@
 // project MFMA (each lane produces the 4 consecutive channels of one pixel
 // that it feeds), so d never leaves registers.  HBM sees x and out once: the
 // E-channel intermediates (6x the block's own bytes) never reach it.
+#include <type_traits>
+
 #include "kernels.hpp"
 #include "npu_device.hpp"
 #include "persistent.hpp"
@@ -49,10 +51,9 @@ __global__ __launch_bounds__(256, E >= 192 ? 1 : 2) void irb_kernel(const float 
   constexpr int XS8 = KC1 * 16 + 8;
   constexpr int XS = (HP * XS8 + HP * ES + 9 * E) * 4 <= 81920 ? XS8 : KC1 * 16 + 4;
   constexpr int FB1 = E / 16;         // expand filter blocks
-  constexpr int FBW = (FB1 + 3) / 4;  // ... per wave (wave w owns w, w+4, ...)
   constexpr int KC2 = E / 16;         // project reduction chunks
   constexpr int FB2 = (C + 15) / 16;  // project filter blocks
-  constexpr int XV = KC1 * 4;         // float4 columns per staged x row
+  constexpr int XV = KC1 * 4;         // 16-byte columns per staged x row
   constexpr int XSEG = HP * XV;
   constexpr int XSEGS = (XSEG + 255) / 256;
   __shared__ __attribute__((aligned(16))) float xs[HP * XS];
@@ -64,55 +65,75 @@ __global__ __launch_bounds__(256, E >= 192 ? 1 : 2) void irb_kernel(const float 
   const TileWalk walk = tile_walk(ntiles);
   if (walk.first >= walk.end) return;  // uniform over the workgroup
 
-  // x halo of tile t into registers (zero-padded to KC1*16 channels; clamped
-  // addresses, zero fill by select).
-  // Raw loads now, zero fill when written to LDS (a select right after a
-  // load would make the wave wait for it, serialising the prefetch).
+  // x halo fetch.  Run s of a thread is halo pixel hp = (tid + 256 s) / XV,
+  // 16-byte column cv; its row and column in the halo and its offset from
+  // the tile origin do not depend on the tile.  Out-of-image runs (and the
+  // columns past C) load the tile origin instead and are zeroed on commit.
+  int xrel[XSEGS], xhyx[XSEGS];  // xhyx: halo row | halo column << 16
+  uint32_t xlds[XSEGS], cbits = 0;
+#pragma unroll
+  for (int s = 0; s < XSEGS; ++s) {
+    const int idx = min(tid + 256 * s, XSEG - 1);
+    const int hp = idx / XV, c = (idx - hp * XV) * 4;
+    const int hy = hp / HW, hx = hp - hy * HW;
+    xhyx[s] = hy | hx << 16;
+    xrel[s] = ((hy - 1) * W + hx - 1) * C + min(c, C - 4);
+    xlds[s] = (uint32_t)((hp * XS + c) * 4);
+    cbits |= (uint32_t)(c < C && tid + 256 * s < XSEG) << s;
+  }
   u32x4 st[XSEGS];
   uint32_t inside_bits = 0;
+  auto tile_origin = [&](int t, int &n, int &ty0, int &tx0) {
+    n = t / tiles_per_image;
+    const int tt = t - n * tiles_per_image;
+    ty0 = (tt / tiles_w) * TH;
+    tx0 = (tt - (tt / tiles_w) * tiles_w) * TW;
+  };
+  // Raw loads now, zero fill when written to LDS (a select right after a
+  // load would make the wave wait for it, serialising the prefetch).
   auto fetch = [&](int t) {
-    const int n = t / tiles_per_image, tt = t - n * tiles_per_image;
-    const int ty0 = (tt / tiles_w) * TH, tx0 = (tt % tiles_w) * TW;
-    const int lt = opaque(tid);
+    int n, ty0, tx0;
+    tile_origin(t, n, ty0, tx0);
+    const float *base = x + ((size_t)(n * H + ty0) * W + tx0) * C;
     inside_bits = 0;
 #pragma unroll
     for (int s = 0; s < XSEGS; ++s) {
-      const int idx = min(lt + 256 * s, XSEG - 1);
-      const int hp = idx / XV, c = (idx - hp * XV) * 4;
-      const int iy = ty0 + hp / HW - 1, ix = tx0 + hp % HW - 1;
-      const bool inside = c < C && iy >= 0 && iy < H && ix >= 0 && ix < W;
-      const int iyc = min(max(iy, 0), H - 1), ixc = min(max(ix, 0), W - 1);
-      st[s] = *reinterpret_cast<const u32x4 *>(
-          x + ((size_t)(n * H + iyc) * W + ixc) * C + min(c, C - 4));
+      const bool inside = ((cbits >> s) & 1u) &&
+                          (unsigned)(ty0 + (xhyx[s] & 0xffff) - 1) < (unsigned)H &&
+                          (unsigned)(tx0 + (xhyx[s] >> 16) - 1) < (unsigned)W;
+      st[s] = *reinterpret_cast<const u32x4 *>(base + (inside ? xrel[s] : 0));
       inside_bits |= (uint32_t)inside << s;
     }
   };
+  char *const xsb = reinterpret_cast<char *>(xs);
   auto commit = [&]() {
-    const int lt = opaque(tid);
 #pragma unroll
-    for (int s = 0; s < XSEGS; ++s) {
-      const int idx = lt + 256 * s;
-      if (idx < XSEG) {
-        const int hp = idx / XV, c = (idx - hp * XV) * 4;
-        *reinterpret_cast<u32x4 *>(xs + hp * XS + c) = masked(st[s], (inside_bits >> s) & 1u);
-      }
-    }
+    for (int s = 0; s < XSEGS; ++s)
+      if (s + 1 < XSEGS || tid + 256 * s < XSEG)
+        *reinterpret_cast<u32x4 *>(xsb + xlds[s]) = masked(st[s], (inside_bits >> s) & 1u);
   };
 
-  // ---- once per workgroup: the first halo, this wave's expand filter
-  //      blocks, every project filter fragment, the depthwise taps (LDS).
+  // ---- once per workgroup: the first halo, every expand and project filter
+  //      fragment (registers), the depthwise taps (LDS).
   fetch(walk.first);
-  Frag16 be[FBW][KC1];
+  // Expand units (filter block fb, pixel block pb), filter-block major, are
+  // split evenly over the four waves; a wave's units span at most NBW
+  // consecutive filter blocks, whose fragments it keeps (A operand: filter
+  // fb*16 + r, input channels kc*16 + 4q .. +3).
+  constexpr int NU = FB1 * HPB;
+  constexpr int NBW = (NU / 4 + 1 + HPB - 1) / HPB + 1;
+  const int fb_lo = wave * NU / 4 / HPB;
+  Frag16 be[NBW][KC1];
 #pragma unroll
-  for (int j = 0; j < FBW; ++j)
+  for (int j = 0; j < NBW; ++j)
 #pragma unroll
     for (int kc = 0; kc < KC1; ++kc) {
-      const int f = min(wave + 4 * j, FB1 - 1) * 16 + r;
       const int k = kc * 16 + 4 * q;
-      Frag16 b = load16(we + f * C + min(k, C - 4));
+      Frag16 b = load16(we + (min(fb_lo + j, FB1 - 1) * 16 + r) * C + min(k, C - 4));
       b.u = masked(b.u, k < C);
       be[j][kc] = b;
     }
+  // project A operand: output channel fb*16 + r, expanded channels kc*16 + 4q .. +3
   Frag16 bp[KC2][FB2];
 #pragma unroll
   for (int kc = 0; kc < KC2; ++kc)
@@ -127,7 +148,7 @@ __global__ __launch_bounds__(256, E >= 192 ? 1 : 2) void irb_kernel(const float 
     reinterpret_cast<f32x4 *>(wds)[i] = reinterpret_cast<const f32x4 *>(wdw)[i];
   commit();
 #pragma unroll
-  for (int j = 0; j < FBW; ++j)
+  for (int j = 0; j < NBW; ++j)
 #pragma unroll
     for (int kc = 0; kc < KC1; ++kc) settle(be[j][kc].u);
 #pragma unroll
@@ -135,6 +156,12 @@ __global__ __launch_bounds__(256, E >= 192 ? 1 : 2) void irb_kernel(const float 
 #pragma unroll
     for (int fb = 0; fb < FB2; ++fb) settle(bp[kc][fb].u);
   __syncthreads();
+
+  // Per-lane constants of the depthwise/project stage: wave w owns output
+  // pixels 16w .. 16w+15 (p), this lane's pixel p = 16w + r.
+  const int p = wave * 16 + r, py = p / TW, px = p - py * TW;
+  const int hbase = py * HW + px;
+  const uint32_t ooff = (uint32_t)(((py * W + px) * C + 4 * q) * 4);
 
   // Pipeline: the halo of tile t+step is in registers while tile t is
   // computed; once every wave is done with xs it goes to LDS and the fetch
@@ -145,51 +172,62 @@ __global__ __launch_bounds__(256, E >= 192 ? 1 : 2) void irb_kernel(const float 
   auto next_of = [&](int t) { return t + walk.step < walk.end ? t + walk.step : t; };
   fetch(next_of(walk.first));
   for (int t = walk.first; t < walk.end; t += walk.step) {
-    const int n = t / tiles_per_image, tt = t - n * tiles_per_image;
-    const int ty0 = (tt / tiles_w) * TH, tx0 = (tt % tiles_w) * TW;
+    int n, ty0, tx0;
+    tile_origin(t, n, ty0, tx0);
 
-    // ---- expand on the halo: wave w computes its filter blocks for all 7
-    //      pixel blocks; the four MFMA steps of a fragment are interleaved
-    //      across the pixel blocks.  Rows past the halo (the last block's 12
-    //      spare rows) read row HP-1: their outputs are never stored.
+    // ---- expand on the halo.  The filters are the A operand and the
+    //      pixels the B operand: a lane's accumulator holds filters 4q..4q+3
+    //      of the block for pixel pb*16 + r, written to LDS as one 16-byte
+    //      store (zero for halo pixels outside the image: the tensor.pad
+    //      before the depthwise).  The pixel blocks of one filter block are
+    //      independent accumulators, interleaved step by step.
+    auto expand = [&](auto wv) {
+      constexpr int U0 = decltype(wv)::value * NU / 4, U1 = (decltype(wv)::value + 1) * NU / 4;
+      constexpr int FLO = U0 / HPB;
+      static_assert((U1 - 1) / HPB - FLO < NBW, "a wave's filter blocks fit its fragments");
 #pragma unroll
-    for (int j = 0; j < FBW; ++j) {
-      const int fb = wave + 4 * j;
-      if (fb >= FB1) break;
-      const int f = fb * 16 + r;
-      f32x4 acc[HPB];
+      for (int fb = U0 / HPB; fb <= (U1 - 1) / HPB; ++fb) {
+        const int p0 = max(U0 - fb * HPB, 0), p1 = min(U1 - fb * HPB, HPB);
+        f32x4 acc[HPB];
 #pragma unroll
-      for (int pb = 0; pb < HPB; ++pb) acc[pb] = f32x4{0.f, 0.f, 0.f, 0.f};
+        for (int pb = p0; pb < p1; ++pb) acc[pb] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int kc = 0; kc < KC1; ++kc) {
-        Frag16 a[HPB];
+        for (int kc = 0; kc < KC1; ++kc) {
+          Frag16 bx[HPB];
 #pragma unroll
-        for (int pb = 0; pb < HPB; ++pb)
-          a[pb] = load16(xs + min(pb * 16 + r, HP - 1) * XS + kc * 16 + 4 * q);
+          for (int pb = p0; pb < p1; ++pb)
+            bx[pb] = load16(xs + min(pb * 16 + r, HP - 1) * XS + kc * 16 + 4 * q);
 #pragma unroll
-        for (int s2 = 0; s2 < 4; ++s2)
+          for (int s2 = 0; s2 < 4; ++s2)
 #pragma unroll
-          for (int pb = 0; pb < HPB; ++pb) MfmaF32::step(acc[pb], a[pb], be[j][kc], s2);
-      }
-      const int lq = opaque(q);
+            for (int pb = p0; pb < p1; ++pb) MfmaF32::step(acc[pb], be[fb - FLO][kc], bx[pb], s2);
+        }
 #pragma unroll
-      for (int pb = 0; pb < HPB; ++pb)
+        for (int pb = p0; pb < p1; ++pb) {
+          const int hp = pb * 16 + r, hy = hp / HW, hx = hp - hy * HW;
+          const bool inside = (unsigned)(ty0 + hy - 1) < (unsigned)H &&
+                              (unsigned)(tx0 + hx - 1) < (unsigned)W;
+          if (pb * 16 + 15 < HP || hp < HP) {
+            f32x4 v;
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const int hp = pb * 16 + 4 * lq + e;
-          if (hp < HP) {
-            const int iy = ty0 + hp / HW - 1, ix = tx0 + hp % HW - 1;
-            const bool inside = iy >= 0 && iy < H && ix >= 0 && ix < W;
-            es[hp * ES + f] = inside ? relu6(acc[pb][e]) : 0.0f;
+            for (int e = 0; e < 4; ++e) v[e] = inside ? relu6(acc[pb][e]) : 0.0f;
+            *reinterpret_cast<f32x4 *>(es + hp * ES + fb * 16 + 4 * q) = v;
           }
         }
+      }
+    };
+    switch (wave) {
+      case 0: expand(std::integral_constant<int, 0>{}); break;
+      case 1: expand(std::integral_constant<int, 1>{}); break;
+      case 2: expand(std::integral_constant<int, 2>{}); break;
+      default: expand(std::integral_constant<int, 3>{}); break;
     }
     __syncthreads();
 
-    // ---- depthwise (in registers, A-operand layout) + project + residual.
-    // Wave w owns output pixels 16w .. 16w+15.
-    const int p = wave * 16 + r;
-    const int hbase = (p / TW) * HW + (p % TW);
+    // ---- depthwise (in registers) + project + residual.  The depthwise
+    //      result of a lane is channels kc*16 + 4q .. +3 of its pixel: the B
+    //      operand of the project MFMA (the project filters are A), so the
+    //      accumulator holds output channels fb*16 + 4q .. +3 of the pixel.
     f32x4 acc2[FB2];
 #pragma unroll
     for (int fb = 0; fb < FB2; ++fb) acc2[fb] = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -207,34 +245,23 @@ __global__ __launch_bounds__(256, E >= 192 ? 1 : 2) void irb_kernel(const float 
       Frag16 a;
       a.f = f32x4{relu6(d[0]), relu6(d[1]), relu6(d[2]), relu6(d[3])};
 #pragma unroll
-      for (int fb = 0; fb < FB2; ++fb) MfmaF32::mma(acc2[fb], a, bp[kc][fb]);
+      for (int fb = 0; fb < FB2; ++fb) MfmaF32::mma(acc2[fb], bp[kc][fb], a);
     }
     // residual added while x is still in LDS; the stores go out after the
     // next halo is committed and the one after it is fetched, so they are
     // the newest memory operations when the loop comes round
-    const int lq = opaque(q);
 #pragma unroll
-    for (int fb = 0; fb < FB2; ++fb) {
-      const int c = min(fb * 16 + r, C - 1);
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const int pe = wave * 16 + 4 * lq + e;
-        acc2[fb][e] += xs[((pe / TW + 1) * HW + (pe % TW) + 1) * XS + c];
-      }
-    }
+    for (int fb = 0; fb < FB2; ++fb)
+      acc2[fb] += *reinterpret_cast<const f32x4 *>(xs + (hbase + HW + 1) * XS + fb * 16 + 4 * q);
     __syncthreads();  // every wave is done with xs and es of this tile
     commit();
     fetch(next_of(next_of(t)));
+    if (ty0 + py < H && tx0 + px < W) {
+      char *ob = reinterpret_cast<char *>(out) + ((size_t)(n * H + ty0) * W + tx0) * C * 4;
 #pragma unroll
-    for (int fb = 0; fb < FB2; ++fb) {
-      const int c = fb * 16 + r;
-      if (c >= C) continue;
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const int pe = wave * 16 + 4 * lq + e;
-        const int oy = ty0 + pe / TW, ox = tx0 + pe % TW;
-        if (oy < H && ox < W) out[((size_t)(n * H + oy) * W + ox) * C + c] = acc2[fb][e];
-      }
+      for (int fb = 0; fb < FB2; ++fb)
+        if (fb * 16 + 4 * q < C)
+          *reinterpret_cast<f32x4 *>(ob + ooff + fb * 64) = acc2[fb];
     }
     __syncthreads();
   }
