@@ -105,6 +105,29 @@ __global__ void lds_read_kernel(int rs, int iters, unsigned long long *cyc) {
   if (threadIdx.x == 0) cyc[0] = t1 - t0;
 }
 
+// Vector-ALU issue rate: 16 waves (four per SIMD) each run `iters` x 8
+// independent 32-bit integer adds; wave 0 times its loop.  With four waves
+// per SIMD the SIMD's issue rate, not a wave's dependency chain, sets the
+// time: clocks per wave instruction per SIMD = cyc / (iters * 8 * 4).
+__global__ void valu_kernel(int iters, int seed, long long *cyc, int *sink) {
+  int a[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) a[i] = (int)threadIdx.x * 7 + i + seed;
+  __syncthreads();
+  const unsigned long long t0 = clock64();
+  for (int it = 0; it < iters; ++it) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) a[i] += seed + i;
+    asm volatile("" ::: "memory");
+  }
+  const unsigned long long t1 = clock64();
+  int acc = 0;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) acc += a[i];
+  if (threadIdx.x == 0) cyc[0] = t1 - t0;
+  if (acc == 0x7fffffff) sink[0] = acc;
+}
+
 // Shader clock over the 100 MHz constant clock.
 __global__ void clock_kernel(long long *out, int spins) {
   if (threadIdx.x != 0) return;
@@ -287,14 +310,29 @@ int main() {
     return 1;
   const double l2_bytes_per_clk_cu = (double)l2n * 16 * reps / (t_l2 * 1e3 * ghz);
 
+  // vector-ALU issue rate (one CU, four waves per SIMD)
+  double valu_clk = 0;
+  {
+    const int iters = 4096;
+    int *dint;
+    CK(hipMalloc(&dint, sizeof(int)));
+    for (int rep = 0; rep < 2; ++rep)
+      hipLaunchKernelGGL(valu_kernel, dim3(1), dim3(1024), 0, 0, iters, 3, dclk, dint);
+    CK(hipDeviceSynchronize());
+    long long c = 0;
+    CK(hipMemcpy(&c, dclk, sizeof c, hipMemcpyDeviceToHost));
+    valu_clk = (double)c / (iters * 8.0 * 4.0);
+    CK(hipFree(dint));
+  }
+
   printf("{\"device\": \"%s\", \"cus\": %d, \"shader_clock_ghz\": %.3f, \"launch_us\": %.3f, "
          "\"launch_full_grid_us\": %.3f, \"graph_launch_us\": %.3f, \"graph_launch_full_grid_us\": %.3f, \"hbm_latency_us\": %.3f, \"hbm_latency_loaded_us\": %.3f, "
          "\"l2_latency_us\": %.3f, \"l2_latency_loaded_us\": %.3f, \"hbm_copy_gbs\": %.1f, \"l2_read_bytes_per_clk_cu\": %.2f, "
          "\"lds_b128_clk_per_wave_instr\": {\"80\": %.1f, \"96\": %.1f, \"128\": %.1f, \"144\": %.1f, \"160\": %.1f}, "
-         "\"lds_bytes_per_clk_cu\": %.1f}\n",
+         "\"lds_bytes_per_clk_cu\": %.1f, \"valu_clk_per_wave_instr\": %.2f, \"valu_instr_per_clk_cu\": %.2f}\n",
          prop.gcnArchName, cus, ghz, t_launch, t_launch_full, t_graph, t_graph_full, lat_hbm, lat_loaded, lat_l2, lat_l2_loaded, copy_gbs,
          l2_bytes_per_clk_cu, lds_clk[0], lds_clk[1], lds_clk[2], lds_clk[3], lds_clk[4],
-         4.0 * 1024 / lds_clk[4]);
+         4.0 * 1024 / lds_clk[4], valu_clk, 4.0 / valu_clk);
   CK(hipFree(src));
   CK(hipFree(dst));
   CK(hipFree(dsink));

@@ -452,8 +452,8 @@ __global__ __launch_bounds__(256, NCH <= 2 ? 2 : 1) void conv3x3_stream_kernel(
 // Vector-ALU instructions per wave and output row of the persistent kernel
 // (counted with SQ_INSTS_VALU less SQ_INSTS_MFMA): a fixed part (epilogue,
 // loop control) and a part per 64-byte input chunk (halo commit, fetch).
-constexpr double STREAM_VALU_ROW_FIXED = 60.0;
-constexpr double STREAM_VALU_ROW_PER_CHUNK = 10.0;
+constexpr double STREAM_VALU_ROW_FIXED = 127.6;
+constexpr double STREAM_VALU_ROW_PER_CHUNK = 0.45;
 
 template <class MM, typename T, int WMAX, int NCH, int WFIX>
 hipError_t launch_stream(const ConvArgs &a, int wgs, hipStream_t s) {

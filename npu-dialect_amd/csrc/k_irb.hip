@@ -278,7 +278,7 @@ hipError_t launch_irb_t(const IrbArgs &a, hipStream_t s) {
     npu_launch_plan p = make_plan("mbv2_inverted_residual", g, wg_per_cu(irb_kernel<C, E>), ntiles, 32);
     p.load_phases = 0;  // the next tile's halo is fetched during this tile
     p.tile_macs = (double)E * HPB * 16 * KC1 * 16 + (double)OP * FB2 * 16 * E;
-    p.tile_valu = 4.0 * 2313 * (E / 144.0);  // counted per wave and tile at E = 144
+    p.tile_valu = 4.0 * 789 * (E / 144.0);  // counted per wave and tile at E = 144
     p.tile_lds_bytes = HP * (KC1 * 16 + 8) * 4.0 +                // halo written
                        (E / 16.0) * KC1 * HPB * 1024 +            // expand A read
                        HP * E * 4.0 +                             // expanded tile written

@@ -38,6 +38,17 @@ __device__ __forceinline__ int clamp_i(int v, int lo, int hi) {
   return v < lo ? lo : (v > hi ? hi : v);
 }
 
+// Requantize four accumulators (output channels c..c+3 of one pixel) and
+// pack them as four bytes, channel c in the low byte.
+__device__ __forceinline__ uint32_t requant4(const i32x4 &acc, const i32x4 &m, const i32x4 &s,
+                                             int lo, int hi) {
+  uint32_t packed = 0;
+#pragma unroll
+  for (int e = 0; e < 4; ++e)
+    packed |= (uint32_t)(clamp_i(requant(acc[e], m[e], s[e]), lo, hi) & 0xff) << (8 * e);
+  return packed;
+}
+
 template <int C, int M1>
 __global__ __launch_bounds__(256) void qbottleneck_kernel(
     const int8_t *__restrict__ x, const int8_t *__restrict__ w1, const int8_t *__restrict__ w2,
@@ -83,13 +94,21 @@ __global__ __launch_bounds__(256) void qbottleneck_kernel(
                        x + ((size_t)(n * H + iyc) * W + ixc) * C + ch * 16),
                    inside);
   }
+  // The filters are each MFMA's A operand and the pixels its B operand, so
+  // a lane's accumulator holds output channels 4q..4q+3 (of a 16-channel
+  // block) of pixel r of a 16-pixel block: it is requantized with four
+  // per-channel scales and leaves as one 4-byte LDS store.
   const int f12 = wave * 16 + r;
   Frag16 b1[C / 64], b2[9];
 #pragma unroll
   for (int kc = 0; kc < C / 64; ++kc) b1[kc] = load16(w1 + f12 * C + kc * 64 + 16 * q);
 #pragma unroll
   for (int t = 0; t < 9; ++t) b2[t] = load16(w2 + (f12 * 9 + t) * M1 + 16 * q);
-  const int mul1 = m1[f12], sh1 = s1[f12], mul2 = m2[f12], sh2 = s2[f12];
+  const int fq = wave * 16 + 4 * q;
+  const i32x4 mul1 = *reinterpret_cast<const i32x4 *>(m1 + fq),
+              sh1 = *reinterpret_cast<const i32x4 *>(s1 + fq),
+              mul2 = *reinterpret_cast<const i32x4 *>(m2 + fq),
+              sh2 = *reinterpret_cast<const i32x4 *>(s2 + fq);
 #pragma unroll
   for (int s = 0; s < SEGS; ++s) {
     const int idx = tid + 256 * s;
@@ -102,32 +121,26 @@ __global__ __launch_bounds__(256) void qbottleneck_kernel(
 
   // conv3's weights are fetched while conv1 and conv2 run.
   Frag16 b3[FB3];
-  int mul3[FB3], sh3[FB3];
 #pragma unroll
-  for (int j = 0; j < FB3; ++j) {
-    const int f = (wave + 4 * j) * 16 + r;
-    b3[j] = load16(w3 + f * M1 + 16 * q);
-    mul3[j] = m3[f];
-    sh3[j] = s3[f];
-  }
+  for (int j = 0; j < FB3; ++j) b3[j] = load16(w3 + ((wave + 4 * j) * 16 + r) * M1 + 16 * q);
 
-  // ---- conv1 (1x1, C -> M1) on all halo pixels, requant + ReLU into y1.
+  // ---- conv1 (1x1, C -> M1) on all halo pixels, requant + ReLU into y1
+  //      (zero for halo pixels outside the image: the pad before conv2).
+  //      Rows past the halo (the last block's 12 spare rows) are written
+  //      too: y1 has room for them and conv2 never reads them.
 #pragma unroll
   for (int pb = 0; pb < HPB; ++pb) {
     i32x4 acc = {0, 0, 0, 0};
 #pragma unroll
     for (int kc = 0; kc < C / 64; ++kc) {
       const Frag16 a = load16(xs + (pb * 16 + r) * XS + kc * 64 + 16 * q);
-      MfmaI8::mma(acc, a, b1[kc]);
+      MfmaI8::mma(acc, b1[kc], a);
     }
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const int hp = pb * 16 + 4 * q + e;
-      const int iy = ty0 + hp / HW - 1, ix = tx0 + hp % HW - 1;
-      const bool inside = hp < HP && iy >= 0 && iy < H && ix >= 0 && ix < W;
-      const int v = inside ? clamp_i(requant(acc[e], mul1, sh1), 0, 127) : 0;
-      y1[hp * YS + f12] = (int8_t)v;
-    }
+    const int hp = pb * 16 + r, hy = hp / HW, hx = hp - hy * HW;
+    const bool inside = hp < HP && (unsigned)(ty0 + hy - 1) < (unsigned)H &&
+                        (unsigned)(tx0 + hx - 1) < (unsigned)W;
+    const uint32_t v = requant4(acc, mul1, sh1, 0, 127);
+    *reinterpret_cast<uint32_t *>(y1 + hp * YS + fq) = inside ? v : 0u;
   }
   __syncthreads();
 
@@ -140,13 +153,9 @@ __global__ __launch_bounds__(256) void qbottleneck_kernel(
 #pragma unroll
     for (int t = 0; t < 9; ++t) {
       const Frag16 a = load16(y1 + (hbase + (t / 3) * HW + (t % 3)) * YS + 16 * q);
-      MfmaI8::mma(acc, a, b2[t]);
+      MfmaI8::mma(acc, b2[t], a);
     }
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const int pe = pb * 16 + 4 * q + e;
-      y2[pe * YS + f12] = (int8_t)clamp_i(requant(acc[e], mul2, sh2), 0, 127);
-    }
+    *reinterpret_cast<uint32_t *>(y2 + p * YS + fq) = requant4(acc, mul2, sh2, 0, 127);
   }
   __syncthreads();
 
@@ -158,18 +167,23 @@ __global__ __launch_bounds__(256) void qbottleneck_kernel(
   for (int pb = 0; pb < OP / 16; ++pb) a3[pb] = load16(y2 + (pb * 16 + r) * YS + 16 * q);
 #pragma unroll
   for (int j = 0; j < FB3; ++j) {
-    const int f = (wave + 4 * j) * 16 + r;
+    const int f4 = (wave + 4 * j) * 16 + 4 * q;
+    const i32x4 mul3 = *reinterpret_cast<const i32x4 *>(m3 + f4),
+                sh3 = *reinterpret_cast<const i32x4 *>(s3 + f4);
 #pragma unroll
     for (int pb = 0; pb < OP / 16; ++pb) {
       i32x4 acc = {0, 0, 0, 0};
-      MfmaI8::mma(acc, a3[pb], b3[j]);
+      MfmaI8::mma(acc, b3[j], a3[pb]);
+      const int p = pb * 16 + r;
+      uint32_t *slot = reinterpret_cast<uint32_t *>(xs + ((p / TW + 1) * HW + (p % TW) + 1) * XS + f4);
+      const uint32_t res = *slot;
+      uint32_t packed = 0;
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        const int pe = pb * 16 + 4 * q + e;
-        const int hp = (pe / TW + 1) * HW + (pe % TW) + 1;
-        const int v = requant(acc[e], mul3[j], sh3[j]) + (int)xs[hp * XS + f];
-        xs[hp * XS + f] = (int8_t)clamp_i(v, 0, 127);
+        const int v = requant(acc[e], mul3[e], sh3[e]) + (int)(int8_t)(res >> (8 * e));
+        packed |= (uint32_t)(clamp_i(v, 0, 127) & 0xff) << (8 * e);
       }
+      *slot = packed;
     }
   }
   __syncthreads();
@@ -186,6 +200,11 @@ __global__ __launch_bounds__(256) void qbottleneck_kernel(
   }
 }
 
+// Vector-ALU instructions per wave and tile (SQ_INSTS_VALU less
+// SQ_INSTS_MFMA): a fixed part and a part per 64 channels of C.
+constexpr double QB_VALU_TILE_FIXED = 453.0;
+constexpr double QB_VALU_TILE_PER_64C = 150.0;
+
 template <int C, int M1>
 hipError_t launch_qb(const QBottleneckArgs &a, hipStream_t s) {
   const int tiles_w = (a.W + TW - 1) / TW, tiles_h = (a.H + TH - 1) / TH;
@@ -196,7 +215,7 @@ hipError_t launch_qb(const QBottleneckArgs &a, hipStream_t s) {
                                   wg_per_cu(qbottleneck_kernel<C, M1>), grid.x * grid.y, 8);
     p.load_phases = 1;  // halo and conv1/conv2 filters together; conv3's during conv1
     p.tile_macs = (double)HPB * 16 * M1 * C + (double)OP * M1 * 9 * M1 + (double)OP * C * M1;
-    p.tile_valu = 4.0 * (1280.0 * (0.25 + 0.75 * C / 256.0));  // counted per wave: 1280 at C = 256
+    p.tile_valu = 4.0 * (QB_VALU_TILE_FIXED + QB_VALU_TILE_PER_64C * C / 64.0);
     p.tile_lds_bytes = HP * (C + 32.0) + 4.0 * HPB * (C / 64) * 1024 + HPB * 16.0 * M1 +
                        4.0 * 4 * 9 * 1024 + OP * M1 + 4.0 * 4 * 1024 + 3.0 * OP * C;
     p.tile_load_bytes = HP * (double)C + 4.0 * 1024 * (C / 64 + 9 + FB3) + 4.0 * 4 * (2 + 2 * FB3) * 64;

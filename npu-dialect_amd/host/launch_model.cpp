@@ -12,22 +12,21 @@ namespace npu {
 
 // Machine constants.  Data sheet: 256 CUs at 2.4 GHz; dense MFMA per CU per
 // clock 128 f32, 2048 bf16 and 4096 i8 multiply-adds (157.3 / 2516.6 /
-// 5033.2 T op/s); 4 SIMDs of 16 lanes, so a wave64 vector instruction takes
-// 4 clocks and a CU issues one per clock.  Measured on an MI355X with
-// npu_calibrate (calib/calibrate.hip) and an LDS read probe: 4.3 TB/s for a
-// 1 GiB device copy, 51 bytes/clock/CU read from L2, 1.2 us dependent-load
-// latency with every CU loading (0.31 us idle; 0.13 us from L2), 186
-// bytes/clock/CU of conflict-free ds_read_b128 (four waves, 22 clocks per
-// wave instruction), 1.58 us per kernel in a captured graph of empty
-// kernels.
+// 5033.2 T op/s).  Measured on an MI355X with npu_calibrate
+// (calib/calibrate.hip): 4.2 TB/s for a 1 GiB device copy, 52 bytes/clock/CU
+// read from L2, 1.2 us dependent-load latency with every CU loading (0.31 us
+// idle; 0.13 us from L2), 204 bytes/clock/CU of conflict-free ds_read_b128
+// (four waves, 20 clocks per wave instruction), one wave64 vector-ALU
+// instruction per SIMD every 2 clocks (2 per CU per clock, four waves per
+// SIMD), 1.58 us per kernel in a captured graph of empty kernels.
 void gpu_params_mi355x(npu_gpu_params *p) {
   p->cus = 256;
   p->reserved = 0;
   p->clock_ghz = 2.4;
   p->hbm_gbs = 4312.0;
   p->l2_bytes_per_clk_cu = 51.0;
-  p->lds_bytes_per_clk_cu = 186.0;
-  p->valu_instr_per_clk_cu = 1.0;
+  p->lds_bytes_per_clk_cu = 204.0;
+  p->valu_instr_per_clk_cu = 2.0;
   p->mfma_macs_per_clk_cu[0] = 128.0;
   p->mfma_macs_per_clk_cu[1] = 2048.0;
   p->mfma_macs_per_clk_cu[2] = 4096.0;

@@ -230,12 +230,14 @@ def test_launch_model_compute_streams():
     """MFMA and vector-ALU issue add up on a SIMD; LDS is the other stream."""
     g = host.mi355x_gpu()
     clk = g.clock_ghz * 1e3
-    # 2048 bf16 MAC/clk/CU: 2048*1000 MACs = 1000 clocks of MFMA, plus 500 VALU instructions
+    # 2048 bf16 MAC/clk/CU: 2048*1000 MACs = 1000 clocks of MFMA, plus 500 VALU
+    # instructions at the CU's vector issue rate
+    assert g.valu_instr_per_clk_cu == 2.0 and g.lds_bytes_per_clk_cu == 204.0  # measured rates
     c = host.predict_launch(_plan(tile_macs=2048.0 * 1000, tile_valu=500.0), g)
-    assert c.tile_compute_us == pytest.approx(1500 / clk)
+    assert c.tile_compute_us == pytest.approx((1000 + 500 / g.valu_instr_per_clk_cu) / clk)
     assert host.BOUNDS[c.bound] == "mfma"
-    # LDS-bound: 186 B/clk/CU
-    c = host.predict_launch(_plan(tile_macs=2048.0 * 10, tile_lds_bytes=186.0 * 4000), g)
+    # LDS-bound: 4000 clocks of LDS reads
+    c = host.predict_launch(_plan(tile_macs=2048.0 * 10, tile_lds_bytes=g.lds_bytes_per_clk_cu * 4000), g)
     assert c.tile_compute_us == pytest.approx(4000 / clk) and host.BOUNDS[c.bound] == "lds"
     # f32 is 16x slower per MAC than bf16
     c32 = host.predict_launch(_plan(tile_macs=128.0 * 1000, mfma_bits=32), g)
