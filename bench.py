@@ -41,6 +41,8 @@ def parse():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--blocks", dest="blocks", action="store_true", default=True)
     ap.add_argument("--no-blocks", dest="blocks", action="store_false")
+    ap.add_argument("--dump-plans", default=None,
+                    help="write every configuration's launch plans and graph time to this JSON file")
     return ap.parse_args()
 
 
@@ -109,8 +111,10 @@ def model_prediction(w):
         w.run(d, o, torch.cuda.current_stream())
     torch.cuda.synchronize()
     total, parts = host.predict_block(cp.plans)
+    plans = [{f: (getattr(pl, f).decode() if f == "kernel" else getattr(pl, f))
+              for f, _ in pl._fields_} for pl in cp.plans]
     return total, [{"kernel": k, "us": round(c.time_us, 3), "bound": host.BOUNDS[c.bound]}
-                   for k, c in parts]
+                   for k, c in parts], plans
 
 
 def cpu_sample(w, budget_s=30.0):
@@ -185,7 +189,8 @@ def main():
     w = configs.by_name(name)
     sec, wall, _ = time_gpu(w, args.steps, args.warmup)
     gsec, gsame = time_graph(w, 20)
-    pred, parts = model_prediction(w)
+    pred, parts, plans = model_prediction(w)
+    dumped = [{"workload": w.name, "graph_us": gsec * 1e6, "plans": plans}]
     line = {
         "metric": "fused-block latency",
         "value": round(sec * 1e6, 3),
@@ -219,7 +224,8 @@ def main():
                 continue
             s, _, _ = time_gpu(other, max(20, args.steps // 2), max(5, args.warmup // 2))
             gs, same = time_graph(other, 20)
-            p, pk = model_prediction(other)
+            p, pk, opl = model_prediction(other)
+            dumped.append({"workload": other.name, "graph_us": gs * 1e6, "plans": opl})
             rl = other.roofline(s)
             blocks.append({"workload": other.name, "latency_us": round(s * 1e6, 3),
                            "traffic": measured_traffic(other.name),
@@ -232,6 +238,9 @@ def main():
         line["blocks"] = blocks
         errs = [abs(line["cost_model"]["error"])] + [abs(b["model_error"]) for b in blocks]
         line["cost_model"]["within_25pct"] = f"{sum(e <= 0.25 for e in errs)}/{len(errs)}"
+    if args.dump_plans:
+        with open(args.dump_plans, "w") as f:
+            json.dump(dumped, f, indent=1)
     print(json.dumps(line), flush=True)
 
 

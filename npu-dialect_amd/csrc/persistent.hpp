@@ -11,6 +11,8 @@
 #pragma once
 #include <hip/hip_runtime.h>
 
+#include "plans.hpp"
+
 namespace npu {
 
 constexpr int kXcds = 8;
@@ -68,19 +70,17 @@ __device__ __forceinline__ void settle(const V &v) {
 
 // Resident workgroups per CU for `kernel` (256 threads), times the CU count,
 // rounded down to whole XCD rounds: the persistent grid.  Queried once per
-// kernel from the runtime (register and LDS use decide it); 0 on failure.
+// kernel and device from the runtime (register and LDS use decide it); 0 on
+// failure.
 template <class K>
 int persistent_grid(K kernel) {
-  static int grid = 0;
-  if (grid == 0) {
-    int dev = 0, cus = 0, per_cu = 0;
-    if (hipGetDevice(&dev) != hipSuccess ||
-        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+  return cached_per_kernel(reinterpret_cast<const void *>(kernel), [&](int dev) {
+    int cus = 0, per_cu = 0;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
         hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, 256, 0) != hipSuccess)
       return 0;
-    grid = (per_cu > 0 ? per_cu : 1) * cus / kXcds * kXcds;
-  }
-  return grid;
+    return (per_cu > 0 ? per_cu : 1) * cus / kXcds * kXcds;
+  });
 }
 
 }  // namespace npu

@@ -6,6 +6,9 @@
 #include <hip/hip_runtime.h>
 
 #include <cstring>
+#include <map>
+#include <mutex>
+#include <utility>
 
 #include "../../include/npu_amd.h"
 
@@ -15,16 +18,33 @@ namespace npu {
 void plans_reset();
 void plans_add(const npu_launch_plan &p);
 
+// Per-kernel, per-device launch facts cached by kernel address (kernels of
+// one signature share a function type, so the type cannot be the key).
+// Returns the cached value of (kernel, current device), computing it with
+// `compute(device)` the first time; 0 if the device cannot be queried or
+// `compute` reports 0.
+template <class F>
+int cached_per_kernel(const void *kernel, F compute) {
+  static std::mutex mu;
+  static std::map<std::pair<const void *, int>, int> cache;
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return 0;
+  std::lock_guard<std::mutex> lock(mu);
+  auto it = cache.find({kernel, dev});
+  if (it != cache.end()) return it->second;
+  const int v = compute(dev);
+  if (v > 0) cache[{kernel, dev}] = v;
+  return v;
+}
+
 // Resident 256-lane workgroups per CU for `kernel`, from the runtime's
-// occupancy calculator (registers and LDS decide it); queried once.
+// occupancy calculator (registers and LDS decide it).
 template <class K>
 int wg_per_cu(K kernel) {
-  static int k = 0;
-  if (k == 0) {
+  return cached_per_kernel(reinterpret_cast<const void *>(kernel), [&](int) {
     int v = 0;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&v, kernel, 256, 0) == hipSuccess) k = v;
-  }
-  return k;
+    return hipOccupancyMaxActiveBlocksPerMultiprocessor(&v, kernel, 256, 0) == hipSuccess ? v : 0;
+  });
 }
 
 inline npu_launch_plan make_plan(const char *kernel, int grid, int per_cu, int tiles,
