@@ -250,17 +250,24 @@ int32_t npu_pass_cost_evaluate(const npu_graph *g, const npu_hw_target *t, const
  * CU's "tiles" being the work tiles its resident workgroups run.  What a GPU
  * adds to that model: several workgroups per CU overlap one another's load
  * latency; compute is the slowest of the MFMA, LDS and vector-ALU streams;
- * every CU shares one HBM.  Per CU with n tiles, k resident workgroups:
- *   compute = max(LDS bytes / LDS rate, macs / MFMA rate + valu / VALU rate)
- *             (a SIMD issues its waves' vector instructions one at a time,
- *             so the MFMA and vector-ALU streams are charged in sequence)
- *   xfer    = (load + store bytes) / per-CU L2 rate
- *   serial  = load_phases * latency + xfer + compute         (one tile alone)
- *   cu      = setup + max(n * max(compute, xfer), n * serial / k)
- *   time    = max(cu, HBM bytes / HBM bandwidth)
- * The machine constants come from the MI355X data sheet (CUs, clock, MFMA
- * rates) and from npu_calibrate (latency, copy bandwidth, L2 and LDS rates,
- * launch cost). */
+ * every CU shares one HBM.  Per CU with n tiles and k resident workgroups
+ * (each of four waves, one per SIMD), in clocks:
+ *   mfma, lds  = macs / MFMA rate, LDS bytes / LDS rate
+ *   valu       = a tile's vector instructions per SIMD (valu / 4), issued by
+ *                one wave every wave_valu_clk clocks, by a SIMD with k waves
+ *                at min(k / wave_valu_clk, valu rate / 4) per clock
+ *   xfer       = (load + store bytes) / per-CU L2 rate
+ *   serial     = load_phases * latency + xfer + mfma + valu (one wave) + lds
+ *                (one tile of one workgroup: its waves' streams in order)
+ *   throughput = n * max(lds, mfma + valu (k waves per SIMD), xfer)
+ *   rounds     = ceil(n / k) * serial       (a workgroup runs its tiles in turn)
+ *   setup      = latency + k * setup bytes / burst rate  (if it has setup data:
+ *                the k workgroups of a CU fetch theirs at once)
+ *   cu         = setup + max(throughput, rounds)
+ *   time       = max(cu / clock, HBM bytes / HBM bandwidth)
+ * The machine constants come from the MI355X data sheet (CUs, MFMA rates)
+ * and from npu_calibrate (clock under MFMA load, latency, copy bandwidth, L2,
+ * LDS and burst rates, vector issue rates, launch cost). */
 typedef struct npu_gpu_params {
   int32_t cus;
   int32_t reserved;
@@ -268,11 +275,14 @@ typedef struct npu_gpu_params {
   double hbm_gbs;               /* achievable HBM bandwidth (device copy)      */
   double l2_bytes_per_clk_cu;   /* L2 -> CU read rate                          */
   double lds_bytes_per_clk_cu;  /* conflict-free 16-byte LDS reads             */
-  double valu_instr_per_clk_cu; /* wave instructions: 4 SIMDs, 4 clocks each   */
+  double valu_instr_per_clk_cu; /* wave vector instructions, four waves/SIMD  */
   double mfma_macs_per_clk_cu[3]; /* f32, bf16, i8 (dense)                    */
   double mem_latency_us;        /* dependent global load with every CU loading */
   double launch_us;             /* per kernel in a captured graph of launches
                                    (an empty kernel's cost, npu_calibrate)    */
+  double wave_valu_clk;         /* clocks between one wave's vector
+                                   instructions                               */
+  double burst_bytes_per_clk_cu; /* one buffer read by every CU at once       */
 } npu_gpu_params;
 void npu_gpu_params_mi355x(npu_gpu_params *p);
 

@@ -32,6 +32,7 @@
 namespace {
 
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 constexpr int kStride = 64;  // int32 slots between chased entries (256 bytes)
 
@@ -126,6 +127,54 @@ __global__ void valu_kernel(int iters, int seed, long long *cyc, int *sink) {
   for (int i = 0; i < 8; ++i) acc += a[i];
   if (threadIdx.x == 0) cyc[0] = t1 - t0;
   if (acc == 0x7fffffff) sink[0] = acc;
+}
+
+// Burst read of one shared buffer by every CU at once: one 256-lane
+// workgroup per CU loads `n16` 16-byte pieces of the same buffer (all
+// issued before any is used), the pattern of a persistent kernel fetching
+// its filter fragments.  Each workgroup records the shader clocks from
+// before its first load to after every lane has its data.
+__global__ void burst_kernel(const u32x4 *__restrict__ src, int n16, long long *cyc, int *sink) {
+  constexpr int kPer = 36;  // loads per lane, issued together
+  __syncthreads();
+  const long long t0 = clock64();
+  u32x4 acc = {0u, 0u, 0u, 0u};
+  for (int base = 0; base < n16; base += 256 * kPer) {
+    u32x4 v[kPer];
+#pragma unroll
+    for (int i = 0; i < kPer; ++i) {
+      const int idx = min(base + i * 256 + (int)threadIdx.x, n16 - 1);
+      v[i] = src[idx];
+    }
+#pragma unroll
+    for (int i = 0; i < kPer; ++i) acc += v[i];
+  }
+  asm volatile("" ::"v"(acc));
+  __syncthreads();
+  const long long t1 = clock64();
+  if (threadIdx.x == 0) cyc[blockIdx.x] = t1 - t0;
+  if (acc[0] == 0x12345678u && acc[1] == 7u) sink[0] = 1;
+}
+
+// Sustained shader clock under a full MFMA load: every CU runs four waves of
+// dependent-free f32 MFMAs for `iters` iterations; wave 0 of workgroup 0
+// reads the shader clock and the 100 MHz clock around its loop.
+__global__ void mfma_clock_kernel(int iters, long long *out, float *sink) {
+  f32x4 acc[4] = {};
+  const float a = (float)threadIdx.x * 1e-3f, b = 1.0f;
+  const long long c0 = clock64(), w0 = wall_clock64();
+  for (int it = 0; it < iters; ++it)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc[j] = __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, acc[j], 0, 0, 0);
+  const long long c1 = clock64(), w1 = wall_clock64();
+  if (blockIdx.x == 0 && threadIdx.x == 0) {
+    out[0] = c1 - c0;
+    out[1] = w1 - w0;
+  }
+  float t = 0;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) t += acc[j][0] + acc[j][1] + acc[j][2] + acc[j][3];
+  if (t == -1.0f) sink[0] = t;
 }
 
 // Shader clock over the 100 MHz constant clock.
@@ -310,29 +359,69 @@ int main() {
     return 1;
   const double l2_bytes_per_clk_cu = (double)l2n * 16 * reps / (t_l2 * 1e3 * ghz);
 
-  // vector-ALU issue rate (one CU, four waves per SIMD)
-  double valu_clk = 0;
+  // vector-ALU issue rate: one CU with four waves per SIMD (the SIMD's
+  // rate), and with one wave per SIMD (a single wave's rate)
+  double valu_clk = 0, wave_valu_clk = 0;
   {
     const int iters = 4096;
     int *dint;
     CK(hipMalloc(&dint, sizeof(int)));
-    for (int rep = 0; rep < 2; ++rep)
-      hipLaunchKernelGGL(valu_kernel, dim3(1), dim3(1024), 0, 0, iters, 3, dclk, dint);
-    CK(hipDeviceSynchronize());
-    long long c = 0;
-    CK(hipMemcpy(&c, dclk, sizeof c, hipMemcpyDeviceToHost));
-    valu_clk = (double)c / (iters * 8.0 * 4.0);
+    for (int waves_per_simd : {4, 1}) {
+      for (int rep = 0; rep < 2; ++rep)
+        hipLaunchKernelGGL(valu_kernel, dim3(1), dim3(256 * waves_per_simd), 0, 0, iters, 3, dclk, dint);
+      CK(hipDeviceSynchronize());
+      long long c = 0;
+      CK(hipMemcpy(&c, dclk, sizeof c, hipMemcpyDeviceToHost));
+      (waves_per_simd == 4 ? valu_clk : wave_valu_clk) = (double)c / (iters * 8.0 * waves_per_simd);
+    }
     CK(hipFree(dint));
+  }
+
+  // burst read of a shared 147456-byte buffer by every CU (the filter
+  // fragments of a 64-filter f32 3x3 workgroup): median over the CUs
+  double burst_bytes_per_clk_cu = 0;
+  {
+    const int n16 = 147456 / 16;
+    int *dint;
+    long long *dcyc;
+    CK(hipMalloc(&dint, sizeof(int)));
+    CK(hipMalloc(&dcyc, cus * sizeof(long long)));
+    for (int rep = 0; rep < 3; ++rep)
+      hipLaunchKernelGGL(burst_kernel, dim3(cus), dim3(256), 0, 0,
+                         reinterpret_cast<const u32x4 *>(src), n16, dcyc, dint);
+    CK(hipDeviceSynchronize());
+    std::vector<long long> cyc(cus);
+    CK(hipMemcpy(cyc.data(), dcyc, cus * sizeof(long long), hipMemcpyDeviceToHost));
+    std::sort(cyc.begin(), cyc.end());
+    burst_bytes_per_clk_cu = 147456.0 / (double)cyc[cus / 2];
+    CK(hipFree(dint));
+    CK(hipFree(dcyc));
+  }
+
+  // shader clock sustained under an all-CU MFMA load
+  double loaded_ghz = 0;
+  {
+    float *dsf;
+    CK(hipMalloc(&dsf, sizeof(float)));
+    for (int rep = 0; rep < 2; ++rep)
+      hipLaunchKernelGGL(mfma_clock_kernel, dim3(cus), dim3(256), 0, 0, 200000, dclk, dsf);
+    CK(hipDeviceSynchronize());
+    long long cw[2];
+    CK(hipMemcpy(cw, dclk, sizeof cw, hipMemcpyDeviceToHost));
+    loaded_ghz = (double)cw[0] / (double)cw[1] * 0.1;
+    CK(hipFree(dsf));
   }
 
   printf("{\"device\": \"%s\", \"cus\": %d, \"shader_clock_ghz\": %.3f, \"launch_us\": %.3f, "
          "\"launch_full_grid_us\": %.3f, \"graph_launch_us\": %.3f, \"graph_launch_full_grid_us\": %.3f, \"hbm_latency_us\": %.3f, \"hbm_latency_loaded_us\": %.3f, "
          "\"l2_latency_us\": %.3f, \"l2_latency_loaded_us\": %.3f, \"hbm_copy_gbs\": %.1f, \"l2_read_bytes_per_clk_cu\": %.2f, "
          "\"lds_b128_clk_per_wave_instr\": {\"80\": %.1f, \"96\": %.1f, \"128\": %.1f, \"144\": %.1f, \"160\": %.1f}, "
-         "\"lds_bytes_per_clk_cu\": %.1f, \"valu_clk_per_wave_instr\": %.2f, \"valu_instr_per_clk_cu\": %.2f}\n",
+         "\"lds_bytes_per_clk_cu\": %.1f, \"valu_clk_per_wave_instr\": %.2f, \"valu_instr_per_clk_cu\": %.2f, "
+         "\"wave_valu_clk\": %.2f, \"burst_bytes_per_clk_cu\": %.1f, \"mfma_loaded_clock_ghz\": %.3f}\n",
          prop.gcnArchName, cus, ghz, t_launch, t_launch_full, t_graph, t_graph_full, lat_hbm, lat_loaded, lat_l2, lat_l2_loaded, copy_gbs,
          l2_bytes_per_clk_cu, lds_clk[0], lds_clk[1], lds_clk[2], lds_clk[3], lds_clk[4],
-         4.0 * 1024 / lds_clk[4], valu_clk, 4.0 / valu_clk);
+         4.0 * 1024 / lds_clk[4], valu_clk, 4.0 / valu_clk, wave_valu_clk, burst_bytes_per_clk_cu,
+         loaded_ghz);
   CK(hipFree(src));
   CK(hipFree(dst));
   CK(hipFree(dsink));

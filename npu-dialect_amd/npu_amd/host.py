@@ -74,7 +74,8 @@ class GpuParams(C.Structure):
         ("hbm_gbs", C.c_double), ("l2_bytes_per_clk_cu", C.c_double),
         ("lds_bytes_per_clk_cu", C.c_double), ("valu_instr_per_clk_cu", C.c_double),
         ("mfma_macs_per_clk_cu", C.c_double * 3), ("mem_latency_us", C.c_double),
-        ("launch_us", C.c_double),
+        ("launch_us", C.c_double), ("wave_valu_clk", C.c_double),
+        ("burst_bytes_per_clk_cu", C.c_double),
     ]
 
 

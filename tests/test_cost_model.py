@@ -226,38 +226,69 @@ def test_launch_model_hbm_bound():
     assert c.time_us == pytest.approx(4.3e9 / (g.hbm_gbs * 1e3))
 
 
+def test_launch_model_measured_constants():
+    """The MI355X constants are npu_calibrate's measurements (sustained clock
+    under MFMA load, vector issue rates, LDS/L2/burst rates, latency)."""
+    g = host.mi355x_gpu()
+    assert (g.cus, g.clock_ghz, g.valu_instr_per_clk_cu, g.wave_valu_clk) == (256, 2.37, 2.0, 8.0)
+    assert (g.lds_bytes_per_clk_cu, g.l2_bytes_per_clk_cu, g.burst_bytes_per_clk_cu) == (204.0, 51.0, 34.4)
+    assert list(g.mfma_macs_per_clk_cu) == [128.0, 2048.0, 4096.0]
+
+
 def test_launch_model_compute_streams():
-    """MFMA and vector-ALU issue add up on a SIMD; LDS is the other stream."""
+    """MFMA and vector-ALU issue add up on a SIMD; LDS is the other stream.
+    A tile's vector instructions are spread over the four SIMDs; one wave
+    issues one every 8 clocks, a SIMD with four or more waves one every 2."""
     g = host.mi355x_gpu()
     clk = g.clock_ghz * 1e3
-    # 2048 bf16 MAC/clk/CU: 2048*1000 MACs = 1000 clocks of MFMA, plus 500 VALU
-    # instructions at the CU's vector issue rate
-    assert g.valu_instr_per_clk_cu == 2.0 and g.lds_bytes_per_clk_cu == 204.0  # measured rates
-    c = host.predict_launch(_plan(tile_macs=2048.0 * 1000, tile_valu=500.0), g)
-    assert c.tile_compute_us == pytest.approx((1000 + 500 / g.valu_instr_per_clk_cu) / clk)
-    assert host.BOUNDS[c.bound] == "mfma"
+    # 2048*1000 bf16 MACs = 1000 clocks of MFMA; 500 instructions = 125 per SIMD
+    one = host.predict_launch(_plan(tile_macs=2048.0 * 1000, tile_valu=500.0), g)
+    assert one.tile_compute_us == pytest.approx((1000 + 125 * 8) / clk)          # one wave per SIMD
+    four = host.predict_launch(_plan(tile_macs=2048.0 * 1000, tile_valu=500.0, wg_per_cu=4,
+                                     grid=1024, tiles=1024), g)
+    assert four.tile_compute_us == pytest.approx((1000 + 125 * 2) / clk)         # four waves per SIMD
+    assert host.BOUNDS[four.bound] == "mfma"
     # LDS-bound: 4000 clocks of LDS reads
-    c = host.predict_launch(_plan(tile_macs=2048.0 * 10, tile_lds_bytes=g.lds_bytes_per_clk_cu * 4000), g)
+    c = host.predict_launch(_plan(tile_macs=2048.0 * 10, tile_lds_bytes=g.lds_bytes_per_clk_cu * 4000,
+                                  wg_per_cu=2, grid=512, tiles=512), g)
     assert c.tile_compute_us == pytest.approx(4000 / clk) and host.BOUNDS[c.bound] == "lds"
     # f32 is 16x slower per MAC than bf16
     c32 = host.predict_launch(_plan(tile_macs=128.0 * 1000, mfma_bits=32), g)
     assert c32.tile_compute_us == pytest.approx(1000 / clk)
 
 
-def test_launch_model_pipeline_and_occupancy():
-    """n tiles per CU: one dependent load per tile is hidden by a second
-    resident workgroup (the reference's pipelined tile formula per CU)."""
+def test_launch_model_rounds_and_occupancy():
+    """n tiles per CU: a workgroup runs its tiles one after another (its
+    waves' streams in order, after its load), so k resident workgroups take
+    ceil(n / k) rounds of that serial time, unless the CU's MFMA stream binds
+    first."""
     g = host.mi355x_gpu()
     clk = g.clock_ghz * 1e3
-    base = dict(tiles=256 * 8, grid=256, tile_macs=2048.0 * 3000, load_phases=1)
-    one = host.predict_launch(_plan(wg_per_cu=1, **base), g)
-    two = host.predict_launch(_plan(wg_per_cu=2, grid=512, **{k: v for k, v in base.items() if k != "grid"}), g)
-    serial = g.mem_latency_us + 3000 / clk
-    assert one.tiles_per_cu == 8
-    assert one.cu_us == pytest.approx(g.mem_latency_us + 8 * serial)       # setup + 8 serial tiles
-    # two overlap their loads; then the MFMA stream itself (8 x 3000 clocks) binds
-    assert two.cu_us == pytest.approx(g.mem_latency_us + max(8 * 3000 / clk, 8 * serial / 2))
-    assert host.BOUNDS[one.bound] == "latency" and host.BOUNDS[two.bound] == "mfma"
+    lat = g.mem_latency_us * clk
+    base = dict(tiles=256 * 8, tile_macs=2048.0 * 3000, load_phases=1)
+    one = host.predict_launch(_plan(wg_per_cu=1, grid=256, **base), g)
+    two = host.predict_launch(_plan(wg_per_cu=2, grid=512, **base), g)
+    serial = lat + 3000
+    assert one.tiles_per_cu == 8 and one.tile_serial_us == pytest.approx(serial / clk)
+    assert one.cu_us == pytest.approx(8 * serial / clk)                       # 8 rounds
+    assert host.BOUNDS[one.bound] == "latency"
+    # two workgroups: 4 rounds of serial time, against 8 x 3000 clocks of MFMA
+    assert two.cu_us == pytest.approx(max(4 * serial, 8 * 3000) / clk)
+    # ragged: 3 tiles on a CU with 2 workgroups take 2 rounds
+    rag = host.predict_launch(_plan(wg_per_cu=2, grid=512, tiles=256 * 3, load_phases=1,
+                                    tile_macs=2048.0 * 10), g)
+    assert rag.cu_us == pytest.approx(2 * (lat + 10) / clk)
+
+
+def test_launch_model_setup_burst():
+    """Setup data (filters fetched once per workgroup) costs a latency plus
+    the k resident workgroups' bytes at the all-CU burst rate; none without."""
+    g = host.mi355x_gpu()
+    clk = g.clock_ghz * 1e3
+    base = dict(tiles=256, tile_macs=2048.0 * 10, wg_per_cu=2, grid=512)
+    none = host.predict_launch(_plan(**base), g)
+    some = host.predict_launch(_plan(wg_setup_bytes=34.4 * 1000, **base), g)
+    assert some.cu_us - none.cu_us == pytest.approx(g.mem_latency_us + 2 * 1000 / clk)
 
 
 def test_launch_model_rejects_empty_plan():
