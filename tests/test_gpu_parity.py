@@ -404,3 +404,48 @@ def test_c5_layer_small_shapes(cuda, S, D, H, F):
     torch.cuda.synchronize()
     for name, (ref, mag) in refs.llama_reference(inp, H, LL_EPS).items():
         check_bound(bf16(_host(o[name])), bf16(ref), mag, RTOL_BF16, what=f"layer {name}")
+
+
+# ------------------------------------------------------------------ host lowering
+@pytest.mark.parametrize("case", ["matmul", "conv_f32", "conv_bf16", "inverted_residual"])
+def test_lowered_blocks_match_the_oracle(cuda, case):
+    """linalg text -> npu_amd.lower -> entry-point calls on the GPU, against
+    the oracle of the same block."""
+    from npu_amd import blocks, lower
+    if case == "matmul":
+        A = rng.uniform(15, 0, (64, 96), -1, 1)
+        B = rng.uniform(15, 1, (96, 48), -1, 1)
+        b = rng.uniform(15, 2, (48,), -1, 1)
+        prog = lower.lower_text(blocks.matmul_bias_act(64, 96, 48, act="relu6"))
+        out = prog.run({"A": _dev(A), "B": _dev(B), "bias": _dev(b)})["%y"]
+        torch.cuda.synchronize()
+        ref, mag = refs.matmul_bias_act(A, B, b, "relu6")
+        check_bound(_host(out), ref, mag, RTOL_F32, what="lowered matmul")
+    elif case.startswith("conv"):
+        elem = "bf16" if case == "conv_bf16" else "f32"
+        x = rng.uniform(16, 0, (2, 9, 7, 32), 0, 1)
+        w = rng.normal(16, 1, (64, 3, 3, 32), 0, math.sqrt(2 / (9 * 32)))
+        b = rng.uniform(16, 2, (64,), -0.1, 0.1)
+        if elem == "bf16":
+            x, w = rng.to_bf16_bits(x), rng.to_bf16_bits(w)
+        prog = lower.lower_text(blocks.conv_bias_act(2, 9, 7, 32, 64, elem=elem))
+        out = prog.run({"x": _dev(x), "w": _dev(w), "bias": _dev(b)})["%y"]
+        torch.cuda.synchronize()
+        ref, mag = refs.conv_bias_act(x, w, b, 1, "relu")
+        if elem == "f32":
+            check_bound(_host(out), ref, mag, RTOL_F32, what="lowered conv")
+        else:
+            check_bound(bf16(_host(out)), bf16(ref), mag, RTOL_BF16, what="lowered conv")
+    else:
+        N, H, W, C, E = 2, 9, 13, 24, 144
+        x = rng.uniform(17, 0, (N, H, W, C), 0, 1)
+        we = rng.normal(17, 1, (E, C), 0, math.sqrt(2 / C))
+        wdw = rng.normal(17, 2, (3, 3, E), 0, math.sqrt(2 / 9))
+        wp = rng.normal(17, 3, (C, E), 0, math.sqrt(2 / E))
+        prog = lower.lower_text(blocks.inverted_residual(N, H, W, C, E))
+        assert prog.entry_points == ["fused_irb_f32"]
+        out = prog.run({"x": _dev(x), "we": _dev(we.reshape(E, 1, 1, C)), "wdw": _dev(wdw),
+                        "wp": _dev(wp.reshape(C, 1, 1, E))})["%y"]
+        torch.cuda.synchronize()
+        ref, mag = refs.irb(x, we, wdw, wp)
+        check_bound(_host(out), ref, mag, RTOL_F32, what="lowered inverted residual")
