@@ -284,24 +284,31 @@ __global__ __launch_bounds__(256) void llama_gemm_kernel(const LlamaGemmArgs a) 
 // slots gives the same sum, so lane (r, q)'s eight slots of a 32-key step
 // are its own keys {4q..4q+3, 16+4q..16+4q+3}, and the V^T operand is read
 // in that same key order (two 8-byte LDS reads).  P never goes through LDS.
-constexpr int AQ = 64;          // queries per workgroup (4 waves x 16)
+constexpr int AQ = 64;          // queries per workgroup (4 waves x 16, per key group)
 constexpr int AK = 64;          // keys per block
 constexpr int LDK = 64 + 16;  // LDS row stride of K rows and V^T rows (elements): 160 bytes
 
-__global__ __launch_bounds__(256) void llama_attention_kernel(const uint16_t *__restrict__ Q,
+// Two key groups of four waves: waves 0-3 take the even key blocks, waves
+// 4-7 the odd ones, for the same 64 queries, each group with its own staged
+// K/V blocks; at the end group 1 hands its online-softmax state (max, sum,
+// unnormalised output) to group 0 through LDS, which merges the two and
+// stores.  Against one group this halves the longest chain of key blocks and
+// puts two waves on every SIMD.
+__global__ __launch_bounds__(512) void llama_attention_kernel(const uint16_t *__restrict__ Q,
                                                               const uint16_t *__restrict__ K,
                                                               const uint16_t *__restrict__ V,
                                                               uint16_t *__restrict__ O, int S,
                                                               int H, float scale) {
   constexpr int DH = 64;
   constexpr float kLog2e = 1.4426950408889634f;
-  __shared__ __attribute__((aligned(16))) uint16_t Ks[2][AK * LDK];   // [key][d]
-  __shared__ __attribute__((aligned(16))) uint16_t Vt[2][DH * LDK];   // [d][key]
+  __shared__ __attribute__((aligned(16))) uint16_t Ks[2][2][AK * LDK];   // [group][buf][key][d]
+  __shared__ __attribute__((aligned(16))) uint16_t Vt[2][2][DH * LDK];   // [group][buf][d][key]
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int kg = wave >> 2, qw = wave & 3, gt = tid & 255;  // key group, query wave, lane in group
   const int r = lane & 15, q = lane >> 4;
   const int q0 = blockIdx.x * AQ, h = blockIdx.y;
   const int D = H * DH;
-  const int i0 = q0 + wave * 16;  // this wave's first query row
+  const int i0 = q0 + qw * 16;  // this wave's first query row
   const int row = i0 + r;         // this lane's query
 
   // query rows past S read row S-1: their outputs are never stored
@@ -316,8 +323,8 @@ __global__ __launch_bounds__(256) void llama_attention_kernel(const uint16_t *__
   // V lanes: 32 consecutive lanes take 32 consecutive key pairs of one
   // 8-wide d group, so the transposed 4-byte LDS writes of a wave hit
   // consecutive words instead of one bank.
-  const int kr = tid >> 2, kd = (tid & 3) * 16;        // K: key kr, d kd..kd+15
-  const int vk = (tid & 31) * 2, vd = (tid >> 5) * 8;  // V: keys vk, vk+1; d vd..vd+7
+  const int kr = gt >> 2, kd = (gt & 3) * 16;        // K: key kr, d kd..kd+15
+  const int vk = (gt & 31) * 2, vd = (gt >> 5) * 8;  // V: keys vk, vk+1; d vd..vd+7
   u32x4 sk[2], sv[2];
   uint32_t okbits = 0;
   auto fetch = [&](int kb) {
@@ -336,11 +343,11 @@ __global__ __launch_bounds__(256) void llama_attention_kernel(const uint16_t *__
   auto commit = [&](int buf) {
 #pragma unroll
     for (int s2 = 0; s2 < 2; ++s2)
-      *reinterpret_cast<u32x4 *>(&Ks[buf][kr * LDK + kd + 8 * s2]) = masked(sk[s2], okbits & 1u);
+      *reinterpret_cast<u32x4 *>(&Ks[kg][buf][kr * LDK + kd + 8 * s2]) = masked(sk[s2], okbits & 1u);
     const u32x4 v0 = masked(sv[0], (okbits >> 1) & 1u), v1 = masked(sv[1], (okbits >> 2) & 1u);
 #pragma unroll
     for (int j = 0; j < 8; ++j)
-      *reinterpret_cast<uint32_t *>(&Vt[buf][(vd + j) * LDK + vk]) = pair_word(v0, v1, j);
+      *reinterpret_cast<uint32_t *>(&Vt[kg][buf][(vd + j) * LDK + vk]) = pair_word(v0, v1, j);
   };
 
   // online softmax state of query `row`, in the log2 domain
@@ -352,24 +359,27 @@ __global__ __launch_bounds__(256) void llama_attention_kernel(const uint16_t *__
 
   const int kend = min(q0 + AQ, S);  // keys beyond the block's last query are masked for all
   const int nblocks = (kend + AK - 1) / AK;
-  fetch(0);
+  const int nsteps = (nblocks + 1) / 2;  // each step: one block per key group
+  fetch(min(kg, nblocks - 1) * AK);
   commit(0);
   __syncthreads();
-  // fetch and commit are unconditional (the last round refetches the last
-  // block into the idle buffer): with a condition on either, the compiler's
-  // wait analysis drains every outstanding load at the loop head.
-  for (int blk = 0; blk < nblocks; ++blk) {
+  // fetch and commit are unconditional (past its last block a group
+  // refetches the last block into its idle buffer): with a condition on
+  // either, the compiler's wait analysis drains every outstanding load at the
+  // loop head.
+  for (int step = 0; step < nsteps; ++step) {
+    const int blk = 2 * step + kg;
     const int kb = blk * AK;
-    fetch(min(blk + 1, nblocks - 1) * AK);
-    const int buf = blk & 1;
-    if (kb <= i0 + 15) {  // some key of the block is visible to this wave (uniform)
+    fetch(min(blk + 2, nblocks - 1) * AK);
+    const int buf = step & 1;
+    if (blk < nblocks && kb <= i0 + 15) {  // some key of the block is visible to this wave (uniform)
       f32x4 s[4];         // s[ct][e]: score of key kb + 16ct + 4q + e
 #pragma unroll
       for (int ct = 0; ct < 4; ++ct) {
         s[ct] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int ks = 0; ks < 2; ++ks) {
-          const Frag16 kf = load16(&Ks[buf][(16 * ct + r) * LDK + 32 * ks + 8 * q]);
+          const Frag16 kf = load16(&Ks[kg][buf][(16 * ct + r) * LDK + 32 * ks + 8 * q]);
           MfmaBF16::mma(s[ct], kf, qb[ks]);
         }
       }
@@ -416,7 +426,7 @@ __global__ __launch_bounds__(256) void llama_attention_kernel(const uint16_t *__
 #pragma unroll
         for (int dt = 0; dt < 4; ++dt) {
           // A operand: V^T rows d = 16dt + r, the same keys in the same slots
-          const uint16_t *vrow = &Vt[buf][(16 * dt + r) * LDK + 32 * ks + 4 * q];
+          const uint16_t *vrow = &Vt[kg][buf][(16 * dt + r) * LDK + 32 * ks + 4 * q];
           const uint2 lo = *reinterpret_cast<const uint2 *>(vrow);
           const uint2 hi = *reinterpret_cast<const uint2 *>(vrow + 16);
           Frag16 va;
@@ -427,6 +437,33 @@ __global__ __launch_bounds__(256) void llama_attention_kernel(const uint16_t *__
     }
     commit(buf ^ 1);
     __syncthreads();
+  }
+  // merge: group 1's state goes through LDS (the K stage is free: every wave
+  // passed the loop's last barrier) to the group-0 wave with the same rows;
+  // a state that saw no key has max -inf and contributes nothing
+  float *xch = reinterpret_cast<float *>(&Ks[0][0][0]);  // 4 waves x 64 lanes x 18 floats
+  static_assert(4 * 64 * 18 * 4 <= 2 * 2 * AK * LDK * 2, "the exchange fits the K stage");
+  float *st = xch + (qw * 64 + lane) * 18;
+  if (kg == 1) {
+    st[0] = m2;
+    st[1] = l;
+#pragma unroll
+    for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) st[2 + 4 * dt + e] = o[dt][e];
+  }
+  __syncthreads();
+  if (kg == 1) return;
+  {
+    const float m1 = st[0], l1 = st[1];
+    const float mm = fmaxf(m2, m1);
+    const float c0 = (m2 == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(m2 - mm);
+    const float c1 = (m1 == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(m1 - mm);
+    l = l * c0 + l1 * c1;
+#pragma unroll
+    for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) o[dt][e] = o[dt][e] * c0 + st[2 + 4 * dt + e] * c1;
   }
   if (row < S) {
     const float inv = 1.0f / l;
@@ -500,9 +537,11 @@ hipError_t launch_llama_attention(const uint16_t *Q, const uint16_t *K, const ui
     // (nqb + 1) / 2 key blocks; every key block costs QK^T and PV MFMAs, the
     // online-softmax update, and one staged K and V^T block.
     const int nqb = grid.x;
-    const double kblocks = (nqb + 1) / 2.0;
-    npu_launch_plan p = make_plan("llama_causal_attention", grid.x * grid.y,
-                                  wg_per_cu(llama_attention_kernel), grid.x * grid.y, 16);
+    const double kblocks = (nqb + 1) / 4.0;
+    // a workgroup is two key groups of four waves: planned as two 4-wave
+    // units per query block, each walking half of its key blocks
+    npu_launch_plan p = make_plan("llama_causal_attention", 2 * grid.x * grid.y,
+                                  wg_per_cu(llama_attention_kernel, 512), 2 * grid.x * grid.y, 16);
     p.load_phases = 1;
     p.tile_macs = kblocks * 2.0 * AQ * AK * 64;
     p.tile_valu = 4.0 * (150.0 + 335.0 * kblocks);  // counted: 1659 per wave at 4.5 blocks
@@ -512,7 +551,7 @@ hipError_t launch_llama_attention(const uint16_t *Q, const uint16_t *K, const ui
     p.hbm_bytes = 4.0 * S * H * 64 * 2;  // Q, K, V in, O out
     plans_add(p);
   }
-  hipLaunchKernelGGL(llama_attention_kernel, grid, dim3(256), 0, s, Q, K, V, O, S, H, scale);
+  hipLaunchKernelGGL(llama_attention_kernel, grid, dim3(512), 0, s, Q, K, V, O, S, H, scale);
   return hipGetLastError();
 }
 

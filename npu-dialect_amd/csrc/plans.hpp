@@ -37,13 +37,17 @@ int cached_per_kernel(const void *kernel, F compute) {
   return v;
 }
 
-// Resident 256-lane workgroups per CU for `kernel`, from the runtime's
-// occupancy calculator (registers and LDS decide it).
+// Resident four-wave units per CU for `kernel` launched with `threads`
+// lanes per workgroup (resident workgroups x threads / 256), from the
+// runtime's occupancy calculator (registers and LDS decide it): the waves
+// each SIMD holds.
 template <class K>
-int wg_per_cu(K kernel) {
+int wg_per_cu(K kernel, int threads = 256) {
   return cached_per_kernel(reinterpret_cast<const void *>(kernel), [&](int) {
     int v = 0;
-    return hipOccupancyMaxActiveBlocksPerMultiprocessor(&v, kernel, 256, 0) == hipSuccess ? v : 0;
+    return hipOccupancyMaxActiveBlocksPerMultiprocessor(&v, kernel, threads, 0) == hipSuccess
+               ? v * threads / 256
+               : 0;
   });
 }
 
