@@ -20,6 +20,9 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <type_traits>
+#include <utility>
+
 namespace npu {
 
 typedef float f32x4 __attribute__((ext_vector_type(4)));
@@ -131,10 +134,81 @@ __device__ __forceinline__ float act_clamp(float v, ActBounds b) {
   return __builtin_elementwise_minimum(__builtin_elementwise_maximum(v, b.lo), b.hi);
 }
 
+// f(std::integral_constant<int, 0>{}) ... f(std::integral_constant<int, N-1>{}),
+// in order: a loop whose body indexes register arrays by its counter, unrolled
+// whatever its length (a `#pragma unroll` loop that the compiler declines to
+// unroll moves such arrays to scratch memory).
+template <class Fn, int... I>
+__device__ __forceinline__ void static_for_impl(Fn &&f, std::integer_sequence<int, I...>) {
+  (f(std::integral_constant<int, I>{}), ...);
+}
+template <int N, class Fn>
+__device__ __forceinline__ void static_for(Fn &&f) {
+  static_for_impl(f, std::make_integer_sequence<int, N>{});
+}
+
 __device__ __forceinline__ Frag16 load16(const void *p) {
   Frag16 r;
   r.u = *reinterpret_cast<const u32x4 *>(p);
   return r;
+}
+
+// ---- f32 products on the bf16 matrix pipe ----------------------------------
+// An f32 value a splits exactly into three bf16 parts, a = h + m + l: h is a
+// with its low 16 bits cleared (its top 8 significant bits; never rounds up
+// to Inf), m is r = a - h rounded to nearest even, and l = r - m, which has
+// at most 8 significant bits and so is a bf16 exactly.  |m| < 2^-7 |a| and
+// |l| <= 2^-8 |m|.  A product a*b is summed from the six part products
+// mm, lh, hl, mh, hm, hh (smallest first); the three left out (ml, lm, ll)
+// add up to less than 2^-21 |a b|.  This is the bf16x6 scheme of Henry,
+// Tang and Heinecke, "Leveraging the bfloat16 Artificial Intelligence
+// Datatype For Higher-Precision Computations" (ARITH 2019), with a
+// truncating first split.  On gfx950 a bf16 MFMA (16 clocks for 16x16x32)
+// does the 16x work of an f32 MFMA (32 clocks for 16x16x4), so the six
+// products take 6 * 16 clocks where the f32 instructions take 8 * 32.
+//
+// Special values: a NaN gives a NaN h (or, when its payload lies in the low
+// bits only, an infinite h and NaN r, m, l), so NaN propagates.  An
+// infinite a gives h = a and r = Inf - Inf = NaN: an infinite operand gives
+// NaN where the f32 sum gives +-Inf.  (Splitting it into (a, 0, 0) would not
+// help: the products of a with the zero parts of a finite b are Inf * 0.)
+struct Parts4 {  // parts of four f32 values, two bf16 per dword
+  uint2 h, m, l;
+};
+__device__ __forceinline__ uint32_t pack_high_halves(uint32_t lo, uint32_t hi) {
+  return __builtin_amdgcn_perm(hi, lo, 0x07060302u);  // (lo >> 16) | (hi & 0xffff0000)
+}
+__device__ __forceinline__ uint32_t cvt_pk_bf16(float a, float b) {
+  typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+  bf16x2 v;
+  v[0] = (__bf16)a;
+  v[1] = (__bf16)b;
+  return __builtin_bit_cast(uint32_t, v);
+}
+__device__ __forceinline__ Parts4 split_parts(u32x4 v) {
+  float r[4];
+  uint32_t hb[4];
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    hb[e] = v[e] & 0xffff0000u;
+    r[e] = __uint_as_float(v[e]) - __uint_as_float(hb[e]);  // exact
+  }
+  Parts4 p;
+  p.h = make_uint2(pack_high_halves(hb[0], hb[1]), pack_high_halves(hb[2], hb[3]));
+  p.m = make_uint2(cvt_pk_bf16(r[0], r[1]), cvt_pk_bf16(r[2], r[3]));
+  const float s0 = r[0] - __uint_as_float(p.m.x << 16), s1 = r[1] - __uint_as_float(p.m.x & 0xffff0000u);
+  const float s2 = r[2] - __uint_as_float(p.m.y << 16), s3 = r[3] - __uint_as_float(p.m.y & 0xffff0000u);
+  p.l = make_uint2(cvt_pk_bf16(s0, s1), cvt_pk_bf16(s2, s3));
+  return p;
+}
+// acc += A * B over one 32-long k run, A and B given as their three parts.
+__device__ __forceinline__ void mma_x6(f32x4 &acc, const Frag16 (&a)[3], const Frag16 (&b)[3]) {
+  acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[1].h, b[1].h, acc, 0, 0, 0);
+  acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[2].h, b[0].h, acc, 0, 0, 0);
+  acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[0].h, b[2].h, acc, 0, 0, 0);
+  acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[1].h, b[0].h, acc, 0, 0, 0);
+  acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[0].h, b[1].h, acc, 0, 0, 0);
+  acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[0].h, b[0].h, acc, 0, 0, 0);
 }
 
 }  // namespace npu

@@ -171,6 +171,54 @@ def test_c2_nan_propagates(cuda, N, H, W, C, F):
     check_bound(got[ok], ref[ok], mag[ok], RTOL_F32, what="conv with NaN")
 
 
+@pytest.mark.parametrize("kind", ["full_mantissa", "wide_exponents", "constant"])
+def test_c2_f32_bf16_split_parity(cuda, kind):
+    """The f32 persistent conv multiplies on the bf16 pipe with each value
+    split into three bf16 parts (six part products).  Values whose 24-bit
+    significands are all used, values spread over 2^-20..2^20, and constant
+    inputs (every product rounds the same way, so dropped terms add up
+    coherently) all stay within the f32 bound of the oracle."""
+    N, H, W, C, F = 64, 16, 56, 64, 64
+    x = rng.uniform(15, 0, (N, H, W, C), 0.5, 1)
+    w = rng.normal(15, 1, (F, 3, 3, C), 0, math.sqrt(2 / (9 * C)))
+    b = rng.uniform(15, 2, (F,), -0.1, 0.1)
+    if kind == "full_mantissa":
+        # set every low significand bit: the h and m parts both matter
+        x = (x.view(np.uint32) | np.uint32(0x7FFF)).view(np.float32)
+        w = (w.view(np.uint32) | np.uint32(0x7FFF)).view(np.float32)
+    elif kind == "wide_exponents":
+        e = rng.randint(15, 3, (N, H, W, C), -20, 20)
+        x = (x * np.exp2(e)).astype(np.float32)
+    else:
+        x = np.full((N, H, W, C), 1.0 + 2.0 ** -9 + 2.0 ** -17 + 2.0 ** -23, np.float32)
+        w = np.full((F, 3, 3, C), -(0.75 + 2.0 ** -10 + 2.0 ** -19 + 2.0 ** -22) / 64, np.float32)
+    out = torch.empty(N, H, W, F, device="cuda", dtype=torch.float32)
+    groups.fused_conv2d_nhwc_bias_act(_dev(x), _dev(w), _dev(b), out, 1, "none")
+    torch.cuda.synchronize()
+    imgs = [0, N - 1]
+    ref, mag = refs.conv_bias_act(x[imgs], w, b, 1, "none")
+    check_bound(_host(out)[imgs], ref, mag, RTOL_F32, what=f"f32 conv, {kind}")
+
+
+def test_c2_f32_infinite_input_gives_nan(cuda):
+    """Documented deviation of the f32 persistent conv: an infinite input
+    splits into Inf plus NaN parts (Inf - Inf), so the outputs it reaches
+    are NaN where the f32 sum gives +-Inf; every other output is unchanged."""
+    N, H, W, C, F = 64, 16, 56, 64, 64
+    x = rng.uniform(16, 0, (N, H, W, C), 0, 1)
+    x[3, 7, 20, 5] = np.inf
+    w = rng.normal(16, 1, (F, 3, 3, C), 0, math.sqrt(2 / (9 * C)))
+    out = torch.empty(N, H, W, F, device="cuda", dtype=torch.float32)
+    groups.fused_conv2d_nhwc_bias_act(_dev(x), _dev(w), None, out, 1, "none")
+    torch.cuda.synchronize()
+    got = _host(out)[3]
+    ref, mag = refs.conv_bias_act(x[3:4], w, None, 1, "none")
+    ref, mag = ref[0], mag[0]
+    hit = ~np.isfinite(ref)
+    assert hit.sum() == 9 * F and np.isnan(got[hit]).all()
+    check_bound(got[~hit], ref[~hit], mag[~hit], RTOL_F32, what="f32 conv next to an Inf")
+
+
 def test_c1_nan_propagates(cuda):
     A = rng.uniform(14, 0, (64, 128), -1, 1)
     A[5, 17] = np.nan
