@@ -454,29 +454,34 @@ __global__ __launch_bounds__(256, NCH <= 2 ? 2 : 1) void conv3x3_stream_kernel(
 // 32-channel run is multiplied with the six part products (mma_x6): 6 x 16
 // MFMA clocks where the f32 MFMA takes 8 x 32.
 //
+// Eight waves, two per SIMD: with one wave per SIMD every LDS read and
+// vector instruction of the wave would stall its own MFMAs; with two, one
+// wave's reads and splits issue while the other's MFMAs run.  Waves w and
+// w + 4 share filter group w & 3 (16 of the workgroup's 64 filters) and
+// split the rest of the work: with 64 channels, wave half c takes channel
+// run c and the two partial sums meet in LDS; with 32 channels, it takes the
+// 16-pixel blocks c, c + 2, ... of the tile.  A wave's filter fragments
+// (nine taps, three parts, its run) stay in registers for the whole walk.
+//
 // The halo is a ring of NSLOT row slots in LDS (a slot: W + 2 records of a
 // pixel's three parts, C bf16 each, then 32 bytes of padding, a record
 // stride of 32 mod 64 bytes).  A tile of TR rows reads TR + 2 slots; the
 // next tile of the same image shares two of them and needs TR new rows,
 // which are fetched into registers a tile ahead, split during this tile's
-// multiply (a 16-byte run every few MFMA groups, in the shadow of the
-// matrix pipe) and written straight into the TR slots this tile does not
-// read.  So each input row is fetched and split once per workgroup, plus the
-// two rows a range or image starts with.  A tile that starts an image has
-// all of its rows written after the previous tile has finished (no prefetch).
-//
-// The filters (this wave's 16, all nine taps) stay in registers as MFMA A
-// fragments; tap 0 is split before the walk, taps 1..8 during the first
-// tile's multiply, each a few MFMA groups before its first use.  Outputs
-// leave straight from the accumulators: a lane holds filters 4q..4q+3 of
-// pixel r of each 16-pixel block, one 16-byte buffer store per block, the
-// buffer's extent ending at the tile so stores past it are dropped.
+// multiply and written straight into the TR slots this tile does not read.
+// So each input row is fetched and split once per workgroup, plus the two
+// rows a range or image starts with.  A tile that starts an image has all
+// of its rows written after the previous tile has finished.  Outputs leave
+// straight from the accumulators: a lane holds filters 4q..4q+3 of pixel r
+// of a 16-pixel block, one 16-byte buffer store per block, the buffer's
+// extent ending at the tile so stores past it are dropped.
 template <int WMAX, int NCX, int WFIX>
-__global__ __launch_bounds__(256, 1) void conv3x3_x6_kernel(
+__global__ __launch_bounds__(512, 1) void conv3x3_x6_kernel(
     const float *__restrict__ x, const float *__restrict__ w, const float *__restrict__ bias,
     float *__restrict__ out, int H, int w_rt, int F, int act, int nrows) {
   const int W = WFIX > 0 ? WFIX : w_rt;
   constexpr int C = 32 * NCX;                        // channels: NCX runs of 32
+  constexpr bool KSPLIT = NCX == 2;                  // wave halves split the channel runs (else blocks)
   constexpr int TR = WMAX <= 56 ? 2 : 1;             // output rows per tile (LDS bounds the ring)
   constexpr int NSLOT = 2 * TR + 2;                  // a tile's TR + 2 halo rows and the next tile's TR
   constexpr int SEGP = C / 4;                        // 16-byte f32 runs per input pixel
@@ -484,53 +489,65 @@ __global__ __launch_bounds__(256, 1) void conv3x3_x6_kernel(
   constexpr int RECB = 3 * PST + 32;                 // LDS halo record (bytes)
   constexpr int HCMAX = WMAX + 2;
   constexpr int SLOTB = HCMAX * RECB;                // bytes per row slot
-  constexpr int LPR = (HCMAX * SEGP + 255) / 256;    // loads per halo row
+  constexpr int NT = 512;                            // threads
+  constexpr int LPR = (HCMAX * SEGP + NT - 1) / NT;  // loads per halo row
   constexpr int NBT = (TR * WMAX + 15) / 16;         // 16-pixel blocks of a full tile
   constexpr int NB1 = (WMAX + 15) / 16;              // ... of a 1-row tile
-  constexpr int FPI = 64 / SEGP;                     // filter runs per load instruction
-  constexpr int NWI = 16 / FPI;                      // load instructions per tap
-  constexpr int WSR = PST + 32;                      // filter staging record: one part of one filter
+  constexpr int NBW = KSPLIT ? NBT : (NBT + 1) / 2;  // blocks per wave, full tile
+  constexpr int NBW1 = KSPLIT ? NB1 : (NB1 + 1) / 2; // ... 1-row tile
+  constexpr int NXB = (NBW + 1) / 2;                 // blocks per partial-sum exchange round
+  constexpr int FPI = 8, NWI = 2;                    // filter loads: 8 filters' 128-byte runs per instruction, 2 per tap
+  constexpr int WSR = 64 + 32;                       // filter staging record: one part of one filter's run
   constexpr int HALOB = NSLOT * SLOTB;
   constexpr int TRASHB = 64 * 8 + 2 * PST;           // lanes' 8-byte trash slots plus the part offsets
-  constexpr int STAGEB = 4 * 16 * WSR;
-  static_assert(HALOB + TRASHB + STAGEB <= 160 * 1024, "LDS");
-  __shared__ __attribute__((aligned(16))) char lds[HALOB + TRASHB + STAGEB];
+  constexpr int XB_SUM = KSPLIT ? 4 * NXB * 64 * 16 : 0;
+  constexpr int XB_STAGE = 8 * 16 * WSR;
+  constexpr int XB = XB_SUM > XB_STAGE ? XB_SUM : XB_STAGE;  // partial sums, or filter staging (before the walk)
+  static_assert(HALOB + TRASHB + XB <= 160 * 1024, "LDS");
+  __shared__ __attribute__((aligned(16))) char lds[HALOB + TRASHB + XB];
   char *const halo = lds;
+  char *const xch = lds + HALOB + TRASHB;
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int r = lane & 15, q = lane >> 4;
+  const int fg = wave & 3, half = wave >> 2;         // filter group; wave half
+  const int run = KSPLIT ? half : 0;                 // this wave's channel run
   const RowRange range = row_range(nrows);
   const size_t row_bytes = (size_t)W * C * 4;
   auto tile_rows = [&](int g) __attribute__((always_inline)) { return min(min(TR, range.end - g), H - g % H); };
 
-  // Pixel blocks: pixel i*16 + r of the tile lies in tile row prow and
-  // halo column pcol + 1 (the +1 and the tap's column shift are folded into
-  // the read offsets).
-  uint32_t colb[NBT];
-  uint32_t prow = 0;  // bit i: block i's pixel of this lane is in the tile's second row
+  // This wave's blocks: b = ii (channel split) or half + 2 ii (block split);
+  // pixel b*16 + r of the tile lies in tile row bit ii of prow, halo
+  // column pcol + 1 (the +1 and the tap's column shift are folded into the
+  // read offsets, and so is the channel run).
+  uint32_t colb[NBW];
+  uint32_t prow = 0;
 #pragma unroll
-  for (int i = 0; i < NBT; ++i) {
-    const int p = min(i * 16 + r, TR * W - 1);
+  for (int ii = 0; ii < NBW; ++ii) {
+    const int b = KSPLIT ? ii : half + 2 * ii;
+    const int p = min(b * 16 + r, TR * W - 1);
     const int pr = p / W, pc = p - pr * W;
-    colb[i] = (uint32_t)(pc * RECB + q * 16);
-    prow |= (uint32_t)pr << i;
+    colb[ii] = (uint32_t)(pc * RECB + run * 64 + q * 16);
+    prow |= (uint32_t)pr << ii;
   }
-  // Halo row fetch: load j covers the row's 16-byte runs tid + 256 j.
+  // Halo row fetch: load j covers the row's 16-byte runs tid + NT j.
   // goff: byte offset in the input row (column clamped into the image);
   // loff: byte offset of the run's h part within a slot, or ~0u for a lane
   // with no record (past the row, or a zero-padding column).
   uint32_t goff[LPR], loff[LPR];
 #pragma unroll
   for (int j = 0; j < LPR; ++j) {
-    const int idx = tid + 256 * j, idxc = min(idx, (W + 2) * SEGP - 1);
+    const int idx = tid + NT * j, idxc = min(idx, (W + 2) * SEGP - 1);
     const int hc = idxc / SEGP, seg = idxc - hc * SEGP;
     goff[j] = (uint32_t)(min(max(hc - 1, 0), W - 1) * C * 4 + seg * 16);
     const bool rec = idx < (W + 2) * SEGP && hc >= 1 && hc <= W;
     loff[j] = rec ? (uint32_t)(hc * RECB + seg * 8) : ~0u;
   }
   const uint32_t trash = (uint32_t)(HALOB + lane * 8);
-  auto waddr = [&](int slot, int j) __attribute__((always_inline)) { return loff[j] == ~0u ? trash : (uint32_t)(slot * SLOTB) + loff[j]; };
-  auto load_row = [&](u32x4 (&dst)[LPR], int grow) {  // grow: a row of the input, in range
+  auto waddr = [&](int slot, int j) __attribute__((always_inline)) {
+    return loff[j] == ~0u ? trash : (uint32_t)(slot * SLOTB) + loff[j];
+  };
+  auto load_row = [&](u32x4 (&dst)[LPR], int grow) __attribute__((always_inline)) {  // grow: an input row
     const char *rb = reinterpret_cast<const char *>(x) + (size_t)grow * row_bytes;
 #pragma unroll
     for (int j = 0; j < LPR; ++j) dst[j] = *reinterpret_cast<const u32x4 *>(rb + goff[j]);
@@ -575,7 +592,7 @@ __global__ __launch_bounds__(256, 1) void conv3x3_x6_kernel(
   };
   // The next tile's new rows (its halo rows 2..TR+1: image rows gn+1..gn+TR
   // for a tile starting at gn), fetched a tile ahead.  Unconditional (rows
-  // clamped into the image): a fetch under a condition would make the
+  // clamped into the input): a fetch under a condition would make the
   // compiler drain every outstanding load at the loop head.
   u32x4 nraw[TR][LPR];
   auto prefetch = [&](int gn) __attribute__((always_inline)) {
@@ -587,99 +604,97 @@ __global__ __launch_bounds__(256, 1) void conv3x3_x6_kernel(
 
   if (range.first >= range.end) return;  // uniform over the workgroup
   // Issue order matters (the counter of outstanding loads is in order):
-  // the first tile's rows, the filters, the bias, then the next tile's new
-  // rows, each waited for in that order.
-  fetch_tile(range.first);
-  // Filters: each tap's 16 runs (of this wave's 16 filters) are loaded
-  // whole (SEGP lanes per run, full cache lines), split, and turned into
-  // A fragments one part at a time through this wave's staging slot.
-  // Taps 0..WA-1 are loaded here, tap t+WA-1 while tap t is staged.
-  constexpr int WA = 4;
+  // the filters (from L2, split while the rest arrives), the first tile's
+  // rows, the bias, then the next tile's new rows, each waited for in that
+  // order.
+  // Filters: this wave's 16 filters, its channel run, every tap: 128-byte
+  // runs loaded whole, split, and turned into A fragments one part at a time
+  // through this wave's staging slot (record stride WSR).
   u32x4 wraw[9][NWI];
-  const char *const wb = reinterpret_cast<const char *>(w) + (size_t)(blockIdx.y * 4 + wave) * 16 * 9 * C * 4;
-  auto load_tap = [&](int t) __attribute__((always_inline)) {
-    const int fl = lane / SEGP, pc = lane - fl * SEGP;
+  {
+    const char *wb = reinterpret_cast<const char *>(w) + ((size_t)(blockIdx.y * 4 + fg) * 16 * 9 * C + run * 32) * 4;
+    const int fl = lane / 8, pc = lane - fl * 8;
 #pragma unroll
-    for (int i = 0; i < NWI; ++i)
-      wraw[t][i] = *reinterpret_cast<const u32x4 *>(wb + ((size_t)(fl + FPI * i) * 9 + t) * C * 4 + pc * 16);
-  };
-#pragma unroll
-  for (int t = 0; t < WA; ++t) load_tap(t);
-  const int fq = (blockIdx.y * 4 + wave) * 16 + 4 * q;
-  float bv[4];
-#pragma unroll
-  for (int e = 0; e < 4; ++e) bv[e] = bias ? bias[fq + e] : 0.0f;
-  const ActBounds ab = act_bounds(act);
-  Frag16 fr[9 * NCX][3];  // [tap * NCX + run][part]
-  Parts4 wp[NWI];
-  char *const wslot = lds + HALOB + TRASHB + wave * 16 * WSR;
-  auto split_tap_run = [&](int t, int i) __attribute__((always_inline)) { wp[i] = split_parts(wraw[t][i]); };
-  auto stage_tap = [&](int t) __attribute__((always_inline)) {  // the split runs of tap t -> its fragments
-    const int fl = lane / SEGP, pc = lane - fl * SEGP;
-#pragma unroll
-    for (int k = 0; k < 3; ++k) {
+    for (int t = 0; t < 9; ++t)
 #pragma unroll
       for (int i = 0; i < NWI; ++i)
-        *reinterpret_cast<uint2 *>(wslot + (fl + FPI * i) * WSR + pc * 8) = k == 0 ? wp[i].h : k == 1 ? wp[i].m : wp[i].l;
+        wraw[t][i] = *reinterpret_cast<const u32x4 *>(wb + ((size_t)(fl + FPI * i) * 9 + t) * C * 4 + pc * 16);
+  }
+  fetch_tile(range.first);
+  const int fq = (blockIdx.y * 4 + fg) * 16 + 4 * q;
+  float bv[4];
 #pragma unroll
-      for (int c = 0; c < NCX; ++c) fr[t * NCX + c][k] = load16(wslot + r * WSR + c * 64 + q * 16);
-    }
-  };
-
+  for (int e = 0; e < 4; ++e) bv[e] = bias && (!KSPLIT || half == 0) ? bias[fq + e] : 0.0f;
+  const ActBounds ab = act_bounds(act);
   prefetch(range.first + tile_rows(range.first));
+  Frag16 fr[9][3];  // [tap][part]
+  {
+    char *const wslot = xch + wave * 16 * WSR;
+    const int fl = lane / 8, pc = lane - fl * 8;
+#pragma unroll
+    for (int t = 0; t < 9; ++t) {
+      Parts4 p[NWI];
+#pragma unroll
+      for (int i = 0; i < NWI; ++i) p[i] = split_parts(wraw[t][i]);
+#pragma unroll
+      for (int k = 0; k < 3; ++k) {
+#pragma unroll
+        for (int i = 0; i < NWI; ++i)
+          *reinterpret_cast<uint2 *>(wslot + (fl + FPI * i) * WSR + pc * 8) = k == 0 ? p[i].h : k == 1 ? p[i].m : p[i].l;
+        fr[t][k] = load16(wslot + r * WSR + q * 16);
+      }
+    }
+  }
   int base = 0;  // slot of the current tile's halo row 0
   put_tile(range.first, base);
-#pragma unroll
-  for (int i = 0; i < NWI; ++i) split_tap_run(0, i);
-  stage_tap(0);
   // zero-padding columns 0 and W+1 of every slot (lanes write no record there)
   constexpr int ZR = 3 * PST / 16;  // 16-byte runs of a record's parts
-  for (int i = tid; i < NSLOT * 2 * ZR; i += 256) {
+  for (int i = tid; i < NSLOT * 2 * ZR; i += NT) {
     const int s = i / (2 * ZR), k = i - s * 2 * ZR, side = k / ZR, seg = k - side * ZR;
     *reinterpret_cast<u32x4 *>(halo + s * SLOTB + side * (W + 1) * RECB + seg * 16) = u32x4{0u, 0u, 0u, 0u};
   }
 #pragma unroll
   for (int e = 0; e < 4; ++e) settle(bv[e]);
-  __syncthreads();
+#pragma unroll
+  for (int t = 0; t < 9; ++t)
+#pragma unroll
+    for (int k = 0; k < 3; ++k) settle(fr[t][k].u);
+  __syncthreads();  // halo, padding and every wave's filter staging done (staging shares the exchange area)
 
-  auto tile = [&](int g, auto first) __attribute__((always_inline)) {
-    constexpr bool FIRST = decltype(first)::value;
+  for (int g = range.first; g < range.end; g += tile_rows(g)) {
     const int rows = tile_rows(g);
     const int bnext = (base + rows) % NSLOT;  // the next tile's halo row 0
-    // this tile's read bases: block i, tap row dy -> slot of halo row (its row + dy)
-    uint32_t rb[NBT][3];
+    // read bases: block ii, tap row dy -> slot of halo row (its row + dy)
+    uint32_t rb[NBW][3];
 #pragma unroll
     for (int dy = 0; dy < 3; ++dy) {
       const uint32_t s0 = (uint32_t)((base + dy) % NSLOT * SLOTB), s1 = (uint32_t)((base + dy + 1) % NSLOT * SLOTB);
 #pragma unroll
-      for (int i = 0; i < NBT; ++i) rb[i][dy] = ((prow >> i) & 1u ? s1 : s0) + colb[i];
+      for (int ii = 0; ii < NBW; ++ii) rb[ii][dy] = ((prow >> ii) & 1u ? s1 : s0) + colb[ii];
     }
     // the next tile's new rows go to its slots 2..TR+1 (slots this tile does
     // not read); rows past the image are zero
-    const int gn = g + rows, nn = gn / H, hn = gn - nn * H;
+    const int gn = g + rows, hn = gn % H;
     uint32_t nok = 0;
 #pragma unroll
     for (int k = 0; k < TR; ++k) nok |= (uint32_t)(hn + 1 + k < H) << k;
-    f32x4 acc[NBT];
+    f32x4 acc[NBW];
 #pragma unroll
-    for (int i = 0; i < NBT; ++i) acc[i] = f32x4{bv[0], bv[1], bv[2], bv[3]};
-    // Steps s = (tap-run j, block i) in order; each reads its block's three
+    for (int ii = 0; ii < NBW; ++ii) acc[ii] = f32x4{bv[0], bv[1], bv[2], bv[3]};
+    // Steps s = (tap t, block ii) in order; each reads its block's three
     // pixel parts from LDS D steps ahead and issues six MFMAs.  From a third
-    // of the way in, one new-row run is split and written every SPS steps;
-    // in the first tile, tap t's filters are split during tap t-1's steps.
+    // of the way in, one new-row run is split and written every SPS steps.
     // The scheduling barrier keeps each step's work in its own region.
     auto multiply = [&](auto nblk) __attribute__((always_inline)) {
       constexpr int NB = decltype(nblk)::value;
-      constexpr int TAPS = NCX * NB;  // steps per tap
-      static_assert(NWI + 2 <= TAPS, "a tap's filters are staged within the previous tap's steps");
-      constexpr int NS = 9 * TAPS, D = 2, RB = D + 1;
+      constexpr int NS = 9 * NB, D = 2, RB = D + 1;
       constexpr int NSPL = TR * LPR, S0 = NS / 3;
       constexpr int SPS = (NS - S0 - 2) / NSPL > 0 ? (NS - S0 - 2) / NSPL : 1;
       static_assert(S0 + SPS * (NSPL - 1) < NS, "every new-row run is written within the multiply");
       Frag16 px[RB][3];
-      auto load_px = [&](Frag16 (&dst)[3], int s) {
-        const int j = s / NB, i = s - j * NB, t = j / NCX, c = j - t * NCX;
-        const char *src = halo + rb[i][t / 3] + (t % 3) * RECB + c * 64;
+      auto load_px = [&](Frag16 (&dst)[3], int s) __attribute__((always_inline)) {
+        const int t = s / NB, ii = s - t * NB;
+        const char *src = halo + rb[ii][t / 3] + (t % 3) * RECB;
 #pragma unroll
         for (int k = 0; k < 3; ++k) dst[k] = load16(src + k * PST);
       };
@@ -698,49 +713,68 @@ __global__ __launch_bounds__(256, 1) void conv3x3_x6_kernel(
           else
             zero_run(a);
         }
-        if constexpr (FIRST && s / TAPS + 1 < 9) {
-          constexpr int t = s / TAPS + 1, u = s % TAPS;
-          if constexpr (u < NWI) split_tap_run(t, u);
-          if constexpr (u == NWI) stage_tap(t);
-          if constexpr (u == NWI + 1 && t + WA - 1 < 9) load_tap(t + WA - 1);
-        }
         __builtin_amdgcn_sched_barrier(0);
       });
     };
     if constexpr (TR == 1)
-      multiply(std::integral_constant<int, NBT>{});
+      multiply(std::integral_constant<int, NBW>{});
     else if (rows == TR)
-      multiply(std::integral_constant<int, NBT>{});
+      multiply(std::integral_constant<int, NBW>{});
     else
-      multiply(std::integral_constant<int, NB1>{});
+      multiply(std::integral_constant<int, NBW1>{});
     // outputs: the buffer ends at the tile, so stores of pixels past it drop
-    {
-      const int npx = rows * W;
-      const __amdgpu_buffer_rsrc_t o = __builtin_amdgcn_make_buffer_rsrc(
-          reinterpret_cast<char *>(out) + ((size_t)g * W * F + blockIdx.y * 64 + wave * 16) * 4, (short)0,
-          (npx - 1) * F * 4 + 64, 0x00020000);
+    const int npx = rows * W;
+    const __amdgpu_buffer_rsrc_t o = __builtin_amdgcn_make_buffer_rsrc(
+        reinterpret_cast<char *>(out) + ((size_t)g * W * F + blockIdx.y * 64 + fg * 16) * 4, (short)0,
+        (npx - 1) * F * 4 + 64, 0x00020000);
+    auto store = [&](int b, f32x4 a) __attribute__((always_inline)) {
+      f32x4 v;
 #pragma unroll
-      for (int i = 0; i < NBT; ++i) {
-        f32x4 v;
+      for (int e = 0; e < 4; ++e) v[e] = act_clamp(a[e], ab);
+      __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v), o,
+                                             (uint32_t)((b * 16 + r) * F * 4 + q * 16), 0, 0);
+    };
+    if constexpr (KSPLIT) {
+      // The two partial sums of a block meet in LDS: blocks [0, NXB) are
+      // finished by half 0, [NXB, NBW) by half 1, in two rounds through an
+      // exchange area of NXB blocks per filter group.
+      char *const xg = xch + fg * NXB * 1024 + lane * 16;
+      if (half == 1) {
 #pragma unroll
-        for (int e = 0; e < 4; ++e) v[e] = act_clamp(acc[i][e], ab);
-        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v), o,
-                                               (uint32_t)((i * 16 + r) * F * 4 + q * 16), 0, 0);
+        for (int ii = 0; ii < NXB; ++ii) *reinterpret_cast<f32x4 *>(xg + ii * 1024) = acc[ii];
       }
+      __syncthreads();
+      if (half == 0) {
+#pragma unroll
+        for (int ii = 0; ii < NXB; ++ii) acc[ii] += *reinterpret_cast<const f32x4 *>(xg + ii * 1024);
+#pragma unroll
+        for (int ii = NXB; ii < NBW; ++ii) *reinterpret_cast<f32x4 *>(xg + (ii - NXB) * 1024) = acc[ii];
+      }
+      __syncthreads();
+      if (half == 0) {
+#pragma unroll
+        for (int ii = 0; ii < NXB; ++ii) store(ii, acc[ii]);
+      } else {
+#pragma unroll
+        for (int ii = NXB; ii < NBW; ++ii) store(ii, acc[ii] + *reinterpret_cast<const f32x4 *>(xg + (ii - NXB) * 1024));
+      }
+    } else {
+#pragma unroll
+      for (int ii = 0; ii < NBW; ++ii) store(half + 2 * ii, acc[ii]);
+      __syncthreads();  // every wave's multiply (halo reads) and new-row writes are done
     }
-    // the tile after next: fetched now, written during the next tile
+    // The tile after next: fetched now, written during the next tile.  With
+    // the channel split no further barrier is needed here: the exchange
+    // barriers already follow every wave's multiply and new-row writes, and
+    // a wave's next exchange writes come after its own reads of this one.
     prefetch(gn + tile_rows(min(gn, range.end - 1)));
-    __syncthreads();  // this tile's halo reads and the next tile's new rows are done
     if (gn < range.end && hn == 0) {  // the next tile starts an image: its rows were not prefetched
       fetch_tile(gn);
       put_tile(gn, bnext);
       __syncthreads();
     }
     base = bnext;
-  };
-  tile(range.first, std::integral_constant<bool, true>{});
-  for (int g = range.first + tile_rows(range.first); g < range.end; g += tile_rows(g))
-    tile(g, std::integral_constant<bool, false>{});
+  }
 }
 
 // Vector-ALU instructions per wave and output row of the persistent kernel
@@ -791,7 +825,7 @@ constexpr double X6_VALU_ROW_PER_RUN = 30.0;
 
 template <int WMAX, int NCX, int WFIX>
 hipError_t launch_x6(const ConvArgs &a, hipStream_t s) {
-  const int wgs = persistent_grid(conv3x3_x6_kernel<WMAX, NCX, WFIX>);
+  const int wgs = persistent_grid(conv3x3_x6_kernel<WMAX, NCX, WFIX>, 512);
   if (wgs == 0) return hipErrorInvalidDeviceFunction;
   if (a.W > WMAX || (WFIX > 0 && a.W != WFIX) || a.C != 32 * NCX || a.F % 64 != 0 || wgs % kXcds != 0)
     return hipErrorInvalidValue;
@@ -802,7 +836,7 @@ hipError_t launch_x6(const ConvArgs &a, hipStream_t s) {
     constexpr int TR = 2, PBW = (TR * WMAX + 15) / 16, RECB = 6 * 32 * NCX + 32;
     constexpr int LPR = ((WMAX + 2) * 8 * NCX + 255) / 256;
     npu_launch_plan p = make_plan("conv3x3_f32_bf16x6", wgs * grid.y,
-                                  wg_per_cu(conv3x3_x6_kernel<WMAX, NCX, WFIX>), nrows * grid.y, 16);
+                                  wg_per_cu(conv3x3_x6_kernel<WMAX, NCX, WFIX>, 512), nrows * grid.y, 16);
     p.load_phases = 0;  // the next tile's halo is fetched during this tile
     p.tile_macs = 6.0 * 4.0 * (PBW / 2.0) * 256 * 9 * a.C;
     p.tile_valu = 4.0 * (X6_VALU_ROW_FIXED + X6_VALU_ROW_PER_RUN * 4 * LPR / 2.0);
@@ -816,7 +850,7 @@ hipError_t launch_x6(const ConvArgs &a, hipStream_t s) {
                   (a.bias ? 4.0 * a.F : 0.0);
     plans_add(p);
   }
-  hipLaunchKernelGGL((conv3x3_x6_kernel<WMAX, NCX, WFIX>), grid, dim3(256), 0, s,
+  hipLaunchKernelGGL((conv3x3_x6_kernel<WMAX, NCX, WFIX>), grid, dim3(512), 0, s,
                      static_cast<const float *>(a.x), static_cast<const float *>(a.w), a.bias,
                      static_cast<float *>(a.out), a.H, a.W, a.F, a.act, nrows);
   return hipGetLastError();

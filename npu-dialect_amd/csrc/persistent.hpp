@@ -68,16 +68,16 @@ __device__ __forceinline__ void settle(const V &v) {
   asm volatile("" ::"v"(v));
 }
 
-// Resident workgroups per CU for `kernel` (256 threads), times the CU count,
-// rounded down to whole XCD rounds: the persistent grid.  Queried once per
-// kernel and device from the runtime (register and LDS use decide it); 0 on
-// failure.
+// Resident workgroups per CU for `kernel` (launched with `threads` lanes per
+// workgroup), times the CU count, rounded down to whole XCD rounds: the
+// persistent grid.  Queried once per kernel and device from the runtime
+// (register and LDS use decide it); 0 on failure.
 template <class K>
-int persistent_grid(K kernel) {
+int persistent_grid(K kernel, int threads = 256) {
   return cached_per_kernel(reinterpret_cast<const void *>(kernel), [&](int dev) {
     int cus = 0, per_cu = 0;
     if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
-        hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, 256, 0) != hipSuccess)
+        hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, threads, 0) != hipSuccess)
       return 0;
     return (per_cu > 0 ? per_cu : 1) * cus / kXcds * kXcds;
   });
