@@ -209,7 +209,8 @@ def main():
         "throughput": {"value": w.units / sec, "unit": f"{w.unit_name}/s"},
         "wall_s_timed_region": wall,
         "roofline": dict(w.roofline(sec), traffic=measured_traffic(w.name),
-                         flops=w.flops, bytes=w.bytes, floor_us=w.floor_s() * 1e6),
+                         flops=w.flops, mfma_flops=w.mfma_flops, bytes=w.bytes,
+                         floor_us=w.floor_s() * 1e6),
         "graph_us": round(gsec * 1e6, 3),
         "graph_matches_eager": gsame,
         "cost_model": {"predicted_us": round(pred, 3), "measured_us": round(gsec * 1e6, 3),

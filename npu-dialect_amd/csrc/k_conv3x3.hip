@@ -626,7 +626,9 @@ __global__ __launch_bounds__(512, 1) void conv3x3_x6_kernel(
 #pragma unroll
   for (int e = 0; e < 4; ++e) bv[e] = bias && (!KSPLIT || half == 0) ? bias[fq + e] : 0.0f;
   const ActBounds ab = act_bounds(act);
-  prefetch(range.first + tile_rows(range.first));
+  // (past the range: the first tile's own rows again, already in L2)
+  const int g1 = range.first + tile_rows(range.first);
+  prefetch(g1 < range.end ? g1 : range.first);
   Frag16 fr[9][3];  // [tap][part]
   {
     char *const wslot = xch + wave * 16 * WSR;
@@ -767,7 +769,9 @@ __global__ __launch_bounds__(512, 1) void conv3x3_x6_kernel(
     // the channel split no further barrier is needed here: the exchange
     // barriers already follow every wave's multiply and new-row writes, and
     // a wave's next exchange writes come after its own reads of this one.
-    prefetch(gn + tile_rows(min(gn, range.end - 1)));
+    // (past the range: this tile's rows again, fetched a tile ago and still in L2)
+    const int g2 = gn + tile_rows(min(gn, range.end - 1));
+    prefetch(g2 < range.end ? g2 : g);
     if (gn < range.end && hn == 0) {  // the next tile starts an image: its rows were not prefetched
       fetch_tile(gn);
       put_tile(gn, bnext);
@@ -819,9 +823,9 @@ hipError_t launch_stream(const ConvArgs &a, int wgs, hipStream_t s) {
 }
 
 // Vector-ALU instructions per wave and output row of the f32 walk on the
-// bf16 pipe: the halo split (about 30 per 16-byte run) on top of the walk.
-constexpr double X6_VALU_ROW_FIXED = 127.6;
-constexpr double X6_VALU_ROW_PER_RUN = 30.0;
+// bf16 pipe (SQ_INSTS_VALU less SQ_INSTS_MFMA over the 32x56x56x64 -> 64
+// launch: 1592 per wave for 7 rows).
+constexpr double X6_VALU_ROW_WAVE = 227.4;
 
 template <int WMAX, int NCX, int WFIX>
 hipError_t launch_x6(const ConvArgs &a, hipStream_t s) {
@@ -832,18 +836,19 @@ hipError_t launch_x6(const ConvArgs &a, hipStream_t s) {
   const int nrows = a.N * a.H;
   dim3 grid(wgs, a.F / 64);
   {
-    // one output row is the plan's work unit; 6 bf16 MACs per f32 MAC
-    constexpr int TR = 2, PBW = (TR * WMAX + 15) / 16, RECB = 6 * 32 * NCX + 32;
-    constexpr int LPR = ((WMAX + 2) * 8 * NCX + 255) / 256;
+    // One output row is the plan's work unit; 6 bf16 MACs per f32 MAC.
+    // Each input row is fetched, split and written to the halo ring once.
+    constexpr int TR = WMAX <= 56 ? 2 : 1, NBT = (TR * WMAX + 15) / 16, RECB = 6 * 32 * NCX + 32;
+    constexpr double BLOCKS_ROW = (double)NBT / TR;  // 16-pixel blocks per output row
     npu_launch_plan p = make_plan("conv3x3_f32_bf16x6", wgs * grid.y,
                                   wg_per_cu(conv3x3_x6_kernel<WMAX, NCX, WFIX>, 512), nrows * grid.y, 16);
-    p.load_phases = 0;  // the next tile's halo is fetched during this tile
-    p.tile_macs = 6.0 * 4.0 * (PBW / 2.0) * 256 * 9 * a.C;
-    p.tile_valu = 4.0 * (X6_VALU_ROW_FIXED + X6_VALU_ROW_PER_RUN * 4 * LPR / 2.0);
-    p.tile_lds_bytes = 2.0 * (a.W + 2) * RECB +                  // halo written
-                       2.0 * PBW * 9 * NCX * 3 * 1024 +          // pixel parts read
-                       2.0 * a.W * (64 * 4 + 32);                // output staged and read
-    p.tile_load_bytes = 2.0 * (a.W + 2) * a.C * 4;
+    p.load_phases = 0;  // the next tile's new rows are fetched a tile ahead
+    p.tile_macs = 6.0 * 4.0 * BLOCKS_ROW * 256 * 9 * a.C;
+    p.tile_valu = 8.0 * X6_VALU_ROW_WAVE;  // eight waves
+    p.tile_lds_bytes = (a.W + 2.0) * RECB +                           // halo row written
+                       4.0 * BLOCKS_ROW * 9 * NCX * 3 * 1024 +        // pixel parts read (four filter groups)
+                       (NCX == 2 ? 2.0 * 4.0 * BLOCKS_ROW / 2 * 1024 : 0.0);  // partial sums exchanged
+    p.tile_load_bytes = (a.W + 2.0) * a.C * 4;
     p.tile_store_bytes = a.W * 64 * 4;
     p.wg_setup_bytes = 4.0 * 16 * 9 * a.C * 4;
     p.hbm_bytes = 4.0 * ((double)a.N * a.H * a.W * a.C + 9.0 * a.F * a.C + (double)a.N * a.H * a.W * a.F) +

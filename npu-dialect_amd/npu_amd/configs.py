@@ -42,29 +42,44 @@ class Workload:
     units: int = 1          # images / sequences per step (throughput unit)
     unit_name: str = "images"
     meta: dict = field(default_factory=dict)
+    # The matrix pipe the launch runs its contractions on and the work it
+    # does there per algorithmic flop: an f32 block that the GPU computes as
+    # three-part bf16 splits runs six bf16 products per f32 product on the
+    # bf16 pipe (mfma_key "bf16", mfma_factor 6).
+    mfma_key: str = ""
+    mfma_factor: int = 1
 
     @property
     def bound(self) -> str:
         """'hbm' or 'mfma': which roofline term is larger at peak."""
         t_mem = self.bytes / PEAK["hbm"]
-        t_cmp = self.flops / PEAK[self.peak_key]
+        t_cmp = self.mfma_flops / PEAK[self.peak_key]
         return "hbm" if t_mem >= t_cmp else "mfma"
 
     @property
     def peak_key(self) -> str:
-        return {"f32": "f32", "bf16": "bf16", "i8": "i8"}[self.dtype]
+        return self.mfma_key or {"f32": "f32", "bf16": "bf16", "i8": "i8"}[self.dtype]
+
+    @property
+    def mfma_flops(self) -> int:
+        """Matrix-pipe work of one launch (flops of the pipe's own type)."""
+        return self.flops * self.mfma_factor
 
     def floor_s(self) -> float:
-        return max(self.bytes / PEAK["hbm"], self.flops / PEAK[self.peak_key])
+        return max(self.bytes / PEAK["hbm"], self.mfma_flops / PEAK[self.peak_key])
 
     def roofline(self, seconds: float) -> dict:
         if self.bound == "hbm":
             achieved = self.bytes / seconds
             return {"bound": "hbm", "achieved": achieved / 1e9, "peak": PEAK["hbm"] / 1e9,
                     "unit": "GB/s", "frac": achieved / PEAK["hbm"]}
-        achieved = self.flops / seconds
-        return {"bound": "mfma", "achieved": achieved / 1e12, "peak": PEAK[self.peak_key] / 1e12,
-                "unit": "TFLOP/s", "frac": achieved / PEAK[self.peak_key]}
+        achieved = self.mfma_flops / seconds
+        out = {"bound": "mfma", "achieved": achieved / 1e12, "peak": PEAK[self.peak_key] / 1e12,
+               "unit": "TFLOP/s", "frac": achieved / PEAK[self.peak_key]}
+        if self.mfma_factor != 1:
+            out["pipe"] = f"{self.peak_key} ({self.mfma_factor} products per {self.dtype} product)"
+            out["algorithmic_tflops"] = self.flops / seconds / 1e12
+        return out
 
 
 def _to_dev(arrs: dict) -> dict:
@@ -138,13 +153,17 @@ def conv3x3_bias_relu(N=1, dtype="f32", H=56, W=56, C=64, F=64,
         groups.fused_conv2d_nhwc_bias_act(d["x"], d["w"], d["bias"], o["out"], 1, "relu", stream)
 
     P = N * H * W
+    # the f32 persistent launch (many row pairs, F a multiple of 64, 32 or
+    # 64 channels) multiplies on the bf16 pipe, six products per f32 product
+    on_bf16 = dtype == "f32" and N * ((H + 1) // 2) >= 512 and F % 64 == 0 and C in (32, 64) and W <= 64
     return Workload(
         name=f"conv3x3_bias_relu_{dtype}_n{N}", config=2, dtype=dtype,
         flops=2 * P * F * KH * KW * C + 2 * P * F,
         bytes=esz * (P * C + P * F + F * KH * KW * C) + 4 * F,
         make_inputs=make_inputs, make_outputs=make_outputs, run=run,
         desc=f"pad->conv2d 3x3 NHWC {N}x{H}x{W}x{C} -> {F} +bias+ReLU ({dtype})", units=N,
-        meta={"N": N, "H": H, "W": W, "C": C, "F": F})
+        meta={"N": N, "H": H, "W": W, "C": C, "F": F},
+        mfma_key="bf16" if on_bf16 else "", mfma_factor=6 if on_bf16 else 1)
 
 
 # ------------------------------------------------------------------ C3
