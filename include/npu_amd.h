@@ -109,7 +109,12 @@ npu_status fused_matmul_bias_act(const npu_memref *A, const npu_memref *B,
  *   bias f32 [F] (aligned may be NULL)
  *   out  [N,Ho,Wo,F] same dtype as x (bf16: fp32 accumulate, one rounding)
  * Stride 1, symmetric zero padding `pad`; Ho = H + 2*pad - KH + 1.
- * Requires C % 16 == 0 (f32) / C % 32 == 0 (bf16) and F % 16 == 0. */
+ * Requires C % 16 == 0 (f32) / C % 32 == 0 (bf16) and F % 16 == 0.
+ * f32 results are within f32 accuracy of the sequential f32 sum.  Batched
+ * 3x3 launches with 32 or 64 channels and F % 64 == 0 compute the products
+ * on the bf16 matrix pipe from exact three-part bf16 splits of every value;
+ * there an infinite input or filter value gives NaN (not +-Inf) in the
+ * outputs it reaches.  NaN propagates everywhere. */
 npu_status fused_conv2d_nhwc_bias_act(const npu_memref *x, const npu_memref *w,
                                       const npu_memref *bias,
                                       const npu_memref *out, int32_t pad,

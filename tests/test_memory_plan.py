@@ -158,12 +158,15 @@ LDS_KERNELS = {
     # xs[100 x 36 floats], wds[9 x 144], es[100 x 152]
     "irb_kernel<24, 144>": ([(IN, 100 * 36 * 4, 0, 9, 0), (IN, 9 * 144 * 4, 1, 9, 0),
                              (MID, 100 * 152 * 4, 2, 5, 0)], 80384),
-    # halo[4 rows x 58 px x 160 B], ostage[2 x 56 px x 160 B]
-    "conv3x3_stream_kernel bf16 C=64": ([(IN, 4 * 58 * 160, 0, 5, 0),
-                                         (OUT, 2 * 56 * 160, 1, 6, 0)], 55296),
-    # halo[4 x 58 x 288 B], ostage[2 x 56 x 288 B]
-    "conv3x3_stream_kernel f32 C=64": ([(IN, 4 * 58 * 288, 0, 5, 0),
-                                        (OUT, 2 * 56 * 288, 1, 6, 0)], 99328),
+    # halo[4 rows x 58 px x 160 B] plus a 16-byte trash slot per lane,
+    # ostage[2 x 56 px x 160 B]
+    "conv3x3_stream_kernel bf16 C=64": ([(IN, 4 * 58 * 160 + 64 * 16, 0, 5, 0),
+                                         (OUT, 2 * 56 * 160, 1, 6, 0)], 56320),
+    # f32 on the bf16 pipe: a ring of 6 halo row slots [58 px x 416 B] plus
+    # 8-byte trash slots (768 B), and the partial-sum exchange [4 filter
+    # groups x 4 blocks x 1 KiB] (the filters' staging before the walk)
+    "conv3x3_x6_kernel<56, 2, 56>": ([(IN, 6 * 58 * 416 + 768, 0, 9, 0),
+                                      (MID, 4 * 4 * 1024, 1, 9, 0)], 162304),
     # xs[112 x 288 B], y1[112 x 96 B], y2[64 x 96 B]
     "qbottleneck_kernel<256, 64>": ([(IN, 112 * 288, 0, 9, 0), (MID, 112 * 96, 1, 4, 0),
                                      (MID, 64 * 96, 2, 6, 0)], 49152),
@@ -177,8 +180,8 @@ LDS_KERNELS = {
     "llama_gemm_kernel<1, 2> (swiglu)": ([(IN, 32 * 144 * 2, 0, 9, 1), (IN, 64 * 144 * 2, 1, 9, 1),
                                           (IN, 64 * 144 * 2, 2, 9, 1),
                                           (MID, 32 * 4, 3, 9, 0)], 92672),
-    # K[64 x 80 bf16] and V^T[64 x 80 bf16] ping/pong
-    "llama_attention_kernel": ([(IN, 64 * 80 * 2, 0, 9, 1), (IN, 64 * 80 * 2, 1, 9, 1)], 40960),
+    # K[2 key groups x 64 x 80 bf16] and V^T[2 x 64 x 80 bf16] ping/pong
+    "llama_attention_kernel": ([(IN, 2 * 64 * 80 * 2, 0, 9, 1), (IN, 2 * 64 * 80 * 2, 1, 9, 1)], 81920),
 }
 
 
