@@ -574,21 +574,22 @@ __global__ __launch_bounds__(512, 1) void conv3x3_x6_kernel(
 #pragma unroll
     for (int hr = 0; hr < TR + 2; ++hr) load_row(fraw[hr], n * H + min(max(h0 + hr - 1, 0), H - 1));
   };
-  auto put_tile = [&](int g, int b) __attribute__((always_inline)) {
-    const int rows = tile_rows(g), h0 = g % H;
-#pragma unroll
-    for (int hr = 0; hr < TR + 2; ++hr) {
-      const int ih = h0 + hr - 1, slot = (b + hr) % NSLOT;
-      if (hr > rows + 1) {
-        // not a halo row of a short tile
-      } else if (ih >= 0 && ih < H) {
-#pragma unroll
-        for (int j = 0; j < LPR; ++j) put_run(waddr(slot, j), split_parts(fraw[hr][j]));
-      } else {
-#pragma unroll
-        for (int j = 0; j < LPR; ++j) zero_run(waddr(slot, j));
-      }
+  // run j of halo row hr of the tile at g, into slot b + hr
+  auto put_fraw = [&](int g, int b, int hr, int j) __attribute__((always_inline)) {
+    const int rows = tile_rows(g), ih = g % H + hr - 1, slot = (b + hr) % NSLOT;
+    if (hr > rows + 1) {
+      // not a halo row of a short tile
+    } else if (ih >= 0 && ih < H) {
+      put_run(waddr(slot, j), split_parts(fraw[hr][j]));
+    } else {
+      zero_run(waddr(slot, j));
     }
+  };
+  auto put_tile = [&](int g, int b, int hr0, int hr1) __attribute__((always_inline)) {
+#pragma unroll
+    for (int hr = hr0; hr < hr1; ++hr)
+#pragma unroll
+      for (int j = 0; j < LPR; ++j) put_fraw(g, b, hr, j);
   };
   // The next tile's new rows (its halo rows 2..TR+1: image rows gn+1..gn+TR
   // for a tile starting at gn), fetched a tile ahead.  Unconditional (rows
@@ -647,8 +648,10 @@ __global__ __launch_bounds__(512, 1) void conv3x3_x6_kernel(
       }
     }
   }
+  // The first tile's halo rows 0 and 1 now; rows 2 and up during the first
+  // third of its multiply (the taps of tap row 0 read rows 0 and 1 only).
   int base = 0;  // slot of the current tile's halo row 0
-  put_tile(range.first, base);
+  put_tile(range.first, base, 0, 2);
   // zero-padding columns 0 and W+1 of every slot (lanes write no record there)
   constexpr int ZR = 3 * PST / 16;  // 16-byte runs of a record's parts
   for (int i = tid; i < NSLOT * 2 * ZR; i += NT) {
@@ -663,7 +666,8 @@ __global__ __launch_bounds__(512, 1) void conv3x3_x6_kernel(
     for (int k = 0; k < 3; ++k) settle(fr[t][k].u);
   __syncthreads();  // halo, padding and every wave's filter staging done (staging shares the exchange area)
 
-  for (int g = range.first; g < range.end; g += tile_rows(g)) {
+  auto tile = [&](int g, auto first) __attribute__((always_inline)) {
+    constexpr bool FIRST = decltype(first)::value;
     const int rows = tile_rows(g);
     const int bnext = (base + rows) % NSLOT;  // the next tile's halo row 0
     // read bases: block ii, tap row dy -> slot of halo row (its row + dy)
@@ -706,6 +710,13 @@ __global__ __launch_bounds__(512, 1) void conv3x3_x6_kernel(
         constexpr int s = decltype(sc)::value;
         if constexpr (s + D < NS) load_px(px[(s + D) % RB], s + D);
         mma_x6(acc[s % NB], fr[s / NB], px[s % RB]);
+        if constexpr (FIRST) {
+          // the first tile's halo rows 2 and 3, then a barrier before tap row 1
+          constexpr int NF = TR * LPR, SPF = (3 * NB - 1) / NF > 0 ? (3 * NB - 1) / NF : 1;
+          static_assert(SPF * (NF - 1) < 3 * NB - 1, "the first tile's last rows are written before tap row 1");
+          if constexpr (s % SPF == 0 && s / SPF < NF) put_fraw(g, 0, 2 + (s / SPF) / LPR, (s / SPF) % LPR);
+          if constexpr (s == 3 * NB - 1) __syncthreads();
+        }
         if constexpr (s >= S0 && (s - S0) % SPS == 0 && (s - S0) / SPS < NSPL) {
           constexpr int e = (s - S0) / SPS, k = e / LPR, j = e % LPR;
           const Parts4 p = split_parts(nraw[k][j]);
@@ -774,11 +785,14 @@ __global__ __launch_bounds__(512, 1) void conv3x3_x6_kernel(
     prefetch(g2 < range.end ? g2 : g);
     if (gn < range.end && hn == 0) {  // the next tile starts an image: its rows were not prefetched
       fetch_tile(gn);
-      put_tile(gn, bnext);
+      put_tile(gn, bnext, 0, TR + 2);
       __syncthreads();
     }
     base = bnext;
-  }
+  };
+  tile(range.first, std::integral_constant<bool, true>{});
+  for (int g = range.first + tile_rows(range.first); g < range.end; g += tile_rows(g))
+    tile(g, std::integral_constant<bool, false>{});
 }
 
 // Vector-ALU instructions per wave and output row of the persistent kernel
