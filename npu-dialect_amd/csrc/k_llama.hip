@@ -33,7 +33,7 @@ namespace npu {
 
 namespace {
 
-constexpr int TM = 32, TN = 64, TK = 128;
+constexpr int TN = 64, TK = 128;
 constexpr int LDA = TK + 16;  // LDS row stride (elements) of the [row][k] tiles: 288 bytes (32 mod 64)
 
 __device__ __forceinline__ float silu(float g) { return g / (1.0f + expf(-g)); }
@@ -62,10 +62,16 @@ __device__ __forceinline__ float sumsq8(const u32x4 &v) {
 template <int N>
 using Slot = std::integral_constant<int, N>;
 
-template <int PRO, int EPI>
-__global__ __launch_bounds__(256) void llama_gemm_kernel(const LlamaGemmArgs a) {
+// WAVES = 4: 32-row tiles; WAVES = 8: 64-row tiles (half the workgroups, each
+// with twice the waves: the QKV and SwiGLU grids then fit one round of the CUs).
+template <int PRO, int EPI, int WAVES>
+__global__ __launch_bounds__(64 * WAVES) void llama_gemm_kernel(const LlamaGemmArgs a) {
   constexpr int NB = (EPI == kEpiSwiglu) ? 2 : 1;
-  constexpr int RPW = TM / 4;  // RMSNorm rows per wave
+  constexpr int TM = 8 * WAVES;      // tile rows: 16 per wave pair
+  constexpr int NT = 64 * WAVES;     // threads
+  constexpr int RPW = TM / WAVES;    // RMSNorm rows per wave
+  constexpr int KPT = 512 / NT;      // B k pairs per thread and chunk
+  constexpr int BKT = 64 / KPT;      // threads per B column group
   __shared__ __attribute__((aligned(16))) uint16_t As[2][TM * LDA];
   __shared__ __attribute__((aligned(16))) uint16_t Bs[2][NB][TN * LDA];
   __shared__ float inv_rms[TM];
@@ -77,8 +83,8 @@ __global__ __launch_bounds__(256) void llama_gemm_kernel(const LlamaGemmArgs a) 
   const int part = (EPI == kEpiQkvRope) ? blockIdx.x / tiles_per_part : 0;
   const int n0 = (blockIdx.x % tiles_per_part) * TN;
   const uint16_t *Bp[2] = {a.B[part], a.B[NB - 1]};
-  // wave (wm, wn): rows 16*wm.., columns 32*wn.. (two 16-column tiles)
-  const int wm = (wave & 1) * 16, wn = (wave >> 1) * 32;
+  // wave (wm, wn): rows wm.. (16), columns wn.. (two 16-column tiles)
+  const int wm = (wave % (WAVES / 2)) * 16, wn = (wave / (WAVES / 2)) * 32;
   const int nchunks = (a.K + TK - 1) / TK;
 
   // Latency, not arithmetic, bounds these small GEMMs: every dependent
@@ -87,8 +93,8 @@ __global__ __launch_bounds__(256) void llama_gemm_kernel(const LlamaGemmArgs a) 
   // together with the RMSNorm row loads, and the K loop keeps two chunks in
   // flight (register slots 0 and 1; chunk j lives in slot j % 2).
   //
-  // staging: A chunk [32 rows][128 k] = two 8-element runs per thread;
-  // B chunk [128 k][64 n] = four k rows (two pairs) x one 8-column run.
+  // staging: A chunk [TM rows][128 k] = two 8-element runs per thread;
+  // B chunk [128 k][64 n] = 2 KPT k rows (KPT pairs) x one 8-column run.
   // fetch() only issues loads (raw, from clamped addresses); the zero fill,
   // the RMSNorm scaling and the B transpose happen in commit().
   // B lanes: 32 consecutive lanes take 32 consecutive k pairs of one 8-column
@@ -96,8 +102,8 @@ __global__ __launch_bounds__(256) void llama_gemm_kernel(const LlamaGemmArgs a) 
   // words (with the column group varying fastest, the rows 8 apart would all
   // fall in one bank: an 8-way conflict on every write).
   const int arow = tid >> 3, akk = (tid & 7) * 8;
-  const int bkp = (tid & 31) * 2, bng = (tid >> 5) * 8;
-  u32x4 sa[2][2], sb[2][NB][4];
+  const int bkp = (tid % BKT) * 2, bng = (tid / BKT) * 8;
+  u32x4 sa[2][2], sb[2][NB][2 * KPT];
   f32x4 sg[2][2][2];  // gamma of this thread's two A runs (RMSNorm prologue)
   uint32_t okbits[2] = {0u, 0u};
   auto fetch = [&](auto slot, int chunk) {
@@ -121,7 +127,7 @@ __global__ __launch_bounds__(256) void llama_gemm_kernel(const LlamaGemmArgs a) 
 #pragma unroll
     for (int b = 0; b < NB; ++b)
 #pragma unroll
-      for (int h = 0; h < 4; ++h) {
+      for (int h = 0; h < 2 * KPT; ++h) {
         const int k = k0 + bkp + (h & 1) + 64 * (h >> 1);
         sb[S][b][h] = load16(Bp[b] + (size_t)min(k, a.K - 1) * a.Npart + n0 + bng).u;
         ok |= (uint32_t)(k < a.K) << (2 + 4 * b + h);
@@ -146,11 +152,11 @@ __global__ __launch_bounds__(256) void llama_gemm_kernel(const LlamaGemmArgs a) 
     }
 #pragma unroll
     for (int b = 0; b < NB; ++b) {
-      u32x4 m[4];
+      u32x4 m[2 * KPT];
 #pragma unroll
-      for (int h = 0; h < 4; ++h) m[h] = masked(sb[S][b][h], (okbits[S] >> (2 + 4 * b + h)) & 1u);
+      for (int h = 0; h < 2 * KPT; ++h) m[h] = masked(sb[S][b][h], (okbits[S] >> (2 + 4 * b + h)) & 1u);
 #pragma unroll
-      for (int hp = 0; hp < 2; ++hp)
+      for (int hp = 0; hp < KPT; ++hp)
 #pragma unroll
         for (int j = 0; j < 8; ++j)
           *reinterpret_cast<uint32_t *>(&Bs[buf][b][(bng + j) * LDA + bkp + 64 * hp]) =
@@ -487,16 +493,17 @@ namespace {
 // chunk's MFMAs, so one exposed load phase plus the prologue's row loads).
 template <class Kern>
 void plan_gemm(const char *name, Kern kern, const LlamaGemmArgs &a, int grid, int nb, bool norm,
-               int epi) {
+               int epi, int waves) {
   const int kchunks = (a.K + TK - 1) / TK;
-  npu_launch_plan p = make_plan(name, grid, wg_per_cu(kern), grid, 16);
+  const int TM = 8 * waves;
+  npu_launch_plan p = make_plan(name, grid, wg_per_cu(kern, 64 * waves), grid, 16);
   p.load_phases = norm ? 2 : 1;
   p.tile_macs = (double)TM * TN * nb * kchunks * TK;
   // counted per wave: 225 + 98 per chunk (residual), 1050 + 160 per chunk
   // (RMSNorm + RoPE), 1100 + 260 per chunk (RMSNorm + SwiGLU, two B operands)
   const double fixed = epi == kEpiResidual ? 225 : (epi == kEpiQkvRope ? 1050 : 1100);
   const double per = epi == kEpiResidual ? 98 : (epi == kEpiQkvRope ? 160 : 260);
-  p.tile_valu = 4.0 * (fixed + per * kchunks);
+  p.tile_valu = 4.0 * (fixed + per * kchunks) * (waves / 4.0);
   p.tile_lds_bytes = 2.0 * ((double)TM + nb * TN) * kchunks * TK * 2;   // written once, read once
   p.tile_load_bytes = ((double)TM + nb * TN) * kchunks * TK * 2 + (norm ? 4.0 * a.K : 0.0);
   p.tile_store_bytes = (double)TM * TN * 2;
@@ -510,19 +517,24 @@ void plan_gemm(const char *name, Kern kern, const LlamaGemmArgs &a, int grid, in
 
 }  // namespace
 
+// The QKV and SwiGLU GEMMs (RMSNorm prologue, 384 and 352 workgroups of 32
+// rows at the layer's M = 512) run 64-row tiles of eight waves so the grid
+// fits one round of the 256 CUs; the residual GEMMs (128 workgroups) keep
+// 32-row tiles of four waves.
 hipError_t launch_llama_gemm(const LlamaGemmArgs &a, int pro, int epi, hipStream_t s) {
   const int tiles_n = (a.Npart / TN) * (epi == kEpiQkvRope ? a.nparts : 1);
+  const int waves = pro == kProRmsnorm ? 8 : 4, TM = 8 * waves;
   dim3 grid(tiles_n, (a.M + TM - 1) / TM);
   const int g = grid.x * grid.y;
   if (pro == kProRmsnorm && epi == kEpiQkvRope) {
-    plan_gemm("llama_rmsnorm_qkv_rope", llama_gemm_kernel<kProRmsnorm, kEpiQkvRope>, a, g, 1, true, epi);
-    hipLaunchKernelGGL((llama_gemm_kernel<kProRmsnorm, kEpiQkvRope>), grid, dim3(256), 0, s, a);
+    plan_gemm("llama_rmsnorm_qkv_rope", llama_gemm_kernel<kProRmsnorm, kEpiQkvRope, 8>, a, g, 1, true, epi, 8);
+    hipLaunchKernelGGL((llama_gemm_kernel<kProRmsnorm, kEpiQkvRope, 8>), grid, dim3(512), 0, s, a);
   } else if (pro == kProPlain && epi == kEpiResidual) {
-    plan_gemm("llama_matmul_residual", llama_gemm_kernel<kProPlain, kEpiResidual>, a, g, 1, false, epi);
-    hipLaunchKernelGGL((llama_gemm_kernel<kProPlain, kEpiResidual>), grid, dim3(256), 0, s, a);
+    plan_gemm("llama_matmul_residual", llama_gemm_kernel<kProPlain, kEpiResidual, 4>, a, g, 1, false, epi, 4);
+    hipLaunchKernelGGL((llama_gemm_kernel<kProPlain, kEpiResidual, 4>), grid, dim3(256), 0, s, a);
   } else if (pro == kProRmsnorm && epi == kEpiSwiglu) {
-    plan_gemm("llama_rmsnorm_swiglu", llama_gemm_kernel<kProRmsnorm, kEpiSwiglu>, a, g, 2, true, epi);
-    hipLaunchKernelGGL((llama_gemm_kernel<kProRmsnorm, kEpiSwiglu>), grid, dim3(256), 0, s, a);
+    plan_gemm("llama_rmsnorm_swiglu", llama_gemm_kernel<kProRmsnorm, kEpiSwiglu, 8>, a, g, 2, true, epi, 8);
+    hipLaunchKernelGGL((llama_gemm_kernel<kProRmsnorm, kEpiSwiglu, 8>), grid, dim3(512), 0, s, a);
   } else {
     return hipErrorInvalidValue;
   }

@@ -170,16 +170,18 @@ LDS_KERNELS = {
     # xs[112 x 288 B], y1[112 x 96 B], y2[64 x 96 B]
     "qbottleneck_kernel<256, 64>": ([(IN, 112 * 288, 0, 9, 0), (MID, 112 * 96, 1, 4, 0),
                                      (MID, 64 * 96, 2, 6, 0)], 49152),
-    # A[32 x 144 bf16] and B[64 x 144 bf16] ping/pong, inv_rms[32 floats]
-    "llama_gemm_kernel<1, 0> (rmsnorm prologue)": ([(IN, 32 * 144 * 2, 0, 9, 1),
-                                                    (IN, 64 * 144 * 2, 1, 9, 1),
-                                                    (MID, 32 * 4, 2, 9, 0)], 55808),
-    "llama_gemm_kernel<0, 1> (no prologue)": ([(IN, 32 * 144 * 2, 0, 9, 1),
-                                               (IN, 64 * 144 * 2, 1, 9, 1)], 55296),
+    # A[64 x 144 bf16] and B[64 x 144 bf16] ping/pong, inv_rms[64 floats]
+    # (64-row tiles of eight waves)
+    "llama_gemm_kernel<1, 0, 8> (rmsnorm prologue)": ([(IN, 64 * 144 * 2, 0, 9, 1),
+                                                       (IN, 64 * 144 * 2, 1, 9, 1),
+                                                       (MID, 64 * 4, 2, 9, 0)], 74240),
+    # A[32 x 144 bf16] and B[64 x 144 bf16] ping/pong (32-row tiles, four waves)
+    "llama_gemm_kernel<0, 1, 4> (no prologue)": ([(IN, 32 * 144 * 2, 0, 9, 1),
+                                                  (IN, 64 * 144 * 2, 1, 9, 1)], 55296),
     # two B operands (gate and up) for the SwiGLU epilogue
-    "llama_gemm_kernel<1, 2> (swiglu)": ([(IN, 32 * 144 * 2, 0, 9, 1), (IN, 64 * 144 * 2, 1, 9, 1),
-                                          (IN, 64 * 144 * 2, 2, 9, 1),
-                                          (MID, 32 * 4, 3, 9, 0)], 92672),
+    "llama_gemm_kernel<1, 2, 8> (swiglu)": ([(IN, 64 * 144 * 2, 0, 9, 1), (IN, 64 * 144 * 2, 1, 9, 1),
+                                             (IN, 64 * 144 * 2, 2, 9, 1),
+                                             (MID, 64 * 4, 3, 9, 0)], 111104),
     # K[2 key groups x 64 x 80 bf16] and V^T[2 x 64 x 80 bf16] ping/pong
     "llama_attention_kernel": ([(IN, 2 * 64 * 80 * 2, 0, 9, 1), (IN, 2 * 64 * 80 * 2, 1, 9, 1)], 81920),
 }
