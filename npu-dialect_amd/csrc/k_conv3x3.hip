@@ -206,8 +206,10 @@ __global__ __launch_bounds__(256) void conv3x3_rows_kernel(
 // is a scalar base plus one loop-invariant lane offset, and the LDS addresses
 // are loop-invariant plus immediates: the per-tile vector-ALU work is the
 // epilogue's clamp and conversion, not index arithmetic.
+// Two workgroups per CU where their registers fit (two chunks, rows of up
+// to 56 pixels), else one.
 template <class MM, typename T, int WMAX, int NCH, int WFIX>
-__global__ __launch_bounds__(256, NCH <= 2 ? 2 : 1) void conv3x3_stream_kernel(
+__global__ __launch_bounds__(256, NCH <= 2 && WMAX <= 56 ? 2 : 1) void conv3x3_stream_kernel(
     const T *__restrict__ x, const T *__restrict__ w, const float *__restrict__ bias,
     T *__restrict__ out, int H, int w_rt, int F, int act, int nrows) {
   const int W = WFIX > 0 ? WFIX : w_rt;
@@ -650,8 +652,11 @@ __global__ __launch_bounds__(512, 1) void conv3x3_x6_kernel(
   }
   // The first tile's halo rows 0 and 1 now; rows 2 and up during the first
   // third of its multiply (the taps of tap row 0 read rows 0 and 1 only).
+  // With the row width known at compile time only: the run-time width's
+  // index registers and those rows held over would not fit without spills.
+  constexpr bool EARLY = WFIX > 0;
   int base = 0;  // slot of the current tile's halo row 0
-  put_tile(range.first, base, 0, 2);
+  put_tile(range.first, base, 0, EARLY ? 2 : TR + 2);
   // zero-padding columns 0 and W+1 of every slot (lanes write no record there)
   constexpr int ZR = 3 * PST / 16;  // 16-byte runs of a record's parts
   for (int i = tid; i < NSLOT * 2 * ZR; i += NT) {
@@ -790,7 +795,7 @@ __global__ __launch_bounds__(512, 1) void conv3x3_x6_kernel(
     }
     base = bnext;
   };
-  tile(range.first, std::integral_constant<bool, true>{});
+  tile(range.first, std::integral_constant<bool, EARLY>{});
   for (int g = range.first + tile_rows(range.first); g < range.end; g += tile_rows(g))
     tile(g, std::integral_constant<bool, false>{});
 }
