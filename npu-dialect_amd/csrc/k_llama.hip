@@ -23,6 +23,7 @@
 // four waves of 16 query rows.  Key blocks of 64 (K rows and V transposed)
 // are staged once in LDS for the four waves, the next block prefetched into
 // registers; online softmax in f32; P rounded to bf16 for its MFMA with V.
+#include <cmath>
 #include <type_traits>
 
 #include "kernels.hpp"
@@ -71,7 +72,6 @@ __global__ __launch_bounds__(64 * WAVES) void llama_gemm_kernel(const LlamaGemmA
   constexpr int NT = 64 * WAVES;     // threads
   constexpr int RPW = TM / WAVES;    // RMSNorm rows per wave
   constexpr int KPT = 512 / NT;      // B k pairs per thread and chunk
-  constexpr int BKT = 64 / KPT;      // threads per B column group
   __shared__ __attribute__((aligned(16))) uint16_t As[2][TM * LDA];
   __shared__ __attribute__((aligned(16))) uint16_t Bs[2][NB][TN * LDA];
   __shared__ float inv_rms[TM];
@@ -97,12 +97,15 @@ __global__ __launch_bounds__(64 * WAVES) void llama_gemm_kernel(const LlamaGemmA
   // B chunk [128 k][64 n] = 2 KPT k rows (KPT pairs) x one 8-column run.
   // fetch() only issues loads (raw, from clamped addresses); the zero fill,
   // the RMSNorm scaling and the B transpose happen in commit().
-  // B lanes: 32 consecutive lanes take 32 consecutive k pairs of one 8-column
-  // group, so each transposed 4-byte LDS write of a wave covers consecutive
-  // words (with the column group varying fastest, the rows 8 apart would all
-  // fall in one bank: an 8-way conflict on every write).
+  // B lanes: item i = tid + NT hp is k pair i / 8 and 8-column group i % 8,
+  // so eight consecutive lanes load one k row's 128 bytes (a wave loads
+  // whole cache lines).  In LDS, B is [n][k] in 16-byte chunks of 8 k, chunk
+  // c of column n stored at c ^ (n / 8): the transposed 4-byte writes of the
+  // eight column groups then fall in eight different chunks (without it, in
+  // one bank), and the MFMA reads undo the swizzle.
   const int arow = tid >> 3, akk = (tid & 7) * 8;
-  const int bkp = (tid % BKT) * 2, bng = (tid / BKT) * 8;
+  const int bng = (tid & 7) * 8;  // this thread's 8-column group (the same for every hp)
+  auto bkp = [&](int hp) { return 2 * ((tid + NT * hp) >> 3); };  // first k of its pair
   u32x4 sa[2][2], sb[2][NB][2 * KPT];
   f32x4 sg[2][2][2];  // gamma of this thread's two A runs (RMSNorm prologue)
   uint32_t okbits[2] = {0u, 0u};
@@ -128,7 +131,7 @@ __global__ __launch_bounds__(64 * WAVES) void llama_gemm_kernel(const LlamaGemmA
     for (int b = 0; b < NB; ++b)
 #pragma unroll
       for (int h = 0; h < 2 * KPT; ++h) {
-        const int k = k0 + bkp + (h & 1) + 64 * (h >> 1);
+        const int k = k0 + bkp(h >> 1) + (h & 1);
         sb[S][b][h] = load16(Bp[b] + (size_t)min(k, a.K - 1) * a.Npart + n0 + bng).u;
         ok |= (uint32_t)(k < a.K) << (2 + 4 * b + h);
       }
@@ -156,11 +159,13 @@ __global__ __launch_bounds__(64 * WAVES) void llama_gemm_kernel(const LlamaGemmA
 #pragma unroll
       for (int h = 0; h < 2 * KPT; ++h) m[h] = masked(sb[S][b][h], (okbits[S] >> (2 + 4 * b + h)) & 1u);
 #pragma unroll
-      for (int hp = 0; hp < KPT; ++hp)
+      for (int hp = 0; hp < KPT; ++hp) {
+        const int kp = bkp(hp) >> 1;
+        const int off = ((((kp >> 2) ^ (bng >> 3)) << 3) + 2 * (kp & 3));
 #pragma unroll
         for (int j = 0; j < 8; ++j)
-          *reinterpret_cast<uint32_t *>(&Bs[buf][b][(bng + j) * LDA + bkp + 64 * hp]) =
-              pair_word(m[2 * hp], m[2 * hp + 1], j);
+          *reinterpret_cast<uint32_t *>(&Bs[buf][b][(bng + j) * LDA + off]) = pair_word(m[2 * hp], m[2 * hp + 1], j);
+      }
     }
   };
 
@@ -228,6 +233,14 @@ __global__ __launch_bounds__(64 * WAVES) void llama_gemm_kernel(const LlamaGemmA
   // read): with a condition on either, the compiler's wait analysis would
   // drain every outstanding load at the loop head.  Unrolled by two so that
   // the register slots are compile-time.
+  // B fragment of column n, k chunk 4 ks + q: stored at chunk (4 ks + q) ^ (n / 8)
+  int bcol[2], bhi[2];
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const int n = wn + 16 * j + r, g = n >> 3;
+    bcol[j] = n * LDA + ((q ^ g) & 3) * 8;
+    bhi[j] = g & 4;
+  }
   auto iteration = [&](auto slot, int c) {
     constexpr int S = decltype(slot)::value;  // = c % 2
     fetch(slot, c + 2);
@@ -239,7 +252,7 @@ __global__ __launch_bounds__(64 * WAVES) void llama_gemm_kernel(const LlamaGemmA
         for (int b = 0; b < NB; ++b)
 #pragma unroll
           for (int j = 0; j < 2; ++j) {
-            const Frag16 bf = load16(&Bs[S][b][(wn + 16 * j + r) * LDA + 32 * ks + 8 * q]);
+            const Frag16 bf = load16(&Bs[S][b][bcol[j] + ((4 * ks) ^ bhi[j]) * 8]);
             MfmaBF16::mma(acc[b][j], af, bf);
           }
       }
@@ -494,19 +507,24 @@ namespace {
 template <class Kern>
 void plan_gemm(const char *name, Kern kern, const LlamaGemmArgs &a, int grid, int nb, bool norm,
                int epi, int waves) {
+  // The plan's unit is four waves (one per SIMD), as its occupancy is: an
+  // eight-wave workgroup is two units that run side by side, each with half
+  // of the workgroup's tile (its rows, and half of the B chunks it shares).
+  const int units = waves / 4;
   const int kchunks = (a.K + TK - 1) / TK;
   const int TM = 8 * waves;
-  npu_launch_plan p = make_plan(name, grid, wg_per_cu(kern, 64 * waves), grid, 16);
+  npu_launch_plan p = make_plan(name, grid * units, wg_per_cu(kern, 64 * waves), grid * units, 16);
   p.load_phases = norm ? 2 : 1;
-  p.tile_macs = (double)TM * TN * nb * kchunks * TK;
-  // counted per wave: 225 + 98 per chunk (residual), 1050 + 160 per chunk
-  // (RMSNorm + RoPE), 1100 + 260 per chunk (RMSNorm + SwiGLU, two B operands)
-  const double fixed = epi == kEpiResidual ? 225 : (epi == kEpiQkvRope ? 1050 : 1100);
+  p.tile_macs = (double)TM * TN * nb * kchunks * TK / units;
+  // vector instructions per wave (SQ_INSTS_VALU less SQ_INSTS_MFMA): 225 + 98
+  // per chunk (residual), 862 + 160 per chunk (RMSNorm + RoPE), 736 + 260 per
+  // chunk (RMSNorm + SwiGLU, two B operands)
+  const double fixed = epi == kEpiResidual ? 225 : (epi == kEpiQkvRope ? 862 : 736);
   const double per = epi == kEpiResidual ? 98 : (epi == kEpiQkvRope ? 160 : 260);
-  p.tile_valu = 4.0 * (fixed + per * kchunks) * (waves / 4.0);
-  p.tile_lds_bytes = 2.0 * ((double)TM + nb * TN) * kchunks * TK * 2;   // written once, read once
-  p.tile_load_bytes = ((double)TM + nb * TN) * kchunks * TK * 2 + (norm ? 4.0 * a.K : 0.0);
-  p.tile_store_bytes = (double)TM * TN * 2;
+  p.tile_valu = 4.0 * (fixed + per * kchunks);
+  p.tile_lds_bytes = 2.0 * ((double)TM + nb * TN) * kchunks * TK * 2 / units;   // written once, read once
+  p.tile_load_bytes = (((double)TM + nb * TN) * kchunks * TK * 2 + (norm ? 4.0 * a.K : 0.0)) / units;
+  p.tile_store_bytes = (double)TM * TN * 2 / units;
   const double parts = epi == kEpiQkvRope ? a.nparts : (epi == kEpiSwiglu ? 2 : 1);
   p.hbm_bytes = 2.0 * ((double)a.M * a.K + parts * a.K * a.Npart +
                        (double)a.M * a.Npart * (epi == kEpiQkvRope ? a.nparts : 1) +
@@ -545,18 +563,20 @@ hipError_t launch_llama_attention(const uint16_t *Q, const uint16_t *K, const ui
                                   uint16_t *O, int S, int H, float scale, hipStream_t s) {
   dim3 grid((S + AQ - 1) / AQ, H);
   {
-    // Causal: query block b sees key blocks 0..b, so the average tile walks
-    // (nqb + 1) / 2 key blocks; every key block costs QK^T and PV MFMAs, the
-    // online-softmax update, and one staged K and V^T block.
+    // Causal: query block b sees key blocks 0..b; every key block costs QK^T
+    // and PV MFMAs, the online-softmax update, and one staged K and V^T
+    // block.  A workgroup is two key groups of four waves, planned as two
+    // 4-wave units per query block, each walking half of its key blocks.
+    // With no more workgroups than CUs the launch lasts as long as its
+    // longest walk, the last query block's: ceil(nqb / 2) key blocks per
+    // unit (the plan's tile is the busiest CU's).
     const int nqb = grid.x;
-    const double kblocks = (nqb + 1) / 4.0;
-    // a workgroup is two key groups of four waves: planned as two 4-wave
-    // units per query block, each walking half of its key blocks
+    const double kblocks = std::ceil(nqb / 2.0);
     npu_launch_plan p = make_plan("llama_causal_attention", 2 * grid.x * grid.y,
                                   wg_per_cu(llama_attention_kernel, 512), 2 * grid.x * grid.y, 16);
     p.load_phases = 1;
     p.tile_macs = kblocks * 2.0 * AQ * AK * 64;
-    p.tile_valu = 4.0 * (150.0 + 335.0 * kblocks);  // counted: 1659 per wave at 4.5 blocks
+    p.tile_valu = 4.0 * (150.0 + 335.0 * kblocks);  // per wave, counted: 832 on average at 2.25 blocks
     p.tile_lds_bytes = kblocks * (2.0 * 2 * AK * 64 * 2 + 4.0 * 2 * AK * 64 * 2);
     p.tile_load_bytes = kblocks * 2.0 * AK * 64 * 2 + AQ * 64 * 2.0;
     p.tile_store_bytes = AQ * 64 * 2.0;
