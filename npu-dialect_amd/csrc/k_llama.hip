@@ -17,7 +17,10 @@
 // chunk is transposed on its way into LDS, two k rows at a time, so that a
 // lane's MFMA operand is one 16-byte k run.  RMSNorm is a prologue (row
 // inverse-RMS, then the normalised bf16 A chunk is formed while staging);
-// RoPE, residual and SiLU-gating are epilogues on the accumulators.
+// RoPE, residual and SiLU-gating are epilogues on the accumulators.  When K
+// fits one 512-wide panel (the layer's d_model), the RMSNorm GEMMs run a
+// variant that normalises the A rows it has just reduced straight into an
+// LDS panel of all of K and has every B chunk in flight from the start.
 //
 // Attention: causal flash attention, one workgroup per (head, 64 queries),
 // four waves of 16 query rows.  Key blocks of 64 (K rows and V transposed)
@@ -35,6 +38,7 @@ namespace npu {
 namespace {
 
 constexpr int TN = 64, TK = 128;
+constexpr int kNormGemmMaxK = 512;  // K of the single-panel RMSNorm GEMM
 constexpr int LDA = TK + 16;  // LDS row stride (elements) of the [row][k] tiles: 288 bytes (32 mod 64)
 
 __device__ __forceinline__ float silu(float g) { return g / (1.0f + expf(-g)); }
@@ -206,10 +210,7 @@ __global__ __launch_bounds__(64 * WAVES) void llama_gemm_kernel(const LlamaGemmA
       for (int rr = 0; rr < RPW; ++rr) s[rr] += sumsq8(v[rr]);
     }
 #pragma unroll
-    for (int rr = 0; rr < RPW; ++rr) {
-#pragma unroll
-      for (int off = 32; off >= 1; off >>= 1) s[rr] += __shfl_xor(s[rr], off);
-    }
+    for (int rr = 0; rr < RPW; ++rr) s[rr] = wave_sum(s[rr]);
     if (lane == 0) {
 #pragma unroll
       for (int rr = 0; rr < RPW; ++rr)
@@ -277,12 +278,165 @@ __global__ __launch_bounds__(64 * WAVES) void llama_gemm_kernel(const LlamaGemmA
       if (EPI == kEpiQkvRope) {
         // RoPE pairs (2t, 2t+1) sit in adjacent lanes (columns r, r^1); the
         // V part (part 2) is not rotated.
-        const float partner = __shfl_xor(v, 1);
+        const float partner = dpp_mov<0xb1>(v);  // lane ^ 1
         const float c = ex0[j][e], s = ex1[j][e];
         const float rot = (n & 1) ? (partner * s + v * c) : (v * c - partner * s);
         y = part < 2 ? rot : v;
       } else if (EPI == kEpiResidual) {
         y = ex0[j][e] + v;
+      } else {
+        y = silu(v) * acc[NB - 1][j][e];
+      }
+      if (m < a.M) a.out[part][(size_t)m * a.Npart + n] = f32_to_bf16(y);
+    }
+  }
+}
+
+// The RMSNorm GEMMs when K fits one panel (K <= 512, the layer's d_model):
+// the loads that feed the RMSNorm are the whole A operand, so each wave
+// normalises its own eight rows in registers right after reducing them
+// (no second fetch of A, no barrier for the row statistics) and writes them
+// into an LDS panel of all of K; every B chunk is in flight from the start
+// (registers), and the K loop only moves B chunks into the double-buffered
+// LDS tile and multiplies.  Eight waves, 64-row x 64-column tiles as the
+// general kernel's eight-wave variant, the same B layout and epilogues.
+template <int EPI>
+__global__ __launch_bounds__(512) void llama_norm_gemm_kernel(const LlamaGemmArgs a) {
+  constexpr int NB = (EPI == kEpiSwiglu) ? 2 : 1;
+  constexpr int TM = 64, RPW = 8;  // tile rows; rows normalised per wave
+  constexpr int NCH = kNormGemmMaxK / TK;
+  __shared__ __attribute__((aligned(16))) uint16_t As[NCH][TM * LDA];
+  __shared__ __attribute__((aligned(16))) uint16_t Bs[2][NB][TN * LDA];
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int r = lane & 15, q = lane >> 4;
+  const int m0 = blockIdx.y * TM;
+  const int tiles_per_part = a.Npart / TN;
+  const int part = (EPI == kEpiQkvRope) ? blockIdx.x / tiles_per_part : 0;
+  const int n0 = (blockIdx.x % tiles_per_part) * TN;
+  const uint16_t *Bp[2] = {a.B[part], a.B[NB - 1]};
+  const int wm = (wave % 4) * 16, wn = (wave / 4) * 32;
+  const int nchunks = (a.K + TK - 1) / TK;
+
+  // A rows (this wave's eight, lane's 8 k) and the gamma of those k, first
+  const int kk = lane * 8, kc = min(kk, a.K - 8);
+  const bool kin = kk < a.K;
+  u32x4 xr[RPW];
+#pragma unroll
+  for (int rr = 0; rr < RPW; ++rr)
+    xr[rr] = load16(a.A + (size_t)min(m0 + wave * RPW + rr, a.M - 1) * a.K + kc).u;
+  const f32x4 g0 = *reinterpret_cast<const f32x4 *>(a.gamma + kc);
+  const f32x4 g1 = *reinterpret_cast<const f32x4 *>(a.gamma + kc + 4);
+  // every B chunk: item k pair tid / 8, 8-column group tid % 8 (eight lanes
+  // load one k row's 128 bytes)
+  const int bng = (tid & 7) * 8, bk = 2 * (tid >> 3);
+  u32x4 sb[NCH][NB][2];
+  static_for<NCH>([&](auto cc) __attribute__((always_inline)) {
+    constexpr int c = decltype(cc)::value;
+    const int k0 = min(c, nchunks - 1) * TK;
+#pragma unroll
+    for (int b = 0; b < NB; ++b)
+#pragma unroll
+      for (int h = 0; h < 2; ++h)
+        sb[c][b][h] = load16(Bp[b] + (size_t)min(k0 + bk + h, a.K - 1) * a.Npart + n0 + bng).u;
+  });
+  // epilogue inputs (cos/sin), from clamped addresses
+  float ex0[2][4], ex1[2][4];
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const int n = n0 + wn + 16 * j + r;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int mc = min(m0 + wm + 4 * q + e, a.M - 1);
+      ex0[j][e] = ex1[j][e] = 0.0f;
+      if (EPI == kEpiQkvRope) {
+        const int t = (n % a.Dh) >> 1;
+        ex0[j][e] = a.cos_t[mc * (a.Dh / 2) + t];
+        ex1[j][e] = a.sin_t[mc * (a.Dh / 2) + t];
+      }
+    }
+  }
+
+  // RMSNorm of this wave's rows: xn = bf16((x * inv_rms) * gamma) into the
+  // panel (zero past K)
+#pragma unroll
+  for (int rr = 0; rr < RPW; ++rr) {
+    const float ssq = wave_sum(kin ? sumsq8(xr[rr]) : 0.0f);
+    const float inv = 1.0f / sqrtf(ssq / (float)a.K + a.eps);
+    u32x4 v;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const f32x4 &gg = j < 2 ? g0 : g1;
+      const float ylo = (bf_lo(xr[rr][j]) * inv) * gg[(2 * j) & 3];
+      const float yhi = (bf_hi(xr[rr][j]) * inv) * gg[(2 * j + 1) & 3];
+      v[j] = (uint32_t)f32_to_bf16(ylo) | ((uint32_t)f32_to_bf16(yhi) << 16);
+    }
+    v = masked(v, kin);
+    *reinterpret_cast<u32x4 *>(&As[kk / TK][(wave * RPW + rr) * LDA + kk % TK]) = v;
+  }
+  // B chunk c into LDS buffer c % 2: transposed to [n][k], 16-byte k chunk
+  // of column n at chunk ^ (n / 8); k past K is zero
+  auto commit_b = [&](auto cc) __attribute__((always_inline)) {
+    constexpr int c = decltype(cc)::value;
+    const int kp = bk >> 1, off = ((((kp >> 2) ^ (bng >> 3)) << 3) + 2 * (kp & 3));
+#pragma unroll
+    for (int b = 0; b < NB; ++b) {
+      const u32x4 m0v = masked(sb[c][b][0], c * TK + bk < a.K);
+      const u32x4 m1v = masked(sb[c][b][1], c * TK + bk + 1 < a.K);
+#pragma unroll
+      for (int j = 0; j < 8; ++j)
+        *reinterpret_cast<uint32_t *>(&Bs[c & 1][b][(bng + j) * LDA + off]) = pair_word(m0v, m1v, j);
+    }
+  };
+  f32x4 acc[NB][2];
+#pragma unroll
+  for (int b = 0; b < NB; ++b)
+#pragma unroll
+    for (int j = 0; j < 2; ++j) acc[b][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+  int bcol[2], bhi[2];
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const int n = wn + 16 * j + r, g = n >> 3;
+    bcol[j] = n * LDA + ((q ^ g) & 3) * 8;
+    bhi[j] = g & 4;
+  }
+  commit_b(std::integral_constant<int, 0>{});
+  __syncthreads();
+  static_for<NCH>([&](auto cc) __attribute__((always_inline)) {
+    constexpr int c = decltype(cc)::value;
+    if (c < nchunks) {
+#pragma unroll
+      for (int ks = 0; ks < TK / 32; ++ks) {
+        const Frag16 af = load16(&As[c][(wm + r) * LDA + 32 * ks + 8 * q]);
+#pragma unroll
+        for (int b = 0; b < NB; ++b)
+#pragma unroll
+          for (int j = 0; j < 2; ++j) {
+            const Frag16 bf = load16(&Bs[c & 1][b][bcol[j] + ((4 * ks) ^ bhi[j]) * 8]);
+            MfmaBF16::mma(acc[b][j], af, bf);
+          }
+      }
+      if constexpr (c + 1 < NCH) {
+        if (c + 1 < nchunks) commit_b(std::integral_constant<int, c + 1>{});
+      }
+      __syncthreads();
+    }
+  });
+
+  // ---- epilogues: element (row m, column n) = acc[.][j][e]
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const int n = n0 + wn + 16 * j + r;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int m = m0 + wm + 4 * q + e;
+      const float v = acc[0][j][e];
+      float y;
+      if (EPI == kEpiQkvRope) {
+        const float partner = dpp_mov<0xb1>(v);  // lane ^ 1
+        const float c = ex0[j][e], s = ex1[j][e];
+        const float rot = (n & 1) ? (partner * s + v * c) : (v * c - partner * s);
+        y = part < 2 ? rot : v;
       } else {
         y = silu(v) * acc[NB - 1][j][e];
       }
@@ -506,7 +660,7 @@ namespace {
 // chunk's MFMAs, so one exposed load phase plus the prologue's row loads).
 template <class Kern>
 void plan_gemm(const char *name, Kern kern, const LlamaGemmArgs &a, int grid, int nb, bool norm,
-               int epi, int waves) {
+               int epi, int waves, bool panel = false) {
   // The plan's unit is four waves (one per SIMD), as its occupancy is: an
   // eight-wave workgroup is two units that run side by side, each with half
   // of the workgroup's tile (its rows, and half of the B chunks it shares).
@@ -514,7 +668,7 @@ void plan_gemm(const char *name, Kern kern, const LlamaGemmArgs &a, int grid, in
   const int kchunks = (a.K + TK - 1) / TK;
   const int TM = 8 * waves;
   npu_launch_plan p = make_plan(name, grid * units, wg_per_cu(kern, 64 * waves), grid * units, 16);
-  p.load_phases = norm ? 2 : 1;
+  p.load_phases = norm && !panel ? 2 : 1;  // the single-panel kernel issues every load up front
   p.tile_macs = (double)TM * TN * nb * kchunks * TK / units;
   // vector instructions per wave (SQ_INSTS_VALU less SQ_INSTS_MFMA): 225 + 98
   // per chunk (residual), 862 + 160 per chunk (RMSNorm + RoPE), 736 + 260 per
@@ -523,7 +677,8 @@ void plan_gemm(const char *name, Kern kern, const LlamaGemmArgs &a, int grid, in
   const double per = epi == kEpiResidual ? 98 : (epi == kEpiQkvRope ? 160 : 260);
   p.tile_valu = 4.0 * (fixed + per * kchunks);
   p.tile_lds_bytes = 2.0 * ((double)TM + nb * TN) * kchunks * TK * 2 / units;   // written once, read once
-  p.tile_load_bytes = (((double)TM + nb * TN) * kchunks * TK * 2 + (norm ? 4.0 * a.K : 0.0)) / units;
+  p.tile_load_bytes = (((double)TM + nb * TN) * kchunks * TK * 2 + (norm ? 4.0 * a.K : 0.0) +
+                       (norm && !panel ? (double)TM * a.K * 2 : 0.0)) / units;  // the general kernel reads A twice
   p.tile_store_bytes = (double)TM * TN * 2 / units;
   const double parts = epi == kEpiQkvRope ? a.nparts : (epi == kEpiSwiglu ? 2 : 1);
   p.hbm_bytes = 2.0 * ((double)a.M * a.K + parts * a.K * a.Npart +
@@ -544,7 +699,14 @@ hipError_t launch_llama_gemm(const LlamaGemmArgs &a, int pro, int epi, hipStream
   const int waves = pro == kProRmsnorm ? 8 : 4, TM = 8 * waves;
   dim3 grid(tiles_n, (a.M + TM - 1) / TM);
   const int g = grid.x * grid.y;
-  if (pro == kProRmsnorm && epi == kEpiQkvRope) {
+  const bool panel = pro == kProRmsnorm && a.K <= kNormGemmMaxK;
+  if (panel && epi == kEpiQkvRope) {
+    plan_gemm("llama_rmsnorm_qkv_rope", llama_norm_gemm_kernel<kEpiQkvRope>, a, g, 1, true, epi, 8, true);
+    hipLaunchKernelGGL((llama_norm_gemm_kernel<kEpiQkvRope>), grid, dim3(512), 0, s, a);
+  } else if (panel && epi == kEpiSwiglu) {
+    plan_gemm("llama_rmsnorm_swiglu", llama_norm_gemm_kernel<kEpiSwiglu>, a, g, 2, true, epi, 8, true);
+    hipLaunchKernelGGL((llama_norm_gemm_kernel<kEpiSwiglu>), grid, dim3(512), 0, s, a);
+  } else if (pro == kProRmsnorm && epi == kEpiQkvRope) {
     plan_gemm("llama_rmsnorm_qkv_rope", llama_gemm_kernel<kProRmsnorm, kEpiQkvRope, 8>, a, g, 1, true, epi, 8);
     hipLaunchKernelGGL((llama_gemm_kernel<kProRmsnorm, kEpiQkvRope, 8>), grid, dim3(512), 0, s, a);
   } else if (pro == kProPlain && epi == kEpiResidual) {

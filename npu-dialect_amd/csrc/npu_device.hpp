@@ -147,6 +147,27 @@ __device__ __forceinline__ void static_for(Fn &&f) {
   static_for_impl(f, std::make_integer_sequence<int, N>{});
 }
 
+// Sum of a float over the 64 lanes of a wave, the same in every lane: DPP
+// within each row of 16 lanes (quad permutes xor 1 and xor 2, then the
+// half-row and row mirrors, each pairing a lane with one that holds the other
+// half of its group), then the four rows' sums read out and added.  Vector-
+// ALU work only, where a __shfl_xor ladder is six dependent LDS-crossbar
+// round trips.
+template <int CTRL>
+__device__ __forceinline__ float dpp_mov(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xf, 0xf, false));
+}
+__device__ __forceinline__ float wave_sum(float v) {
+  v += dpp_mov<0xb1>(v);   // quad_perm [1,0,3,2]
+  v += dpp_mov<0x4e>(v);   // quad_perm [2,3,0,1]
+  v += dpp_mov<0x141>(v);  // row_half_mirror
+  v += dpp_mov<0x140>(v);  // row_mirror
+  const int u = __float_as_int(v);
+  return ((__int_as_float(__builtin_amdgcn_readlane(u, 0)) + __int_as_float(__builtin_amdgcn_readlane(u, 16))) +
+          __int_as_float(__builtin_amdgcn_readlane(u, 32))) +
+         __int_as_float(__builtin_amdgcn_readlane(u, 48));
+}
+
 __device__ __forceinline__ Frag16 load16(const void *p) {
   Frag16 r;
   r.u = *reinterpret_cast<const u32x4 *>(p);

@@ -182,6 +182,13 @@ LDS_KERNELS = {
     "llama_gemm_kernel<1, 2, 8> (swiglu)": ([(IN, 64 * 144 * 2, 0, 9, 1), (IN, 64 * 144 * 2, 1, 9, 1),
                                              (IN, 64 * 144 * 2, 2, 9, 1),
                                              (MID, 64 * 4, 3, 9, 0)], 111104),
+    # the single-panel RMSNorm GEMMs (K <= 512): the normalised A panel
+    # [4 chunks x 64 x 144 bf16] and B [64 x 144 bf16] ping/pong (two for SwiGLU)
+    "llama_norm_gemm_kernel<0> (qkv, one panel)": ([(IN, 4 * 64 * 144 * 2, 0, 9, 0),
+                                                    (IN, 64 * 144 * 2, 1, 9, 1)], 110592),
+    "llama_norm_gemm_kernel<2> (swiglu, one panel)": ([(IN, 4 * 64 * 144 * 2, 0, 9, 0),
+                                                       (IN, 64 * 144 * 2, 1, 9, 1),
+                                                       (IN, 64 * 144 * 2, 2, 9, 1)], 147456),
     # K[2 key groups x 64 x 80 bf16] and V^T[2 x 64 x 80 bf16] ping/pong
     "llama_attention_kernel": ([(IN, 2 * 64 * 80 * 2, 0, 9, 1), (IN, 2 * 64 * 80 * 2, 1, 9, 1)], 81920),
 }
