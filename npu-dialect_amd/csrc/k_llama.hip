@@ -672,8 +672,11 @@ void plan_gemm(const char *name, Kern kern, const LlamaGemmArgs &a, int grid, in
   p.tile_macs = (double)TM * TN * nb * kchunks * TK / units;
   // vector instructions per wave (SQ_INSTS_VALU less SQ_INSTS_MFMA): 225 + 98
   // per chunk (residual), 862 + 160 per chunk (RMSNorm + RoPE), 736 + 260 per
-  // chunk (RMSNorm + SwiGLU, two B operands)
-  const double fixed = epi == kEpiResidual ? 225 : (epi == kEpiQkvRope ? 862 : 736);
+  // chunk (RMSNorm + SwiGLU, two B operands); the single-panel variants
+  // count 1345 and 1563 at four chunks (705 and 523 fixed)
+  const double fixed = epi == kEpiResidual ? 225
+                       : epi == kEpiQkvRope ? (panel ? 705 : 862)
+                                            : (panel ? 523 : 736);
   const double per = epi == kEpiResidual ? 98 : (epi == kEpiQkvRope ? 160 : 260);
   p.tile_valu = 4.0 * (fixed + per * kchunks);
   p.tile_lds_bytes = 2.0 * ((double)TM + nb * TN) * kchunks * TK * 2 / units;   // written once, read once
