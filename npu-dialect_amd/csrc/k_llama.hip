@@ -23,9 +23,10 @@
 // LDS panel of all of K and has every B chunk in flight from the start.
 //
 // Attention: causal flash attention, one workgroup per (head, 64 queries),
-// four waves of 16 query rows.  Key blocks of 64 (K rows and V transposed)
-// are staged once in LDS for the four waves, the next block prefetched into
-// registers; online softmax in f32; P rounded to bf16 for its MFMA with V.
+// four key groups of four waves of 16 query rows.  Key blocks of 64 (K rows
+// and V transposed) are staged once in LDS for a group's four waves, the
+// next block prefetched into registers; online softmax in f32; P rounded to
+// bf16 for its MFMA with V.
 #include <cmath>
 #include <type_traits>
 
@@ -461,21 +462,23 @@ constexpr int AQ = 64;          // queries per workgroup (4 waves x 16, per key 
 constexpr int AK = 64;          // keys per block
 constexpr int LDK = 64 + 16;  // LDS row stride of K rows and V^T rows (elements): 160 bytes
 
-// Two key groups of four waves: waves 0-3 take the even key blocks, waves
-// 4-7 the odd ones, for the same 64 queries, each group with its own staged
-// K/V blocks; at the end group 1 hands its online-softmax state (max, sum,
-// unnormalised output) to group 0 through LDS, which merges the two and
-// stores.  Against one group this halves the longest chain of key blocks and
-// puts two waves on every SIMD.
-__global__ __launch_bounds__(512) void llama_attention_kernel(const uint16_t *__restrict__ Q,
+// AG key groups of four waves: group g takes key blocks g, g + AG, ... for
+// the same 64 queries, each group with its own staged K/V blocks; at the end
+// groups 1 .. AG-1 hand their online-softmax state (max, sum, unnormalised
+// output) to group 0 through LDS, which merges them in order and stores.
+// Against one group this divides the longest chain of key blocks (the last
+// query block's) by AG; four groups put four waves on every SIMD and fill
+// the CU's 160 KiB of LDS with their double-buffered K/V stages.
+constexpr int AG = 4;
+__global__ __launch_bounds__(256 * AG) void llama_attention_kernel(const uint16_t *__restrict__ Q,
                                                               const uint16_t *__restrict__ K,
                                                               const uint16_t *__restrict__ V,
                                                               uint16_t *__restrict__ O, int S,
                                                               int H, float scale) {
   constexpr int DH = 64;
   constexpr float kLog2e = 1.4426950408889634f;
-  __shared__ __attribute__((aligned(16))) uint16_t Ks[2][2][AK * LDK];   // [group][buf][key][d]
-  __shared__ __attribute__((aligned(16))) uint16_t Vt[2][2][DH * LDK];   // [group][buf][d][key]
+  __shared__ __attribute__((aligned(16))) uint16_t Ks[AG][2][AK * LDK];  // [group][buf][key][d]
+  __shared__ __attribute__((aligned(16))) uint16_t Vt[AG][2][DH * LDK];  // [group][buf][d][key]
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int kg = wave >> 2, qw = wave & 3, gt = tid & 255;  // key group, query wave, lane in group
   const int r = lane & 15, q = lane >> 4;
@@ -498,26 +501,31 @@ __global__ __launch_bounds__(512) void llama_attention_kernel(const uint16_t *__
   // consecutive words instead of one bank.
   const int kr = gt >> 2, kd = (gt & 3) * 16;        // K: key kr, d kd..kd+15
   const int vk = (gt & 31) * 2, vd = (gt >> 5) * 8;  // V: keys vk, vk+1; d vd..vd+7
-  u32x4 sk[2], sv[2];
-  uint32_t okbits = 0;
-  auto fetch = [&](int kb) {
+  // Two register slots: a group's block j lives in slot j % 2 from its
+  // fetch (two steps ahead) to its commit into LDS buffer j % 2.
+  u32x4 sk[2][2], sv[2][2];
+  uint32_t okbits[2] = {0u, 0u};
+  auto fetch = [&](auto slot, int kb) __attribute__((always_inline)) {
+    constexpr int SL = decltype(slot)::value;
     const int key = kb + kr;
 #pragma unroll
     for (int s2 = 0; s2 < 2; ++s2)
-      sk[s2] = load16(K + (size_t)min(key, S - 1) * D + h * DH + kd + 8 * s2).u;
-    okbits = (uint32_t)(key < S);
+      sk[SL][s2] = load16(K + (size_t)min(key, S - 1) * D + h * DH + kd + 8 * s2).u;
+    uint32_t ok = (uint32_t)(key < S);
 #pragma unroll
     for (int s2 = 0; s2 < 2; ++s2) {
       const int vkey = kb + vk + s2;
-      sv[s2] = load16(V + (size_t)min(vkey, S - 1) * D + h * DH + vd).u;
-      okbits |= (uint32_t)(vkey < S) << (1 + s2);
+      sv[SL][s2] = load16(V + (size_t)min(vkey, S - 1) * D + h * DH + vd).u;
+      ok |= (uint32_t)(vkey < S) << (1 + s2);
     }
+    okbits[SL] = ok;
   };
-  auto commit = [&](int buf) {
+  auto commit = [&](auto slot, int buf) __attribute__((always_inline)) {
+    constexpr int SL = decltype(slot)::value;
 #pragma unroll
     for (int s2 = 0; s2 < 2; ++s2)
-      *reinterpret_cast<u32x4 *>(&Ks[kg][buf][kr * LDK + kd + 8 * s2]) = masked(sk[s2], okbits & 1u);
-    const u32x4 v0 = masked(sv[0], (okbits >> 1) & 1u), v1 = masked(sv[1], (okbits >> 2) & 1u);
+      *reinterpret_cast<u32x4 *>(&Ks[kg][buf][kr * LDK + kd + 8 * s2]) = masked(sk[SL][s2], okbits[SL] & 1u);
+    const u32x4 v0 = masked(sv[SL][0], (okbits[SL] >> 1) & 1u), v1 = masked(sv[SL][1], (okbits[SL] >> 2) & 1u);
 #pragma unroll
     for (int j = 0; j < 8; ++j)
       *reinterpret_cast<uint32_t *>(&Vt[kg][buf][(vd + j) * LDK + vk]) = pair_word(v0, v1, j);
@@ -532,19 +540,21 @@ __global__ __launch_bounds__(512) void llama_attention_kernel(const uint16_t *__
 
   const int kend = min(q0 + AQ, S);  // keys beyond the block's last query are masked for all
   const int nblocks = (kend + AK - 1) / AK;
-  const int nsteps = (nblocks + 1) / 2;  // each step: one block per key group
-  fetch(min(kg, nblocks - 1) * AK);
-  commit(0);
+  const int nsteps = (nblocks + AG - 1) / AG;  // each step: one block per key group
+  fetch(Slot<0>{}, min(kg, nblocks - 1) * AK);
+  fetch(Slot<1>{}, min(kg + AG, nblocks - 1) * AK);
+  commit(Slot<0>{}, 0);
   __syncthreads();
   // fetch and commit are unconditional (past its last block a group
   // refetches the last block into its idle buffer): with a condition on
   // either, the compiler's wait analysis drains every outstanding load at the
-  // loop head.
-  for (int step = 0; step < nsteps; ++step) {
-    const int blk = 2 * step + kg;
+  // loop head.  Steps go in pairs so that the register slots are
+  // compile-time; a step past nsteps has no visible block (blk >= nblocks).
+  auto step_fn = [&](auto slot, int step) __attribute__((always_inline)) {
+    constexpr int buf = decltype(slot)::value;  // = step % 2
+    const int blk = AG * step + kg;
     const int kb = blk * AK;
-    fetch(min(blk + 2, nblocks - 1) * AK);
-    const int buf = step & 1;
+    fetch(slot, min(blk + 2 * AG, nblocks - 1) * AK);  // this step's slot: its block is in LDS
     if (blk < nblocks && kb <= i0 + 15) {  // some key of the block is visible to this wave (uniform)
       f32x4 s[4];         // s[ct][e]: score of key kb + 16ct + 4q + e
 #pragma unroll
@@ -556,31 +566,47 @@ __global__ __launch_bounds__(512) void llama_attention_kernel(const uint16_t *__
           MfmaBF16::mma(s[ct], kf, qb[ks]);
         }
       }
+      // Raw scores: the scale is folded into the exponent (sc2 > 0, so the
+      // maximum of the scaled scores is the scaled maximum).  Keys past a
+      // query or past S are masked only in a block that reaches either
+      // (wave-uniform test).
       float mx = -INFINITY;
+      if (kb + AK - 1 > i0 || kb + AK > S) {
 #pragma unroll
-      for (int ct = 0; ct < 4; ++ct)
+        for (int ct = 0; ct < 4; ++ct)
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const int key = kb + 16 * ct + 4 * q + e;
-          const float v = (key <= row && key < S) ? s[ct][e] * sc2 : -INFINITY;
-          s[ct][e] = v;
-          mx = fmaxf(mx, v);
-        }
-      mx = fmaxf(mx, __shfl_xor(mx, 16));
-      mx = fmaxf(mx, __shfl_xor(mx, 32));
-      const float mnew = fmaxf(m2, mx);
+          for (int e = 0; e < 4; ++e) {
+            const int key = kb + 16 * ct + 4 * q + e;
+            const float v = (key <= row && key < S) ? s[ct][e] : -INFINITY;
+            s[ct][e] = v;
+            mx = fmaxf(mx, v);
+          }
+      } else {
+#pragma unroll
+        for (int ct = 0; ct < 4; ++ct)
+#pragma unroll
+          for (int e = 0; e < 4; ++e) mx = fmaxf(mx, s[ct][e]);
+      }
+      // over the four lanes of query r (r, r+16, r+32, r+48)
+      LanePair pr = lane_pair16(mx);
+      mx = fmaxf(pr.lo, pr.hi);
+      pr = lane_pair32(mx);
+      mx = fmaxf(pr.lo, pr.hi);
+      const float mnew = fmaxf(m2, mx * sc2);
       const float corr = (mnew == -INFINITY) ? 1.0f : __builtin_amdgcn_exp2f(m2 - mnew);
       float sum = 0.0f;
 #pragma unroll
       for (int ct = 0; ct < 4; ++ct)
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-          const float p = (mnew == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(s[ct][e] - mnew);
+          const float p = (mnew == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(fmaf(s[ct][e], sc2, -mnew));
           s[ct][e] = p;
           sum += p;
         }
-      sum += __shfl_xor(sum, 16);
-      sum += __shfl_xor(sum, 32);
+      pr = lane_pair16(sum);
+      sum = pr.lo + pr.hi;
+      pr = lane_pair32(sum);
+      sum = pr.lo + pr.hi;
       l = l * corr + sum;
       m2 = mnew;
 #pragma unroll
@@ -591,10 +617,8 @@ __global__ __launch_bounds__(512) void llama_attention_kernel(const uint16_t *__
         Frag16 pb;
 #pragma unroll
         for (int e2 = 0; e2 < 2; ++e2) {
-          pb.u[e2] = (uint32_t)f32_to_bf16(s[2 * ks][2 * e2]) |
-                     ((uint32_t)f32_to_bf16(s[2 * ks][2 * e2 + 1]) << 16);
-          pb.u[2 + e2] = (uint32_t)f32_to_bf16(s[2 * ks + 1][2 * e2]) |
-                         ((uint32_t)f32_to_bf16(s[2 * ks + 1][2 * e2 + 1]) << 16);
+          pb.u[e2] = cvt_pk_bf16(s[2 * ks][2 * e2], s[2 * ks][2 * e2 + 1]);
+          pb.u[2 + e2] = cvt_pk_bf16(s[2 * ks + 1][2 * e2], s[2 * ks + 1][2 * e2 + 1]);
         }
 #pragma unroll
         for (int dt = 0; dt < 4; ++dt) {
@@ -608,16 +632,21 @@ __global__ __launch_bounds__(512) void llama_attention_kernel(const uint16_t *__
         }
       }
     }
-    commit(buf ^ 1);
+    commit(Slot<1 - buf>{}, 1 - buf);
     __syncthreads();
+  };
+  for (int step = 0; step < nsteps; step += 2) {
+    step_fn(Slot<0>{}, step);
+    step_fn(Slot<1>{}, step + 1);
   }
-  // merge: group 1's state goes through LDS (the K stage is free: every wave
-  // passed the loop's last barrier) to the group-0 wave with the same rows;
-  // a state that saw no key has max -inf and contributes nothing
-  float *xch = reinterpret_cast<float *>(&Ks[0][0][0]);  // 4 waves x 64 lanes x 18 floats
-  static_assert(4 * 64 * 18 * 4 <= 2 * 2 * AK * LDK * 2, "the exchange fits the K stage");
-  float *st = xch + (qw * 64 + lane) * 18;
-  if (kg == 1) {
+  // merge: the states of groups 1 .. AG-1 go through LDS (the K stage is
+  // free: every wave passed the loop's last barrier) to the group-0 wave with
+  // the same rows, which folds them in group order; a state that saw no key
+  // has max -inf and contributes nothing
+  float *xch = reinterpret_cast<float *>(&Ks[0][0][0]);  // (AG-1) groups x 4 waves x 64 lanes x 18 floats
+  static_assert((AG - 1) * 4 * 64 * 18 * 4 <= AG * 2 * AK * LDK * 2, "the exchange fits the K stage");
+  if (kg != 0) {
+    float *st = xch + (((kg - 1) * 4 + qw) * 64 + lane) * 18;
     st[0] = m2;
     st[1] = l;
 #pragma unroll
@@ -626,13 +655,16 @@ __global__ __launch_bounds__(512) void llama_attention_kernel(const uint16_t *__
       for (int e = 0; e < 4; ++e) st[2 + 4 * dt + e] = o[dt][e];
   }
   __syncthreads();
-  if (kg == 1) return;
-  {
+  if (kg != 0) return;
+#pragma unroll
+  for (int g = 1; g < AG; ++g) {
+    const float *st = xch + (((g - 1) * 4 + qw) * 64 + lane) * 18;
     const float m1 = st[0], l1 = st[1];
     const float mm = fmaxf(m2, m1);
     const float c0 = (m2 == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(m2 - mm);
     const float c1 = (m1 == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(m1 - mm);
     l = l * c0 + l1 * c1;
+    m2 = mm;
 #pragma unroll
     for (int dt = 0; dt < 4; ++dt)
 #pragma unroll
@@ -730,15 +762,15 @@ hipError_t launch_llama_attention(const uint16_t *Q, const uint16_t *K, const ui
   {
     // Causal: query block b sees key blocks 0..b; every key block costs QK^T
     // and PV MFMAs, the online-softmax update, and one staged K and V^T
-    // block.  A workgroup is two key groups of four waves, planned as two
-    // 4-wave units per query block, each walking half of its key blocks.
+    // block.  A workgroup is AG key groups of four waves, planned as AG
+    // 4-wave units per query block, each walking 1/AG of its key blocks.
     // With no more workgroups than CUs the launch lasts as long as its
-    // longest walk, the last query block's: ceil(nqb / 2) key blocks per
+    // longest walk, the last query block's: ceil(nqb / AG) key blocks per
     // unit (the plan's tile is the busiest CU's).
     const int nqb = grid.x;
-    const double kblocks = std::ceil(nqb / 2.0);
-    npu_launch_plan p = make_plan("llama_causal_attention", 2 * grid.x * grid.y,
-                                  wg_per_cu(llama_attention_kernel, 512), 2 * grid.x * grid.y, 16);
+    const double kblocks = std::ceil(nqb / (double)AG);
+    npu_launch_plan p = make_plan("llama_causal_attention", AG * grid.x * grid.y,
+                                  wg_per_cu(llama_attention_kernel, 256 * AG), AG * grid.x * grid.y, 16);
     p.load_phases = 1;
     p.tile_macs = kblocks * 2.0 * AQ * AK * 64;
     p.tile_valu = 4.0 * (150.0 + 335.0 * kblocks);  // per wave, counted: 832 on average at 2.25 blocks
@@ -748,7 +780,7 @@ hipError_t launch_llama_attention(const uint16_t *Q, const uint16_t *K, const ui
     p.hbm_bytes = 4.0 * S * H * 64 * 2;  // Q, K, V in, O out
     plans_add(p);
   }
-  hipLaunchKernelGGL(llama_attention_kernel, grid, dim3(512), 0, s, Q, K, V, O, S, H, scale);
+  hipLaunchKernelGGL(llama_attention_kernel, grid, dim3(256 * AG), 0, s, Q, K, V, O, S, H, scale);
   return hipGetLastError();
 }
 

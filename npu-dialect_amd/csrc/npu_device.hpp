@@ -168,6 +168,23 @@ __device__ __forceinline__ float wave_sum(float v) {
          __int_as_float(__builtin_amdgcn_readlane(u, 48));
 }
 
+// A lane's value and that of lane ^ 16 (or ^ 32), in vector registers:
+// gfx950's v_permlane16_swap (v_permlane32_swap) of (x, x) leaves, in every
+// lane, the value of the even 16-lane row (lower 32-lane half) of its pair
+// in .lo and that of the odd one in .hi.  lo op hi is then the pair's
+// reduction, the same in both lanes, with no LDS-crossbar round trip.
+struct LanePair {
+  float lo, hi;
+};
+__device__ __forceinline__ LanePair lane_pair16(float x) {
+  const auto p = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return LanePair{__uint_as_float(p[0]), __uint_as_float(p[1])};
+}
+__device__ __forceinline__ LanePair lane_pair32(float x) {
+  const auto p = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return LanePair{__uint_as_float(p[0]), __uint_as_float(p[1])};
+}
+
 __device__ __forceinline__ Frag16 load16(const void *p) {
   Frag16 r;
   r.u = *reinterpret_cast<const u32x4 *>(p);

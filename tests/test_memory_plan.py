@@ -189,8 +189,8 @@ LDS_KERNELS = {
     "llama_norm_gemm_kernel<2> (swiglu, one panel)": ([(IN, 4 * 64 * 144 * 2, 0, 9, 0),
                                                        (IN, 64 * 144 * 2, 1, 9, 1),
                                                        (IN, 64 * 144 * 2, 2, 9, 1)], 147456),
-    # K[2 key groups x 64 x 80 bf16] and V^T[2 x 64 x 80 bf16] ping/pong
-    "llama_attention_kernel": ([(IN, 2 * 64 * 80 * 2, 0, 9, 1), (IN, 2 * 64 * 80 * 2, 1, 9, 1)], 81920),
+    # K[4 key groups x 64 x 80 bf16] and V^T[4 x 64 x 80 bf16] ping/pong
+    "llama_attention_kernel": ([(IN, 4 * 64 * 80 * 2, 0, 9, 1), (IN, 4 * 64 * 80 * 2, 1, 9, 1)], 163840),
 }
 
 
