@@ -493,25 +493,34 @@ __global__ __launch_bounds__(256 * AG) void llama_attention_kernel(const uint16_
   for (int ks = 0; ks < 2; ++ks)
     qb[ks] = load16(Q + (size_t)min(row, S - 1) * D + h * DH + 32 * ks + 8 * q);
 
-  // staging: K block [64 keys][64 d] = 2 runs of 8 per thread; V block
-  // transposed: two keys x 8 d per thread.  Raw loads in fetch(), the zero
+  // staging: K block [64 keys][64 d] and V block [64 keys][64 d], each two
+  // 16-byte runs per thread, eight consecutive lanes on one key row's 128
+  // bytes (a wave loads whole cache lines).  Raw loads in fetch(), the zero
   // fill of keys past S in commit(), so the loads overlap the block's MFMAs.
-  // V lanes: 32 consecutive lanes take 32 consecutive key pairs of one
-  // 8-wide d group, so the transposed 4-byte LDS writes of a wave hit
-  // consecutive words instead of one bank.
-  const int kr = gt >> 2, kd = (gt & 3) * 16;        // K: key kr, d kd..kd+15
-  const int vk = (gt & 31) * 2, vd = (gt >> 5) * 8;  // V: keys vk, vk+1; d vd..vd+7
+  // K: keys kr and kr + 32, d kc..kc+7.  V: keys vk and vk + 1, d vd..vd+7,
+  // written transposed (V^T rows are d) as 4-byte key pairs.
+  const int kr = gt >> 3, kc = (gt & 7) * 8;
+  const int vk = (gt >> 3) * 2, vd = (gt & 7) * 8;
+  // V^T rows keep each 32-key half in the order the PV operand reads it:
+  // keys 4q..4q+3, 16+4q..16+4q+3 at 8q..8q+7, so a lane's eight keys are one
+  // 16-byte read (a key pair stays adjacent); and the 16-byte key chunk c of
+  // row d is stored at c ^ (d / 8 % 8), so the eight d groups' writes of one
+  // key pair fall in eight different chunks (without it, in one bank).
+  const int vkpos = (vk & ~31) + ((vk & 15) >> 2) * 8 + ((vk & 31) >> 4) * 4 + (vk & 3);
+  const int vkw = (((vkpos >> 3) ^ (vd >> 3)) << 3) + (vkpos & 7);  // d group vd / 8 = row / 8
   // Two register slots: a group's block j lives in slot j % 2 from its
   // fetch (two steps ahead) to its commit into LDS buffer j % 2.
   u32x4 sk[2][2], sv[2][2];
   uint32_t okbits[2] = {0u, 0u};
   auto fetch = [&](auto slot, int kb) __attribute__((always_inline)) {
     constexpr int SL = decltype(slot)::value;
-    const int key = kb + kr;
+    uint32_t ok = 0;
 #pragma unroll
-    for (int s2 = 0; s2 < 2; ++s2)
-      sk[SL][s2] = load16(K + (size_t)min(key, S - 1) * D + h * DH + kd + 8 * s2).u;
-    uint32_t ok = (uint32_t)(key < S);
+    for (int s2 = 0; s2 < 2; ++s2) {
+      const int key = kb + kr + 32 * s2;
+      sk[SL][s2] = load16(K + (size_t)min(key, S - 1) * D + h * DH + kc).u;
+      ok |= (uint32_t)(key < S) << (3 + s2);
+    }
 #pragma unroll
     for (int s2 = 0; s2 < 2; ++s2) {
       const int vkey = kb + vk + s2;
@@ -524,13 +533,17 @@ __global__ __launch_bounds__(256 * AG) void llama_attention_kernel(const uint16_
     constexpr int SL = decltype(slot)::value;
 #pragma unroll
     for (int s2 = 0; s2 < 2; ++s2)
-      *reinterpret_cast<u32x4 *>(&Ks[kg][buf][kr * LDK + kd + 8 * s2]) = masked(sk[SL][s2], okbits[SL] & 1u);
+      *reinterpret_cast<u32x4 *>(&Ks[kg][buf][(kr + 32 * s2) * LDK + kc]) =
+          masked(sk[SL][s2], (okbits[SL] >> (3 + s2)) & 1u);
     const u32x4 v0 = masked(sv[SL][0], (okbits[SL] >> 1) & 1u), v1 = masked(sv[SL][1], (okbits[SL] >> 2) & 1u);
 #pragma unroll
     for (int j = 0; j < 8; ++j)
-      *reinterpret_cast<uint32_t *>(&Vt[kg][buf][(vd + j) * LDK + vk]) = pair_word(v0, v1, j);
+      *reinterpret_cast<uint32_t *>(&Vt[kg][buf][(vd + j) * LDK + vkw]) = pair_word(v0, v1, j);
   };
 
+  int vsw[4];  // the chunk swizzle of V^T rows 16 dt + r
+#pragma unroll
+  for (int dt = 0; dt < 4; ++dt) vsw[dt] = (2 * dt + (r >> 3)) & 7;
   // online softmax state of query `row`, in the log2 domain
   float m2 = -INFINITY, l = 0.0f;
   f32x4 o[4];  // o[dt][e] = O[row][16*dt + 4q + e] (unnormalised)
@@ -623,11 +636,7 @@ __global__ __launch_bounds__(256 * AG) void llama_attention_kernel(const uint16_
 #pragma unroll
         for (int dt = 0; dt < 4; ++dt) {
           // A operand: V^T rows d = 16dt + r, the same keys in the same slots
-          const uint16_t *vrow = &Vt[kg][buf][(16 * dt + r) * LDK + 32 * ks + 4 * q];
-          const uint2 lo = *reinterpret_cast<const uint2 *>(vrow);
-          const uint2 hi = *reinterpret_cast<const uint2 *>(vrow + 16);
-          Frag16 va;
-          va.u = u32x4{lo.x, lo.y, hi.x, hi.y};
+          const Frag16 va = load16(&Vt[kg][buf][(16 * dt + r) * LDK + (((4 * ks + q) ^ vsw[dt]) << 3)]);
           MfmaBF16::mma(o[dt], va, pb);
         }
       }
