@@ -782,7 +782,7 @@ hipError_t launch_llama_attention(const uint16_t *Q, const uint16_t *K, const ui
                                   wg_per_cu(llama_attention_kernel, 256 * AG), AG * grid.x * grid.y, 16);
     p.load_phases = 1;
     p.tile_macs = kblocks * 2.0 * AQ * AK * 64;
-    p.tile_valu = 4.0 * (150.0 + 335.0 * kblocks);  // per wave, counted: 832 on average at 2.25 blocks
+    p.tile_valu = 4.0 * (150.0 + 335.0 * kblocks);  // per wave; counted: 551 on average at 1.125 blocks
     p.tile_lds_bytes = kblocks * (2.0 * 2 * AK * 64 * 2 + 4.0 * 2 * AK * 64 * 2);
     p.tile_load_bytes = kblocks * 2.0 * AK * 64 * 2 + AQ * 64 * 2.0;
     p.tile_store_bytes = AQ * 64 * 2.0;
