@@ -442,7 +442,11 @@ def test_c5_layer_end_to_end(cuda, llama_case):
         check_bound(bf16(_host(o[name])), bf16(ref), mag, RTOL_BF16, what=f"layer {name}")
 
 
-@pytest.mark.parametrize("S,D,H,F", [(64, 128, 2, 192), (128, 64, 1, 64), (96, 128, 2, 128)])
+# S = 1088: the last query block's 17 key blocks give each of the
+# attention's four key groups five steps (an odd count), with K/V blocks
+# refetched into both register slots on the way.
+@pytest.mark.parametrize("S,D,H,F", [(64, 128, 2, 192), (128, 64, 1, 64), (96, 128, 2, 128),
+                                     (1088, 128, 2, 128)])
 def test_c5_layer_small_shapes(cuda, S, D, H, F):
     w = configs.llama_layer(S=S, D=D, H=H, F=F, seed=91 + S)
     inp = w.make_inputs()
