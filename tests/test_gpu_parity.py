@@ -126,6 +126,7 @@ def test_c2_conv_config_n32(cuda, dtype):
     # four 64-byte chunks) at a run-time width, an odd H, two 64-filter
     # blocks, a 64-wide row and four bf16 chunks
     (64, 17, 9, 32, 128, 3, 1, "relu", True, "f32"),
+    (64, 17, 30, 64, 64, 3, 1, "relu", True, "f32"),  # 64 channels at a run-time width
     (32, 32, 64, 64, 64, 3, 1, "relu", True, "f32"),
     (40, 26, 60, 64, 64, 3, 1, "relu6", False, "bf16"),
     (64, 16, 20, 128, 64, 3, 1, "none", True, "bf16"),
