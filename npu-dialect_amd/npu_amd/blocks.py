@@ -132,3 +132,35 @@ def inverted_residual(N, H, W, C, E, elem="f32"):
     text += _conv("%pr", "%d", "%wp", es, [C, 1, 1, E], xs, elem)
     text += _epilogue("%y", "%pr", None, xs, elem, "none", residual="%x")
     return text + f"  return %y : {_t(xs, elem)}\n}}\n"
+
+
+def mlp(M, K, H, N, elem="f32"):
+    """Two matmul -> ReLU layers, out = relu(relu(x @ w1) @ w2): the workload of
+    test/mlp.mlir (128x256 . 256x512 . 512x256 in f16 there), written by this
+    builder with the same ops, types and generic bodies."""
+    def layer(i, x, w, xs, ws, os_):
+        return (f"  %init{i} = tensor.empty() : {_t(os_, elem)}\n"
+                f"  %fill{i} = linalg.fill ins(%cst : {elem}) outs(%init{i} : {_t(os_, elem)}) -> "
+                f"{_t(os_, elem)}\n"
+                f"  %mm{i} = linalg.matmul ins({x}, {w} : {_t(xs, elem)}, {_t(ws, elem)}) "
+                f"outs(%fill{i} : {_t(os_, elem)}) -> {_t(os_, elem)}\n" +
+                _epilogue(f"%relu{i}", f"%mm{i}", None, os_, elem, "relu"))
+    return (f"func.func @mlp(%input: {_t([M, K], elem)}, %w1: {_t([K, H], elem)}, "
+            f"%w2: {_t([H, N], elem)}) -> {_t([M, N], elem)} {{\n"
+            f"  %cst = arith.constant 0.0 : {elem}\n" +
+            layer(1, "%input", "%w1", [M, K], [K, H], [M, H]) +
+            layer(2, "%relu1", "%w2", [M, H], [H, N], [M, N]) +
+            f"  return %relu2 : {_t([M, N], elem)}\n}}\n")
+
+
+def reference_workload(name):
+    """Builder text of a reference test workload, by its file name:
+    test/matmul_relu.mlir (fill -> matmul 128x256 . 256x512 -> ReLU, f16) and
+    test/mlp.mlir.  They run on the GPU where the reference's files are not
+    present; a CPU test checks that each has the same ops, types, indexing maps
+    and generic bodies as the reference's file."""
+    if name == "matmul_relu.mlir":
+        return matmul_bias_act(128, 256, 512, act="relu", bias=False, elem="f16")
+    if name == "mlp.mlir":
+        return mlp(128, 256, 512, 256, elem="f16")
+    raise KeyError(name)

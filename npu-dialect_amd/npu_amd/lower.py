@@ -11,7 +11,9 @@ to the function's arguments and to earlier calls' results, and returns a Program
 that runs those calls on the GPU.  Matched:
 
 * {fill, matmul, generic...}: bias add and ReLU / ReLU6 / none in the generic
-  bodies -> fused_matmul_bias_act (f32);
+  bodies -> fused_matmul_bias_act (f32).  A group holding several matmul
+  chains (test/mlp.mlir's matmul -> ReLU -> matmul -> ReLU) becomes one call
+  per chain, in order;
 * {fill, conv_2d_nhwc_fhwc, generic...}, its input optionally a tensor.pad of
   zeros symmetric in H and W -> fused_conv2d_nhwc_bias_act (f32 / bf16), the pad
   folded into the call;
@@ -21,11 +23,23 @@ that runs those calls on the GPU.  Matched:
   shapes) -> one fused_irb_f32 call (f32), the expanded tensor never leaving
   the chip.
 
-Anything else -- an op no group covers, another dtype, a stride -- raises
-NotImplementedError naming it: there is no fallback implementation.
+A generic is matched by what its region computes, not by the names of the ops
+in it: the yielded value must be the chain's value plus, optionally, a bias
+(indexing map: the last output dimension only) and a residual (identity map),
+through `arith.addf`, then optionally `arith.maximumf(., 0.0)` (ReLU) and
+`arith.minimumf(., 6.0)` on top of it (ReLU6); every `linalg.fill` and
+`tensor.pad` must write 0.0.  Anything else -- an op no group covers, another
+body, another dtype, a stride or dilation -- raises NotImplementedError naming
+it: there is no fallback implementation.
+
+f16 text is run the way the reference harness runs it: every `f16` of the text
+becomes `f32` before anything else (tools/harness/e2e_verify.py:163-164), so
+`lower_text` of test/matmul_relu.mlir executes the f32 function the
+reference's CPU path executes.
 """
 from __future__ import annotations
 
+import re
 from dataclasses import dataclass, field
 
 from . import mlir, pipeline
@@ -41,15 +55,14 @@ class Call:
     views: dict = field(default_factory=dict)    # SSA name -> shape the entry point takes
 
 
-_TORCH_DTYPE = {"f32": "float32", "bf16": "bfloat16"}
+_TORCH_DTYPE = {"f32": "float32", "bf16": "bfloat16", "i8": "int8", "i32": "int32"}
 
 
-def _act(body_ops):
-    if "arith.minimumf" in body_ops:
-        return "relu6"
-    if "arith.maximumf" in body_ops:
-        return "relu"
-    return "none"
+def harness_f32(text: str) -> str:
+    """The reference harness's element-type rule: the text's f16 becomes f32
+    (tools/harness/e2e_verify.py:163-164, `original.replace('f16', 'f32')`).
+    The reference's texts hold no bf16; here bf16 is left as it is."""
+    return re.sub(r"(?<!b)f16", "f32", text)
 
 
 class _Fn:
@@ -68,32 +81,139 @@ class _Fn:
         return self.f.types[v]
 
 
+def _float(literal):
+    """The value of an arith.constant literal ("0.0", "6.000000e+00"), or None."""
+    if literal is None:
+        return None
+    try:
+        return float(str(literal).split(":")[0].strip())
+    except ValueError:
+        return None
+
+
+def _const(fn: _Fn, v):
+    op = fn.op(v)
+    if op is None or op.name != "arith.constant":
+        return None
+    return _float(op.attrs.get("value"))
+
+
+def _body_value(g):
+    """The yielded value of generic `g` as an expression: ("arg", k) for block
+    argument k, ("const", x), or (op name, lhs, rhs) for a binary arith op."""
+    args, body, yielded = g.attrs.get("block_args", []), g.attrs.get("body", []), \
+        g.attrs.get("yield", [])
+    env = {a: ("arg", k) for k, a in enumerate(args)}
+    for b in body:
+        if b.name == "arith.constant":
+            env[b.result] = ("const", _float(b.value))
+        elif b.name in ("arith.addf", "arith.maximumf", "arith.minimumf") and len(b.operands) == 2:
+            if any(o not in env for o in b.operands):
+                raise NotImplementedError(f"{g.results[0]}: generic body reads a value "
+                                          f"defined outside it ({b.operands})")
+            env[b.result] = (b.name, env[b.operands[0]], env[b.operands[1]])
+        else:
+            raise NotImplementedError(f"{g.results[0]}: {b.name} in a generic body "
+                                      "(epilogues are addf / maximumf / minimumf)")
+    if len(yielded) != 1 or yielded[0] not in env:
+        raise NotImplementedError(f"{g.results[0]}: generic yields {yielded}")
+    return env[yielded[0]]
+
+
+def _clamp(e, op, bound):
+    """x when e is op(x, bound) or op(bound, x), else None."""
+    if e[0] != op:
+        return None
+    a, b = e[1], e[2]
+    if b == ("const", bound):
+        return a
+    if a == ("const", bound):
+        return b
+    return None
+
+
+def _sum_leaves(e):
+    if e[0] == "arith.addf":
+        return _sum_leaves(e[1]) + _sum_leaves(e[2])
+    return [e]
+
+
+def _match_generic(fn: _Fn, g, v, shape):
+    """(bias, residual, act) of one epilogue generic applied to chain value v."""
+    rank = len(shape)
+    ident = list(range(rank))
+    name = g.results[0]
+    maps = g.attrs.get("maps", [])
+    if len(g.results) != 1 or len(g.outs) != 1:
+        raise NotImplementedError(f"{name}: generic with {len(g.results)} results")
+    if g.iterators != ["parallel"] * rank:
+        raise NotImplementedError(f"{name}: iterators {g.iterators} (epilogues are parallel)")
+    if len(maps) != len(g.ins) + 1 or maps[-1] != ident:
+        raise NotImplementedError(f"{name}: indexing maps {maps}")
+    if v not in g.ins:
+        raise NotImplementedError(f"{name}: epilogue not on the chain from {v}")
+    e = _body_value(g)
+    act = "none"
+    inner = _clamp(e, "arith.minimumf", 6.0)
+    if inner is not None:
+        x = _clamp(inner, "arith.maximumf", 0.0)
+        if x is None:
+            raise NotImplementedError(f"{name}: minimumf(., 6.0) not over maximumf(., 0.0)")
+        act, e = "relu6", x
+    else:
+        x = _clamp(e, "arith.maximumf", 0.0)
+        if x is not None:
+            act, e = "relu", x
+    bias = residual = None
+    seen_chain = False
+    for leaf in _sum_leaves(e):
+        if leaf[0] != "arg" or leaf[1] >= len(g.ins):
+            raise NotImplementedError(f"{name}: generic body term {leaf} "
+                                      "(a block argument of an input expected)")
+        operand, m = g.ins[leaf[1]], maps[leaf[1]]
+        t = fn.ty(operand)
+        if operand == v and m == ident and not seen_chain:
+            seen_chain = True
+        elif m == [rank - 1] and t.shape == [shape[-1]] and bias is None:
+            bias = operand
+        elif m == ident and t.shape == list(shape) and residual is None:
+            residual = operand
+        else:
+            raise NotImplementedError(f"{name}: operand {operand} {t} with map {m} "
+                                      "in the epilogue")
+    if not seen_chain:
+        raise NotImplementedError(f"{name}: the chain value {v} is not a term of the result")
+    return bias, residual, act
+
+
 def _epilogue(fn: _Fn, generics, src, shape):
-    """Bias (a 1-D operand of the last dimension), residual (a same-shape
-    operand) and activation of the generics that follow `src` in a group."""
+    """Bias, residual and activation of the generics that follow `src` in a
+    group, applied in order; returns (bias, residual, act, last value)."""
     bias = residual = None
     act = "none"
     v = src
     for g in generics:
-        if v not in g.ins:
-            raise NotImplementedError(f"{g.results[0]}: epilogue not on the chain from {src}")
-        for o in g.ins:
-            if o == v:
-                continue
-            t = fn.ty(o)
-            if t.shape == [shape[-1]] and bias is None:
-                bias = o
-            elif t.shape == list(shape) and residual is None:
-                residual = o
-            else:
-                raise NotImplementedError(f"{g.results[0]}: operand {o} {t} in the epilogue")
-        a = _act(g.body_ops)
-        if a != "none":
-            if act != "none":
-                raise NotImplementedError(f"{g.results[0]}: a second activation")
-            act = a
+        b, r, a = _match_generic(fn, g, v, shape)
+        if act != "none" and (b or r or a != "none"):
+            raise NotImplementedError(f"{g.results[0]}: epilogue after the activation")
+        if b is not None:
+            if bias is not None or residual is not None:
+                raise NotImplementedError(f"{g.results[0]}: a second bias / bias after a residual")
+            bias = b
+        if r is not None:
+            if residual is not None:
+                raise NotImplementedError(f"{g.results[0]}: a second residual")
+            residual = r
+        act = a if a != "none" else act
         v = g.results[0]
     return bias, residual, act, v
+
+
+def _check_fill(fn: _Fn, fill):
+    c = _const(fn, fill.ins[0]) if fill.ins else None
+    if c != 0.0:
+        raise NotImplementedError(f"{fill.results[0]}: linalg.fill with {fill.ins} "
+                                  "(accumulators start at 0.0)")
 
 
 def _pad_of(fn: _Fn, v):
@@ -104,11 +224,21 @@ def _pad_of(fn: _Fn, v):
     lo, hi = op.attrs.get("low", []), op.attrs.get("high", [])
     if len(lo) != 4 or lo != hi or lo[0] or lo[3] or lo[1] != lo[2]:
         raise NotImplementedError(f"{v}: pad low {lo} high {hi} (entry points pad H and W equally)")
+    if _const(fn, op.attrs.get("yield")) != 0.0:
+        raise NotImplementedError(f"{v}: tensor.pad yields {op.attrs.get('yield')} (zero padding)")
     return op.operands[0], lo[1]
 
 
-def _strided(op):
-    return any(s != 1 for s in op.attrs.get("strides", [1, 1]))
+def _check_conv(op):
+    if any(s != 1 for s in op.attrs.get("strides", [1, 1])):
+        raise NotImplementedError(f"{op.results[0]}: strided convolution")
+    if "dilations" in op.text and "dilations = dense<1>" not in op.text.replace("  ", " "):
+        raise NotImplementedError(f"{op.results[0]}: dilated convolution")
+
+
+def _check_matmul(op):
+    if "indexing_maps" in op.text:
+        raise NotImplementedError(f"{op.results[0]}: linalg.matmul with indexing maps")
 
 
 def _elem(fn, v, allowed, what):
@@ -118,52 +248,87 @@ def _elem(fn, v, allowed, what):
     return e
 
 
+ANCHORS = ("linalg.matmul", "linalg.conv_2d_nhwc_fhwc")
+
+
+def _segments(name, ops):
+    """Splits a group's ops into chains [fills..., anchor, generics...]: each
+    fill goes with the anchor whose accumulator it initialises, each generic
+    with the chain whose value it reads."""
+    anchors = [o for o in ops if o.name in ANCHORS]
+    if not anchors:
+        raise NotImplementedError(f"{name}: no MI355X entry point runs ops "
+                                  f"{[o.name for o in ops if o.name != 'linalg.fill']}")
+    segs = [{"anchor": a, "fills": [], "generics": [], "value": a.results[0]} for a in anchors]
+    for o in ops:
+        if o.name in ANCHORS:
+            continue
+        if o.name == "linalg.fill":
+            owner = [s for s in segs if o.results[0] in s["anchor"].outs]
+            if len(owner) != 1:
+                raise NotImplementedError(f"{name}: {o.results[0]} fills no accumulator")
+            owner[0]["fills"].append(o)
+        elif o.name == "linalg.generic":
+            owner = [s for s in segs if s["value"] in o.ins]
+            if len(owner) != 1:
+                raise NotImplementedError(f"{name}: {o.results[0]} is on no matmul/conv chain")
+            owner[0]["generics"].append(o)
+            owner[0]["value"] = o.results[0]
+        else:
+            raise NotImplementedError(f"{name}: no MI355X entry point runs {o.name} in a group")
+    for s in segs:
+        if len(s["fills"]) != 1:
+            raise NotImplementedError(f"{name}: {s['anchor'].results[0]} accumulates into a "
+                                      "value that is not a fill of 0.0")
+    return segs
+
+
 def lower(func: mlir.MFunc, target=None) -> "Program":
     """Matches func's outlined groups to entry points; see the module docstring."""
     fn = _Fn(func)
     rep = pipeline.run(func, target)
     groups = {g["name"]: [func.ops[i] for i in g["ops"]] for g in rep["functions"]}
     calls, covered, consumed = [], set(), set()
-    kinds = lambda ops: [o.name for o in ops if o.name != "linalg.fill"]
     for name, ops in groups.items():
         if name in consumed:
             continue
-        k = kinds(ops)
-        gens = [o for o in ops if o.name == "linalg.generic"]
-        if k[:1] == ["linalg.matmul"] and all(x == "linalg.generic" for x in k[1:]):
-            mm = ops[[o.name for o in ops].index("linalg.matmul")]
-            shape = fn.ty(mm.results[0]).shape
-            bias, res, act, out = _epilogue(fn, gens, mm.results[0], shape)
-            if res is not None:
-                raise NotImplementedError(f"{name}: residual add after a matmul")
-            _elem(fn, mm.ins[0], ("f32",), name)
-            calls.append(Call("fused_matmul_bias_act", [name], [mm.ins[0], mm.ins[1], bias], out,
-                              {"act": act}))
-        elif k[:1] == ["linalg.conv_2d_nhwc_fhwc"] and all(x == "linalg.generic" for x in k[1:]):
-            conv = ops[[o.name for o in ops].index("linalg.conv_2d_nhwc_fhwc")]
-            if _strided(conv):
-                raise NotImplementedError(f"{name}: strided convolution")
-            shape = fn.ty(conv.results[0]).shape
-            bias, res, act, out = _epilogue(fn, gens, conv.results[0], shape)
-            x, pad = _pad_of(fn, conv.ins[0])
+        segs = _segments(name, ops)
+        for s in segs:
+            _check_fill(fn, s["fills"][0])
+            a = s["anchor"]
+            shape = fn.ty(a.results[0]).shape
+            bias, res, act, out = _epilogue(fn, s["generics"], a.results[0], shape)
+            if a.name == "linalg.matmul":
+                _check_matmul(a)
+                if res is not None:
+                    raise NotImplementedError(f"{name}: residual add after a matmul")
+                _elem(fn, a.ins[0], ("f32",), name)
+                calls.append(Call("fused_matmul_bias_act", [name], [a.ins[0], a.ins[1], bias], out,
+                                  {"act": act}))
+                continue
+            _check_conv(a)
+            x, pad = _pad_of(fn, a.ins[0])
             # the expand group of an inverted residual chain: fold the chain
-            chain = _irb_chain(fn, groups, name, conv, out, x, act, bias, res)
+            chain = _irb_chain(fn, groups, name, a, out, x, act, bias, res) if len(segs) == 1 \
+                else None
             if chain is not None:
                 calls.append(chain)
                 consumed.update(chain.functions)
                 covered.update(r for f2 in chain.functions for o in groups[f2] for r in o.results)
-                p = fn.op(chain.params["padded"])
-                covered.update(p.results)
+                covered.update(fn.op(chain.params["padded"]).results)
                 continue
             if res is not None:
                 raise NotImplementedError(f"{name}: residual add after a convolution")
-            _elem(fn, x, ("f32", "bf16"), name)
-            calls.append(Call("fused_conv2d_nhwc_bias_act", [name], [x, conv.ins[1], bias], out,
-                              {"pad": pad, "act": act}))
+            e = _elem(fn, x, ("f32", "bf16"), name)
+            params = {"pad": pad, "act": act}
+            if bias is not None and fn.ty(bias).elem != "f32":
+                if fn.ty(bias).elem != e:
+                    raise NotImplementedError(f"{name}: bias type {fn.ty(bias).elem}")
+                params["bias_to_f32"] = True  # exact widening; the group adds in f32
+            calls.append(Call("fused_conv2d_nhwc_bias_act", [name], [x, a.ins[1], bias], out,
+                              params))
             if pad:
-                covered.add(conv.ins[0])
-        else:
-            raise NotImplementedError(f"{name}: no MI355X entry point runs ops {k}")
+                covered.add(a.ins[0])
         covered.update(r for o in ops for r in o.results)
     # every computing op must be part of a call
     for op in func.ops:
@@ -205,8 +370,10 @@ def _irb_chain(fn, groups, name, conv, e_out, x, act, bias, res):
     b1, r1, a1, d = _epilogue(fn, [g1], dw.results[0], fn.ty(dw.results[0]).shape)
     pr = user(d, "linalg.conv_2d_nhwc_fhwc")
     g2 = pr and user(pr.results[0], "linalg.generic")
-    if g2 is None or (b1, r1, a1) != (None, None, "relu6") or _strided(dw) or _strided(pr):
+    if g2 is None or (b1, r1, a1) != (None, None, "relu6"):
         return None
+    _check_conv(dw)
+    _check_conv(pr)
     b2, r2, a2, y = _epilogue(fn, [g2], pr.results[0], fn.ty(pr.results[0]).shape)
     if (b2, a2) != (None, "none") or r2 != x:
         return None
@@ -219,11 +386,14 @@ def _irb_chain(fn, groups, name, conv, e_out, x, act, bias, res):
             return None
         if n not in names:
             names.append(n)
-    # the chain's groups hold only these ops (and fills)
+    # the chain's groups hold only these ops (and fills of 0.0)
     chain_ops = {id(o) for o in (dw, g1, pr, g2)}
     for n in names[1:]:
-        if any(o.name != "linalg.fill" and id(o) not in chain_ops for o in groups[n]):
-            return None
+        for o in groups[n]:
+            if o.name == "linalg.fill":
+                _check_fill(fn, o)
+            elif id(o) not in chain_ops:
+                return None
     _elem(fn, x, ("f32",), names[-1])
     E, C = wshape[0], wshape[3]
     return Call("fused_irb_f32", names, [x, conv.ins[1], dw.ins[1], pr.ins[1]], y,
@@ -242,6 +412,25 @@ class Program:
     def entry_points(self):
         return [c.entry for c in self.calls]
 
+    def check_inputs(self, inputs: dict) -> dict:
+        """Binds every argument to its tensor and checks the tensor's dtype and
+        shape against the function's signature."""
+        import torch
+
+        vals = {}
+        for a, t in self.func.args:
+            x = inputs.get(a, inputs.get(a.lstrip("%")))
+            if x is None:
+                raise KeyError(f"no tensor for argument {a}")
+            want = getattr(torch, _TORCH_DTYPE.get(t.elem, "void"), None)
+            if x.dtype != want:
+                raise TypeError(f"argument {a}: tensor of {x.dtype}, the function takes {t}")
+            if list(x.shape) != list(t.shape):
+                raise ValueError(f"argument {a}: tensor of shape {list(x.shape)}, "
+                                 f"the function takes {t}")
+            vals[a] = x
+        return vals
+
     def run(self, inputs: dict, stream=None) -> dict:
         """inputs: argument name (with or without %) -> tensor.  Returns the
         function's results by SSA name."""
@@ -249,12 +438,7 @@ class Program:
 
         from . import groups
 
-        vals = {}
-        for a, _ in self.func.args:
-            t = inputs.get(a, inputs.get(a.lstrip("%")))
-            if t is None:
-                raise KeyError(f"no tensor for argument {a}")
-            vals[a] = t
+        vals = self.check_inputs(inputs)
         for c in self.calls:
             args = []
             for v in c.args:
@@ -271,7 +455,8 @@ class Program:
             if c.entry == "fused_matmul_bias_act":
                 groups.fused_matmul_bias_act(args[0], args[1], args[2], out, c.params["act"], stream)
             elif c.entry == "fused_conv2d_nhwc_bias_act":
-                groups.fused_conv2d_nhwc_bias_act(args[0], args[1], args[2], out, c.params["pad"],
+                bias = args[2].float() if c.params.get("bias_to_f32") else args[2]
+                groups.fused_conv2d_nhwc_bias_act(args[0], args[1], bias, out, c.params["pad"],
                                                   c.params["act"], stream)
             elif c.entry == "fused_irb_f32":
                 groups.fused_irb_f32(args[0], args[1], args[2], args[3], out, stream)
@@ -284,5 +469,6 @@ class Program:
 
 
 def lower_text(text: str, target=None) -> "Program":
-    """`lower` on the first function of an MLIR text."""
-    return lower(mlir.parse_functions(text)[0], target)
+    """`lower` on the first function of an MLIR text, after the harness's
+    f16 -> f32 rule."""
+    return lower(mlir.parse_functions(harness_f32(text))[0], target)

@@ -162,6 +162,56 @@ def _statements(body: str):
     return stmts
 
 
+@dataclass
+class BodyOp:
+    """One operation of a linalg.generic region: ``result = name operands``
+    (``value`` holds an arith.constant's literal)."""
+    result: str
+    name: str
+    operands: list
+    value: str = None
+
+
+def parse_maps(attr_text: str) -> list:
+    """indexing_maps -> one list of result expressions per operand, in the
+    map's own dimension names replaced by their positions ("d1" -> 1; any
+    other expression is kept as text)."""
+    out = []
+    for dims, res in re.findall(r"affine_map<\(([^)]*)\)\s*->\s*\(([^)]*)\)>", attr_text):
+        names = [d.strip() for d in dims.split(",") if d.strip()]
+        exprs = []
+        for e in (x.strip() for x in res.split(",") if x.strip()):
+            exprs.append(names.index(e) if e in names else e)
+        out.append(exprs)
+    return out
+
+
+def parse_region(region: str):
+    """A generic's region -> (block argument names, [BodyOp], yielded values)."""
+    if not region:
+        return [], [], []
+    m = re.match(r"\^bb\d*\(([^)]*)\)\s*:", region)
+    args = [a.split(":")[0].strip() for a in m.group(1).split(",")] if m else []
+    body, yielded = [], []
+    for line in region[m.end() if m else 0:].split("\n"):
+        line = line.split("//", 1)[0].strip().rstrip("}").strip()
+        if not line:
+            continue
+        y = re.match(r"linalg\.yield\s+(.*?)\s*:", line)
+        if y:
+            yielded = [v.strip() for v in y.group(1).split(",")]
+            continue
+        b = re.match(r"(%[\w]+)\s*=\s*([\w\.]+)\s*(.*)$", line)
+        if not b:
+            continue
+        res, name, tail = b.groups()
+        if name == "arith.constant":
+            body.append(BodyOp(res, name, [], tail.rsplit(":", 1)[0].strip()))
+        else:
+            body.append(BodyOp(res, name, re.findall(r"%[\w]+", tail.split(":", 1)[0])))
+    return args, body, yielded
+
+
 def parse_op(stmt: str) -> MOp:
     s = stmt.strip()
     results = []
@@ -189,6 +239,8 @@ def parse_op(stmt: str) -> MOp:
         m2 = re.search(r":\s*(tensor<[^>]*>)\s*to\s*(tensor<[^>]*>)", flat)
         op.result_types = [parse_type(m2.group(2))]
         op.attrs["source_type"] = parse_type(m2.group(1))
+        y = re.search(r"tensor\.yield\s+(%[\w]+)", rest)
+        op.attrs["yield"] = y.group(1) if y else None
     elif name in ("return", "func.return"):
         op.name = "func.return"
         names = flat.split(":", 1)[0]
@@ -222,6 +274,8 @@ def parse_op(stmt: str) -> MOp:
             op.iterators = re.findall(r'"(\w+)"', it.group(1)) if it else []
             region = rest[rest.rfind("^bb"):] if "^bb" in rest else ""
             op.body_ops = re.findall(r"\b(arith\.\w+|math\.\w+)", region)
+            op.attrs["maps"] = parse_maps(rest[:rest.find("^bb")] if "^bb" in rest else rest)
+            op.attrs["block_args"], op.attrs["body"], op.attrs["yield"] = parse_region(region)
         if name == "linalg.transpose":
             p = re.search(r"permutation\s*=\s*\[([^\]]*)\]", rest)
             op.attrs["permutation"] = [int(x) for x in p.group(1).split(",")] if p else []

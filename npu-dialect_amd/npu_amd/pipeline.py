@@ -28,10 +28,7 @@ from __future__ import annotations
 from . import host, mlir
 
 # outlined op chain (index stripped) -> MI355X entry point
-try:
-    from .groups import OUTLINED_NAMES
-except Exception:  # groups imports the HIP library binding lazily; names only
-    OUTLINED_NAMES = {}
+from .names import OUTLINED_NAMES
 
 STEPS = ("fusion", "outline", "spatial", "core-map", "temporal", "canonicalize", "bufferize",
          "sram-alloc", "barrier-alloc", "cost-eval")

@@ -2,7 +2,7 @@
 
 The known answers are the reference's formulas (lib/Analysis/CostModel.cpp)
 evaluated by hand at the reference's default target on the reference's own
-test inputs (tests/golden/mlir/, copied from test/ and test/lit/):
+test inputs (test/ and test/lit/, read in place by tests/reference_inputs.py):
 * roofline of test/lit/cost_evaluate.mlir (CostModel.cpp:174-226): the walk
   counts linalg.fill as 1024 MACs, so 33 556 480 FLOP over 589 824 bytes,
   AI 56.89, 1.8432e-5 s, memory-bound against the ridge of 128;
@@ -13,17 +13,16 @@ test inputs (tests/golden/mlir/, copied from test/ and test/lit/):
 Each number is also recomputed here from the formula's terms, so a wrong
 term in the C++ shows up as a mismatch in a named quantity.
 """
-import os
 
 import pytest
 
+import reference_inputs
 from npu_amd import host, mlir
 
-GOLD = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "mlir")
 
 
 def load(name):
-    return host.Graph(mlir.parse_file(os.path.join(GOLD, name))[0])
+    return host.Graph(mlir.parse_file(reference_inputs.path(name))[0])
 
 
 @pytest.fixture(scope="module")
@@ -167,7 +166,7 @@ def test_specs_match_reference_tables(npu):
     conv = g.find("linalg.conv_2d_nchw_fchw")
     assert cm.spec_splits(conv) == [(0, 0, True), (1, 1, True), (2, 2, True), (3, 3, True),
                                     (-1, 4, False)]
-    mm = host.Graph(mlir.parse_file(os.path.join(GOLD, "matmul_relu.mlir"))[0])
+    mm = host.Graph(mlir.parse_file(reference_inputs.path("matmul_relu.mlir"))[0])
     cmm = host.CostModel(mm, npu)
     assert cmm.spec_splits(mm.find("linalg.matmul")) == [(0, 0, True), (1, 1, True),
                                                          (-1, 2, False)]

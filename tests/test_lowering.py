@@ -6,13 +6,12 @@ through its tile loop nests; each becomes one call of the entry point that runs
 the whole nest.  What no entry point runs is refused by name, never run
 another way.  (The GPU runs of these programs are in test_gpu_parity.py.)
 """
-import os
 
 import pytest
 
+import reference_inputs
 from npu_amd import blocks, lower, mlir, pipeline
 
-GOLD = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "mlir")
 
 
 def test_matmul_bias_act_is_one_call():
@@ -32,7 +31,10 @@ def test_conv_folds_the_pad(K, pad, elem):
     (c,) = p.calls
     assert c.entry == "fused_conv2d_nhwc_bias_act"
     assert c.functions == ["fused_fill_linalg_conv_2d_nhwc_fhwc_generic_0"]
-    assert c.args == ["%x", "%w", "%bias"] and c.params == {"pad": pad, "act": "relu"}
+    assert c.args == ["%x", "%w", "%bias"]
+    # a bf16 bias is widened to f32 exactly before the call (the group adds in f32)
+    want = {"pad": pad, "act": "relu", **({"bias_to_f32": True} if elem == "bf16" else {})}
+    assert c.params == want
 
 
 @pytest.mark.parametrize("shape,ngroups", [((1, 8, 8, 24, 144), 2), ((2, 9, 13, 24, 144), 3)])
@@ -53,15 +55,123 @@ def test_inverted_residual_chain_is_one_call(shape, ngroups):
     assert c.views == {"%we": [144, 24], "%wp": [24, 144]}
 
 
-@pytest.mark.parametrize("path,what", [
-    ("mlp.mlir", "no MI355X entry point"),        # matmul -> relu -> matmul -> relu, one group
-    ("conv2d_relu.mlir", "no MI355X entry point"),  # NCHW convolution
-    ("matmul_relu.mlir", "element type f16"),
-])
-def test_unsupported_is_refused(path, what):
-    f = mlir.parse_file(os.path.join(GOLD, path))[0]
-    with pytest.raises(NotImplementedError, match=what):
-        lower.lower(f)
+def test_nchw_conv_is_refused():
+    """test/conv2d_relu.mlir is NCHW: no entry point runs linalg.conv_2d_nchw_fchw."""
+    with pytest.raises(NotImplementedError, match="no MI355X entry point"):
+        lower.lower_text(reference_inputs.read("conv2d_relu.mlir"))
+
+
+def test_reference_matmul_relu_lowers_through_the_harness_rule():
+    """test/matmul_relu.mlir is f16; the reference harness runs it as f32
+    (e2e_verify.py:163-164), and so does the lowering: one call, ReLU, no bias."""
+    p = lower.lower_text(reference_inputs.read("matmul_relu.mlir"))
+    (c,) = p.calls
+    assert c.entry == "fused_matmul_bias_act" and c.args == ["%A", "%B", None]
+    assert c.params == {"act": "relu"} and c.out == "%relu"
+    assert all(t.elem == "f32" for _, t in p.func.args)
+
+
+def test_reference_mlp_is_two_calls():
+    """test/mlp.mlir outlines as one group of two matmul -> ReLU chains; it
+    runs as two calls, the second reading the first's result."""
+    p = lower.lower_text(reference_inputs.read("mlp.mlir"))
+    assert [c.entry for c in p.calls] == ["fused_matmul_bias_act"] * 2
+    assert p.calls[0].args == ["%input", "%w1", None] and p.calls[0].out == "%relu1"
+    assert p.calls[1].args == ["%relu1", "%w2", None] and p.calls[1].out == "%relu2"
+    assert p.calls[0].functions == p.calls[1].functions
+
+
+def _shape_of(func):
+    """The function with SSA names replaced by first-appearance numbers: op
+    names, operand/result types, indexing maps, iterators, generic bodies."""
+    ids = {}
+
+    def n(v):
+        return ids.setdefault(v, f"v{len(ids)}")
+    for a, _ in func.args:
+        n(a)
+    out = [[str(t) for _, t in func.args], [str(t) for t in func.result_types]]
+    for op in func.ops:
+        if op.name == "tensor.empty":
+            continue  # placeholders: the builder names one per generic
+        for r in op.results:
+            n(r)
+        body = [(b.name, b.value) for b in op.attrs.get("body", [])]
+        out.append((op.name, [n(v) for v in op.ins + op.operands if v in ids],
+                    [str(func.types[r]) for r in op.results], op.attrs.get("maps"),
+                    op.iterators, body, op.attrs.get("value")))
+    return out
+
+
+@pytest.mark.parametrize("name", ["matmul_relu.mlir", "mlp.mlir"])
+def test_builder_text_is_the_reference_workload(name):
+    """The GPU box has no reference checkout, so the GPU runs the builder's
+    text of these workloads; here it is checked against the reference's file."""
+    ref = mlir.parse_functions(reference_inputs.read(name))[0]
+    own = mlir.parse_functions(blocks.reference_workload(name))[0]
+    assert _shape_of(own) == _shape_of(ref)
+
+
+def _replace_body(text, old, new):
+    assert old in text
+    return text.replace(old, new)
+
+
+def test_bias_through_mulf_is_refused():
+    t = _replace_body(blocks.matmul_bias_act(8, 16, 8), "%s0 = arith.addf %in, %b",
+                      "%s0 = arith.mulf %in, %b")
+    with pytest.raises(NotImplementedError, match="arith.mulf"):
+        lower.lower_text(t)
+
+
+def test_bias_on_the_row_dimension_is_refused():
+    t = _replace_body(blocks.matmul_bias_act(8, 16, 8), "affine_map<(d0, d1) -> (d1)>",
+                      "affine_map<(d0, d1) -> (d0)>")
+    with pytest.raises(NotImplementedError, match="map"):
+        lower.lower_text(t)
+
+
+def test_nonzero_fill_and_clamp_are_refused():
+    t = _replace_body(blocks.matmul_bias_act(8, 16, 8), "%cst = arith.constant 0.0 : f32",
+                      "%cst = arith.constant 1.0 : f32")
+    with pytest.raises(NotImplementedError, match="fill"):
+        lower.lower_text(t)
+    t = _replace_body(blocks.matmul_bias_act(8, 16, 8), "%z = arith.constant 0.0 : f32",
+                      "%z = arith.constant 3.0 : f32")
+    with pytest.raises(NotImplementedError):
+        lower.lower_text(t)
+
+
+def test_relu6_bound_and_order_are_checked():
+    t = _replace_body(blocks.matmul_bias_act(8, 16, 8, act="relu6"),
+                      "%six = arith.constant 6.0 : f32", "%six = arith.constant 5.0 : f32")
+    with pytest.raises(NotImplementedError):
+        lower.lower_text(t)
+
+
+def test_output_block_argument_is_refused():
+    """Reading the generic's `outs` block argument accumulates into the
+    destination, which no entry point does."""
+    t = _replace_body(blocks.matmul_bias_act(8, 16, 8), "%s0 = arith.addf %in, %b",
+                      "%s0 = arith.addf %in, %out")
+    with pytest.raises(NotImplementedError, match="block argument"):
+        lower.lower_text(t)
+
+
+def test_nonzero_pad_is_refused():
+    t = blocks.conv_bias_act(1, 8, 8, 16, 16)
+    t = _replace_body(t, "tensor.yield %cst : f32", "tensor.yield %one : f32")
+    t = _replace_body(t, "%cst = arith.constant 0.0 : f32\n",
+                      "%cst = arith.constant 0.0 : f32\n  %one = arith.constant 1.0 : f32\n")
+    with pytest.raises(NotImplementedError, match="pad"):
+        lower.lower_text(t)
+
+
+def test_dilated_conv_is_refused():
+    t = _replace_body(blocks.conv_bias_act(1, 8, 8, 16, 16, pad=0), "dilations = dense<1>",
+                      "dilations = dense<2>")
+    with pytest.raises(NotImplementedError, match="dilated"):
+        lower.lower_text(t)
 
 
 def test_strided_and_asymmetric_pads_are_refused():
@@ -74,3 +184,23 @@ def test_strided_and_asymmetric_pads_are_refused():
         "tensor<1x10x10x16xf32>, tensor<16x3x3x16xf32>", "tensor<1x11x11x16xf32>, tensor<16x3x3x16xf32>")
     with pytest.raises(NotImplementedError, match="pad"):
         lower.lower_text(t)
+
+
+def test_program_checks_inputs_against_the_signature():
+    import torch
+    p = lower.lower_text(blocks.matmul_bias_act(8, 16, 4))
+    ok = {"A": torch.zeros(8, 16), "B": torch.zeros(16, 4), "bias": torch.zeros(4)}
+    assert set(p.check_inputs(ok)) == {"%A", "%B", "%bias"}
+    with pytest.raises(TypeError, match="%bias"):
+        p.check_inputs(dict(ok, bias=torch.zeros(4, dtype=torch.bfloat16)))
+    with pytest.raises(ValueError, match="%B"):
+        p.check_inputs(dict(ok, B=torch.zeros(4, 16)))
+    with pytest.raises(KeyError):
+        p.check_inputs({"A": ok["A"]})
+
+
+def test_pipeline_names_entry_points_without_the_hip_library():
+    from npu_amd import names
+    rep = pipeline.run(mlir.parse_functions(blocks.matmul_bias_act(8, 16, 4))[0])
+    assert rep["functions"][0]["entry_point"] == "fused_matmul_bias_act"
+    assert names.OUTLINED_NAMES["fused_fill_matmul_generic"] == "fused_matmul_bias_act"

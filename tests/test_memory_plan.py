@@ -8,13 +8,12 @@ the reference simulator's check (tools/harness/sram_simulator.py:243-256);
 the cost record's roofline numbers are the test/lit/cost_evaluate.mlir KAT.
 """
 import json
-import os
 
 import pytest
 
+import reference_inputs
 from npu_amd import host, mlir, pipeline
 
-GOLD = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "mlir")
 IN, OUT, MID = 0, 1, 2
 
 
@@ -75,7 +74,7 @@ def test_spill_and_single_buffer_fallback():
 def test_bufferize_inserts_dma_for_loop_operands():
     """test/lit/bufferize_dma.mlir: npu.alloc_sram and a dram_to_sram
     npu.dma_copy for the operands used inside the tile loop."""
-    g = host.Graph(mlir.parse_file(os.path.join(GOLD, "lit/bufferize_dma.mlir"))[0])
+    g = host.Graph(mlir.parse_file(reference_inputs.path("lit/bufferize_dma.mlir"))[0])
     b = host.bufferize(g, g.linalg_ops())
     names = {v: k for k, v in g.value_id.items()}
     got = {names[x.value]: (host.ROLES[x.role], x.bytes) for x in b}
@@ -88,9 +87,7 @@ def test_bufferize_inserts_dma_for_loop_operands():
     assert [x.bytes for x in b2 if names[x.value] == "%A"] == [22 * 256 * 2]
 
 
-@pytest.mark.parametrize("path", sorted(
-    [os.path.join("lit", f) for f in os.listdir(os.path.join(GOLD, "lit"))] +
-    [f for f in os.listdir(GOLD) if f.endswith(".mlir")]))
+@pytest.mark.parametrize("path", reference_inputs.all_inputs())
 def test_pipeline_plans_fit_the_sram(path):
     """Every reference test input through the pipeline: each planned buffer
     lies inside the SRAM (the simulator's offset + size <= SRAM check), and
@@ -99,7 +96,7 @@ def test_pipeline_plans_fit_the_sram(path):
             "efficiency", "dma_in_bytes", "dma_out_bytes", "matrix_cycles", "dsp_cycles",
             "peak_sram_bytes", "num_tile_iterations", "num_linalg_ops", "sram_budget", "bottleneck"]
     t = host.default_target()
-    for rep in pipeline.run_file(os.path.join(GOLD, path), t):
+    for rep in pipeline.run_file(reference_inputs.path(path), t):
         assert rep["steps"][0] == "fusion" and rep["steps"][-1] == "cost-eval"
         assert len(rep["cost_json"]) == len(rep["functions"])
         for f, line in zip(rep["functions"], rep["cost_json"]):
@@ -116,7 +113,7 @@ def test_pipeline_plans_fit_the_sram(path):
 def test_cost_record_roofline_kat():
     """test/lit/cost_evaluate.mlir: the walk also counts linalg.fill at the
     default 1024 MACs: 33 554 432 + 2 048 FLOP over 589 824 bytes."""
-    rep = pipeline.run_file(os.path.join(GOLD, "lit/cost_evaluate.mlir"))[0]
+    rep = pipeline.run_file(reference_inputs.path("lit/cost_evaluate.mlir"))[0]
     rec = json.loads(rep["cost_json"][0][len("COST_JSON: "):])
     assert rec["flops"] == 33556480 and rec["mem_bytes"] == 589824
     assert rec["arithmetic_intensity"] == pytest.approx(33556480 / 589824)
@@ -125,7 +122,7 @@ def test_cost_record_roofline_kat():
 
 
 def test_pipeline_maps_groups_to_entry_points():
-    rep = pipeline.run_file(os.path.join(GOLD, "matmul_relu.mlir"))[0]
+    rep = pipeline.run_file(reference_inputs.path("matmul_relu.mlir"))[0]
     (f,) = rep["functions"]
     assert f["name"] == "fused_fill_matmul_generic_0"
     assert f["entry_point"] == "fused_matmul_bias_act"
