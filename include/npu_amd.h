@@ -187,6 +187,93 @@ npu_status fused_llama_rmsnorm_swiglu(const npu_memref *h, const npu_memref *g2,
                                       const npu_memref *act, float eps,
                                       npu_stream stream);
 
+/* ---- the outlined-group boundary -----------------------------------------
+ * A host module produced by the reference's pipeline calls each fused group
+ * as `func.call @fused_<ops>_<idx>(external inputs...)` with the group's
+ * external inputs in first-use order and its results after them
+ * (OutlineFusedGroupsPass.cpp:218-257, 306-316); after bufferization the
+ * shaped arguments are memrefs, passed through MLIR's memref C interface
+ * (tools/harness/e2e_verify.py:221).  npu_group_launch is that call: it is
+ * keyed by the outlined name and takes the arguments in that order.
+ *
+ * Descriptors: a ranked memref of rank R has MLIR's StridedMemRefType<T, R>
+ * layout, declared below for R = 1..4 (the element type is not part of the
+ * descriptor, as in MLIR); an argument is MLIR's UnrankedMemRefType
+ * ({rank, descriptor}) followed by what the function type says of it: its
+ * element type, and for a scalar argument (the `arith.constant` a
+ * linalg.fill writes, which the outliner passes as an argument) its value. */
+#define NPU_STRIDED_MEMREF(R)  \
+  struct {                     \
+    void *allocated;           \
+    void *aligned;             \
+    int64_t offset;            \
+    int64_t sizes[R];          \
+    int64_t strides[R];        \
+  }
+typedef NPU_STRIDED_MEMREF(1) npu_strided_memref_1d;
+typedef NPU_STRIDED_MEMREF(2) npu_strided_memref_2d;
+typedef NPU_STRIDED_MEMREF(3) npu_strided_memref_3d;
+typedef NPU_STRIDED_MEMREF(4) npu_strided_memref_4d;
+
+#define NPU_ARG_MEMREF 0
+#define NPU_ARG_SCALAR 1
+typedef struct npu_arg {
+  int64_t rank;      /* UnrankedMemRefType::rank (0 for a scalar)               */
+  void *descriptor;  /* UnrankedMemRefType::descriptor: a StridedMemRefType
+                        layout of `rank` (NULL for a scalar)                    */
+  int32_t dtype;     /* element type from the function type: NPU_F32 ...        */
+  int32_t kind;      /* NPU_ARG_MEMREF or NPU_ARG_SCALAR                        */
+  double scalar;     /* the value of a scalar argument                          */
+} npu_arg;
+
+/* What the outlined body computes beyond its signature: constants inside the
+ * generic regions and the folding of a feeding tensor.pad. */
+#define NPU_GROUP_MAX_CHAINS 4
+typedef struct npu_group_attrs {
+  int32_t act[NPU_GROUP_MAX_CHAINS]; /* NPU_ACT_* of each matmul/conv chain of
+                                        the group, in order                    */
+  int32_t pad;     /* > 0: the convolution's padded-input argument is given
+                      unpadded and this zero padding is folded into the launch
+                      (the host lowering removed the tensor.pad); 0: the
+                      argument is the padded tensor itself                      */
+  int32_t n_heads; /* attention: heads of 64                                   */
+  float eps;       /* RMSNorm epsilon                                          */
+  float scale;     /* attention score scale                                    */
+} npu_group_attrs;
+
+/* Runs one outlined group, or a chain of outlined groups that the host
+ * lowering fuses across a tensor.pad, as one launch sequence on `stream`.
+ *
+ * outlined_name: the outliner's symbol, `fused_` + the short op names +
+ *   `_<idx>` (OutlineFusedGroupsPass.cpp:69-82, 259-263); the index is
+ *   ignored.  A chain of groups is their names joined by '+', in order.
+ * in: the external inputs in first-use order over the group's ops (for a
+ *   chain: over all its ops, values produced inside the chain left out);
+ *   out: the results.  Arguments that come from tensor.empty (a fill's or a
+ *   generic's destination) carry their shape; their data are never read and
+ *   may be NULL, except where the group keeps an intermediate result there,
+ *   as the bufferized function writes its destinations (the first matmul's
+ *   ReLU destination of a two-layer chain).  The fill value must be 0.0.
+ *
+ * Groups (chain key = the names with `fused_` and the index removed):
+ *   fill_matmul_generic                   -> fused_matmul_bias_act
+ *     (cst, init[M,N], A[M,K], B[K,N], [bias[N]], dest[M,N]) -> (out[M,N])
+ *   fill_matmul_generic repeated k <= 4 times (test/mlp.mlir: one group of
+ *     two matmul -> ReLU chains)          -> k fused_matmul_bias_act calls
+ *     (cst, init1, x, w1, [b1], dest1, init2, w2, [b2], dest2, ...) -> (out)
+ *   fill_linalg_conv_2d_nhwc_fhwc_generic -> fused_conv2d_nhwc_bias_act
+ *     (cst, init, x, w, [bias f32 [F]], dest) -> (out)
+ *   fill_linalg_conv_2d_nhwc_fhwc_generic + the depthwise / project group(s)
+ *     of an inverted residual block after its tensor.pad -> fused_irb_f32
+ *     (cst, init_e, x, we[E,1,1,C], dest_e, init_d, wdw[3,3,E], dest_d,
+ *      init_p, wp[C,1,1,E], dest) -> (out)
+ * Shapes, element types and counts are checked against the group before any
+ * launch (NPU_ERR_INVALID_ARG); an unknown chain is NPU_ERR_UNSUPPORTED.
+ * Launch plans of every launch of the sequence are recorded. */
+npu_status npu_group_launch(const char *outlined_name, const npu_group_attrs *attrs,
+                            const npu_arg *in, int32_t n_in, const npu_arg *out,
+                            int32_t n_out, npu_stream stream);
+
 /* ---- launch plans ------------------------------------------------------
  * What each kernel launch of the calling thread's most recent entry-point
  * call does per work tile: the input of the MI355X launch model in

@@ -32,6 +32,14 @@ namespace {
 
 thread_local std::string g_last_error;
 
+}  // namespace
+
+namespace npu {
+void set_last_error(const char *msg) { g_last_error = msg ? msg : ""; }
+}  // namespace npu
+
+namespace {
+
 npu_status fail(npu_status code, const char *fmt, ...) {
   char buf[512];
   va_list ap;

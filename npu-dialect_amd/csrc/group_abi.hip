@@ -1,0 +1,345 @@
+// group_abi.hip -- npu_group_launch: the outlined-group boundary.
+//
+// A host module calls a fused group by the outliner's name with the group's
+// external inputs in first-use order, then its results
+// (lib/Transforms/OutlineFusedGroupsPass.cpp:218-263, 306-316).  This file
+// reads those arguments -- MLIR memref descriptors of any rank plus the fill
+// constant -- checks them against the group's signature, and runs the group
+// through the typed entry points of abi.hip, which validate shapes again and
+// launch.  No kernel lives here.
+#include <hip/hip_runtime.h>
+
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <string>
+#include <vector>
+
+#include "../../include/npu_amd.h"
+#include "plans.hpp"
+
+namespace {
+
+// The message of the first rejection; npu_group_launch hands it to
+// npu_last_error() (a typed entry point's own message is copied here first).
+thread_local std::string g_group_error;
+
+npu_status gfail(npu_status code, const char *fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof buf, fmt, ap);
+  va_end(ap);
+  g_group_error = buf;
+  return code;
+}
+
+// One argument read from its StridedMemRefType layout.
+struct Arg {
+  bool scalar = false;
+  double value = 0.0;
+  npu_memref m{};
+};
+
+npu_status read_arg(const npu_arg *a, int idx, const char *side, Arg *out) {
+  if (a->kind == NPU_ARG_SCALAR) {
+    out->scalar = true;
+    out->value = a->scalar;
+    return NPU_OK;
+  }
+  if (a->kind != NPU_ARG_MEMREF)
+    return gfail(NPU_ERR_INVALID_ARG, "%s[%d]: kind %d is neither memref nor scalar", side, idx,
+                 a->kind);
+  if (a->rank < 1 || a->rank > NPU_MAX_RANK)
+    return gfail(NPU_ERR_UNSUPPORTED, "%s[%d]: rank %lld (ranks 1..%d are taken)", side, idx,
+                 (long long)a->rank, NPU_MAX_RANK);
+  if (!a->descriptor) return gfail(NPU_ERR_INVALID_ARG, "%s[%d]: null descriptor", side, idx);
+  // StridedMemRefType<T, R>: two pointers, then offset, sizes[R], strides[R].
+  const char *d = static_cast<const char *>(a->descriptor);
+  const int R = (int)a->rank;
+  std::memcpy(&out->m.allocated, d, sizeof(void *));
+  std::memcpy(&out->m.aligned, d + sizeof(void *), sizeof(void *));
+  const int64_t *w = reinterpret_cast<const int64_t *>(d + 2 * sizeof(void *));
+  out->m.offset = w[0];
+  for (int i = 0; i < R; ++i) {
+    out->m.sizes[i] = w[1 + i];
+    out->m.strides[i] = w[1 + R + i];
+  }
+  out->m.rank = R;
+  out->m.dtype = a->dtype;
+  return NPU_OK;
+}
+
+bool same_shape(const npu_memref &m, std::initializer_list<int64_t> shape) {
+  if (m.rank != (int)shape.size()) return false;
+  int i = 0;
+  for (int64_t s : shape)
+    if (m.sizes[i++] != s) return false;
+  return true;
+}
+
+std::string shape_str(const npu_memref &m) {
+  std::string s = "[";
+  for (int i = 0; i < m.rank; ++i) s += (i ? "," : "") + std::to_string((long long)m.sizes[i]);
+  return s + "]";
+}
+
+// A view of a row-major [A,1,1,B] filter as [A,B].
+npu_status squeeze_1x1(const npu_memref &m, const char *what, npu_memref *v) {
+  if (m.strides[3] != 1 || (m.sizes[0] > 1 && m.strides[0] != m.sizes[3]))
+    return gfail(NPU_ERR_UNSUPPORTED, "%s: only a row-major filter is supported", what);
+  *v = m;
+  v->rank = 2;
+  v->sizes[0] = m.sizes[0];
+  v->sizes[1] = m.sizes[3];
+  v->strides[0] = m.sizes[3];
+  v->strides[1] = 1;
+  return NPU_OK;
+}
+
+// Chain key: each '+'-separated name without `fused_` and its `_<idx>`,
+// joined by '_'.
+std::string chain_key(const char *name) {
+  std::string all(name), key;
+  size_t start = 0;
+  while (start <= all.size()) {
+    size_t end = all.find('+', start);
+    if (end == std::string::npos) end = all.size();
+    std::string part = all.substr(start, end - start);
+    if (part.rfind("fused_", 0) == 0) part = part.substr(6);
+    const size_t us = part.rfind('_');
+    if (us != std::string::npos && us + 1 < part.size() &&
+        part.find_first_not_of("0123456789", us + 1) == std::string::npos)
+      part = part.substr(0, us);
+    if (!key.empty()) key += "_";
+    key += part;
+    start = end + 1;
+  }
+  return key;
+}
+
+class Cursor {
+ public:
+  Cursor(std::vector<Arg> &args) : a_(args) {}
+  size_t pos() const { return i_; }
+  bool done() const { return i_ == a_.size(); }
+  const Arg *peek() const { return i_ < a_.size() ? &a_[i_] : nullptr; }
+  // The fill constant: a scalar 0.0.
+  npu_status fill_value() {
+    if (done()) return gfail(NPU_ERR_INVALID_ARG, "in[%zu]: missing the fill value", i_);
+    const Arg &x = a_[i_];
+    if (!x.scalar)
+      return gfail(NPU_ERR_INVALID_ARG, "in[%zu]: the fill value must be a scalar argument", i_);
+    if (x.value != 0.0)
+      return gfail(NPU_ERR_UNSUPPORTED, "in[%zu]: fill value %g (accumulators start at 0.0)", i_,
+                   x.value);
+    ++i_;
+    return NPU_OK;
+  }
+  // A memref argument of the given rank.
+  npu_status memref(int rank, const char *what, const npu_memref **m) {
+    if (done()) return gfail(NPU_ERR_INVALID_ARG, "in[%zu]: missing %s", i_, what);
+    const Arg &x = a_[i_];
+    if (x.scalar || x.m.rank != rank)
+      return gfail(NPU_ERR_INVALID_ARG, "in[%zu] (%s): expected a rank-%d memref", i_, what, rank);
+    *m = &x.m;
+    ++i_;
+    return NPU_OK;
+  }
+  // A tensor.empty destination of exactly `shape`.
+  npu_status dest(std::initializer_list<int64_t> shape, const char *what,
+                  const npu_memref **m = nullptr) {
+    const npu_memref *d;
+    npu_status s = memref((int)shape.size(), what, &d);
+    if (s != NPU_OK) return s;
+    if (!same_shape(*d, shape))
+      return gfail(NPU_ERR_INVALID_ARG, "in[%zu] (%s): shape %s does not match the group",
+                   i_ - 1, what, shape_str(*d).c_str());
+    if (m) *m = d;
+    return NPU_OK;
+  }
+  // Optional rank-1 operand (a bias) when the next argument has rank 1.
+  bool next_is_rank1() const { return peek() && !peek()->scalar && peek()->m.rank == 1; }
+
+ private:
+  std::vector<Arg> &a_;
+  size_t i_ = 0;
+};
+
+#define G_TRY(expr)              \
+  do {                           \
+    npu_status _s = (expr);      \
+    if (_s != NPU_OK) return _s; \
+  } while (0)
+
+// Keeps the launch plans of every typed call of a sequence (each call
+// replaces the thread's plan list).
+struct PlanLog {
+  std::vector<npu_launch_plan> plans;
+  void take() {
+    const int n = npu_last_launch_plans(nullptr, 0);
+    const size_t at = plans.size();
+    plans.resize(at + n);
+    npu_last_launch_plans(plans.data() + at, n);
+  }
+  void publish() {
+    npu::plans_reset();
+    for (const auto &p : plans) npu::plans_add(p);
+  }
+};
+
+npu_status typed(npu_status s) {
+  if (s != NPU_OK) g_group_error = npu_last_error();
+  return s;
+}
+
+npu_status run_matmuls(Cursor &c, const npu_group_attrs &at, int chains, const npu_memref *out,
+                       npu_stream stream, PlanLog &log) {
+  G_TRY(c.fill_value());
+  const npu_memref *x = nullptr;
+  struct Step { const npu_memref *init, *A, *B, *bias, *dest; };
+  std::vector<Step> steps;
+  for (int k = 0; k < chains; ++k) {
+    Step s{};
+    G_TRY(c.memref(2, "matmul accumulator (tensor.empty)", &s.init));
+    if (k == 0) G_TRY(c.memref(2, "A", &x));
+    s.A = x;
+    G_TRY(c.memref(2, "B", &s.B));
+    if (c.next_is_rank1()) G_TRY(c.memref(1, "bias", &s.bias));
+    const int64_t M = s.A->sizes[0], N = s.B->sizes[1];
+    if (!same_shape(*s.init, {M, N}))
+      return gfail(NPU_ERR_INVALID_ARG, "matmul %d: accumulator %s, expected [%lld,%lld]", k,
+                   shape_str(*s.init).c_str(), (long long)M, (long long)N);
+    G_TRY(c.dest({M, N}, "generic destination (tensor.empty)", &s.dest));
+    if (k + 1 < chains && !s.dest->aligned)
+      return gfail(NPU_ERR_INVALID_ARG, "matmul %d: its destination holds the intermediate "
+                   "result and must have data", k);
+    steps.push_back(s);
+    x = s.dest;  // the next chain reads this chain's result
+  }
+  if (!c.done())
+    return gfail(NPU_ERR_INVALID_ARG, "%zu arguments left over after the group's inputs", c.pos());
+  for (int k = 0; k < chains; ++k) {
+    const Step &s = steps[k];
+    const npu_memref *dst = k + 1 == chains ? out : s.dest;
+    npu_memref none{};
+    none.rank = 1;
+    G_TRY(typed(fused_matmul_bias_act(s.A, s.B, s.bias ? s.bias : &none, dst, at.act[k], stream)));
+    log.take();
+  }
+  return NPU_OK;
+}
+
+npu_status run_conv(Cursor &c, const npu_group_attrs &at, const npu_memref *out,
+                    npu_stream stream, PlanLog &log) {
+  G_TRY(c.fill_value());
+  const npu_memref *init, *x, *w, *bias = nullptr;
+  G_TRY(c.memref(4, "conv accumulator (tensor.empty)", &init));
+  G_TRY(c.memref(4, "x", &x));
+  G_TRY(c.memref(4, "w", &w));
+  if (c.next_is_rank1()) G_TRY(c.memref(1, "bias", &bias));
+  G_TRY(c.dest({out->sizes[0], out->sizes[1], out->sizes[2], out->sizes[3]},
+               "generic destination (tensor.empty)"));
+  if (!c.done())
+    return gfail(NPU_ERR_INVALID_ARG, "%zu arguments left over after the group's inputs", c.pos());
+  if (!same_shape(*init, {out->sizes[0], out->sizes[1], out->sizes[2], out->sizes[3]}))
+    return gfail(NPU_ERR_INVALID_ARG, "conv accumulator %s does not match the result %s",
+                 shape_str(*init).c_str(), shape_str(*out).c_str());
+  npu_memref none{};
+  none.rank = 1;
+  G_TRY(typed(fused_conv2d_nhwc_bias_act(x, w, bias ? bias : &none, out, at.pad, at.act[0],
+                                         stream)));
+  log.take();
+  return NPU_OK;
+}
+
+npu_status run_irb(Cursor &c, const npu_memref *out, npu_stream stream, PlanLog &log) {
+  G_TRY(c.fill_value());
+  const npu_memref *init_e, *x, *we, *wdw, *wp;
+  G_TRY(c.memref(4, "expand accumulator (tensor.empty)", &init_e));
+  G_TRY(c.memref(4, "x", &x));
+  G_TRY(c.memref(4, "we [E,1,1,C]", &we));
+  const int64_t N = x->sizes[0], H = x->sizes[1], W = x->sizes[2], C = x->sizes[3];
+  const int64_t E = we->sizes[0];
+  if (!same_shape(*we, {E, 1, 1, C}))
+    return gfail(NPU_ERR_INVALID_ARG, "we: %s, expected [E,1,1,%lld]", shape_str(*we).c_str(),
+                 (long long)C);
+  if (!same_shape(*init_e, {N, H, W, E}))
+    return gfail(NPU_ERR_INVALID_ARG, "expand accumulator: %s", shape_str(*init_e).c_str());
+  G_TRY(c.dest({N, H, W, E}, "expand destination (tensor.empty)"));
+  G_TRY(c.dest({N, H, W, E}, "depthwise accumulator (tensor.empty)"));
+  G_TRY(c.memref(3, "wdw [3,3,E]", &wdw));
+  G_TRY(c.dest({N, H, W, E}, "depthwise destination (tensor.empty)"));
+  G_TRY(c.dest({N, H, W, C}, "project accumulator (tensor.empty)"));
+  G_TRY(c.memref(4, "wp [C,1,1,E]", &wp));
+  if (!same_shape(*wp, {C, 1, 1, E}))
+    return gfail(NPU_ERR_INVALID_ARG, "wp: %s, expected [%lld,1,1,%lld]", shape_str(*wp).c_str(),
+                 (long long)C, (long long)E);
+  G_TRY(c.dest({N, H, W, C}, "result destination (tensor.empty)"));
+  if (!c.done())
+    return gfail(NPU_ERR_INVALID_ARG, "%zu arguments left over after the group's inputs", c.pos());
+  npu_memref we2, wp2;
+  G_TRY(squeeze_1x1(*we, "we", &we2));
+  G_TRY(squeeze_1x1(*wp, "wp", &wp2));
+  G_TRY(typed(fused_irb_f32(x, &we2, wdw, &wp2, out, stream)));
+  log.take();
+  return NPU_OK;
+}
+
+const char *kMatmul = "fill_matmul_generic";
+const char *kConv = "fill_linalg_conv_2d_nhwc_fhwc_generic";
+const char *kIrb =
+    "fill_linalg_conv_2d_nhwc_fhwc_generic_fill_linalg_depthwise_conv_2d_nhwc_hwc_generic_"
+    "fill_linalg_conv_2d_nhwc_fhwc_generic";
+
+// k when key is `fill_matmul_generic` repeated k times, else 0.
+int matmul_chains(const std::string &key) {
+  const std::string one = kMatmul;
+  int k = 0;
+  size_t p = 0;
+  while (p < key.size()) {
+    if (key.compare(p, one.size(), one) != 0) return 0;
+    p += one.size();
+    ++k;
+    if (p == key.size()) return k;
+    if (key[p] != '_') return 0;
+    ++p;
+  }
+  return 0;
+}
+
+}  // namespace
+
+extern "C" npu_status npu_group_launch(const char *outlined_name, const npu_group_attrs *attrs,
+                                       const npu_arg *in, int32_t n_in, const npu_arg *out,
+                                       int32_t n_out, npu_stream stream) {
+  npu::plans_reset();
+  g_group_error.clear();
+  PlanLog log;
+  npu_status st = [&]() -> npu_status {
+    if (!outlined_name) return gfail(NPU_ERR_INVALID_ARG, "null group name");
+    if (!attrs) return gfail(NPU_ERR_INVALID_ARG, "null group attributes");
+    if (n_in < 0 || (n_in > 0 && !in)) return gfail(NPU_ERR_INVALID_ARG, "bad input list");
+    if (n_out != 1 || !out)
+      return gfail(NPU_ERR_UNSUPPORTED, "%d results (every group here returns one)", n_out);
+    std::vector<Arg> args(n_in);
+    for (int i = 0; i < n_in; ++i) G_TRY(read_arg(&in[i], i, "in", &args[i]));
+    Arg res;
+    G_TRY(read_arg(&out[0], 0, "out", &res));
+    if (res.scalar) return gfail(NPU_ERR_INVALID_ARG, "out[0]: a result must be a memref");
+    const std::string key = chain_key(outlined_name);
+    Cursor c(args);
+    if (const int k = matmul_chains(key)) {
+      if (k > NPU_GROUP_MAX_CHAINS)
+        return gfail(NPU_ERR_UNSUPPORTED, "%d matmul chains (at most %d)", k,
+                     NPU_GROUP_MAX_CHAINS);
+      return run_matmuls(c, *attrs, k, &res.m, stream, log);
+    }
+    if (key == kConv) return run_conv(c, *attrs, &res.m, stream, log);
+    if (key == kIrb) return run_irb(c, &res.m, stream, log);
+    return gfail(NPU_ERR_UNSUPPORTED, "no MI355X group runs the outlined chain '%s'", key.c_str());
+  }();
+  log.publish();
+  if (st != NPU_OK) npu::set_last_error(g_group_error.c_str());
+  return st;
+}

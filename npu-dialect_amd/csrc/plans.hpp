@@ -17,6 +17,8 @@ namespace npu {
 // Thread-local plan list of the current entry-point call (defined in abi.hip).
 void plans_reset();
 void plans_add(const npu_launch_plan &p);
+// Sets the calling thread's npu_last_error() message (defined in abi.hip).
+void set_last_error(const char *msg);
 
 // Per-kernel, per-device launch facts cached by kernel address (kernels of
 // one signature share a function type, so the type cannot be the key).

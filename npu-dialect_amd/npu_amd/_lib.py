@@ -56,6 +56,42 @@ class NpuLaunchPlan(C.Structure):
         ("hbm_bytes", C.c_double),
     ]
 
+def strided_memref_type(rank: int):
+    """MLIR's StridedMemRefType<T, rank> layout: {allocated, aligned, offset,
+    sizes[rank], strides[rank]} (include/npu_amd.h NPU_STRIDED_MEMREF)."""
+    class StridedMemref(C.Structure):
+        _fields_ = [("allocated", C.c_void_p), ("aligned", C.c_void_p), ("offset", C.c_int64),
+                    ("sizes", C.c_int64 * rank), ("strides", C.c_int64 * rank)]
+    return StridedMemref
+
+
+class NpuArg(C.Structure):
+    """npu_arg: MLIR's UnrankedMemRefType {rank, descriptor}, then the element
+    type and, for a scalar argument, its value."""
+
+    _fields_ = [
+        ("rank", C.c_int64),
+        ("descriptor", C.c_void_p),
+        ("dtype", C.c_int32),
+        ("kind", C.c_int32),
+        ("scalar", C.c_double),
+    ]
+
+
+class NpuGroupAttrs(C.Structure):
+    """npu_group_attrs: per-chain activations, folded pad, heads, eps, scale."""
+
+    _fields_ = [
+        ("act", C.c_int32 * 4),
+        ("pad", C.c_int32),
+        ("n_heads", C.c_int32),
+        ("eps", C.c_float),
+        ("scale", C.c_float),
+    ]
+
+
+_ARG = C.POINTER(NpuArg)
+
 SIGNATURES = {
     "npu_version": (C.c_char_p, []),
     "npu_last_error": (C.c_char_p, []),
@@ -69,6 +105,8 @@ SIGNATURES = {
     "fused_llama_attention": (_I32, [_MR] * 4 + [_I32, C.c_float, _P]),
     "fused_llama_matmul_residual": (_I32, [_MR] * 4 + [_P]),
     "fused_llama_rmsnorm_swiglu": (_I32, [_MR] * 5 + [C.c_float, _P]),
+    "npu_group_launch": (_I32, [C.c_char_p, C.POINTER(NpuGroupAttrs), _ARG, _I32, _ARG, _I32,
+                                _P]),
     "npu_last_launch_plans": (_I32, [C.POINTER(NpuLaunchPlan), _I32]),
 }
 

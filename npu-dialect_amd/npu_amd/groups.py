@@ -10,6 +10,8 @@ The group names follow the op chains the reference's outliner groups
 """
 from __future__ import annotations
 
+import ctypes as C
+
 from . import _lib
 from .memref import absent, from_tensor, ref
 from .names import OUTLINED_NAMES  # noqa: F401  (re-exported)
@@ -127,6 +129,65 @@ def fused_llama_rmsnorm_swiglu(h, g2, wg, wu, act, eps=1e-5, stream=None):
     st = _lib.lib().fused_llama_rmsnorm_swiglu(*[ref(m) for m in ms], float(eps), _stream(stream))
     _check(st, "fused_llama_rmsnorm_swiglu")
     return act
+
+
+class Empty:
+    """A tensor.empty argument of an outlined group: a shape and element type,
+    and optionally the tensor that holds it (None: no data; the group never
+    reads it)."""
+
+    def __init__(self, shape, dtype="f32", tensor=None):
+        self.shape, self.dtype, self.tensor = list(shape), dtype, tensor
+
+
+_DT = {"f32": 0, "bf16": 1, "i8": 2, "i32": 3}
+
+
+def _group_arg(x, keep):
+    """One npu_arg for a tensor, an Empty or a scalar fill value."""
+    a = _lib.NpuArg()
+    if isinstance(x, (int, float)):
+        a.kind, a.dtype, a.scalar, a.rank = 1, _DT["f32"], float(x), 0
+        return a
+    if isinstance(x, Empty):
+        if x.tensor is not None:
+            return _group_arg(x.tensor, keep)
+        shape, dtype, ptr, offset, strides = x.shape, _DT[x.dtype], 0, 0, None
+    else:
+        m = from_tensor(x)
+        shape, dtype, ptr, offset = list(x.shape), m.dtype, m.aligned, m.offset
+        strides = list(x.stride())
+    if strides is None:
+        strides = [1] * len(shape)
+        for i in range(len(shape) - 2, -1, -1):
+            strides[i] = strides[i + 1] * shape[i + 1]
+    d = _lib.strided_memref_type(len(shape))()
+    d.allocated = d.aligned = ptr
+    d.offset = offset
+    for i, (sz, st) in enumerate(zip(shape, strides)):
+        d.sizes[i], d.strides[i] = sz, st
+    keep.append(d)
+    a.rank, a.descriptor, a.dtype, a.kind = len(shape), C.addressof(d), dtype, 0
+    return a
+
+
+def group_launch(outlined_name, ins, outs, act=("none",), pad=0, n_heads=0, eps=0.0, scale=0.0,
+                 stream=None):
+    """npu_group_launch: runs the outlined group(s) `outlined_name` ('+'-joined
+    for a chain) on its arguments in the outlined function's order: ``ins``
+    are tensors, Empty placeholders and the fill value (a float); ``outs`` the
+    result tensors."""
+    keep = []
+    ia = (_lib.NpuArg * max(len(ins), 1))(*[_group_arg(x, keep) for x in ins])
+    oa = (_lib.NpuArg * max(len(outs), 1))(*[_group_arg(x, keep) for x in outs])
+    at = _lib.NpuGroupAttrs()
+    for i, a in enumerate(act):
+        at.act[i] = ACT[a]
+    at.pad, at.n_heads, at.eps, at.scale = int(pad), int(n_heads), float(eps), float(scale)
+    st = _lib.lib().npu_group_launch(outlined_name.encode(), C.byref(at), ia, len(ins), oa,
+                                     len(outs), _stream(stream))
+    _check(st, f"npu_group_launch({outlined_name})")
+    return outs
 
 
 def llama_layer(p, bufs, n_heads, eps=1e-5, stream=None):

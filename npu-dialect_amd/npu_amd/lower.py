@@ -55,6 +55,21 @@ class Call:
     views: dict = field(default_factory=dict)    # SSA name -> shape the entry point takes
 
 
+@dataclass
+class Launch:
+    """One npu_group_launch: the outlined group(s) by name, their external
+    inputs in first-use order (SSA names), the result and the attributes."""
+    name: str                  # outlined names joined by '+'
+    ins: list                  # SSA names, the outlined function's argument order
+    out: str
+    acts: list                 # activation of each matmul/conv chain
+    pad: int = 0               # > 0: the padded input `padded` is passed unpadded
+    padded: str = None
+    pad_source: str = None
+    stores: list = field(default_factory=list)   # tensor.empty values holding intermediates
+    widen: list = field(default_factory=list)    # bf16 biases passed widened to f32
+
+
 _TORCH_DTYPE = {"f32": "float32", "bf16": "bfloat16", "i8": "int8", "i32": "int32"}
 
 
@@ -288,7 +303,7 @@ def lower(func: mlir.MFunc, target=None) -> "Program":
     fn = _Fn(func)
     rep = pipeline.run(func, target)
     groups = {g["name"]: [func.ops[i] for i in g["ops"]] for g in rep["functions"]}
-    calls, covered, consumed = [], set(), set()
+    calls, covered, consumed, dests = [], set(), set(), {}
     for name, ops in groups.items():
         if name in consumed:
             continue
@@ -305,6 +320,8 @@ def lower(func: mlir.MFunc, target=None) -> "Program":
                 _elem(fn, a.ins[0], ("f32",), name)
                 calls.append(Call("fused_matmul_bias_act", [name], [a.ins[0], a.ins[1], bias], out,
                                   {"act": act}))
+                dests[id(calls[-1])] = (s["generics"][-1].outs[0] if s["generics"]
+                                        else s["fills"][0].outs[0])
                 continue
             _check_conv(a)
             x, pad = _pad_of(fn, a.ins[0])
@@ -336,7 +353,46 @@ def lower(func: mlir.MFunc, target=None) -> "Program":
             if not op.results or op.results[0] not in covered:
                 raise NotImplementedError(f"{op.results[0] if op.results else op.name}: "
                                           f"{op.name} is in no group an entry point runs")
-    return Program(func, calls)
+    return Program(func, calls, _launches(fn, rep, calls, dests))
+
+
+def _launches(fn: _Fn, rep, calls, dests):
+    """Groups the calls into npu_group_launch calls: consecutive calls of the
+    same outlined functions are one launch (a group of several matmul chains);
+    a call spanning several groups (the inverted residual chain) is one
+    launch of their '+'-joined names."""
+    by_name = {f["name"]: f for f in rep["functions"]}
+    out, i = [], 0
+    while i < len(calls):
+        j = i + 1
+        while j < len(calls) and calls[j].functions == calls[i].functions:
+            j += 1
+        cs = calls[i:j]
+        names = cs[0].functions
+        inside = set()
+        for n in names:
+            for k in by_name[n]["ops"]:
+                inside.update(fn.f.ops[k].results)
+        padded = cs[0].params.get("padded")
+        if padded:
+            inside.add(padded)
+        ins = []
+        for n in names:
+            for v in by_name[n]["inputs"]:
+                if v not in inside and v not in ins:
+                    ins.append(v)
+        L = Launch("+".join(names), ins, cs[-1].out,
+                   [c.params.get("act", "none") for c in cs])
+        c0 = cs[0]
+        if c0.entry == "fused_conv2d_nhwc_bias_act" and c0.params.get("pad"):
+            conv_in = [v for v in ins if fn.op(v) is not None and fn.op(v).name == "tensor.pad"]
+            L.pad, L.padded, L.pad_source = c0.params["pad"], conv_in[0], c0.args[0]
+        if c0.params.get("bias_to_f32"):
+            L.widen.append(c0.args[2])
+        L.stores = [dests[id(c)] for c in cs[:-1]]
+        out.append(L)
+        i = j
+    return out
 
 
 def _irb_chain(fn, groups, name, conv, e_out, x, act, bias, res):
@@ -404,9 +460,10 @@ class Program:
     """The entry-point calls of a lowered function, run in order on torch
     tensors that live on the GPU."""
 
-    def __init__(self, func: mlir.MFunc, calls: list):
+    def __init__(self, func: mlir.MFunc, calls: list, launches: list = ()):
         self.func = func
         self.calls = calls
+        self.launches = list(launches)
 
     @property
     def entry_points(self):
@@ -432,37 +489,40 @@ class Program:
         return vals
 
     def run(self, inputs: dict, stream=None) -> dict:
-        """inputs: argument name (with or without %) -> tensor.  Returns the
-        function's results by SSA name."""
+        """inputs: argument name (with or without %) -> tensor.  Runs every
+        launch through npu_group_launch and returns the function's results by
+        SSA name."""
         import torch
 
         from . import groups
 
         vals = self.check_inputs(inputs)
-        for c in self.calls:
-            args = []
-            for v in c.args:
-                if v is None:
-                    args.append(None)
-                    continue
-                t = vals[v]
-                if v in c.views:
-                    t = t.reshape(c.views[v])
-                args.append(t)
-            oty = self.func.types[c.out]
-            dt = getattr(torch, _TORCH_DTYPE[oty.elem])
-            out = torch.empty(oty.shape, dtype=dt, device=args[0].device)
-            if c.entry == "fused_matmul_bias_act":
-                groups.fused_matmul_bias_act(args[0], args[1], args[2], out, c.params["act"], stream)
-            elif c.entry == "fused_conv2d_nhwc_bias_act":
-                bias = args[2].float() if c.params.get("bias_to_f32") else args[2]
-                groups.fused_conv2d_nhwc_bias_act(args[0], args[1], bias, out, c.params["pad"],
-                                                  c.params["act"], stream)
-            elif c.entry == "fused_irb_f32":
-                groups.fused_irb_f32(args[0], args[1], args[2], args[3], out, stream)
-            else:  # pragma: no cover - lower() emits only the entries above
-                raise NotImplementedError(c.entry)
-            vals[c.out] = out
+        types = self.func.types
+        tdt = lambda e: getattr(torch, _TORCH_DTYPE[e])
+        dev = next(iter(vals.values())).device
+        prod = {r: op for op in self.func.ops for r in op.results}
+        for L in self.launches:
+            ins = []
+            for v in L.ins:
+                op = prod.get(v)
+                if v == L.padded:
+                    ins.append(vals[L.pad_source])
+                elif v in vals:
+                    t = vals[v]
+                    ins.append(t.float() if v in L.widen else t)
+                elif op is not None and op.name == "arith.constant":
+                    ins.append(_float(op.attrs.get("value")))
+                elif op is not None and op.name == "tensor.empty":
+                    t = types[v]
+                    keep = torch.empty(t.shape, dtype=tdt(t.elem), device=dev) \
+                        if v in L.stores else None
+                    ins.append(groups.Empty(t.shape, t.elem, keep))
+                else:  # pragma: no cover - lower() binds every input
+                    raise KeyError(f"{L.name}: no value for {v}")
+            oty = types[L.out]
+            out = torch.empty(oty.shape, dtype=tdt(oty.elem), device=dev)
+            groups.group_launch(L.name, ins, [out], act=L.acts, pad=L.pad, stream=stream)
+            vals[L.out] = out
         ret = [op for op in self.func.ops if op.name == "func.return"]
         names = ret[0].operands if ret else []
         return {n: vals[n] for n in names}

@@ -127,3 +127,53 @@ def test_qbottleneck_rejects_bad_descriptors():
     xx, ww1 = _mr([1, 8, 8, 192], I8), _mr([64, 192], I8)
     assert call(xx, ww1, w2, _mr([192, 64], I8), *q[:4], _mr([192], I32), _mr([192], I32),
                 _mr([1, 8, 8, 192], I8)) == 2 and "no kernel instance" in _err()
+
+
+C_TEST = os.path.join(ROOT, "tests", "c", "group_launch_test")
+
+
+def test_compiled_c_caller_gets_rejections_before_launch():
+    """A C program calls npu_group_launch with wrong counts, shapes, ranks,
+    fill values and chain names; each is refused with a status and message."""
+    import subprocess
+    assert os.path.exists(C_TEST), "build tests/c first (__graft_entry__.build())"
+    r = subprocess.run([C_TEST, "validate"], capture_output=True, text=True, timeout=60)
+    assert r.returncode == 0, r.stdout + r.stderr
+
+
+def _arg2(shape, ptr=0x10000):
+    from npu_amd import groups
+    d = _lib.strided_memref_type(len(shape))()
+    d.allocated = d.aligned = ptr
+    st = 1
+    for i in range(len(shape) - 1, -1, -1):
+        d.sizes[i], d.strides[i] = shape[i], st
+        st *= shape[i]
+    a = _lib.NpuArg()
+    a.rank, a.descriptor, a.dtype, a.kind = len(shape), C.addressof(d), F32, 0
+    a._keep = d
+    return a
+
+
+def test_group_launch_reads_strided_memref_layouts():
+    """The descriptor is MLIR's StridedMemRefType layout for each rank: a conv
+    group's 4-D and 1-D arguments are read from their own layouts (the
+    rejection names the right shapes)."""
+    lib = npu_amd.lib()
+    sc = _lib.NpuArg()
+    sc.kind, sc.scalar = 1, 0.0
+    at = _lib.NpuGroupAttrs()
+    at.act[0], at.pad = 1, 1
+    ins = [sc, _arg2([2, 8, 8, 32]), _arg2([2, 8, 8, 16]), _arg2([32, 3, 3, 16]), _arg2([31]),
+           _arg2([2, 8, 8, 32])]
+    outs = [_arg2([2, 8, 8, 32])]
+    ia, oa = (_lib.NpuArg * 6)(*ins), (_lib.NpuArg * 1)(*outs)
+    st = lib.npu_group_launch(b"fused_fill_linalg_conv_2d_nhwc_fhwc_generic_0", C.byref(at),
+                              ia, 6, oa, 1, None)
+    assert st == 1 and "bias: size 31, expected F = 32" in _err()
+    # one dimension off in the accumulator
+    ins[1] = _arg2([2, 8, 7, 32])
+    ia = (_lib.NpuArg * 6)(*ins)
+    st = lib.npu_group_launch(b"fused_fill_linalg_conv_2d_nhwc_fhwc_generic_0", C.byref(at),
+                              ia, 6, oa, 1, None)
+    assert st == 1 and "accumulator" in _err()

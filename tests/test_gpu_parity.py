@@ -15,9 +15,9 @@ import torch
 
 import oracle
 import refs
-from npu_amd import configs, groups
+from npu_amd import blocks, configs, groups, lower
 from npu_amd import inputs as rng
-from tolerance import RTOL_BF16, RTOL_F32, bf16, check_bound
+from tolerance import RTOL_BF16, RTOL_F32, bf16, check_bf16_rounded, check_bound
 
 pytestmark = pytest.mark.gpu
 
@@ -84,7 +84,7 @@ def test_c2_conv_config_n1(cuda, dtype):
     if dtype == "f32":
         check_bound(out["out"], ref, mag, RTOL_F32, what=w.name)
     else:
-        check_bound(bf16(out["out"]), bf16(ref), mag, RTOL_BF16, what=w.name)
+        check_bf16_rounded(out["out"], ref, mag, 9 * 64 + 1, what=w.name)
 
 
 @pytest.mark.parametrize("dtype", ["f32", "bf16"])
@@ -97,7 +97,7 @@ def test_c2_conv_config_n32(cuda, dtype):
     if dtype == "f32":
         check_bound(got, ref, mag, RTOL_F32, what=w.name)
     else:
-        check_bound(bf16(got), bf16(ref), mag, RTOL_BF16, what=w.name)
+        check_bf16_rounded(got, ref, mag, 9 * 64 + 1, what=w.name)
     # size-independent property over the whole batch: ReLU output, finite,
     # and image i's result depends only on image i (batch permutation commutes)
     full = out["out"] if dtype == "f32" else bf16(out["out"])
@@ -150,7 +150,7 @@ def test_c2_conv_shapes(cuda, N, H, W, C, F, K, pad, act, bias, dtype):
     if dtype == "f32":
         check_bound(_host(out), ref, mag, RTOL_F32, what="conv")
     else:
-        check_bound(bf16(_host(out)), bf16(ref), mag, RTOL_BF16, what="conv")
+        check_bf16_rounded(_host(out), ref, mag, K * K * C + 1, what="conv")
 
 
 @pytest.mark.parametrize("N,H,W,C,F", [(2, 5, 7, 16, 16), (64, 17, 9, 32, 128)])
@@ -466,7 +466,6 @@ def test_c5_layer_small_shapes(cuda, S, D, H, F):
 def test_lowered_blocks_match_the_oracle(cuda, case):
     """linalg text -> npu_amd.lower -> entry-point calls on the GPU, against
     the oracle of the same block."""
-    from npu_amd import blocks, lower
     if case == "matmul":
         A = rng.uniform(15, 0, (64, 96), -1, 1)
         B = rng.uniform(15, 1, (96, 48), -1, 1)
@@ -482,15 +481,18 @@ def test_lowered_blocks_match_the_oracle(cuda, case):
         w = rng.normal(16, 1, (64, 3, 3, 32), 0, math.sqrt(2 / (9 * 32)))
         b = rng.uniform(16, 2, (64,), -0.1, 0.1)
         if elem == "bf16":
-            x, w = rng.to_bf16_bits(x), rng.to_bf16_bits(w)
+            # every argument in its declared type: the bias too (the group
+            # widens it to f32 exactly and adds in f32)
+            x, w, b = rng.to_bf16_bits(x), rng.to_bf16_bits(w), rng.to_bf16_bits(b)
         prog = lower.lower_text(blocks.conv_bias_act(2, 9, 7, 32, 64, elem=elem))
         out = prog.run({"x": _dev(x), "w": _dev(w), "bias": _dev(b)})["%y"]
         torch.cuda.synchronize()
-        ref, mag = refs.conv_bias_act(x, w, b, 1, "relu")
+        bias32 = bf16(b).astype(np.float32) if elem == "bf16" else b
+        ref, mag = refs.conv_bias_act(x, w, bias32, 1, "relu")
         if elem == "f32":
             check_bound(_host(out), ref, mag, RTOL_F32, what="lowered conv")
         else:
-            check_bound(bf16(_host(out)), bf16(ref), mag, RTOL_BF16, what="lowered conv")
+            check_bf16_rounded(_host(out), ref, mag, 9 * 32 + 1, what="lowered conv")
     else:
         N, H, W, C, E = 2, 9, 13, 24, 144
         x = rng.uniform(17, 0, (N, H, W, C), 0, 1)
@@ -504,3 +506,51 @@ def test_lowered_blocks_match_the_oracle(cuda, case):
         torch.cuda.synchronize()
         ref, mag = refs.irb(x, we, wdw, wp)
         check_bound(_host(out), ref, mag, RTOL_F32, what="lowered inverted residual")
+
+
+# ------------------------------------------------------------------ reference workloads
+def _harness_fills(prog):
+    """The reference harness's argument fills: argument i holds 0.01 * (i + 1)
+    (tools/harness/e2e_verify.py:186-203)."""
+    ins = {}
+    for i, (a, t) in enumerate(prog.func.args):
+        ins[a] = torch.full(t.shape, 0.01 * (i + 1), dtype=torch.float32, device="cuda")
+    return ins
+
+
+@pytest.mark.parametrize("name", ["matmul_relu.mlir", "mlp.mlir"])
+def test_reference_workloads_run_on_the_gpu(cuda, name):
+    """test/matmul_relu.mlir and test/mlp.mlir (the builder's text of them,
+    checked against the reference's files on the CPU), f16 run as f32 the way
+    the harness runs them, with the harness's fills, through the lowering and
+    npu_group_launch: the closed forms 0.0512 (K = 256) and
+    512 * 0.0512 * 0.03 = 0.786432, and the oracle's unfused loops."""
+    prog = lower.lower_text(blocks.reference_workload(name))
+    ins = _harness_fills(prog)
+    (res,) = prog.run(ins).values()
+    torch.cuda.synchronize()
+    got = _host(res).astype(np.float64)
+    host_ins = [_host(ins[a]) for a, _ in prog.func.args]
+    if name == "matmul_relu.mlir":
+        assert np.all(np.abs(got - 0.0512) <= 1e-4 * 0.0512)
+        ref = oracle.block_matmul_bias_act(host_ins[0], host_ins[1], None, "relu")
+    else:
+        assert len(prog.launches) == 1 and [c.entry for c in prog.calls] == \
+            ["fused_matmul_bias_act"] * 2
+        assert np.all(np.abs(got - 0.786432) <= 1e-5 * 0.786432 * 2)
+        h = oracle.block_matmul_bias_act(host_ins[0], host_ins[1], None, "relu")
+        ref = oracle.block_matmul_bias_act(h, host_ins[2], None, "relu")
+    assert np.all(np.abs(got - ref) <= 1e-5 * np.abs(ref) * 2)
+
+
+def test_compiled_c_caller_on_the_gpu(cuda):
+    """The C program that calls npu_group_launch by outlined name with MLIR
+    memref descriptors: the matmul_relu and mlp closed forms and the C1 group
+    with a bias against the oracle."""
+    import os
+    import subprocess
+    exe = os.path.join(os.path.dirname(os.path.abspath(__file__)), "c", "group_launch_test")
+    print("running", exe, "gpu", flush=True)
+    r = subprocess.run([exe, "gpu"], capture_output=True, text=True, timeout=120)
+    print(r.stdout, r.stderr, flush=True)
+    assert r.returncode == 0, r.stdout + r.stderr
