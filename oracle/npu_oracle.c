@@ -2,10 +2,15 @@
  * npu_oracle.c -- TEST INFRASTRUCTURE: the checker, never the product.
  *
  * CPU restatement of the reference's "lower linalg to loops, run on the
- * CPU" execution (tools/harness/e2e_verify.py:232-251).  Single-threaded,
- * built with -O2 -ffp-contract=off and without fast-math so every
+ * CPU" execution (tools/harness/e2e_verify.py:232-251).  Single-threaded
+ * (libnpu_oracle.so), built with -O2 -ffp-contract=off and without fast-math
+ * so every
  * arith.mulf / arith.addf is its own IEEE-754 binary32 operation, as the
  * scalar code that convert-linalg-to-loops + convert-arith-to-llvm produce.
+ * The `omp parallel for` pragmas split only the outer parallel loops of a
+ * nest: each output element is still computed by one thread in the same
+ * order, so the OpenMP build (libnpu_oracle_omp.so, the all-cores CPU
+ * baseline) returns the same bits as the single-threaded one.
  * See npu_oracle.h for the op forms and the parity status of each function.
  */
 #include "npu_oracle.h"
@@ -33,9 +38,11 @@ static inline uint16_t f2bf(float f) {
 }
 
 void orc_trunc_f32_bf16(const float *in, uint16_t *out, int64_t n) {
+  #pragma omp parallel for
   for (int64_t i = 0; i < n; ++i) out[i] = f2bf(in[i]);
 }
 void orc_ext_bf16_f32(const uint16_t *in, float *out, int64_t n) {
+  #pragma omp parallel for
   for (int64_t i = 0; i < n; ++i) out[i] = bf2f(in[i]);
 }
 
@@ -53,11 +60,13 @@ static inline float minimumf(float a, float b) {
 /* elementary ops                                                            */
 /* ------------------------------------------------------------------------ */
 void orc_fill_f32(float *out, int64_t n, float v) {
+  #pragma omp parallel for
   for (int64_t i = 0; i < n; ++i) out[i] = v;
 }
 
 void orc_matmul_f32(const float *A, int64_t lda, const float *B, int64_t ldb,
                     float *C, int64_t ldc, int64_t M, int64_t N, int64_t K) {
+  #pragma omp parallel for
   for (int64_t m = 0; m < M; ++m)
     for (int64_t n = 0; n < N; ++n)
       for (int64_t k = 0; k < K; ++k) {
@@ -69,6 +78,7 @@ void orc_matmul_f32(const float *A, int64_t lda, const float *B, int64_t ldb,
 void orc_matmul_bf16_f32(const uint16_t *A, int64_t lda, const uint16_t *B,
                          int64_t ldb, float *C, int64_t ldc, int64_t M,
                          int64_t N, int64_t K) {
+  #pragma omp parallel for
   for (int64_t m = 0; m < M; ++m)
     for (int64_t n = 0; n < N; ++n)
       for (int64_t k = 0; k < K; ++k) {
@@ -87,6 +97,7 @@ void orc_matmul_tiled_m_f32(const float *A, const float *B, float *C,
 
 void orc_batch_matmul_f32(const float *A, const float *B, float *C,
                           int64_t Bt, int64_t M, int64_t N, int64_t K) {
+  #pragma omp parallel for collapse(2)
   for (int64_t b = 0; b < Bt; ++b)
     for (int64_t m = 0; m < M; ++m)
       for (int64_t n = 0; n < N; ++n)
@@ -97,21 +108,26 @@ void orc_batch_matmul_f32(const float *A, const float *B, float *C,
 }
 
 void orc_relu_f32(const float *in, float *out, int64_t n) {
+  #pragma omp parallel for
   for (int64_t i = 0; i < n; ++i) out[i] = maximumf(in[i], 0.0f);
 }
 void orc_relu6_f32(const float *in, float *out, int64_t n) {
+  #pragma omp parallel for
   for (int64_t i = 0; i < n; ++i) out[i] = minimumf(maximumf(in[i], 0.0f), 6.0f);
 }
 void orc_add_f32(const float *a, const float *b, float *out, int64_t n) {
+  #pragma omp parallel for
   for (int64_t i = 0; i < n; ++i) out[i] = a[i] + b[i];
 }
 void orc_bias_add_f32(const float *in, const float *bias, float *out,
                       int64_t rows, int64_t cols) {
+  #pragma omp parallel for
   for (int64_t r = 0; r < rows; ++r)
     for (int64_t c = 0; c < cols; ++c)
       out[r * cols + c] = in[r * cols + c] + bias[c];
 }
 void orc_silu_mul_f32(const float *g, const float *u, float *out, int64_t n) {
+  #pragma omp parallel for
   for (int64_t i = 0; i < n; ++i) {
     float e = expf(-g[i]);
     float den = 1.0f + e;
@@ -125,6 +141,7 @@ void orc_pad_nchw_f32(const float *in, float *out, int64_t N, int64_t C,
                       int64_t H, int64_t W, int64_t pt, int64_t pb,
                       int64_t pl, int64_t pr, float v) {
   int64_t Hp = H + pt + pb, Wp = W + pl + pr;
+  #pragma omp parallel for collapse(2)
   for (int64_t n = 0; n < N; ++n)
     for (int64_t c = 0; c < C; ++c)
       for (int64_t h = 0; h < Hp; ++h)
@@ -139,6 +156,7 @@ void orc_pad_nchw_f32(const float *in, float *out, int64_t N, int64_t C,
 
 #define PAD_NHWC_BODY(T, ZERO)                                               \
   int64_t Hp = H + pt + pb, Wp = W + pl + pr;                                \
+  _Pragma("omp parallel for collapse(2)")                                    \
   for (int64_t n = 0; n < N; ++n)                                            \
     for (int64_t h = 0; h < Hp; ++h)                                         \
       for (int64_t w = 0; w < Wp; ++w)                                       \
@@ -171,6 +189,7 @@ void orc_conv2d_nchw_fchw_f32(const float *in, const float *w, float *out,
                               int64_t F, int64_t KH, int64_t KW, int64_t SH,
                               int64_t SW) {
   int64_t Ho = (Hp - KH) / SH + 1, Wo = (Wp - KW) / SW + 1;
+  #pragma omp parallel for collapse(2)
   for (int64_t n = 0; n < N; ++n)
     for (int64_t f = 0; f < F; ++f)
       for (int64_t oh = 0; oh < Ho; ++oh)
@@ -191,6 +210,7 @@ void orc_conv2d_nhwc_fhwc_f32(const float *in, const float *w, float *out,
                               int64_t F, int64_t KH, int64_t KW, int64_t SH,
                               int64_t SW) {
   int64_t Ho = (Hp - KH) / SH + 1, Wo = (Wp - KW) / SW + 1;
+  #pragma omp parallel for collapse(2)
   for (int64_t n = 0; n < N; ++n)
     for (int64_t oh = 0; oh < Ho; ++oh)
       for (int64_t ow = 0; ow < Wo; ++ow)
@@ -213,6 +233,7 @@ void orc_conv2d_nhwc_fhwc_bf16_f32(const uint16_t *in, const uint16_t *w,
                                    int64_t KH, int64_t KW, int64_t SH,
                                    int64_t SW) {
   int64_t Ho = (Hp - KH) / SH + 1, Wo = (Wp - KW) / SW + 1;
+  #pragma omp parallel for collapse(2)
   for (int64_t n = 0; n < N; ++n)
     for (int64_t oh = 0; oh < Ho; ++oh)
       for (int64_t ow = 0; ow < Wo; ++ow)
@@ -234,6 +255,7 @@ void orc_conv2d_nhwc_fhwc_i8_i32(const int8_t *in, const int8_t *w,
                                  int64_t Wp, int64_t C, int64_t F, int64_t KH,
                                  int64_t KW, int64_t SH, int64_t SW) {
   int64_t Ho = (Hp - KH) / SH + 1, Wo = (Wp - KW) / SW + 1;
+  #pragma omp parallel for collapse(2)
   for (int64_t n = 0; n < N; ++n)
     for (int64_t oh = 0; oh < Ho; ++oh)
       for (int64_t ow = 0; ow < Wo; ++ow)
@@ -256,6 +278,7 @@ void orc_depthwise_conv2d_nhwc_hwc_f32(const float *in, const float *w,
                                        int64_t Wp, int64_t C, int64_t KH,
                                        int64_t KW, int64_t SH, int64_t SW) {
   int64_t Ho = (Hp - KH) / SH + 1, Wo = (Wp - KW) / SW + 1;
+  #pragma omp parallel for collapse(2)
   for (int64_t n = 0; n < N; ++n)
     for (int64_t oh = 0; oh < Ho; ++oh)
       for (int64_t ow = 0; ow < Wo; ++ow)
@@ -274,6 +297,7 @@ void orc_depthwise_conv2d_nhwc_hwc_f32(const float *in, const float *w,
 void orc_apply_scale_i32(const int32_t *acc, const int32_t *mult,
                          const int32_t *shift, int32_t *out, int64_t rows,
                          int64_t cols) {
+  #pragma omp parallel for
   for (int64_t r = 0; r < rows; ++r)
     for (int64_t c = 0; c < cols; ++c) {
       int64_t v = (int64_t)acc[r * cols + c] * (int64_t)mult[c];
@@ -283,13 +307,16 @@ void orc_apply_scale_i32(const int32_t *acc, const int32_t *mult,
     }
 }
 void orc_add_i32(const int32_t *a, const int32_t *b, int32_t *out, int64_t n) {
+  #pragma omp parallel for
   for (int64_t i = 0; i < n; ++i) out[i] = a[i] + b[i];
 }
 void orc_add_i32_i8(const int32_t *a, const int8_t *b, int32_t *out, int64_t n) {
+  #pragma omp parallel for
   for (int64_t i = 0; i < n; ++i) out[i] = a[i] + (int32_t)b[i];
 }
 void orc_clamp_i32_i8(const int32_t *in, int8_t *out, int64_t n, int32_t lo,
                       int32_t hi) {
+  #pragma omp parallel for
   for (int64_t i = 0; i < n; ++i) {
     int32_t v = in[i] < lo ? lo : in[i];
     v = v > hi ? hi : v;
@@ -299,6 +326,7 @@ void orc_clamp_i32_i8(const int32_t *in, int8_t *out, int64_t n, int32_t lo,
 
 void orc_rmsnorm_f32(const float *x, const float *g, float *out, int64_t rows,
                      int64_t d, float eps) {
+  #pragma omp parallel for
   for (int64_t r = 0; r < rows; ++r) {
     const float *xr = x + r * d;
     float s = 0.0f;
@@ -318,6 +346,7 @@ void orc_rmsnorm_f32(const float *x, const float *g, float *out, int64_t rows,
 void orc_rope_f32(const float *x, const float *cos_t, const float *sin_t,
                   float *out, int64_t S, int64_t H, int64_t Dh) {
   int64_t half = Dh / 2, D = H * Dh;
+  #pragma omp parallel for collapse(2)
   for (int64_t s = 0; s < S; ++s)
     for (int64_t h = 0; h < H; ++h)
       for (int64_t i = 0; i < half; ++i) {
@@ -331,6 +360,7 @@ void orc_rope_f32(const float *x, const float *cos_t, const float *sin_t,
 
 void orc_causal_softmax_f32(float *s, int64_t rows, int64_t cols) {
   int64_t off = cols - rows;
+  #pragma omp parallel for
   for (int64_t i = 0; i < rows; ++i) {
     float *r = s + i * cols;
     int64_t last = i + off; /* keys 0..last are visible */
@@ -526,6 +556,7 @@ void orc_llama_attention_bf16(const uint16_t *Q, const uint16_t *K,
       }
     orc_fill_f32(s, S * S, 0.0f);
     orc_matmul_f32(qh, Dh, kt, S, s, S, S, S, Dh);
+    #pragma omp parallel for
     for (int64_t i = 0; i < S * S; ++i) s[i] = s[i] * scale;
     orc_causal_softmax_f32(s, S, S);
     orc_fill_f32(o, S * Dh, 0.0f);

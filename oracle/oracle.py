@@ -19,7 +19,9 @@ import numpy as np
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
 _LIB_PATH = os.path.join(_HERE, "libnpu_oracle.so")
-_lib = None
+_OMP_PATH = os.path.join(_HERE, "libnpu_oracle_omp.so")
+_libs = {}
+_threaded = False
 
 _I64 = C.c_int64
 _F32 = C.c_float
@@ -32,12 +34,27 @@ def build() -> None:
 
 
 def lib():
-    global _lib
-    if _lib is None:
-        if not os.path.exists(_LIB_PATH):
-            raise RuntimeError(f"oracle library missing: {_LIB_PATH} (run make -C oracle)")
-        _lib = C.CDLL(_LIB_PATH)
-    return _lib
+    path = _OMP_PATH if _threaded else _LIB_PATH
+    if path not in _libs:
+        if not os.path.exists(path):
+            raise RuntimeError(f"oracle library missing: {path} (run make -C oracle)")
+        _libs[path] = C.CDLL(path)
+    return _libs[path]
+
+
+class threaded:
+    """Context manager: the oracle calls inside it run the OpenMP build
+    (outer parallel loops over OMP_NUM_THREADS threads; same results)."""
+
+    def __enter__(self):
+        global _threaded
+        self._prev, _threaded = _threaded, True
+        return self
+
+    def __exit__(self, *exc):
+        global _threaded
+        _threaded = self._prev
+        return False
 
 
 def _p(a: np.ndarray):

@@ -30,6 +30,14 @@ def _host(t):
     return configs.to_host(t)
 
 
+def _widened_conv(x_bits, w_bits, b, pad, act):
+    """The oracle's f32 value of a bf16 conv chain before its final rounding:
+    the f32 loops over the inputs widened to f32 (bf16 x bf16 products are
+    exact in f32, summed in the same order)."""
+    return refs.conv_bias_act(bf16(x_bits).astype(np.float32), bf16(w_bits).astype(np.float32),
+                              b, pad, act)
+
+
 def _run_workload(w):
     arrs = w.make_inputs()
     d = configs.to_device(arrs)
@@ -84,7 +92,8 @@ def test_c2_conv_config_n1(cuda, dtype):
     if dtype == "f32":
         check_bound(out["out"], ref, mag, RTOL_F32, what=w.name)
     else:
-        check_bf16_rounded(out["out"], ref, mag, 9 * 64 + 1, what=w.name)
+        ref32, _ = _widened_conv(arrs["x"], arrs["w"], arrs["bias"], 1, "relu")
+        check_bf16_rounded(out["out"], ref32, mag, 9 * 64 + 1, what=w.name)
 
 
 @pytest.mark.parametrize("dtype", ["f32", "bf16"])
@@ -97,7 +106,8 @@ def test_c2_conv_config_n32(cuda, dtype):
     if dtype == "f32":
         check_bound(got, ref, mag, RTOL_F32, what=w.name)
     else:
-        check_bf16_rounded(got, ref, mag, 9 * 64 + 1, what=w.name)
+        ref32, _ = _widened_conv(arrs["x"][imgs], arrs["w"], arrs["bias"], 1, "relu")
+        check_bf16_rounded(got, ref32, mag, 9 * 64 + 1, what=w.name)
     # size-independent property over the whole batch: ReLU output, finite,
     # and image i's result depends only on image i (batch permutation commutes)
     full = out["out"] if dtype == "f32" else bf16(out["out"])
@@ -150,7 +160,8 @@ def test_c2_conv_shapes(cuda, N, H, W, C, F, K, pad, act, bias, dtype):
     if dtype == "f32":
         check_bound(_host(out), ref, mag, RTOL_F32, what="conv")
     else:
-        check_bf16_rounded(_host(out), ref, mag, K * K * C + 1, what="conv")
+        ref32, _ = _widened_conv(x, w, b, pad, act)
+        check_bf16_rounded(_host(out), ref32, mag, K * K * C + 1, what="conv")
 
 
 @pytest.mark.parametrize("N,H,W,C,F", [(2, 5, 7, 16, 16), (64, 17, 9, 32, 128)])
@@ -492,7 +503,8 @@ def test_lowered_blocks_match_the_oracle(cuda, case):
         if elem == "f32":
             check_bound(_host(out), ref, mag, RTOL_F32, what="lowered conv")
         else:
-            check_bf16_rounded(_host(out), ref, mag, 9 * 32 + 1, what="lowered conv")
+            ref32, _ = _widened_conv(x, w, bias32, 1, "relu")
+            check_bf16_rounded(_host(out), ref32, mag, 9 * 32 + 1, what="lowered conv")
     else:
         N, H, W, C, E = 2, 9, 13, 24, 144
         x = rng.uniform(17, 0, (N, H, W, C), 0, 1)

@@ -439,3 +439,67 @@ def test_block_llama_layer_vs_float64():
     mago = (href.abs() + act.abs() @ T(wd).abs()).numpy()
     check_bound(bf16(h), href.numpy(), magh, RTOL_BF16, what="h")
     check_bound(bf16(out), oref.numpy(), mago, RTOL_BF16, what="out")
+
+
+# ------------------------------------------------------------ the OpenMP build
+@pytest.mark.parametrize("which", ["matmul", "conv_f32", "conv_bf16", "irb", "qbottleneck",
+                                   "llama"])
+def test_threaded_oracle_returns_the_same_bits(which):
+    """The all-cores CPU baseline runs libnpu_oracle_omp.so: the same loops
+    with the outer parallel loops split over threads.  Every output must be
+    bit-identical to the single-threaded checker's."""
+    import refs
+    from npu_amd import configs
+    w = {"matmul": lambda: configs.matmul_bias_relu(64, 128, 32),
+         "conv_f32": lambda: configs.conv3x3_bias_relu(2, "f32", H=7, W=9, C=16, F=16),
+         "conv_bf16": lambda: configs.conv3x3_bias_relu(2, "bf16", H=7, W=9, C=32, F=16),
+         "irb": lambda: configs.irb(2, H=6, W=5),
+         "qbottleneck": lambda: configs.qbottleneck(2, H=6, W=7, C=64, M1=64),
+         "llama": lambda: configs.llama_layer(S=64, D=128, H=2, F=256)}[which]()
+    inp = w.make_inputs()
+    name = w.name
+    if which == "llama":
+        old = refs.LLAMA_HEADS
+        refs.LLAMA_HEADS = 2
+    try:
+        serial = refs.run_oracle(name, inp)
+        with oracle.threaded():
+            par = refs.run_oracle(name, inp)
+    finally:
+        if which == "llama":
+            refs.LLAMA_HEADS = old
+    for k in serial:
+        assert np.array_equal(np.asarray(serial[k]), np.asarray(par[k])), k
+
+
+def test_bf16_conv_is_the_widened_f32_chain_rounded_once():
+    """The bf16 GPU checks compare against the oracle's f32 value before its
+    final rounding, computed as the f32 chain over the widened inputs: that
+    value rounded to bf16 must be the bf16 oracle's output bit for bit."""
+    import refs
+    x = rng.to_bf16_bits(rng.uniform(60, 0, (2, 7, 9, 32), 0, 1))
+    w = rng.to_bf16_bits(rng.normal(60, 1, (16, 3, 3, 32), 0, math.sqrt(2 / 288)))
+    b = rng.uniform(60, 2, (16,), -0.1, 0.1)
+    outb = oracle.block_conv_bias_act(x, w, b, 1, "relu")
+    ref32, _ = refs.conv_bias_act(bf16(x).astype(np.float32), bf16(w).astype(np.float32), b, 1,
+                                  "relu")
+    assert np.array_equal(rng.to_bf16_bits(ref32), outb)
+
+
+def test_bf16_rounding_bound_rejects_one_dropped_channel_of_one_tap():
+    """Planted mistake at the full C2 bf16 shape (one image): the chain with
+    channel 5 of tap (1, 1) dropped, rounded to bf16, fails the rounding-aware
+    bound the GPU test applies, while the correct chain rounded passes."""
+    import refs
+    from npu_amd import configs
+    from tolerance import check_bf16_rounded
+    wl = configs.conv3x3_bias_relu(1, "bf16")
+    a = wl.make_inputs()
+    xf, wf = bf16(a["x"]).astype(np.float32), bf16(a["w"]).astype(np.float32)
+    ref32, mag = refs.conv_bias_act(xf, wf, a["bias"], 1, "relu")
+    check_bf16_rounded(rng.to_bf16_bits(ref32), ref32, mag, 9 * 64 + 1, what="correct")
+    w_bad = wf.copy()
+    w_bad[:, 1, 1, 5] = 0.0
+    bad32, _ = refs.conv_bias_act(xf, w_bad, a["bias"], 1, "relu")
+    with pytest.raises(AssertionError, match="outside the bf16 rounding bound"):
+        check_bf16_rounded(rng.to_bf16_bits(bad32), ref32, mag, 9 * 64 + 1, what="planted")

@@ -9,13 +9,16 @@ n * eps * mag, so the bound is independent of cancellation in the result.
 rtol is 1e-5 for fp32 paths and 2e-2 for bf16 paths.  Integer paths are
 compared bit for bit.
 
-A bf16 result whose inputs are the same on both sides and that is rounded
-once, from an f32 accumulation of n products, is held to the rounding-aware
-bound of ``check_bf16_rounded`` instead:
-    |gpu - oracle| <= 2^-8 |oracle| + n 2^-23 mag
-(two f32 sums of n terms differ by at most 2 n 2^-24 mag; each side's one
-round-to-nearest-even to bf16 adds at most 2^-9 of its value).  It is far
-tighter than 2e-2 mag: a single dropped product of the sum is outside it.
+A bf16 result rounded once, from an f32 accumulation of n products of the
+same bf16 inputs on both sides, is held to the rounding-aware bound of
+``check_bf16_rounded``, against the oracle's f32 value of the chain before that
+rounding (the f32 loops over the widened inputs, which form the same exact
+products in the same order):
+    |gpu - oracle_f32| <= 2^-8 (1 + 2^-7) |oracle_f32| + 2 n 2^-23 mag
+(the two f32 sums differ by at most 2 n 2^-24 mag; the GPU's one
+round-to-nearest-even to bf16 adds at most 2^-8 of its value).  It is far
+tighter than 2e-2 mag: a dropped product larger than about 2^-8 of the result
+is outside it.
 """
 import numpy as np
 
@@ -46,14 +49,15 @@ def bf16(x):
     return (x.astype(np.uint32) << 16).view(np.float32).astype(np.float64)
 
 
-def check_bf16_rounded(gpu_bits, ref_bits, mag, n_terms, what=""):
-    """The rounding-aware bf16 bound (module docstring) on bf16 bit patterns."""
-    g, r = bf16(gpu_bits), bf16(ref_bits)
+def check_bf16_rounded(gpu_bits, ref_f32, mag, n_terms, what=""):
+    """The rounding-aware bf16 bound (module docstring): bf16 bit patterns
+    against the oracle's f32 value before its rounding."""
+    g, r = bf16(gpu_bits), np.asarray(ref_f32, np.float64)
     mag = np.asarray(mag, np.float64)
     assert g.shape == r.shape == mag.shape, (g.shape, r.shape, mag.shape)
     assert np.all(np.isfinite(g)), f"{what}: non-finite GPU output"
     err = np.abs(g - r)
-    bound = 2.0 ** -8 * np.abs(r) * (1 + 2.0 ** -7) + n_terms * 2.0 ** -23 * mag
+    bound = 2.0 ** -8 * (1 + 2.0 ** -7) * np.abs(r) + 2 * n_terms * 2.0 ** -23 * mag
     bad = err > bound
     if bad.any():
         i = np.unravel_index(np.argmax(err - bound), err.shape)
