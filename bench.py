@@ -10,15 +10,25 @@ synchronize on both sides; HIP events recorded on that same stream give the
 average device time per step.  The JSON line's ``value`` is that latency in
 microseconds (lower is better).
 
-``roofline`` relates the algorithmic work of one launch (compulsory HBM
-bytes, or MFMA FLOPs, of the fused block) to the measured launch duration and
-the MI355X published peak.  ``graph_us`` is the same step's device time with
-the host's per-launch cost removed (20 steps captured in one HIP graph,
-replayed); ``cost_model`` compares it with the MI355X launch model's
-prediction from the launch plans the entry points record.  ``cpu_baseline`` times the CPU restatement of the
-reference's execution path (the oracle: unfused scalar loop nests, one
-thread) on a bounded sample of the same workload on this host.  ``blocks``
-repeats the GPU measurement for every other configuration.
+Per configuration (the headline and every entry of ``blocks``):
+* ``median_us`` / ``p10_us`` / ``p90_us``: per-launch device time from an
+  event pair around each of max(100, K) launches (warm caches);
+  ``cold_median_us``: the same with L2 and MALL flushed before every launch
+  (a 2 x 256 MiB device copy between launches);
+* ``graph_us``: device time per step with the host's per-launch cost removed
+  (20 steps captured in one HIP graph, replayed 10 times), outputs checked
+  equal to an eager run's;
+* ``roofline``: the algorithmic work of one launch (compulsory HBM bytes, or
+  MFMA FLOPs, of the fused block) over the median launch time, against the
+  MI355X published peak, with the measured HBM ``traffic`` per launch
+  (rocprofv3 counters, profiles/<workload>_hbm_traffic.txt);
+* ``cost_model``: the MI355X launch model's prediction from the launch plans
+  the entry points record, against ``graph_us``;
+* ``cpu_baseline``: the CPU restatement of the reference's execution path
+  (the oracle: unfused scalar loop nests) on this host, one thread, on the
+  full workload when that fits about 30 s (else as many images as fit,
+  scaled); ``cpu_all_cores``: the OpenMP build of the same loops (outer
+  parallel loops split over the threads, same results) on every thread given.
 """
 from __future__ import annotations
 
@@ -66,6 +76,40 @@ def time_gpu(w, steps, warmup):
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
     return start.elapsed_time(end) * 1e-3 / steps, wall, o
+
+
+def time_per_launch(w, reps=100, warmup=10, cold=False):
+    """Per-launch device times (seconds): an event pair around each of `reps`
+    launches on the launch stream.  cold: before every launch, a device copy
+    between two 256 MiB buffers pushes the block's data out of L2 and MALL."""
+    import torch
+
+    from npu_amd import configs
+    d = configs.to_device(w.make_inputs())
+    o = w.make_outputs(d)
+    stream = torch.cuda.current_stream()
+    flush = None
+    if cold:
+        flush = (torch.empty(64 << 20, dtype=torch.float32, device="cuda"),
+                 torch.empty(64 << 20, dtype=torch.float32, device="cuda"))
+        flush[0].zero_()
+    for _ in range(warmup):
+        w.run(d, o, stream)
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+          for _ in range(reps)]
+    torch.cuda.synchronize()
+    for a, b in ev:
+        if flush is not None:
+            flush[1].copy_(flush[0])
+        a.record(stream)
+        w.run(d, o, stream)
+        b.record(stream)
+    torch.cuda.synchronize()
+    return sorted(a.elapsed_time(b) * 1e-3 for a, b in ev)
+
+
+def _pct(xs, q):
+    return xs[min(len(xs) - 1, int(round(q * (len(xs) - 1))))]
 
 
 def time_graph(w, steps, reps=10):
@@ -117,35 +161,53 @@ def model_prediction(w):
                    for k, c in parts], plans
 
 
-def cpu_sample(w, budget_s=30.0):
-    """Times the oracle on a bounded sample; returns the cpu_baseline object.
+def cpu_threads():
+    """Threads the all-cores baseline uses: OMP_NUM_THREADS when set (the GPU
+    box sets it to its CPU share), else every logical CPU visible."""
+    try:
+        return max(1, int(os.environ.get("OMP_NUM_THREADS", "")))
+    except ValueError:
+        return os.cpu_count() or 1
+
+
+def cpu_sample(w, budget_s=30.0, threaded=False):
+    """Times the oracle on a bounded sample; returns the baseline object.
 
     Batched workloads time one image first; if the whole batch is estimated
     to fit the budget it is timed in full, otherwise as many images as fit,
-    scaled to the batch (images are independent)."""
+    scaled to the batch (images are independent).  threaded: the OpenMP
+    build of the oracle on cpu_threads() threads."""
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import contextlib
+
+    import oracle
     import refs
 
+    ctx = oracle.threaded if threaded else contextlib.nullcontext
     inp = w.make_inputs()
     n = w.units
-    if w.unit_name == "images" and n > 1:
+    with ctx():
+        if w.unit_name == "images" and n > 1:
+            t0 = time.perf_counter()
+            refs.run_oracle(w.name, inp, images=[0])
+            one = time.perf_counter() - t0
+            k = max(1, min(n, int(budget_s / max(one, 1e-6))))
+            imgs = list(range(k))
+        else:
+            k, imgs = n, None
         t0 = time.perf_counter()
-        refs.run_oracle(w.name, inp, images=[0])
-        one = time.perf_counter() - t0
-        k = max(1, min(n, int(budget_s / max(one, 1e-6))))
-        imgs = list(range(k))
-    else:
-        k, imgs = n, None
-    t0 = time.perf_counter()
-    refs.run_oracle(w.name, inp, images=imgs)
-    dt = time.perf_counter() - t0
+        refs.run_oracle(w.name, inp, images=imgs)
+        dt = time.perf_counter() - t0
     if imgs is not None and k < n:
         sample = f"{k} of {n} images (images are independent), scaled x{n / k:g}"
         dt *= n / k
     else:
         sample = "the full workload"
-    return {"value": dt * 1e6, "unit": "us", "cores": 1, "kind": "port",
-            "sample": sample + "; unfused scalar loop nests, -O2 -ffp-contract=off, 1 thread",
+    cores = cpu_threads() if threaded else 1
+    how = (f"OpenMP build, outer parallel loops over {cores} threads" if threaded
+           else "1 thread")
+    return {"value": round(dt * 1e6, 1), "unit": "us", "cores": cores, "kind": "port",
+            "sample": sample + f"; unfused scalar loop nests, -O2 -ffp-contract=off, {how}",
             "host": host_cpu()}
 
 
@@ -163,12 +225,46 @@ def measured_traffic(workload_name):
 
 def host_cpu():
     try:
+        nproc = len(os.sched_getaffinity(0))
+    except (AttributeError, OSError):
+        nproc = os.cpu_count()
+    try:
         for line in open("/proc/cpuinfo"):
             if line.startswith("model name"):
-                return f"{line.split(':', 1)[1].strip()} ({os.cpu_count()} logical CPUs visible)"
+                return (f"{line.split(':', 1)[1].strip()} (nproc {nproc}, "
+                        f"{os.cpu_count()} logical CPUs visible)")
     except OSError:
         pass
-    return f"{os.cpu_count()} logical CPUs"
+    return f"nproc {nproc}, {os.cpu_count()} logical CPUs"
+
+
+def measure(w, steps, warmup, cpu=True):
+    """Every figure of one configuration (see the module docstring)."""
+    import functools
+    w.make_inputs = functools.lru_cache(maxsize=1)(w.make_inputs)  # seeded: same arrays
+    sec, wall, _ = time_gpu(w, steps, warmup)
+    warm = time_per_launch(w, max(100, steps), max(10, warmup))
+    cold = time_per_launch(w, max(100, steps), max(10, warmup), cold=True)
+    gsec, gsame = time_graph(w, 20)
+    pred, parts, plans = model_prediction(w)
+    med = _pct(warm, 0.5)
+    rl = dict(w.roofline(med), traffic=measured_traffic(w.name), flops=w.flops,
+              mfma_flops=w.mfma_flops, bytes=w.bytes, floor_us=round(w.floor_s() * 1e6, 3))
+    rl["timed_on"] = "median_us"
+    if rl["traffic"]:
+        rl["traffic_over_algorithmic"] = round(rl["traffic"] / w.bytes, 3)
+    m = {"workload": w.name, "latency_us": round(sec * 1e6, 3), "wall_s": wall,
+         "median_us": round(med * 1e6, 3), "p10_us": round(_pct(warm, 0.1) * 1e6, 3),
+         "p90_us": round(_pct(warm, 0.9) * 1e6, 3), "reps": len(warm),
+         "cold_median_us": round(_pct(cold, 0.5) * 1e6, 3),
+         "graph_us": round(gsec * 1e6, 3), "graph_matches_eager": gsame,
+         "roofline": rl, "cold_frac": round(w.roofline(_pct(cold, 0.5))["frac"], 4),
+         "model_us": round(pred, 3), "model_error": round(pred / (gsec * 1e6) - 1, 3),
+         "model_kernels": parts, "plans": plans}
+    if cpu:
+        m["cpu_baseline"] = cpu_sample(w)
+        m["cpu_all_cores"] = cpu_sample(w, budget_s=15.0, threaded=True)
+    return m
 
 
 def main():
@@ -187,13 +283,12 @@ def main():
 
     name = args.workload or configs.HEADLINE
     w = configs.by_name(name)
-    sec, wall, _ = time_gpu(w, args.steps, args.warmup)
-    gsec, gsame = time_graph(w, 20)
-    pred, parts, plans = model_prediction(w)
-    dumped = [{"workload": w.name, "graph_us": gsec * 1e6, "plans": plans}]
+    head = measure(w, args.steps, args.warmup, cpu=not args.no_cpu)
+    sec = head["latency_us"] * 1e-6
+    dumped = [{"workload": w.name, "graph_us": head["graph_us"], "plans": head.pop("plans")}]
     line = {
         "metric": "fused-block latency",
-        "value": round(sec * 1e6, 3),
+        "value": head["latency_us"],
         "unit": "us",
         "n_gpus": 1,
         "steps": args.steps,
@@ -207,35 +302,31 @@ def main():
         "config": {"workload": w.name, "desc": w.desc, "batch": w.units,
                    "parallelism": "single GPU"},
         "throughput": {"value": w.units / sec, "unit": f"{w.unit_name}/s"},
-        "wall_s_timed_region": wall,
-        "roofline": dict(w.roofline(sec), traffic=measured_traffic(w.name),
-                         flops=w.flops, mfma_flops=w.mfma_flops, bytes=w.bytes,
-                         floor_us=w.floor_s() * 1e6),
-        "graph_us": round(gsec * 1e6, 3),
-        "graph_matches_eager": gsame,
-        "cost_model": {"predicted_us": round(pred, 3), "measured_us": round(gsec * 1e6, 3),
-                       "error": round(pred / (gsec * 1e6) - 1, 3), "kernels": parts},
+        "wall_s_timed_region": head.pop("wall_s"),
+        "median_us": head["median_us"], "p10_us": head["p10_us"], "p90_us": head["p90_us"],
+        "reps": head["reps"], "cold_median_us": head["cold_median_us"],
+        "roofline": head["roofline"],
+        "graph_us": head["graph_us"],
+        "graph_matches_eager": head["graph_matches_eager"],
+        "cost_model": {"predicted_us": head["model_us"], "measured_us": head["graph_us"],
+                       "error": head["model_error"], "kernels": head["model_kernels"]},
     }
-    if not args.no_cpu:
-        line["cpu_baseline"] = cpu_sample(w)
+    if "cpu_baseline" in head:
+        line["cpu_baseline"] = head["cpu_baseline"]
+        line["cpu_all_cores"] = head["cpu_all_cores"]
     if args.blocks:
         blocks = []
         for other in configs.all_workloads():
             if other.name == w.name:
                 continue
-            s, _, _ = time_gpu(other, max(20, args.steps // 2), max(5, args.warmup // 2))
-            gs, same = time_graph(other, 20)
-            p, pk, opl = model_prediction(other)
-            dumped.append({"workload": other.name, "graph_us": gs * 1e6, "plans": opl})
-            rl = other.roofline(s)
-            blocks.append({"workload": other.name, "latency_us": round(s * 1e6, 3),
-                           "traffic": measured_traffic(other.name),
-                           "graph_us": round(gs * 1e6, 3), "graph_matches_eager": same,
-                           "bound": rl["bound"], "frac": round(rl["frac"], 4),
-                           "graph_frac": round(other.roofline(gs)["frac"], 4),
-                           "floor_us": round(other.floor_s() * 1e6, 3),
-                           "model_us": round(p, 3), "model_error": round(p / (gs * 1e6) - 1, 3),
-                           "model_kernels": pk})
+            b = measure(other, max(100, args.steps // 2), max(10, args.warmup // 2),
+                        cpu=not args.no_cpu)
+            dumped.append({"workload": other.name, "graph_us": b["graph_us"],
+                           "plans": b.pop("plans")})
+            b.pop("wall_s")
+            blocks.append(b)
+            print(f"# {other.name}: median {b['median_us']} us, frac "
+                  f"{b['roofline']['frac']:.3f}", file=sys.stderr, flush=True)
         line["blocks"] = blocks
         errs = [abs(line["cost_model"]["error"])] + [abs(b["model_error"]) for b in blocks]
         line["cost_model"]["within_25pct"] = f"{sum(e <= 0.25 for e in errs)}/{len(errs)}"

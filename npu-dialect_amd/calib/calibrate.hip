@@ -62,6 +62,58 @@ __global__ void copy_kernel(const float4 *__restrict__ src, float4 *__restrict__
   }
 }
 
+// Streaming kernels for the attainable HBM rate: grid-stride over n 16-byte
+// elements, U independent 16-byte accesses per lane in flight, every access
+// bounds-checked, non-temporal (streaming) loads and stores.  The read kernel
+// folds what it loads into one value per lane and stores it only when it
+// equals a value no finite input produces, so the loads are kept without
+// adding traffic.
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+template <int U>
+__global__ void stream_read_kernel(const f32x4 *__restrict__ src, size_t n, float *out) {
+  const size_t lanes = (size_t)gridDim.x * blockDim.x;
+  f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+  for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < n; i += U * lanes) {
+    f32x4 v[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      v[u] = f32x4{0.f, 0.f, 0.f, 0.f};
+      if (i + u * lanes < n) v[u] = __builtin_nontemporal_load(&src[i + u * lanes]);
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) acc += v[u];
+  }
+  const float t = acc.x + acc.y + acc.z + acc.w;
+  if (t == -1.f) out[blockIdx.x] = t;
+}
+
+template <int U>
+__global__ void stream_write_kernel(f32x4 *__restrict__ dst, size_t n) {
+  const size_t lanes = (size_t)gridDim.x * blockDim.x;
+  const f32x4 z = {1.f, 2.f, 3.f, 4.f};
+  for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < n; i += U * lanes) {
+#pragma unroll
+    for (int u = 0; u < U; ++u)
+      if (i + u * lanes < n) __builtin_nontemporal_store(z, &dst[i + u * lanes]);
+  }
+}
+
+template <int U>
+__global__ void stream_copy_kernel(const f32x4 *__restrict__ src, f32x4 *__restrict__ dst,
+                                   size_t n) {
+  const size_t lanes = (size_t)gridDim.x * blockDim.x;
+  for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < n; i += U * lanes) {
+    f32x4 v[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u)
+      if (i + u * lanes < n) v[u] = __builtin_nontemporal_load(&src[i + u * lanes]);
+#pragma unroll
+    for (int u = 0; u < U; ++u)
+      if (i + u * lanes < n) __builtin_nontemporal_store(v[u], &dst[i + u * lanes]);
+  }
+}
+
 // Each workgroup reads the same L2-resident buffer `reps` times, eight
 // independent 16-byte loads in flight per lane.  n is a multiple of 8 x blockDim.
 __global__ void l2_read_kernel(const float4 *__restrict__ src, size_t n, int reps, float *out) {
@@ -347,6 +399,38 @@ int main() {
     return 1;
   const double copy_gbs = 2.0 * bytes / (t_copy * 1e3);
 
+  // Attainable HBM rate: the streaming kernels over 1 GiB, best over grids
+  // of 4..32 workgroups per CU and 4 or 8 accesses in flight per lane.
+  double best_read = 0, best_write = 0, best_copy = 0;
+  int best_read_cfg = 0, best_write_cfg = 0, best_copy_cfg = 0;
+  float *rsink;
+  CK(hipMalloc(&rsink, 64 * cus * sizeof(float)));
+  const size_t n16 = bytes / 16;
+  for (int per_cu : {4, 8, 16, 32})
+    for (int u : {4, 8}) {
+      const dim3 g(per_cu * cus), b(256);
+      double t;
+      if (time_us([&] {
+            if (u == 4) hipLaunchKernelGGL(stream_read_kernel<4>, g, b, 0, 0, reinterpret_cast<const f32x4 *>(src), n16, rsink);
+            else hipLaunchKernelGGL(stream_read_kernel<8>, g, b, 0, 0, reinterpret_cast<const f32x4 *>(src), n16, rsink);
+          }, 10, &t))
+        return 1;
+      if (bytes / (t * 1e3) > best_read) best_read = bytes / (t * 1e3), best_read_cfg = per_cu * 10 + u;
+      if (time_us([&] {
+            if (u == 4) hipLaunchKernelGGL(stream_write_kernel<4>, g, b, 0, 0, reinterpret_cast<f32x4 *>(dst), n16);
+            else hipLaunchKernelGGL(stream_write_kernel<8>, g, b, 0, 0, reinterpret_cast<f32x4 *>(dst), n16);
+          }, 10, &t))
+        return 1;
+      if (bytes / (t * 1e3) > best_write) best_write = bytes / (t * 1e3), best_write_cfg = per_cu * 10 + u;
+      if (time_us([&] {
+            if (u == 4) hipLaunchKernelGGL(stream_copy_kernel<4>, g, b, 0, 0, reinterpret_cast<const f32x4 *>(src), reinterpret_cast<f32x4 *>(dst), n16);
+            else hipLaunchKernelGGL(stream_copy_kernel<8>, g, b, 0, 0, reinterpret_cast<const f32x4 *>(src), reinterpret_cast<f32x4 *>(dst), n16);
+          }, 10, &t))
+        return 1;
+      if (2.0 * bytes / (t * 1e3) > best_copy) best_copy = 2.0 * bytes / (t * 1e3), best_copy_cfg = per_cu * 10 + u;
+    }
+  CK(hipFree(rsink));
+
   // per-CU read rate from L2: one 1024-lane workgroup per CU, 256 KiB buffer
   // read 64 times (l2n is a multiple of 8 x 1024)
   const size_t l2n = (256 << 10) / 16;
@@ -417,11 +501,14 @@ int main() {
          "\"l2_latency_us\": %.3f, \"l2_latency_loaded_us\": %.3f, \"hbm_copy_gbs\": %.1f, \"l2_read_bytes_per_clk_cu\": %.2f, "
          "\"lds_b128_clk_per_wave_instr\": {\"80\": %.1f, \"96\": %.1f, \"128\": %.1f, \"144\": %.1f, \"160\": %.1f}, "
          "\"lds_bytes_per_clk_cu\": %.1f, \"valu_clk_per_wave_instr\": %.2f, \"valu_instr_per_clk_cu\": %.2f, "
-         "\"wave_valu_clk\": %.2f, \"burst_bytes_per_clk_cu\": %.1f, \"mfma_loaded_clock_ghz\": %.3f}\n",
+         "\"wave_valu_clk\": %.2f, \"burst_bytes_per_clk_cu\": %.1f, \"mfma_loaded_clock_ghz\": %.3f, "
+         "\"hbm_stream_read_gbs\": %.1f, \"hbm_stream_write_gbs\": %.1f, \"hbm_stream_copy_gbs\": %.1f, "
+         "\"hbm_stream_best_cfg\": {\"read\": \"%d wg/cu x %d\", \"write\": \"%d wg/cu x %d\", \"copy\": \"%d wg/cu x %d\"}}\n",
          prop.gcnArchName, cus, ghz, t_launch, t_launch_full, t_graph, t_graph_full, lat_hbm, lat_loaded, lat_l2, lat_l2_loaded, copy_gbs,
          l2_bytes_per_clk_cu, lds_clk[0], lds_clk[1], lds_clk[2], lds_clk[3], lds_clk[4],
          4.0 * 1024 / lds_clk[4], valu_clk, 4.0 / valu_clk, wave_valu_clk, burst_bytes_per_clk_cu,
-         loaded_ghz);
+         loaded_ghz, best_read, best_write, best_copy, best_read_cfg / 10, best_read_cfg % 10,
+         best_write_cfg / 10, best_write_cfg % 10, best_copy_cfg / 10, best_copy_cfg % 10);
   CK(hipFree(src));
   CK(hipFree(dst));
   CK(hipFree(dsink));
