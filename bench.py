@@ -51,13 +51,56 @@ def parse():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--blocks", dest="blocks", action="store_true", default=True)
     ap.add_argument("--no-blocks", dest="blocks", action="store_false")
+    ap.add_argument("--quick", action="store_true",
+                    help="time only the K back-to-back launches of each configuration (for "
+                         "counter and trace runs: every launch is then the workload itself)")
     ap.add_argument("--dump-plans", default=None,
                     help="write every configuration's launch plans and graph time to this JSON file")
     return ap.parse_args()
 
 
+_SPIN_CYCLES_PER_US = None
+
+
+def _spin_cycles_per_us():
+    """Clock rate of torch's spin kernel (torch.cuda._sleep), measured once."""
+    global _SPIN_CYCLES_PER_US
+    if _SPIN_CYCLES_PER_US is None:
+        import torch
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda._sleep(1000)
+        a.record()
+        torch.cuda._sleep(2_000_000)
+        b.record()
+        torch.cuda.synchronize()
+        _SPIN_CYCLES_PER_US = 2_000_000 / max(a.elapsed_time(b) * 1e3, 1.0)
+    return _SPIN_CYCLES_PER_US
+
+
+def hold_stream(host_us):
+    """Queues a spin kernel long enough for the host to enqueue `host_us` of
+    launch calls behind it, so the timed launches then run back to back on
+    the device and the events time device work only (not the host's launch
+    cost).  The spin precedes the first timed event."""
+    import torch
+    torch.cuda._sleep(int((2.0 * host_us + 2000.0) * _spin_cycles_per_us()))
+
+
+def _enqueue_us(w, d, o, stream, n=20):
+    """Host microseconds per launch call of the block."""
+    import torch
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(n):
+        w.run(d, o, stream)
+    t = (time.perf_counter() - t0) / n * 1e6
+    torch.cuda.synchronize()
+    return t
+
+
 def time_gpu(w, steps, warmup):
-    """Returns (avg seconds per launch from HIP events, wall seconds, outputs)."""
+    """Returns (avg seconds per launch from HIP events, wall seconds, outputs):
+    `steps` launches back to back behind a stream hold, between two events."""
     import torch
 
     from npu_amd import configs
@@ -66,9 +109,11 @@ def time_gpu(w, steps, warmup):
     stream = torch.cuda.current_stream()
     for _ in range(warmup):
         w.run(d, o, stream)
-    torch.cuda.synchronize()
+    host = _enqueue_us(w, d, o, stream)
     start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
     t0 = time.perf_counter()
+    hold_stream(host * steps)
     start.record(stream)
     for _ in range(steps):
         w.run(d, o, stream)
@@ -80,8 +125,9 @@ def time_gpu(w, steps, warmup):
 
 def time_per_launch(w, reps=100, warmup=10, cold=False):
     """Per-launch device times (seconds): an event pair around each of `reps`
-    launches on the launch stream.  cold: before every launch, a device copy
-    between two 256 MiB buffers pushes the block's data out of L2 and MALL."""
+    launches, queued behind a stream hold.  cold: before every launch, a
+    device copy between two 256 MiB buffers pushes the block's data out of L2
+    and MALL."""
     import torch
 
     from npu_amd import configs
@@ -95,9 +141,11 @@ def time_per_launch(w, reps=100, warmup=10, cold=False):
         flush[0].zero_()
     for _ in range(warmup):
         w.run(d, o, stream)
+    host = _enqueue_us(w, d, o, stream) + (30.0 if cold else 10.0)
     ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
           for _ in range(reps)]
     torch.cuda.synchronize()
+    hold_stream(host * reps)
     for a, b in ev:
         if flush is not None:
             flush[1].copy_(flush[0])
@@ -238,11 +286,19 @@ def host_cpu():
     return f"nproc {nproc}, {os.cpu_count()} logical CPUs"
 
 
-def measure(w, steps, warmup, cpu=True):
+def measure(w, steps, warmup, cpu=True, quick=False):
     """Every figure of one configuration (see the module docstring)."""
     import functools
     w.make_inputs = functools.lru_cache(maxsize=1)(w.make_inputs)  # seeded: same arrays
     sec, wall, _ = time_gpu(w, steps, warmup)
+    if quick:
+        rl = dict(w.roofline(sec), traffic=measured_traffic(w.name), bytes=w.bytes)
+        rl["timed_on"] = "latency_us"
+        return {"workload": w.name, "latency_us": round(sec * 1e6, 3), "wall_s": wall,
+                "median_us": None, "p10_us": None, "p90_us": None, "reps": steps,
+                "cold_median_us": None, "graph_us": None, "graph_matches_eager": None,
+                "roofline": rl, "model_us": None, "model_error": 0.0, "model_kernels": [],
+                "plans": []}
     warm = time_per_launch(w, max(100, steps), max(10, warmup))
     cold = time_per_launch(w, max(100, steps), max(10, warmup), cold=True)
     gsec, gsame = time_graph(w, 20)
@@ -283,7 +339,7 @@ def main():
 
     name = args.workload or configs.HEADLINE
     w = configs.by_name(name)
-    head = measure(w, args.steps, args.warmup, cpu=not args.no_cpu)
+    head = measure(w, args.steps, args.warmup, cpu=not args.no_cpu, quick=args.quick)
     sec = head["latency_us"] * 1e-6
     dumped = [{"workload": w.name, "graph_us": head["graph_us"], "plans": head.pop("plans")}]
     line = {
@@ -319,13 +375,14 @@ def main():
         for other in configs.all_workloads():
             if other.name == w.name:
                 continue
-            b = measure(other, max(100, args.steps // 2), max(10, args.warmup // 2),
-                        cpu=not args.no_cpu)
+            b = measure(other, args.steps if args.quick else max(100, args.steps // 2),
+                        args.warmup if args.quick else max(10, args.warmup // 2),
+                        cpu=not args.no_cpu, quick=args.quick)
             dumped.append({"workload": other.name, "graph_us": b["graph_us"],
                            "plans": b.pop("plans")})
             b.pop("wall_s")
             blocks.append(b)
-            print(f"# {other.name}: median {b['median_us']} us, frac "
+            print(f"# {other.name}: {b['latency_us']} us avg, median {b['median_us']} us, frac "
                   f"{b['roofline']['frac']:.3f}", file=sys.stderr, flush=True)
         line["blocks"] = blocks
         errs = [abs(line["cost_model"]["error"])] + [abs(b["model_error"]) for b in blocks]
