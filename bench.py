@@ -11,10 +11,14 @@ average device time per step.  The JSON line's ``value`` is that latency in
 microseconds (lower is better).
 
 Per configuration (the headline and every entry of ``blocks``):
-* ``median_us`` / ``p10_us`` / ``p90_us``: per-launch device time from an
-  event pair around each of max(100, K) launches (warm caches);
-  ``cold_median_us``: the same with L2 and MALL flushed before every launch
-  (a 2 x 256 MiB device copy between launches);
+* ``latency_us``: the K-launch average as for ``value`` (the roofline's time);
+  ``median_us`` / ``p10_us`` / ``p90_us``: over 100 event pairs, each around
+  10 back-to-back launches (an event pair adds about 2 us to what it
+  brackets); ``event_pair_median_us``: single launches between event pairs;
+  ``cold_event_pair_median_us``: the same with L2 and MALL flushed before
+  every launch (a 2 x 256 MiB device copy), and ``cold_median_us`` that less
+  the pair's own cost.  Every timed launch is queued behind a spin kernel, so
+  the events time device work only, not the host's launch calls;
 * ``graph_us``: device time per step with the host's per-launch cost removed
   (20 steps captured in one HIP graph, replayed 10 times), outputs checked
   equal to an eager run's;
@@ -123,9 +127,12 @@ def time_gpu(w, steps, warmup):
     return start.elapsed_time(end) * 1e-3 / steps, wall, o
 
 
-def time_per_launch(w, reps=100, warmup=10, cold=False):
-    """Per-launch device times (seconds): an event pair around each of `reps`
-    launches, queued behind a stream hold.  cold: before every launch, a
+def time_per_launch(w, reps=100, warmup=10, cold=False, batch=1):
+    """Device times per launch (seconds, sorted): an event pair around each of
+    `reps` batches of `batch` back-to-back launches, queued behind a stream
+    hold, divided by `batch`.  An event pair adds about 2 us to what it
+    brackets, so batches of 10 give the per-launch time; single launches
+    between event pairs carry the pair's cost.  cold: before every batch, a
     device copy between two 256 MiB buffers pushes the block's data out of L2
     and MALL."""
     import torch
@@ -141,7 +148,7 @@ def time_per_launch(w, reps=100, warmup=10, cold=False):
         flush[0].zero_()
     for _ in range(warmup):
         w.run(d, o, stream)
-    host = _enqueue_us(w, d, o, stream) + (30.0 if cold else 10.0)
+    host = _enqueue_us(w, d, o, stream) * batch + (30.0 if cold else 10.0)
     ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
           for _ in range(reps)]
     torch.cuda.synchronize()
@@ -150,10 +157,11 @@ def time_per_launch(w, reps=100, warmup=10, cold=False):
         if flush is not None:
             flush[1].copy_(flush[0])
         a.record(stream)
-        w.run(d, o, stream)
+        for _ in range(batch):
+            w.run(d, o, stream)
         b.record(stream)
     torch.cuda.synchronize()
-    return sorted(a.elapsed_time(b) * 1e-3 for a, b in ev)
+    return sorted(a.elapsed_time(b) * 1e-3 / batch for a, b in ev)
 
 
 def _pct(xs, q):
@@ -299,22 +307,29 @@ def measure(w, steps, warmup, cpu=True, quick=False):
                 "cold_median_us": None, "graph_us": None, "graph_matches_eager": None,
                 "roofline": rl, "model_us": None, "model_error": 0.0, "model_kernels": [],
                 "plans": []}
-    warm = time_per_launch(w, max(100, steps), max(10, warmup))
-    cold = time_per_launch(w, max(100, steps), max(10, warmup), cold=True)
+    warm = time_per_launch(w, 100, max(10, warmup), batch=10)
+    pair = time_per_launch(w, 100, max(10, warmup))
+    cold = time_per_launch(w, 100, max(10, warmup), cold=True)
     gsec, gsame = time_graph(w, 20)
     pred, parts, plans = model_prediction(w)
     med = _pct(warm, 0.5)
-    rl = dict(w.roofline(med), traffic=measured_traffic(w.name), flops=w.flops,
+    # cold: the single-launch event-pair time with caches flushed, less the
+    # pair's own cost (warm single launches minus the warm median)
+    cold_us = _pct(cold, 0.5) - (_pct(pair, 0.5) - med)
+    rl = dict(w.roofline(sec), traffic=measured_traffic(w.name), flops=w.flops,
               mfma_flops=w.mfma_flops, bytes=w.bytes, floor_us=round(w.floor_s() * 1e6, 3))
-    rl["timed_on"] = "median_us"
+    rl["timed_on"] = "latency_us"
     if rl["traffic"]:
         rl["traffic_over_algorithmic"] = round(rl["traffic"] / w.bytes, 3)
     m = {"workload": w.name, "latency_us": round(sec * 1e6, 3), "wall_s": wall,
          "median_us": round(med * 1e6, 3), "p10_us": round(_pct(warm, 0.1) * 1e6, 3),
-         "p90_us": round(_pct(warm, 0.9) * 1e6, 3), "reps": len(warm),
-         "cold_median_us": round(_pct(cold, 0.5) * 1e6, 3),
+         "p90_us": round(_pct(warm, 0.9) * 1e6, 3), "reps": f"{len(warm)} x 10 launches",
+         "event_pair_median_us": round(_pct(pair, 0.5) * 1e6, 3),
+         "cold_event_pair_median_us": round(_pct(cold, 0.5) * 1e6, 3),
+         "cold_median_us": round(cold_us * 1e6, 3),
          "graph_us": round(gsec * 1e6, 3), "graph_matches_eager": gsame,
-         "roofline": rl, "cold_frac": round(w.roofline(_pct(cold, 0.5))["frac"], 4),
+         "roofline": rl, "median_frac": round(w.roofline(med)["frac"], 4),
+         "cold_frac": round(w.roofline(cold_us)["frac"], 4),
          "model_us": round(pred, 3), "model_error": round(pred / (gsec * 1e6) - 1, 3),
          "model_kernels": parts, "plans": plans}
     if cpu:
@@ -361,6 +376,8 @@ def main():
         "wall_s_timed_region": head.pop("wall_s"),
         "median_us": head["median_us"], "p10_us": head["p10_us"], "p90_us": head["p90_us"],
         "reps": head["reps"], "cold_median_us": head["cold_median_us"],
+        "event_pair_median_us": head.get("event_pair_median_us"),
+        "cold_event_pair_median_us": head.get("cold_event_pair_median_us"),
         "roofline": head["roofline"],
         "graph_us": head["graph_us"],
         "graph_matches_eager": head["graph_matches_eager"],
