@@ -159,6 +159,16 @@ def default_target() -> HWTarget:
     return t
 
 
+def target_from_params(params: dict) -> HWTarget:
+    """The default target with a module's #npu.target parameters applied, as
+    CostModelAnalysis does (lib/Analysis/CostModel.cpp:985-1000): the seven
+    parameters replace the defaults, every other field keeps its default."""
+    t = default_target()
+    for k, v in params.items():
+        setattr(t, k, int(v))
+    return t
+
+
 def mi355x_target(elem_bits=32) -> HWTarget:
     t = HWTarget()
     lib().npu_hw_target_mi355x(C.byref(t), elem_bits)

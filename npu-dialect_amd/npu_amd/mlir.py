@@ -65,6 +65,41 @@ class MFunc:
     result_types: list
     ops: list           # [MOp]
     types: dict         # SSA name -> TType
+    target: dict = None  # the enclosing module's #npu.target parameters, if it has one
+
+
+TARGET_PARAMS = ("num_cores", "sram_per_core", "dram_bandwidth", "sram_bandwidth",
+                 "matrix_throughput", "dsp_throughput", "dma_channels")
+
+
+def parse_target(text: str):
+    """The module's `npu.target` attribute (include/npu/Dialect/NPU/NPUDialect.td:100-113:
+    `#npu.target<num_cores = .., sram_per_core = .., ...>`, the seven int64
+    parameters in any order), given inline in `module attributes {...}` or
+    through an attribute alias (`#t = #npu.target<...>` ... `npu.target = #t`).
+    Returns {param: value} or None when the module sets none."""
+    m = re.search(r"\bnpu\.target\s*=\s*(#[\w.]+(?:<[^>]*>)?)", text)
+    if not m:
+        return None
+    ref = m.group(1)
+    if not ref.startswith("#npu.target<"):
+        alias = re.search(r"^\s*" + re.escape(ref) + r"\s*=\s*(#npu\.target<[^>]*>)", text, re.M)
+        if not alias:
+            raise ValueError(f"npu.target refers to {ref}, which the text does not define")
+        ref = alias.group(1)
+    body = ref[len("#npu.target<"):-1]
+    vals = {}
+    for part in _split_top(body):
+        if not part:
+            continue
+        k, v = (x.strip() for x in part.split("=", 1))
+        if k not in TARGET_PARAMS:
+            raise ValueError(f"#npu.target: unknown parameter {k}")
+        vals[k] = int(v.split(":")[0].strip())
+    missing = [k for k in TARGET_PARAMS if k not in vals]
+    if missing:
+        raise ValueError(f"#npu.target: missing {missing}")
+    return vals
 
 
 def parse_type(s: str) -> TType:
@@ -333,6 +368,9 @@ def parse_functions(text: str) -> list:
             for r, t in zip(op.results, op.result_types):
                 types[r] = t
         funcs.append(MFunc(m.group(1), args, rtypes, ops, types))
+    target = parse_target(text)
+    for f in funcs:
+        f.target = target
     return funcs
 
 

@@ -48,8 +48,16 @@ def _tiles(sizes):
 
 def run(func: mlir.MFunc, target: host.HWTarget = None, cores: int = None,
         sram_size: int = None) -> dict:
-    """Replays npu-pipeline's decisions on `func`; see the module docstring."""
-    t = target or host.default_target()
+    """Replays npu-pipeline's decisions on `func`; see the module docstring.
+    The target is `target` when given, else the module's #npu.target (as
+    CostModelAnalysis reads it, lib/Analysis/CostModel.cpp:985-1000), else
+    the reference's default NPU."""
+    if target is not None:
+        t = target
+    elif func.target:
+        t = host.target_from_params(func.target)
+    else:
+        t = host.default_target()
     cores = cores or t.num_cores
     sram = sram_size or t.sram_per_core
     g = host.Graph(func)

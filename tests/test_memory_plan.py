@@ -203,3 +203,56 @@ def test_lds_plans_of_the_kernels(name):
               [x.addr_pong + x.bytes for x in b if x.addr_pong >= 0])
     high = lds - min([x.addr for x in b if x.role == OUT], default=lds)
     assert (low + high + 511) // 512 * 512 == traced
+
+
+NPU_TARGET_TEXT = """
+#big = #npu.target<num_cores = 8, sram_per_core = 163840, dram_bandwidth = 8000,
+                   sram_bandwidth = 1024, matrix_throughput = 2048, dsp_throughput = 512,
+                   dma_channels = 4>
+module attributes {npu.target = #big} {
+""" + '''  func.func @mm(%A: tensor<128x256xf32>, %B: tensor<256x512xf32>) -> tensor<128x512xf32> {
+    %cst = arith.constant 0.0 : f32
+    %init = tensor.empty() : tensor<128x512xf32>
+    %fill = linalg.fill ins(%cst : f32) outs(%init : tensor<128x512xf32>) -> tensor<128x512xf32>
+    %mm = linalg.matmul ins(%A, %B : tensor<128x256xf32>, tensor<256x512xf32>)
+                        outs(%fill : tensor<128x512xf32>) -> tensor<128x512xf32>
+    return %mm : tensor<128x512xf32>
+  }
+}
+'''
+
+
+def test_module_target_attribute_retargets_the_pipeline():
+    """#npu.target on the module (NPUDialect.td:100-113) replaces the seven
+    parameters of the default target, as CostModelAnalysis does
+    (CostModel.cpp:985-1000); the other fields keep their defaults."""
+    f = mlir.parse_functions(NPU_TARGET_TEXT)[0]
+    assert f.target == {"num_cores": 8, "sram_per_core": 163840, "dram_bandwidth": 8000,
+                        "sram_bandwidth": 1024, "matrix_throughput": 2048, "dsp_throughput": 512,
+                        "dma_channels": 4}
+    rep = pipeline.run(f)
+    t = rep["target"]
+    assert t["num_cores"] == 8 and t["sram_per_core"] == 163840 and t["dram_bandwidth"] == 8000
+    d = host.default_target().as_dict()
+    assert t["clock_ghz"] == d["clock_ghz"] and t["noc_bandwidth"] == d["noc_bandwidth"]
+    # the SRAM plan and cost record use the module's target
+    rec = json.loads(rep["cost_json"][0][len("COST_JSON: "):])
+    assert rec["sram_budget"] == 163840
+    # the same function without the attribute: the default NPU
+    plain = mlir.parse_functions(NPU_TARGET_TEXT[NPU_TARGET_TEXT.index("  func.func"):]
+                                 .rsplit("}", 1)[0])[0]
+    assert plain.target is None
+    assert json.loads(pipeline.run(plain)["cost_json"][0][len("COST_JSON: "):])["sram_budget"] \
+        == 2 * 1024 * 1024
+
+
+def test_inline_target_and_errors():
+    txt = NPU_TARGET_TEXT.replace("#big = #npu.target", "#unused = #npu.target").replace(
+        "npu.target = #big", "npu.target = #npu.target<num_cores = 2, sram_per_core = 4096, "
+        "dram_bandwidth = 1, sram_bandwidth = 2, matrix_throughput = 3, dsp_throughput = 4, "
+        "dma_channels = 1>")
+    assert mlir.parse_target(txt)["num_cores"] == 2
+    with pytest.raises(ValueError, match="missing"):
+        mlir.parse_target("module attributes {npu.target = #npu.target<num_cores = 2>} {}")
+    with pytest.raises(ValueError, match="does not define"):
+        mlir.parse_target("module attributes {npu.target = #nowhere} {}")
