@@ -488,44 +488,95 @@ class Program:
             vals[a] = x
         return vals
 
-    def run(self, inputs: dict, stream=None) -> dict:
-        """inputs: argument name (with or without %) -> tensor.  Runs every
-        launch through npu_group_launch and returns the function's results by
-        SSA name."""
+    def run_launch(self, index: int, vals: dict, stream=None):
+        """Runs launch `index` on the values bound so far (function arguments
+        and earlier launches' results, by SSA name) and binds its result."""
         import torch
 
         from . import groups
 
-        vals = self.check_inputs(inputs)
+        L = self.launches[index]
         types = self.func.types
         tdt = lambda e: getattr(torch, _TORCH_DTYPE[e])
         dev = next(iter(vals.values())).device
         prod = {r: op for op in self.func.ops for r in op.results}
-        for L in self.launches:
-            ins = []
-            for v in L.ins:
-                op = prod.get(v)
-                if v == L.padded:
-                    ins.append(vals[L.pad_source])
-                elif v in vals:
-                    t = vals[v]
-                    ins.append(t.float() if v in L.widen else t)
-                elif op is not None and op.name == "arith.constant":
-                    ins.append(_float(op.attrs.get("value")))
-                elif op is not None and op.name == "tensor.empty":
-                    t = types[v]
-                    keep = torch.empty(t.shape, dtype=tdt(t.elem), device=dev) \
-                        if v in L.stores else None
-                    ins.append(groups.Empty(t.shape, t.elem, keep))
-                else:  # pragma: no cover - lower() binds every input
-                    raise KeyError(f"{L.name}: no value for {v}")
-            oty = types[L.out]
-            out = torch.empty(oty.shape, dtype=tdt(oty.elem), device=dev)
-            groups.group_launch(L.name, ins, [out], act=L.acts, pad=L.pad, stream=stream)
-            vals[L.out] = out
+        ins = []
+        for v in L.ins:
+            op = prod.get(v)
+            if v == L.padded:
+                ins.append(vals[L.pad_source])
+            elif v in vals:
+                t = vals[v]
+                ins.append(t.float() if v in L.widen else t)
+            elif op is not None and op.name == "arith.constant":
+                ins.append(_float(op.attrs.get("value")))
+            elif op is not None and op.name == "tensor.empty":
+                t = types[v]
+                keep = torch.empty(t.shape, dtype=tdt(t.elem), device=dev) \
+                    if v in L.stores else None
+                ins.append(groups.Empty(t.shape, t.elem, keep))
+            else:  # pragma: no cover - lower() binds every input
+                raise KeyError(f"{L.name}: no value for {v}")
+        oty = types[L.out]
+        if L.out not in vals:
+            vals[L.out] = torch.empty(oty.shape, dtype=tdt(oty.elem), device=dev)
+        groups.group_launch(L.name, ins, [vals[L.out]], act=L.acts, pad=L.pad, stream=stream)
+
+    def run(self, inputs: dict, stream=None) -> dict:
+        """inputs: argument name (with or without %) -> tensor.  Runs every
+        launch through npu_group_launch and returns the function's results by
+        SSA name."""
+        vals = self.check_inputs(inputs)
+        for i in range(len(self.launches)):
+            self.run_launch(i, vals, stream)
         ret = [op for op in self.func.ops if op.name == "func.return"]
         names = ret[0].operands if ret else []
         return {n: vals[n] for n in names}
+
+
+def cost_report(program: "Program", inputs: dict, reps: int = 20, stream=None) -> list:
+    """The pipeline's COST_JSON records of the program's outlined functions
+    (CostEvaluatePass.cpp:135-158, the reference's keys in its order) with
+    what the MI355X adds after them: the entry point that runs the function,
+    the launch model's prediction for that launch (``mi355x_predicted_us``,
+    from the launch plans the entry point records) and the launch's measured
+    device time (``measured_us``: `reps` launches back to back between HIP
+    events, queued behind a stream hold so that only device work is timed).
+    A launch that runs several outlined functions (a chain fused across a
+    tensor.pad) reports its figures on each of them, with its name."""
+    import json
+
+    import torch
+
+    from . import groups, host
+
+    rep = pipeline.run(program.func)
+    records = {f["name"]: json.loads(line[len("COST_JSON: "):])
+               for f, line in zip(rep["functions"], rep["cost_json"])}
+    out = []
+    vals = program.check_inputs(inputs)
+    for li, L in enumerate(program.launches):
+        def one():
+            program.run_launch(li, vals, stream)
+        with groups.collect_plans() as cp:
+            one()
+        torch.cuda.synchronize()
+        pred, _ = host.predict_block(cp.plans)
+        st = torch.cuda.current_stream() if stream is None else stream
+        torch.cuda._sleep(2_000_000)
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record(st)
+        for _ in range(reps):
+            one()
+        b.record(st)
+        torch.cuda.synchronize()
+        meas = a.elapsed_time(b) * 1e3 / reps
+        for name in L.name.split("+"):
+            r = dict(records[name])
+            r.update({"entry_point": L.name if "+" in L.name else name,
+                      "mi355x_predicted_us": round(pred, 3), "measured_us": round(meas, 3)})
+            out.append("COST_JSON: " + json.dumps(r))
+    return out
 
 
 def lower_text(text: str, target=None) -> "Program":

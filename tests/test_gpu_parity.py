@@ -566,3 +566,37 @@ def test_compiled_c_caller_on_the_gpu(cuda):
     r = subprocess.run([exe, "gpu"], capture_output=True, text=True, timeout=120)
     print(r.stdout, r.stderr, flush=True)
     assert r.returncode == 0, r.stdout + r.stderr
+
+
+COST_KEYS = ["name", "flops", "mem_bytes", "arithmetic_intensity", "time_sec", "is_memory_bound",
+             "efficiency", "dma_in_bytes", "dma_out_bytes", "matrix_cycles", "dsp_cycles",
+             "peak_sram_bytes", "num_tile_iterations", "num_linalg_ops", "sram_budget", "bottleneck"]
+
+
+@pytest.mark.parametrize("which", ["mlp", "irb"])
+def test_cost_records_carry_prediction_and_measurement(cuda, which):
+    """COST_JSON records of a lowered program: the reference's keys in its
+    order (CostEvaluatePass.cpp:135-158), then the entry point, the MI355X
+    launch model's prediction and the measured device time of that launch;
+    summed like tools/harness/optimize.py:73-94 sums time_sec."""
+    import json
+    if which == "mlp":
+        prog = lower.lower_text(blocks.reference_workload("mlp.mlir"))
+        ins = _harness_fills(prog)
+    else:
+        N, H, W, C, E = 2, 9, 13, 24, 144
+        prog = lower.lower_text(blocks.inverted_residual(N, H, W, C, E))
+        ins = {"x": _dev(rng.uniform(17, 0, (N, H, W, C), 0, 1)),
+               "we": _dev(rng.normal(17, 1, (E, 1, 1, C), 0, 0.3)),
+               "wdw": _dev(rng.normal(17, 2, (3, 3, E), 0, 0.5)),
+               "wp": _dev(rng.normal(17, 3, (C, 1, 1, E), 0, 0.1))}
+    lines = lower.cost_report(prog, ins, reps=10)
+    recs = [json.loads(line[len("COST_JSON: "):]) for line in lines]
+    assert len(recs) == sum(len(L.name.split("+")) for L in prog.launches)
+    for r in recs:
+        assert list(r)[:len(COST_KEYS)] == COST_KEYS
+        assert list(r)[len(COST_KEYS):] == ["entry_point", "mi355x_predicted_us", "measured_us"]
+        assert r["mi355x_predicted_us"] > 0 and r["measured_us"] > 0
+    total_measured = sum({r["entry_point"]: r["measured_us"] for r in recs}.values())
+    print("measured", total_measured, "predicted",
+          sum({r["entry_point"]: r["mi355x_predicted_us"] for r in recs}.values()))
