@@ -267,6 +267,10 @@ typedef struct npu_group_attrs {
  *     of an inverted residual block after its tensor.pad -> fused_irb_f32
  *     (cst, init_e, x, we[E,1,1,C], dest_e, init_d, wdw[3,3,E], dest_d,
  *      init_p, wp[C,1,1,E], dest) -> (out)
+ *   the three conv -> requantizing generic groups of the int8 bottleneck,
+ *     across the pad before the 3x3 conv   -> fused_qbottleneck_i8
+ *     (cst, init1, x, w1[M1,1,1,C], m1, s1, dest1, init2, w2[M1,3,3,M1], m2,
+ *      s2, dest2, init3, w3[C,1,1,M1], m3, s3, dest) -> (out)
  * Shapes, element types and counts are checked against the group before any
  * launch (NPU_ERR_INVALID_ARG); an unknown chain is NPU_ERR_UNSUPPORTED.
  * Launch plans of every launch of the sequence are recorded. */

@@ -286,8 +286,55 @@ npu_status run_irb(Cursor &c, const npu_memref *out, npu_stream stream, PlanLog 
   return NPU_OK;
 }
 
+npu_status run_qbottleneck(Cursor &c, const npu_memref *out, npu_stream stream, PlanLog &log) {
+  G_TRY(c.fill_value());
+  const npu_memref *x, *w1, *w2, *w3, *m1, *s1, *m2, *s2, *m3, *s3;
+  const npu_memref *init1, *init2, *init3;
+  G_TRY(c.memref(4, "conv1 accumulator (tensor.empty)", &init1));
+  G_TRY(c.memref(4, "x", &x));
+  G_TRY(c.memref(4, "w1 [M1,1,1,C]", &w1));
+  const int64_t N = x->sizes[0], H = x->sizes[1], W = x->sizes[2], C = x->sizes[3];
+  const int64_t M1 = w1->sizes[0];
+  if (!same_shape(*w1, {M1, 1, 1, C}))
+    return gfail(NPU_ERR_INVALID_ARG, "w1: %s, expected [M1,1,1,%lld]", shape_str(*w1).c_str(),
+                 (long long)C);
+  if (!same_shape(*init1, {N, H, W, M1}))
+    return gfail(NPU_ERR_INVALID_ARG, "conv1 accumulator: %s", shape_str(*init1).c_str());
+  G_TRY(c.memref(1, "m1", &m1));
+  G_TRY(c.memref(1, "s1", &s1));
+  G_TRY(c.dest({N, H, W, M1}, "y1 destination (tensor.empty)"));
+  G_TRY(c.memref(4, "conv2 accumulator (tensor.empty)", &init2));
+  if (!same_shape(*init2, {N, H, W, M1}))
+    return gfail(NPU_ERR_INVALID_ARG, "conv2 accumulator: %s", shape_str(*init2).c_str());
+  G_TRY(c.memref(4, "w2 [M1,3,3,M1]", &w2));
+  G_TRY(c.memref(1, "m2", &m2));
+  G_TRY(c.memref(1, "s2", &s2));
+  G_TRY(c.dest({N, H, W, M1}, "y2 destination (tensor.empty)"));
+  G_TRY(c.memref(4, "conv3 accumulator (tensor.empty)", &init3));
+  if (!same_shape(*init3, {N, H, W, C}))
+    return gfail(NPU_ERR_INVALID_ARG, "conv3 accumulator: %s", shape_str(*init3).c_str());
+  G_TRY(c.memref(4, "w3 [C,1,1,M1]", &w3));
+  if (!same_shape(*w3, {C, 1, 1, M1}))
+    return gfail(NPU_ERR_INVALID_ARG, "w3: %s, expected [%lld,1,1,%lld]", shape_str(*w3).c_str(),
+                 (long long)C, (long long)M1);
+  G_TRY(c.memref(1, "m3", &m3));
+  G_TRY(c.memref(1, "s3", &s3));
+  G_TRY(c.dest({N, H, W, C}, "result destination (tensor.empty)"));
+  if (!c.done())
+    return gfail(NPU_ERR_INVALID_ARG, "%zu arguments left over after the group's inputs", c.pos());
+  npu_memref w1v, w3v;
+  G_TRY(squeeze_1x1(*w1, "w1", &w1v));
+  G_TRY(squeeze_1x1(*w3, "w3", &w3v));
+  G_TRY(typed(fused_qbottleneck_i8(x, &w1v, w2, &w3v, m1, s1, m2, s2, m3, s3, out, stream)));
+  log.take();
+  return NPU_OK;
+}
+
 const char *kMatmul = "fill_matmul_generic";
 const char *kConv = "fill_linalg_conv_2d_nhwc_fhwc_generic";
+const char *kQBottleneck =
+    "fill_linalg_conv_2d_nhwc_fhwc_generic_fill_linalg_conv_2d_nhwc_fhwc_generic_"
+    "fill_linalg_conv_2d_nhwc_fhwc_generic";
 const char *kIrb =
     "fill_linalg_conv_2d_nhwc_fhwc_generic_fill_linalg_depthwise_conv_2d_nhwc_hwc_generic_"
     "fill_linalg_conv_2d_nhwc_fhwc_generic";
@@ -337,6 +384,7 @@ extern "C" npu_status npu_group_launch(const char *outlined_name, const npu_grou
     }
     if (key == kConv) return run_conv(c, *attrs, &res.m, stream, log);
     if (key == kIrb) return run_irb(c, &res.m, stream, log);
+    if (key == kQBottleneck) return run_qbottleneck(c, &res.m, stream, log);
     return gfail(NPU_ERR_UNSUPPORTED, "no MI355X group runs the outlined chain '%s'", key.c_str());
   }();
   log.publish();

@@ -164,3 +164,81 @@ def reference_workload(name):
     if name == "mlp.mlir":
         return mlp(128, 256, 512, 256, elem="f16")
     raise KeyError(name)
+
+
+def _requant(res, acc, m, s, shape, residual=None):
+    """`res` (i8) = clamp(apply_scale(acc) [+ residual], 0, 127) as one
+    linalg.generic: TOSA apply_scale_32 with single rounding written in arith
+    -- (i64(acc) * i64(m) + (1 << (s - 1))) >> s, truncated to i32 -- then
+    the residual added in i32, the clamp (ReLU folded into [0, 127]) and the
+    truncation to i8.  m and s are per output channel (the last dimension)."""
+    rank = len(shape)
+    ids = ", ".join(f"d{i}" for i in range(rank))
+    full, chan = f"affine_map<({ids}) -> ({ids})>", f"affine_map<({ids}) -> (d{rank - 1})>"
+    ins, tys, maps, args = [acc, m, s], [_t(shape, "i32"), _t([shape[-1]], "i32"),
+                                         _t([shape[-1]], "i32")], [full, chan, chan], \
+        ["%a: i32", "%m: i32", "%s: i32"]
+    if residual is not None:
+        ins.append(residual)
+        tys.append(_t(shape, "i8"))
+        maps.append(full)
+        args.append("%x: i8")
+    maps.append(full)
+    body = ["    %a64 = arith.extsi %a : i32 to i64",
+            "    %m64 = arith.extsi %m : i32 to i64",
+            "    %s64 = arith.extsi %s : i32 to i64",
+            "    %p = arith.muli %a64, %m64 : i64",
+            "    %one = arith.constant 1 : i64",
+            "    %sm1 = arith.subi %s64, %one : i64",
+            "    %rnd = arith.shli %one, %sm1 : i64",
+            "    %t = arith.addi %p, %rnd : i64",
+            "    %q = arith.shrsi %t, %s64 : i64",
+            "    %q32 = arith.trunci %q : i64 to i32"]
+    v = "%q32"
+    if residual is not None:
+        body += ["    %x32 = arith.extsi %x : i8 to i32", "    %r = arith.addi %q32, %x32 : i32"]
+        v = "%r"
+    body += ["    %lo = arith.constant 0 : i32", "    %hi = arith.constant 127 : i32",
+             f"    %c1 = arith.maxsi {v}, %lo : i32", "    %c2 = arith.minsi %c1, %hi : i32",
+             "    %o = arith.trunci %c2 : i32 to i8"]
+    it = ", ".join(['"parallel"'] * rank)
+    return (f"  {res}_e = tensor.empty() : {_t(shape, 'i8')}\n"
+            f"  {res} = linalg.generic {{indexing_maps = [{', '.join(maps)}],\n"
+            f"    iterator_types = [{it}]}} ins({', '.join(ins)} : {', '.join(tys)}) "
+            f"outs({res}_e : {_t(shape, 'i8')}) {{\n"
+            f"  ^bb0({', '.join(args)}, %out: i8):\n" + "\n".join(body) +
+            f"\n    linalg.yield %o : i8\n  }} -> {_t(shape, 'i8')}\n")
+
+
+def _iconv(res, x, w, xshape, wshape, oshape, zero="%c0"):
+    return (f"  {res}_i = tensor.empty() : {_t(oshape, 'i32')}\n"
+            f"  {res}_f = linalg.fill ins({zero} : i32) outs({res}_i : {_t(oshape, 'i32')}) -> "
+            f"{_t(oshape, 'i32')}\n"
+            f"  {res} = linalg.conv_2d_nhwc_fhwc {{dilations = dense<1> : tensor<2xi64>, "
+            f"strides = dense<1> : tensor<2xi64>}}\n"
+            f"    ins({x}, {w} : {_t(xshape, 'i8')}, {_t(wshape, 'i8')}) "
+            f"outs({res}_f : {_t(oshape, 'i32')}) -> {_t(oshape, 'i32')}\n")
+
+
+def qbottleneck(N, H, W, C, M1):
+    """C4 (int8 ResNet-50 bottleneck, NHWC, zero points 0): 1x1 C -> M1,
+    requant + ReLU; pad; 3x3 M1 -> M1, requant + ReLU; 1x1 M1 -> C, requant,
+    + x, ReLU (the int8 restatement of test/resnet50_block.mlir:5-105)."""
+    xs, ys = [N, H, W, C], [N, H, W, M1]
+    ps = [N, H + 2, W + 2, M1]
+    sig = (f"%x: {_t(xs, 'i8')}, %w1: {_t([M1, 1, 1, C], 'i8')}, %w2: {_t([M1, 3, 3, M1], 'i8')}, "
+           f"%w3: {_t([C, 1, 1, M1], 'i8')}, %m1: {_t([M1], 'i32')}, %s1: {_t([M1], 'i32')}, "
+           f"%m2: {_t([M1], 'i32')}, %s2: {_t([M1], 'i32')}, %m3: {_t([C], 'i32')}, "
+           f"%s3: {_t([C], 'i32')}")
+    text = (f"func.func @qbottleneck({sig}) -> {_t(xs, 'i8')} {{\n"
+            f"  %c0 = arith.constant 0 : i32\n  %z8 = arith.constant 0 : i8\n")
+    text += _iconv("%acc1", "%x", "%w1", xs, [M1, 1, 1, C], ys)
+    text += _requant("%y1", "%acc1", "%m1", "%s1", ys)
+    text += (f"  %y1p = tensor.pad %y1 low[0, 1, 1, 0] high[0, 1, 1, 0] {{\n"
+             f"  ^bb0(%i0: index, %i1: index, %i2: index, %i3: index):\n"
+             f"    tensor.yield %z8 : i8\n  }} : {_t(ys, 'i8')} to {_t(ps, 'i8')}\n")
+    text += _iconv("%acc2", "%y1p", "%w2", ps, [M1, 3, 3, M1], ys)
+    text += _requant("%y2", "%acc2", "%m2", "%s2", ys)
+    text += _iconv("%acc3", "%y2", "%w3", ys, [C, 1, 1, M1], xs)
+    text += _requant("%y3", "%acc3", "%m3", "%s3", xs, residual="%x")
+    return text + f"  return %y3 : {_t(xs, 'i8')}\n}}\n"

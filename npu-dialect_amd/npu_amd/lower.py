@@ -135,6 +135,93 @@ def _body_value(g):
     return env[yielded[0]]
 
 
+def _tree(g):
+    """The yielded value of generic `g` as a full expression tree: ("arg", k),
+    ("const", literal, type) or (op name, type, operand trees...)."""
+    args, body, yielded = g.attrs.get("block_args", []), g.attrs.get("body", []), \
+        g.attrs.get("yield", [])
+    env = {a: ("arg", k) for k, a in enumerate(args)}
+    for b in body:
+        if b.name == "arith.constant":
+            env[b.result] = ("const", b.value, b.type)
+        else:
+            if any(o not in env for o in b.operands):
+                raise NotImplementedError(f"{g.results[0]}: generic body reads a value "
+                                          f"defined outside it ({b.operands})")
+            env[b.result] = (b.name, b.type) + tuple(env[o] for o in b.operands)
+    if len(yielded) != 1 or yielded[0] not in env:
+        raise NotImplementedError(f"{g.results[0]}: generic yields {yielded}")
+    return env[yielded[0]]
+
+
+def _matches(tree, tmpl, binds):
+    """Structural match of an expression tree against a template whose leaves
+    are ("$name",) placeholders (bound to one subtree each, consistently)."""
+    if len(tmpl) == 1 and tmpl[0].startswith("$"):
+        key = tmpl[0]
+        if key in binds:
+            return binds[key] == tree
+        binds[key] = tree
+        return True
+    if tmpl[0] == "const":
+        return tree[0] == "const" and _float(tree[1]) == _float(tmpl[1]) and tree[2] == tmpl[2]
+    if len(tree) != len(tmpl) or tree[0] != tmpl[0] or tree[1] != tmpl[1]:
+        return False
+    return all(_matches(a, b, binds) for a, b in zip(tree[2:], tmpl[2:]))
+
+
+def _apply_scale_tmpl():
+    """TOSA apply_scale_32, single rounding, in arith (i64), truncated to i32:
+    trunci((extsi(acc) * extsi(m) + (1 << (extsi(s) - 1))) >> extsi(s))."""
+    s64 = ("arith.extsi", "i32 to i64", ("$s",))
+    one = ("const", "1", "i64")
+    prod = ("arith.muli", "i64", ("arith.extsi", "i32 to i64", ("$acc",)),
+            ("arith.extsi", "i32 to i64", ("$m",)))
+    rnd = ("arith.shli", "i64", one, ("arith.subi", "i64", s64, one))
+    return ("arith.trunci", "i64 to i32",
+            ("arith.shrsi", "i64", ("arith.addi", "i64", prod, rnd), s64))
+
+
+def _requant_of(fn: "_Fn", g, acc, shape):
+    """(m, s, residual) when generic `g` computes the int8 requantization of
+    accumulator `acc`: trunci(minsi(maxsi(apply_scale(acc) [+ extsi(x)], 0),
+    127)) to i8, m and s per output channel (the last dimension), the
+    residual x of the output's shape; else raises NotImplementedError."""
+    rank = len(shape)
+    ident = list(range(rank))
+    name = g.results[0]
+    maps = g.attrs.get("maps", [])
+    if len(g.results) != 1 or g.iterators != ["parallel"] * rank or len(maps) != len(g.ins) + 1 \
+            or maps[-1] != ident or not g.ins or g.ins[0] != acc or maps[0] != ident:
+        raise NotImplementedError(f"{name}: not a requantization of {acc}")
+    scale = _apply_scale_tmpl()
+    for resid in (False, True):
+        inner = ("arith.addi", "i32", scale, ("arith.extsi", "i8 to i32", ("$x",))) if resid else scale
+        tmpl = ("arith.trunci", "i32 to i8",
+                ("arith.minsi", "i32", ("arith.maxsi", "i32", inner, ("const", "0", "i32")),
+                 ("const", "127", "i32")))
+        b = {}
+        if not _matches(_tree(g), tmpl, b):
+            continue
+        pos = {k: b[k][1] for k in b if b[k][0] == "arg"}
+        if set(pos) != ({"$acc", "$m", "$s", "$x"} if resid else {"$acc", "$m", "$s"}) or \
+                pos["$acc"] != 0:
+            break
+        m, sh = g.ins[pos["$m"]], g.ins[pos["$s"]]
+        if maps[pos["$m"]] != [rank - 1] or maps[pos["$s"]] != [rank - 1]:
+            break
+        if fn.ty(m).shape != [shape[-1]] or fn.ty(sh).shape != [shape[-1]]:
+            break
+        x = None
+        if resid:
+            x = g.ins[pos["$x"]]
+            if maps[pos["$x"]] != ident or fn.ty(x).shape != list(shape):
+                break
+        return m, sh, x
+    raise NotImplementedError(f"{name}: generic body is not the int8 requantization "
+                              "(apply_scale, optional residual, clamp to [0, 127])")
+
+
 def _clamp(e, op, bound):
     """x when e is op(x, bound) or op(bound, x), else None."""
     if e[0] != op:
@@ -312,6 +399,14 @@ def lower(func: mlir.MFunc, target=None) -> "Program":
             _check_fill(fn, s["fills"][0])
             a = s["anchor"]
             shape = fn.ty(a.results[0]).shape
+            if a.name != "linalg.matmul" and fn.ty(a.ins[0]).elem == "i8":
+                _check_conv(a)
+                chain = _qbottleneck_chain(fn, groups, name, segs)
+                calls.append(chain)
+                consumed.update(chain.functions)
+                covered.update(r for f2 in chain.functions for o in groups[f2] for r in o.results)
+                covered.update(fn.op(chain.params["padded"]).results)
+                break
             bias, res, act, out = _epilogue(fn, s["generics"], a.results[0], shape)
             if a.name == "linalg.matmul":
                 _check_matmul(a)
@@ -393,6 +488,67 @@ def _launches(fn: _Fn, rep, calls, dests):
         out.append(L)
         i = j
     return out
+
+
+def _qbottleneck_chain(fn, groups, name, segs):
+    """The call running an int8 bottleneck chain whose first group is `name`:
+    1x1 conv -> requant -> tensor.pad (zeros, 1 in H and W) -> 3x3 conv ->
+    requant -> 1x1 conv -> requant + the chain's input -> fused_qbottleneck_i8,
+    the intermediates never leaving the chip.  Raises NotImplementedError for
+    any other int8 group."""
+    if len(segs) != 1 or len(segs[0]["generics"]) != 1:
+        raise NotImplementedError(f"{name}: int8 group other than conv -> requant")
+    c1, g1 = segs[0]["anchor"], segs[0]["generics"][0]
+    _check_fill(fn, segs[0]["fills"][0])
+    x, w1 = c1.ins
+    xs = fn.ty(x).shape
+    if fn.ty(w1).shape[1:3] != [1, 1] or fn.ty(x).elem != "i8" or fn.ty(w1).elem != "i8":
+        raise NotImplementedError(f"{name}: int8 chain must start with a 1x1 conv of int8 values")
+    m1, s1, r1 = _requant_of(fn, g1, c1.results[0], fn.ty(c1.results[0]).shape)
+    y1 = g1.results[0]
+
+    def user(v, kind):
+        us = [o for o in fn.f.ops if o.name == kind and (v in o.ins or v in o.operands)]
+        if len(us) != 1:
+            raise NotImplementedError(f"{v}: expected one {kind} user")
+        return us[0]
+
+    pad = user(y1, "tensor.pad")
+    src, p = _pad_of(fn, pad.results[0])
+    if p != 1 or src != y1:
+        raise NotImplementedError(f"{pad.results[0]}: the 3x3 conv's pad must be 1 in H and W")
+    c2 = user(pad.results[0], "linalg.conv_2d_nhwc_fhwc")
+    _check_conv(c2)
+    g2 = user(c2.results[0], "linalg.generic")
+    m2, s2, r2 = _requant_of(fn, g2, c2.results[0], fn.ty(c2.results[0]).shape)
+    c3 = user(g2.results[0], "linalg.conv_2d_nhwc_fhwc")
+    _check_conv(c3)
+    g3 = user(c3.results[0], "linalg.generic")
+    m3, s3, r3 = _requant_of(fn, g3, c3.results[0], fn.ty(c3.results[0]).shape)
+    if r1 is not None or r2 is not None or r3 != x:
+        raise NotImplementedError(f"{g3.results[0]}: the residual must be the chain's input only")
+    w2, w3 = c2.ins[1], c3.ins[1]
+    M1 = fn.ty(w1).shape[0]
+    if fn.ty(w2).shape != [M1, 3, 3, M1] or fn.ty(w3).shape != [xs[3], 1, 1, M1]:
+        raise NotImplementedError(f"{name}: filter shapes {fn.ty(w2).shape} {fn.ty(w3).shape}")
+    group_of = {o.results[0]: n for n, ops in groups.items() for o in ops if o.results}
+    names = []
+    for o in (c1, g1, c2, g2, c3, g3):
+        n = group_of.get(o.results[0])
+        if n is None:
+            raise NotImplementedError(f"{o.results[0]} is in no outlined group")
+        if n not in names:
+            names.append(n)
+    chain_ops = {id(o) for o in (c1, g1, c2, g2, c3, g3)}
+    for n in names:
+        for o in groups[n]:
+            if o.name == "linalg.fill":
+                _check_fill(fn, o)
+            elif id(o) not in chain_ops:
+                raise NotImplementedError(f"{n}: {o.name} in the int8 chain")
+    C = xs[3]
+    return Call("fused_qbottleneck_i8", names, [x, w1, w2, w3, m1, s1, m2, s2, m3, s3],
+                g3.results[0], {"padded": pad.results[0]}, {w1: [M1, C], w3: [C, M1]})
 
 
 def _irb_chain(fn, groups, name, conv, e_out, x, act, bias, res):

@@ -200,11 +200,13 @@ def _statements(body: str):
 @dataclass
 class BodyOp:
     """One operation of a linalg.generic region: ``result = name operands``
-    (``value`` holds an arith.constant's literal)."""
+    (``value`` holds an arith.constant's literal, ``type`` the text after the
+    colon, e.g. "i64" or "i64 to i32")."""
     result: str
     name: str
     operands: list
     value: str = None
+    type: str = ""
 
 
 def parse_maps(attr_text: str) -> list:
@@ -240,10 +242,11 @@ def parse_region(region: str):
         if not b:
             continue
         res, name, tail = b.groups()
+        ty = tail.split(":", 1)[1].strip() if ":" in tail else ""
         if name == "arith.constant":
-            body.append(BodyOp(res, name, [], tail.rsplit(":", 1)[0].strip()))
+            body.append(BodyOp(res, name, [], tail.rsplit(":", 1)[0].strip(), ty))
         else:
-            body.append(BodyOp(res, name, re.findall(r"%[\w]+", tail.split(":", 1)[0])))
+            body.append(BodyOp(res, name, re.findall(r"%[\w]+", tail.split(":", 1)[0]), None, ty))
     return args, body, yielded
 
 

@@ -600,3 +600,20 @@ def test_cost_records_carry_prediction_and_measurement(cuda, which):
     total_measured = sum({r["entry_point"]: r["measured_us"] for r in recs}.values())
     print("measured", total_measured, "predicted",
           sum({r["entry_point"]: r["mi355x_predicted_us"] for r in recs}.values()))
+
+
+@pytest.mark.parametrize("N,H,W,C", [(2, 7, 9, 64), (1, 12, 10, 256)])
+def test_lowered_int8_bottleneck_is_bit_exact(cuda, N, H, W, C):
+    """The int8 bottleneck's linalg text (apply_scale requant generics, pad,
+    residual) through the lowering and npu_group_launch: bit-exact against
+    the oracle's unfused loops."""
+    w = configs.qbottleneck(N, H=H, W=W, C=C, M1=64)
+    a = w.make_inputs()
+    prog = lower.lower_text(blocks.qbottleneck(N, H, W, C, 64))
+    ins = {k: _dev(v) for k, v in a.items()}
+    ins["w1"] = ins["w1"].reshape(64, 1, 1, C)
+    ins["w3"] = ins["w3"].reshape(C, 1, 1, 64)
+    (out,) = prog.run(ins).values()
+    torch.cuda.synchronize()
+    ref = refs.qbottleneck(a)
+    assert np.array_equal(_host(out), ref)

@@ -204,3 +204,35 @@ def test_pipeline_names_entry_points_without_the_hip_library():
     rep = pipeline.run(mlir.parse_functions(blocks.matmul_bias_act(8, 16, 4))[0])
     assert rep["functions"][0]["entry_point"] == "fused_matmul_bias_act"
     assert names.OUTLINED_NAMES["fused_fill_matmul_generic"] == "fused_matmul_bias_act"
+
+
+def test_int8_bottleneck_lowers_to_one_call():
+    """The int8 bottleneck text (apply_scale requant generics, a zero pad
+    before the 3x3 conv, the residual in the last generic) outlines as two
+    groups around the pad and runs as one fused_qbottleneck_i8 launch."""
+    p = lower.lower_text(blocks.qbottleneck(2, 7, 9, 64, 64))
+    (c,) = p.calls
+    assert c.entry == "fused_qbottleneck_i8" and len(c.functions) == 2
+    assert c.args == ["%x", "%w1", "%w2", "%w3", "%m1", "%s1", "%m2", "%s2", "%m3", "%s3"]
+    assert c.views == {"%w1": [64, 64], "%w3": [64, 64]}
+    (L,) = p.launches
+    assert L.name == "+".join(c.functions) and len(L.ins) == 17 and "%y1p" not in L.ins
+
+
+@pytest.mark.parametrize("old,new", [
+    ("%rnd = arith.shli %one, %sm1 : i64", "%rnd = arith.shli %one, %s64 : i64"),  # wrong rounding
+    ("%q = arith.shrsi %t, %s64 : i64", "%q = arith.shrui %t, %s64 : i64"),     # logical shift
+    ("%hi = arith.constant 127 : i32", "%hi = arith.constant 100 : i32"),       # clamp bound
+    ("%p = arith.muli %a64, %m64 : i64", "%p = arith.addi %a64, %m64 : i64"),   # not a product
+])
+def test_int8_requant_bodies_are_checked(old, new):
+    t = blocks.qbottleneck(1, 4, 4, 64, 64)
+    assert old in t
+    with pytest.raises(NotImplementedError):
+        lower.lower_text(t.replace(old, new, 1))
+
+
+def test_int8_residual_must_be_the_input():
+    t = blocks.qbottleneck(1, 4, 4, 64, 64).replace("ins(%acc3, %m3, %s3, %x :", "ins(%acc3, %m3, %s3, %y2 :")
+    with pytest.raises(NotImplementedError):
+        lower.lower_text(t)
