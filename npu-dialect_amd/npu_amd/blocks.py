@@ -9,6 +9,8 @@ holds the bias add and the activation (`arith.maximumf` with 0 for ReLU, then
 """
 from __future__ import annotations
 
+import math
+
 
 def _t(shape, elem):
     return "tensor<" + "x".join(str(d) for d in shape) + "x" + elem + ">"
@@ -242,3 +244,182 @@ def qbottleneck(N, H, W, C, M1):
     text += _iconv("%acc3", "%y2", "%w3", ys, [C, 1, 1, M1], xs)
     text += _requant("%y3", "%acc3", "%m3", "%s3", xs, residual="%x")
     return text + f"  return %y3 : {_t(xs, 'i8')}\n}}\n"
+
+
+def _gen(res, ins, in_types, out_elem, out_shape, maps, iters, args, body, yielded, init=None):
+    """One linalg.generic, its destination a tensor.empty (or `init`)."""
+    it = ", ".join(f'"{x}"' for x in iters)
+    dest = init or f"{res}_e"
+    pre = "" if init else f"  {res}_e = tensor.empty() : {_t(out_shape, out_elem)}\n"
+    return (pre + f"  {res} = linalg.generic {{indexing_maps = [{', '.join(maps)}],\n"
+            f"    iterator_types = [{it}]}} ins({', '.join(ins)} : {', '.join(in_types)}) "
+            f"outs({dest} : {_t(out_shape, out_elem)}) {{\n"
+            f"  ^bb0({', '.join(args)}):\n" + "\n".join("    " + b for b in body) +
+            f"\n    linalg.yield {yielded} : {out_elem}\n  }} -> {_t(out_shape, out_elem)}\n")
+
+
+def _amap(n, res):
+    ids = ", ".join(f"d{i}" for i in range(n))
+    return f"affine_map<({ids}) -> ({res})>"
+
+
+def _fill(res, shape, elem, value):
+    return (f"  {res}_i = tensor.empty() : {_t(shape, elem)}\n"
+            f"  {res} = linalg.fill ins({value} : {elem}) outs({res}_i : {_t(shape, elem)}) -> "
+            f"{_t(shape, elem)}\n")
+
+
+def _rmsnorm(res, x, g, S, D, eps):
+    """res (bf16) = bf16(x * (1 / sqrt(sum(x^2) / D + eps)) * g), the sum of
+    squares a reduction generic over the row."""
+    idd, row, col = _amap(2, "d0, d1"), _amap(2, "d0"), _amap(2, "d1")
+    t = _fill(f"{res}_ss0", [S], "f32", "%zf")
+    t += _gen(f"{res}_ss", [x], [_t([S, D], "bf16")], "f32", [S], [idd, row],
+              ["parallel", "reduction"], ["%a: bf16", "%acc: f32"],
+              ["%e = arith.extf %a : bf16 to f32", "%q = arith.mulf %e, %e : f32",
+               "%s = arith.addf %acc, %q : f32"], "%s", init=f"{res}_ss0")
+    t += _gen(res, [x, f"{res}_ss", g], [_t([S, D], "bf16"), _t([S], "f32"), _t([D], "f32")],
+              "bf16", [S, D], [idd, row, col, idd], ["parallel", "parallel"],
+              ["%a: bf16", "%s: f32", "%g: f32", "%o: bf16"],
+              [f"%d = arith.constant {float(D)!r} : f32", f"%eps = arith.constant {eps!r} : f32",
+               "%one = arith.constant 1.0 : f32", "%e = arith.extf %a : bf16 to f32",
+               "%ms = arith.divf %s, %d : f32", "%v = arith.addf %ms, %eps : f32",
+               "%r = math.sqrt %v : f32", "%inv = arith.divf %one, %r : f32",
+               "%t = arith.mulf %e, %inv : f32", "%u = arith.mulf %t, %g : f32",
+               "%b = arith.truncf %u : f32 to bf16"], "%b")
+    return t
+
+
+def _mm(res, a, w, M, K, N, ea="bf16"):
+    t = _fill(f"{res}_f", [M, N], "f32", "%zf")
+    return t + (f"  {res} = linalg.matmul ins({a}, {w} : {_t([M, K], ea)}, {_t([K, N], 'bf16')}) "
+                f"outs({res}_f : {_t([M, N], 'f32')}) -> {_t([M, N], 'f32')}\n")
+
+
+def _residual(res, r, acc, S, N):
+    idd = _amap(2, "d0, d1")
+    return _gen(res, [r, acc], [_t([S, N], "bf16"), _t([S, N], "f32")], "bf16", [S, N],
+                [idd, idd, idd], ["parallel", "parallel"], ["%r: bf16", "%a: f32", "%o: bf16"],
+                ["%e = arith.extf %r : bf16 to f32", "%s = arith.addf %e, %a : f32",
+                 "%t = arith.truncf %s : f32 to bf16"], "%t")
+
+
+def _trunc(res, a, shape):
+    idd = _amap(len(shape), ", ".join(f"d{i}" for i in range(len(shape))))
+    return _gen(res, [a], [_t(shape, "f32")], "bf16", shape, [idd, idd],
+                ["parallel"] * len(shape), ["%a: f32", "%o: bf16"],
+                ["%t = arith.truncf %a : f32 to bf16"], "%t")
+
+
+def _rope(res, acc, S, D, H, dh=64):
+    """res (bf16, [S, D]) = RoPE of the f32 accumulator on interleaved pairs:
+    (x0, x1) -> (x0 c - x1 s, x0 s + x1 c), over the [S, H, dh / 2, 2] view."""
+    v4 = [S, H, dh // 2, 2]
+    t = (f"  {res}_4 = tensor.expand_shape {acc} [[0], [1, 2, 3]] output_shape [{S}, {H}, {dh // 2}, 2] "
+         f": {_t([S, D], 'f32')} into {_t(v4, 'f32')}\n")
+    t += _gen(f"{res}_r", [f"{res}_4", f"{res}_4", "%cos", "%sin"],
+              [_t(v4, "f32"), _t(v4, "f32"), _t([S, dh // 2], "f32"), _t([S, dh // 2], "f32")],
+              "bf16", v4,
+              [_amap(4, "d0, d1, d2, 0"), _amap(4, "d0, d1, d2, 1"), _amap(4, "d0, d2"),
+               _amap(4, "d0, d2"), _amap(4, "d0, d1, d2, d3")], ["parallel"] * 4,
+              ["%x0: f32", "%x1: f32", "%c: f32", "%s: f32", "%o: bf16"],
+              ["%a = arith.mulf %x0, %c : f32", "%b = arith.mulf %x1, %s : f32",
+               "%e = arith.mulf %x0, %s : f32", "%f = arith.mulf %x1, %c : f32",
+               "%ev = arith.subf %a, %b : f32", "%od = arith.addf %e, %f : f32",
+               "%j = linalg.index 3 : index", "%c0 = arith.constant 0 : index",
+               "%is0 = arith.cmpi eq, %j, %c0 : index", "%v = arith.select %is0, %ev, %od : f32",
+               "%t = arith.truncf %v : f32 to bf16"], "%t")
+    t += (f"  {res} = tensor.collapse_shape {res}_r [[0], [1, 2, 3]] : {_t(v4, 'bf16')} into "
+          f"{_t([S, D], 'bf16')}\n")
+    return t
+
+
+def _heads(res, v, S, H, perm, dh=64):
+    """[S, D] -> [S, H, dh] -> transposed by `perm` (bf16)."""
+    s3 = [S, H, dh]
+    out = [s3[p] for p in perm]
+    return (f"  {res}_3 = tensor.expand_shape {v} [[0], [1, 2]] output_shape [{S}, {H}, {dh}] : "
+            f"{_t([S, H * dh], 'bf16')} into {_t(s3, 'bf16')}\n"
+            f"  {res}_e = tensor.empty() : {_t(out, 'bf16')}\n"
+            f"  {res} = linalg.transpose ins({res}_3 : {_t(s3, 'bf16')}) outs({res}_e : "
+            f"{_t(out, 'bf16')}) permutation = [{', '.join(map(str, perm))}]\n")
+
+
+def _attention(res, Q, K, V, S, H, scale, dh=64):
+    """Causal softmax attention per head, in the oracle's order: S = Q K^T,
+    scaled, keys after the query set to -inf, softmax (max, exp, sum,
+    divide) in f32, O = P V, A = bf16(O) as [S, D]."""
+    D = H * dh
+    id3, row3 = _amap(3, "d0, d1, d2"), _amap(3, "d0, d1")
+    t = _heads(f"{res}_q", Q, S, H, [1, 0, 2], dh) + _heads(f"{res}_k", K, S, H, [1, 2, 0], dh) + \
+        _heads(f"{res}_v", V, S, H, [1, 0, 2], dh)
+    t += _fill(f"{res}_s0", [H, S, S], "f32", "%zf")
+    t += (f"  {res}_s = linalg.batch_matmul ins({res}_q, {res}_k : {_t([H, S, dh], 'bf16')}, "
+          f"{_t([H, dh, S], 'bf16')}) outs({res}_s0 : {_t([H, S, S], 'f32')}) -> "
+          f"{_t([H, S, S], 'f32')}\n")
+    t += _gen(f"{res}_sm", [f"{res}_s"], [_t([H, S, S], "f32")], "f32", [H, S, S], [id3, id3],
+              ["parallel"] * 3, ["%a: f32", "%o: f32"],
+              [f"%sc = arith.constant {scale!r} : f32", "%v = arith.mulf %a, %sc : f32",
+               "%i = linalg.index 1 : index", "%j = linalg.index 2 : index",
+               "%gt = arith.cmpi ugt, %j, %i : index", "%ninf = arith.constant 0xFF800000 : f32",
+               "%r = arith.select %gt, %ninf, %v : f32"], "%r")
+    t += _fill(f"{res}_m0", [H, S], "f32", "%ninf")
+    t += _gen(f"{res}_m", [f"{res}_sm"], [_t([H, S, S], "f32")], "f32", [H, S], [id3, row3],
+              ["parallel", "parallel", "reduction"], ["%a: f32", "%acc: f32"],
+              ["%m = arith.maximumf %acc, %a : f32"], "%m", init=f"{res}_m0")
+    t += _gen(f"{res}_x", [f"{res}_sm", f"{res}_m"], [_t([H, S, S], "f32"), _t([H, S], "f32")],
+              "f32", [H, S, S], [id3, row3, id3], ["parallel"] * 3, ["%a: f32", "%m: f32", "%o: f32"],
+              ["%d = arith.subf %a, %m : f32", "%e = math.exp %d : f32"], "%e")
+    t += _fill(f"{res}_l0", [H, S], "f32", "%zf")
+    t += _gen(f"{res}_l", [f"{res}_x"], [_t([H, S, S], "f32")], "f32", [H, S], [id3, row3],
+              ["parallel", "parallel", "reduction"], ["%a: f32", "%acc: f32"],
+              ["%s = arith.addf %acc, %a : f32"], "%s", init=f"{res}_l0")
+    t += _gen(f"{res}_p", [f"{res}_x", f"{res}_l"], [_t([H, S, S], "f32"), _t([H, S], "f32")],
+              "f32", [H, S, S], [id3, row3, id3], ["parallel"] * 3, ["%a: f32", "%l: f32", "%o: f32"],
+              ["%r = arith.divf %a, %l : f32"], "%r")
+    t += _fill(f"{res}_o0", [H, S, dh], "f32", "%zf")
+    t += (f"  {res}_o = linalg.batch_matmul ins({res}_p, {res}_v : {_t([H, S, S], 'f32')}, "
+          f"{_t([H, S, dh], 'bf16')}) outs({res}_o0 : {_t([H, S, dh], 'f32')}) -> "
+          f"{_t([H, S, dh], 'f32')}\n")
+    t += (f"  {res}_ot_e = tensor.empty() : {_t([S, H, dh], 'f32')}\n"
+          f"  {res}_ot = linalg.transpose ins({res}_o : {_t([H, S, dh], 'f32')}) outs({res}_ot_e : "
+          f"{_t([S, H, dh], 'f32')}) permutation = [1, 0, 2]\n"
+          f"  {res}_o2 = tensor.collapse_shape {res}_ot [[0], [1, 2]] : {_t([S, H, dh], 'f32')} "
+          f"into {_t([S, D], 'f32')}\n")
+    return t + _trunc(res, f"{res}_o2", [S, D])
+
+
+def llama_layer(S, D, H, F, eps=1e-05, dh=None):
+    """C5, one Llama decoder layer in bf16 storage (the oracle's semantics):
+    RMSNorm -> Q, K, V projections (RoPE on Q and K) -> causal softmax
+    attention -> O projection + x -> RMSNorm -> gate / up projections, SiLU
+    gating -> down projection + h.  The reference's test/llama_attention.mlir
+    replaces softmax by ReLU and has no norm, RoPE or gating; this is the real
+    layer, written with the ops the reference's passes read."""
+    dh = dh or D // H
+    scale = 1.0 / math.sqrt(dh)
+    sig = (f"%x: {_t([S, D], 'bf16')}, %g1: {_t([D], 'f32')}, %wq: {_t([D, D], 'bf16')}, "
+           f"%wk: {_t([D, D], 'bf16')}, %wv: {_t([D, D], 'bf16')}, %wo: {_t([D, D], 'bf16')}, "
+           f"%g2: {_t([D], 'f32')}, %wg: {_t([D, F], 'bf16')}, %wu: {_t([D, F], 'bf16')}, "
+           f"%wd: {_t([F, D], 'bf16')}, %cos: {_t([S, dh // 2], 'f32')}, "
+           f"%sin: {_t([S, dh // 2], 'f32')}")
+    t = (f"func.func @llama_layer({sig}) -> {_t([S, D], 'bf16')} {{\n"
+         f"  %zf = arith.constant 0.0 : f32\n  %ninf = arith.constant 0xFF800000 : f32\n")
+    t += _rmsnorm("%xn", "%x", "%g1", S, D, eps)
+    t += _mm("%qa", "%xn", "%wq", S, D, D) + _mm("%ka", "%xn", "%wk", S, D, D) + \
+        _mm("%va", "%xn", "%wv", S, D, D)
+    t += _rope("%Q", "%qa", S, D, H, dh) + _rope("%K", "%ka", S, D, H, dh) + \
+        _trunc("%V", "%va", [S, D])
+    t += _attention("%A", "%Q", "%K", "%V", S, H, scale, dh)
+    t += _mm("%oa", "%A", "%wo", S, D, D) + _residual("%h", "%x", "%oa", S, D)
+    t += _rmsnorm("%hn", "%h", "%g2", S, D, eps)
+    t += _mm("%ga", "%hn", "%wg", S, D, F) + _mm("%ua", "%hn", "%wu", S, D, F)
+    idd = _amap(2, "d0, d1")
+    t += _gen("%act", ["%ga", "%ua"], [_t([S, F], "f32"), _t([S, F], "f32")], "bf16", [S, F],
+              [idd, idd, idd], ["parallel", "parallel"], ["%g: f32", "%u: f32", "%o: bf16"],
+              ["%n = arith.negf %g : f32", "%e = math.exp %n : f32",
+               "%one = arith.constant 1.0 : f32", "%den = arith.addf %one, %e : f32",
+               "%s = arith.divf %g, %den : f32", "%m = arith.mulf %s, %u : f32",
+               "%t = arith.truncf %m : f32 to bf16"], "%t")
+    t += _mm("%da", "%act", "%wd", S, F, D) + _residual("%out", "%h", "%da", S, D)
+    return t + f"  return %out : {_t([S, D], 'bf16')}\n}}\n"

@@ -53,6 +53,7 @@ class Call:
     out: str                   # SSA name of the result
     params: dict = field(default_factory=dict)   # pad, act
     views: dict = field(default_factory=dict)    # SSA name -> shape the entry point takes
+    outs: list = None          # every result, when the entry point writes several
 
 
 @dataclass
@@ -68,6 +69,9 @@ class Launch:
     pad_source: str = None
     stores: list = field(default_factory=list)   # tensor.empty values holding intermediates
     widen: list = field(default_factory=list)    # bf16 biases passed widened to f32
+    entry: str = "npu_group_launch"   # or a typed entry point taking `ins`, `outs`, `params`
+    outs: list = None
+    params: dict = field(default_factory=dict)
 
 
 _TORCH_DTYPE = {"f32": "float32", "bf16": "bfloat16", "i8": "int8", "i32": "int32"}
@@ -97,11 +101,17 @@ class _Fn:
 
 
 def _float(literal):
-    """The value of an arith.constant literal ("0.0", "6.000000e+00"), or None."""
+    """The value of an arith.constant literal ("0.0", "6.000000e+00",
+    "0xFF800000"), or None."""
     if literal is None:
         return None
+    text = str(literal).split(":")[0].strip()
+    if re.fullmatch(r"0x[0-9A-Fa-f]{8}", text):  # MLIR's f32 bit-pattern form (inf, nan)
+        import struct
+
+        return struct.unpack("<f", struct.pack("<I", int(text, 16)))[0]
     try:
-        return float(str(literal).split(":")[0].strip())
+        return float(text)
     except ValueError:
         return None
 
@@ -144,6 +154,13 @@ def _tree(g):
     for b in body:
         if b.name == "arith.constant":
             env[b.result] = ("const", b.value, b.type)
+        elif b.name == "linalg.index":
+            env[b.result] = (b.name, b.type, ("dim", int(b.value)))
+        elif b.name in ("arith.cmpi", "arith.cmpf"):
+            if any(o not in env for o in b.operands):
+                raise NotImplementedError(f"{g.results[0]}: generic body reads a value "
+                                          f"defined outside it ({b.operands})")
+            env[b.result] = (b.name, b.type, ("pred", b.value)) + tuple(env[o] for o in b.operands)
         else:
             if any(o not in env for o in b.operands):
                 raise NotImplementedError(f"{g.results[0]}: generic body reads a value "
@@ -154,9 +171,16 @@ def _tree(g):
     return env[yielded[0]]
 
 
+_COMMUTATIVE = ("arith.addf", "arith.mulf", "arith.maximumf", "arith.minimumf",
+                "arith.addi", "arith.muli")
+
+
 def _matches(tree, tmpl, binds):
     """Structural match of an expression tree against a template whose leaves
-    are ("$name",) placeholders (bound to one subtree each, consistently)."""
+    are ("$name",) placeholders (bound to one subtree each, consistently).
+    The two operands of a commutative op (IEEE addition, multiplication,
+    maximum and minimum give the same bits in either order) match in either
+    order; nothing is reassociated."""
     if len(tmpl) == 1 and tmpl[0].startswith("$"):
         key = tmpl[0]
         if key in binds:
@@ -167,7 +191,16 @@ def _matches(tree, tmpl, binds):
         return tree[0] == "const" and _float(tree[1]) == _float(tmpl[1]) and tree[2] == tmpl[2]
     if len(tree) != len(tmpl) or tree[0] != tmpl[0] or tree[1] != tmpl[1]:
         return False
-    return all(_matches(a, b, binds) for a, b in zip(tree[2:], tmpl[2:]))
+    orders = [tmpl[2:]]
+    if tmpl[0] in _COMMUTATIVE and len(tmpl) == 4:
+        orders.append((tmpl[3], tmpl[2]))
+    for order in orders:
+        trial = dict(binds)
+        if all(_matches(a, b, trial) for a, b in zip(tree[2:], order)):
+            binds.clear()
+            binds.update(trial)
+            return True
+    return False
 
 
 def _apply_scale_tmpl():
@@ -387,13 +420,30 @@ def _segments(name, ops):
 
 def lower(func: mlir.MFunc, target=None) -> "Program":
     """Matches func's outlined groups to entry points; see the module docstring."""
+    from . import lower_llama
+
     fn = _Fn(func)
     rep = pipeline.run(func, target)
     groups = {g["name"]: [func.ops[i] for i in g["ops"]] for g in rep["functions"]}
     calls, covered, consumed, dests = [], set(), set(), {}
+    # a Llama layer: its calls span the pipeline's groups, which hold only its ops
+    llama = lower_llama.llama_calls(fn)
+    in_llama = {r for c in llama for o in c["ops"] for r in o.results}
+    for c in llama:
+        names = [n for n, ops in groups.items() if n != func.name
+                 and any(r in in_llama and any(r in o.results for o in c["ops"])
+                        for op in ops for r in op.results)]
+        calls.append(Call(c["entry"], names, c["args"], c["outs"][-1], c["params"],
+                          outs=c["outs"]))
+    covered |= in_llama
     for name, ops in groups.items():
         if name in consumed:
             continue
+        inside = [r for o in ops if o.name != "linalg.fill" for r in o.results]
+        if inside and all(r in in_llama for r in inside):
+            continue
+        if any(r in in_llama for r in inside):
+            raise NotImplementedError(f"{name}: group mixes the Llama layer's ops with others")
         segs = _segments(name, ops)
         for s in segs:
             _check_fill(fn, s["fills"][0])
@@ -444,10 +494,14 @@ def lower(func: mlir.MFunc, target=None) -> "Program":
         covered.update(r for o in ops for r in o.results)
     # every computing op must be part of a call
     for op in func.ops:
-        if op.name.startswith("linalg.") or op.name == "tensor.pad":
+        if op.name.startswith("linalg.") or op.name in ("tensor.pad", "tensor.expand_shape",
+                                                          "tensor.collapse_shape"):
             if not op.results or op.results[0] not in covered:
                 raise NotImplementedError(f"{op.results[0] if op.results else op.name}: "
                                           f"{op.name} is in no group an entry point runs")
+    # dataflow order: a call runs after the calls whose results it reads
+    pos = {r: i for i, op in enumerate(func.ops) for r in op.results}
+    calls.sort(key=lambda c: max(pos[v] for v in (c.outs or [c.out])))
     return Program(func, calls, _launches(fn, rep, calls, dests))
 
 
@@ -459,6 +513,12 @@ def _launches(fn: _Fn, rep, calls, dests):
     by_name = {f["name"]: f for f in rep["functions"]}
     out, i = [], 0
     while i < len(calls):
+        if calls[i].outs is not None:  # a typed Llama entry point
+            c = calls[i]
+            out.append(Launch("+".join(c.functions), list(c.args), c.out, [], entry=c.entry,
+                              outs=list(c.outs), params=dict(c.params)))
+            i += 1
+            continue
         j = i + 1
         while j < len(calls) and calls[j].functions == calls[i].functions:
             j += 1
@@ -655,6 +715,13 @@ class Program:
         types = self.func.types
         tdt = lambda e: getattr(torch, _TORCH_DTYPE[e])
         dev = next(iter(vals.values())).device
+        if L.entry != "npu_group_launch":
+            for v in L.outs:
+                if v not in vals:
+                    vals[v] = torch.empty(types[v].shape, dtype=tdt(types[v].elem), device=dev)
+            ins, outs = [vals[v] for v in L.ins], [vals[v] for v in L.outs]
+            getattr(groups, L.entry)(*ins, *outs, **L.params, stream=stream)
+            return
         prod = {r: op for op in self.func.ops for r in op.results}
         ins = []
         for v in L.ins:
@@ -729,7 +796,8 @@ def cost_report(program: "Program", inputs: dict, reps: int = 20, stream=None) -
         meas = a.elapsed_time(b) * 1e3 / reps
         for name in L.name.split("+"):
             r = dict(records[name])
-            r.update({"entry_point": L.name if "+" in L.name else name,
+            r.update({"entry_point": L.entry if L.entry != "npu_group_launch"
+                      else (L.name if "+" in L.name else name),
                       "mi355x_predicted_us": round(pred, 3), "measured_us": round(meas, 3)})
             out.append("COST_JSON: " + json.dumps(r))
     return out

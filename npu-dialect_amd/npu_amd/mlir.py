@@ -245,6 +245,11 @@ def parse_region(region: str):
         ty = tail.split(":", 1)[1].strip() if ":" in tail else ""
         if name == "arith.constant":
             body.append(BodyOp(res, name, [], tail.rsplit(":", 1)[0].strip(), ty))
+        elif name == "linalg.index":  # the value is the iteration dimension
+            body.append(BodyOp(res, name, [], tail.split(":", 1)[0].strip(), ty))
+        elif name in ("arith.cmpi", "arith.cmpf"):  # the value is the predicate
+            pred, _, ops = tail.split(":", 1)[0].partition(",")
+            body.append(BodyOp(res, name, re.findall(r"%[\w]+", ops), pred.strip(), ty))
         else:
             body.append(BodyOp(res, name, re.findall(r"%[\w]+", tail.split(":", 1)[0]), None, ty))
     return args, body, yielded
@@ -286,6 +291,11 @@ def parse_op(stmt: str) -> MOp:
     elif name in ("tensor.collapse_shape", "tensor.expand_shape"):
         op.operands = [re.match(r"\s*(%[\w]+)", flat).group(1)]
         op.result_types = [parse_type(flat.rsplit("into", 1)[1])]
+        ra = re.search(r"\[\s*(\[[\d,\s\[\]]*\])\s*\]", flat)
+        op.attrs["reassociation"] = [[int(d) for d in grp.split(",") if d.strip()]
+                                     for grp in re.findall(r"\[([\d,\s]*)\]", ra.group(1))] \
+            if ra else []
+        op.attrs["source_type"] = parse_type(flat.rsplit("into", 1)[0].rsplit(":", 1)[1])
     elif name == "func.call":
         m2 = re.match(r"\s*@([\w]+)\(([^)]*)\)\s*:\s*\(([^)]*)\)\s*->\s*(.*)$", flat.strip(), re.S)
         op.attrs["callee"] = m2.group(1)

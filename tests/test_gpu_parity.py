@@ -573,7 +573,7 @@ COST_KEYS = ["name", "flops", "mem_bytes", "arithmetic_intensity", "time_sec", "
              "peak_sram_bytes", "num_tile_iterations", "num_linalg_ops", "sram_budget", "bottleneck"]
 
 
-@pytest.mark.parametrize("which", ["mlp", "irb"])
+@pytest.mark.parametrize("which", ["mlp", "irb", "llama"])
 def test_cost_records_carry_prediction_and_measurement(cuda, which):
     """COST_JSON records of a lowered program: the reference's keys in its
     order (CostEvaluatePass.cpp:135-158), then the entry point, the MI355X
@@ -583,6 +583,9 @@ def test_cost_records_carry_prediction_and_measurement(cuda, which):
     if which == "mlp":
         prog = lower.lower_text(blocks.reference_workload("mlp.mlir"))
         ins = _harness_fills(prog)
+    elif which == "llama":
+        prog = lower.lower_text(blocks.llama_layer(128, 256, 4, 512))
+        ins = _llama_text_inputs(configs.llama_layer(S=128, D=256, H=4, F=512).make_inputs())
     else:
         N, H, W, C, E = 2, 9, 13, 24, 144
         prog = lower.lower_text(blocks.inverted_residual(N, H, W, C, E))
@@ -600,6 +603,30 @@ def test_cost_records_carry_prediction_and_measurement(cuda, which):
     total_measured = sum({r["entry_point"]: r["measured_us"] for r in recs}.values())
     print("measured", total_measured, "predicted",
           sum({r["entry_point"]: r["mi355x_predicted_us"] for r in recs}.values()))
+
+
+def _llama_text_inputs(inp):
+    d = configs.to_device(inp)
+    d["cos"], d["sin"] = d.pop("cos_t"), d.pop("sin_t")
+    return d
+
+
+@pytest.mark.parametrize("S,D,H,F", [(64, 128, 2, 192), (256, 512, 8, 1408)])
+def test_lowered_llama_layer_matches_the_oracle(cuda, S, D, H, F):
+    """The Llama layer's linalg text through the lowering: five calls of the
+    Llama entry points, bit-identical to calling them directly, and within
+    the bf16 bound of the oracle's layer."""
+    w = configs.llama_layer(S=S, D=D, H=H, F=F, seed=77 + S)
+    inp = w.make_inputs()
+    prog = lower.lower_text(blocks.llama_layer(S, D, H, F))
+    vals = prog.run(_llama_text_inputs(inp))
+    d = configs.to_device(inp)
+    o = w.make_outputs(d)
+    groups.llama_layer(d, o, H, LL_EPS)
+    torch.cuda.synchronize()
+    assert np.array_equal(_host(vals["%out"]), _host(o["out"]))
+    ref, mag = refs.llama_reference(inp, H, LL_EPS)["out"]
+    check_bound(bf16(_host(vals["%out"])), bf16(ref), mag, RTOL_BF16, what="lowered layer")
 
 
 @pytest.mark.parametrize("N,H,W,C", [(2, 7, 9, 64), (1, 12, 10, 256)])

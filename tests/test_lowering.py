@@ -236,3 +236,64 @@ def test_int8_residual_must_be_the_input():
     t = blocks.qbottleneck(1, 4, 4, 64, 64).replace("ins(%acc3, %m3, %s3, %x :", "ins(%acc3, %m3, %s3, %y2 :")
     with pytest.raises(NotImplementedError):
         lower.lower_text(t)
+
+
+def test_llama_layer_lowers_to_the_four_entry_points():
+    """The Llama decoder layer in linalg (RMSNorm, RoPE on interleaved pairs,
+    causal softmax attention over per-head views, residual projections,
+    SwiGLU) outlines into ten groups; the matcher follows the dataflow and
+    runs it as five calls of the four Llama entry points."""
+    p = lower.lower_text(blocks.llama_layer(64, 128, 2, 192))
+    got = [(c.entry, c.args, c.outs, c.params) for c in p.calls]
+    assert got == [
+        ("fused_llama_qkv_rope", ["%x", "%g1", "%wq", "%wk", "%wv", "%cos", "%sin"],
+         ["%Q", "%K", "%V"], {"eps": 1e-05}),
+        ("fused_llama_attention", ["%Q", "%K", "%V"], ["%A"], {"n_heads": 2, "scale": 0.125}),
+        ("fused_llama_matmul_residual", ["%A", "%wo", "%x"], ["%h"], {}),
+        ("fused_llama_rmsnorm_swiglu", ["%h", "%g2", "%wg", "%wu"], ["%act"], {"eps": 1e-05}),
+        ("fused_llama_matmul_residual", ["%act", "%wd", "%h"], ["%out"], {}),
+    ]
+    assert [L.entry for L in p.launches] == [c.entry for c in p.calls]
+    assert all(n.startswith("fused_") for c in p.calls for n in c.functions)
+
+
+def test_llama_roles_follow_the_attention_views():
+    """Which rotated projection is the query is read from the attention's
+    views (Q: [1, 0, 2], K: [1, 2, 0]), not from the order of the matmuls."""
+    t = blocks.llama_layer(64, 128, 2, 192)
+    t = t.replace("%A_q_3 = tensor.expand_shape %Q ", "%A_q_3 = tensor.expand_shape %TMP ")
+    t = t.replace("%A_k_3 = tensor.expand_shape %K ", "%A_k_3 = tensor.expand_shape %Q ")
+    t = t.replace("%A_q_3 = tensor.expand_shape %TMP ", "%A_q_3 = tensor.expand_shape %K ")
+    c = lower.lower_text(t).calls[0]
+    assert c.args[2:4] == ["%wk", "%wq"] and c.outs == ["%K", "%Q", "%V"]
+
+
+@pytest.mark.parametrize("old,new", [
+    # RMSNorm: x * (inv * g) is another rounding than (x * inv) * g
+    ("%t = arith.mulf %e, %inv : f32\n    %u = arith.mulf %t, %g : f32",
+     "%t = arith.mulf %inv, %g : f32\n    %u = arith.mulf %e, %t : f32"),
+    ("%d = arith.constant 128.0 : f32", "%d = arith.constant 64.0 : f32"),     # mean over D
+    ("%ev = arith.subf %a, %b : f32", "%ev = arith.addf %a, %b : f32"),          # rotation sign
+    ("%is0 = arith.cmpi eq, %j, %c0 : index", "%is0 = arith.cmpi ne, %j, %c0 : index"),
+    ("%gt = arith.cmpi ugt, %j, %i : index", "%gt = arith.cmpi uge, %j, %i : index"),  # diagonal
+    ("%d = arith.subf %a, %m : f32", "%d = arith.subf %m, %a : f32"),            # exp(m - s)
+    ("%m = arith.maximumf %acc, %a : f32", "%m = arith.minimumf %acc, %a : f32"),
+    ("%s = arith.divf %g, %den : f32", "%s = arith.mulf %g, %den : f32"),          # not SiLU
+    ("%s = arith.addf %e, %a : f32", "%s = arith.subf %e, %a : f32"),             # residual
+])
+def test_llama_bodies_are_checked(old, new):
+    t = blocks.llama_layer(64, 128, 2, 192)
+    assert old in t
+    with pytest.raises(NotImplementedError):
+        lower.lower_text(t.replace(old, new, 1))
+
+
+def test_llama_views_and_head_size_are_checked():
+    t = blocks.llama_layer(64, 128, 2, 192)
+    # K viewed like Q (no transpose of the key) is not Q K^T
+    bad = t.replace("permutation = [1, 2, 0]", "permutation = [1, 0, 2]", 1)
+    with pytest.raises(NotImplementedError):
+        lower.lower_text(bad)
+    # heads of 32: the attention entry point's head dimension is 64
+    with pytest.raises(NotImplementedError, match="head dimension is 64"):
+        lower.lower_text(blocks.llama_layer(64, 128, 4, 192, dh=32))
