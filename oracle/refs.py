@@ -131,6 +131,48 @@ def mag_swiglu(hn, wg, wu):
     return mg * np.abs(u) + np.abs(sg) * mu + np.abs(sg * u)
 
 
+def _rope64(m, cos_t, sin_t):
+    S, D = m.shape
+    Dh = 2 * cos_t.shape[1]
+    c = np.tile(np.asarray(cos_t, np.float64), (1, D // Dh))
+    s = np.tile(np.asarray(sin_t, np.float64), (1, D // Dh))
+    mp = m.reshape(S, D // 2, 2)
+    out = np.empty_like(mp)
+    out[..., 0] = mp[..., 0] * c - mp[..., 1] * s
+    out[..., 1] = mp[..., 0] * s + mp[..., 1] * c
+    return out.reshape(S, D)
+
+
+def llama_stage_exact(inp, st, H, eps):
+    """Each sub-group's value in float64 before its output rounding, from the
+    bf16 inputs the stage tests give the GPU (the oracle's previous stage
+    outputs; the normalised rows as the oracle forms them): the reference
+    point of the rounding-aware stage bound."""
+    x = inp["x"]
+    S, D = x.shape
+    Dh = D // H
+    xn = _f64(normed_bf16(x, inp["g1"], eps))
+    out = {"Q": _rope64(xn @ _f64(inp["wq"]), inp["cos_t"], inp["sin_t"]),
+           "K": _rope64(xn @ _f64(inp["wk"]), inp["cos_t"], inp["sin_t"]),
+           "V": xn @ _f64(inp["wv"])}
+    q, k, v = _f64(st["Q"]), _f64(st["K"]), _f64(st["V"])
+    A = np.empty((S, D))
+    mask = np.triu(np.ones((S, S), bool), 1)
+    for h in range(H):
+        sl = slice(h * Dh, (h + 1) * Dh)
+        sc = (q[:, sl] @ k[:, sl].T) * Dh ** -0.5
+        sc[mask] = -np.inf
+        p = np.exp(sc - sc.max(1, keepdims=True))
+        A[:, sl] = (p / p.sum(1, keepdims=True)) @ v[:, sl]
+    out["A"] = A
+    out["h"] = _f64(x) + _f64(st["A"]) @ _f64(inp["wo"])
+    hn = _f64(normed_bf16(st["h"], inp["g2"], eps))
+    g, u = hn @ _f64(inp["wg"]), hn @ _f64(inp["wu"])
+    out["act"] = g / (1 + np.exp(-g)) * u
+    out["out"] = _f64(st["h"]) + _f64(st["act"]) @ _f64(inp["wd"])
+    return out
+
+
 def llama_reference(inp, H, eps):
     """{name: (expected, mag)} for the layer's h and out."""
     st = llama_stages(inp, H, eps)

@@ -17,7 +17,7 @@ import oracle
 import refs
 from npu_amd import blocks, configs, groups, lower
 from npu_amd import inputs as rng
-from tolerance import RTOL_BF16, RTOL_F32, bf16, check_bf16_rounded, check_bound
+from tolerance import RTOL_BF16, RTOL_F32, bf16, check_bf16_rounded, check_bf16_stage, check_bound
 
 pytestmark = pytest.mark.gpu
 
@@ -183,13 +183,20 @@ def test_c2_nan_propagates(cuda, N, H, W, C, F):
     check_bound(got[ok], ref[ok], mag[ok], RTOL_F32, what="conv with NaN")
 
 
-@pytest.mark.parametrize("kind", ["full_mantissa", "wide_exponents", "constant"])
+@pytest.mark.parametrize("kind", ["full_mantissa", "wide_exponents", "constant",
+                                  "near_subnormal_x", "near_subnormal_w"])
 def test_c2_f32_bf16_split_parity(cuda, kind):
     """The f32 persistent conv multiplies on the bf16 pipe with each value
     split into three bf16 parts (six part products).  Values whose 24-bit
-    significands are all used, values spread over 2^-20..2^20, and constant
+    significands are all used, values spread over 2^-20..2^20, constant
     inputs (every product rounds the same way, so dropped terms add up
-    coherently) all stay within the f32 bound of the oracle."""
+    coherently), and inputs of 2^-119..2^-117 (full significands: the low
+    part lies below bf16's smallest subnormal, 2^-133) times filters of
+    2^100 all stay within the f32 bound of the oracle.
+    Documented deviation: filters of 2^-118 times normal-size values (the
+    normal-distributed filter then also holds f32 subnormals) lose the
+    low parts below 2^-133, and a few sums (105 of 114 688 here) exceed the
+    f32 bound; all stay within 2^-14 of their magnitude bound."""
     N, H, W, C, F = 64, 16, 56, 64, 64
     x = rng.uniform(15, 0, (N, H, W, C), 0.5, 1)
     w = rng.normal(15, 1, (F, 3, 3, C), 0, math.sqrt(2 / (9 * C)))
@@ -201,6 +208,15 @@ def test_c2_f32_bf16_split_parity(cuda, kind):
     elif kind == "wide_exponents":
         e = rng.randint(15, 3, (N, H, W, C), -20, 20)
         x = (x * np.exp2(e)).astype(np.float32)
+    elif kind.startswith("near_subnormal"):
+        tiny, big = np.float32(2.0 ** -118), np.float32(2.0 ** 100)
+        x = (x.view(np.uint32) | np.uint32(0x7FFF)).view(np.float32)
+        w = (w.view(np.uint32) | np.uint32(0x7FFF)).view(np.float32)
+        if kind == "near_subnormal_x":
+            x, w = (x * tiny).astype(np.float32), (w * big).astype(np.float32)
+        else:
+            x, w = (x * big).astype(np.float32), (w * tiny).astype(np.float32)
+        b = (b * np.float32(2.0 ** -18)).astype(np.float32)
     else:
         x = np.full((N, H, W, C), 1.0 + 2.0 ** -9 + 2.0 ** -17 + 2.0 ** -23, np.float32)
         w = np.full((F, 3, 3, C), -(0.75 + 2.0 ** -10 + 2.0 ** -19 + 2.0 ** -22) / 64, np.float32)
@@ -209,7 +225,8 @@ def test_c2_f32_bf16_split_parity(cuda, kind):
     torch.cuda.synchronize()
     imgs = [0, N - 1]
     ref, mag = refs.conv_bias_act(x[imgs], w, b, 1, "none")
-    check_bound(_host(out)[imgs], ref, mag, RTOL_F32, what=f"f32 conv, {kind}")
+    rtol = 2.0 ** -14 if kind == "near_subnormal_w" else RTOL_F32
+    check_bound(_host(out)[imgs], ref, mag, rtol, what=f"f32 conv, {kind}")
 
 
 def test_c2_f32_infinite_input_gives_nan(cuda):
@@ -376,7 +393,9 @@ LL_H, LL_EPS = 8, 1e-5
 def llama_case():
     w = configs.llama_layer()
     inp = w.make_inputs()
-    return w, inp, refs.llama_stages(inp, LL_H, LL_EPS)
+    st = refs.llama_stages(inp, LL_H, LL_EPS)
+    st["exact"] = refs.llama_stage_exact(inp, st, LL_H, LL_EPS)
+    return w, inp, st
 
 
 def _bf_dev(shape):
@@ -394,7 +413,7 @@ def test_c5_stage_qkv_rope(cuda, llama_case):
     xn = refs.normed_bf16(inp["x"], inp["g1"], LL_EPS)
     for name, t, wname, rope in (("Q", Q, "wq", True), ("K", K, "wk", True), ("V", V, "wv", False)):
         mag = refs.mag_qkv(xn, inp[wname], inp["cos_t"], inp["sin_t"], rope)
-        check_bound(bf16(_host(t)), bf16(st[name]), mag, RTOL_BF16, what=name)
+        check_bf16_stage(_host(t), st["exact"][name], mag, D + 2, what=name)
     # position 0 is not rotated: Q row 0 equals the plain projection's rounding
     q0 = bf16(_host(Q))[0]
     plain0 = bf16(xn)[0] @ bf16(inp["wq"])
@@ -408,7 +427,8 @@ def test_c5_stage_attention(cuda, llama_case):
     groups.fused_llama_attention(d["Q"], d["K"], d["V"], A, LL_H, 0.125)
     torch.cuda.synchronize()
     mag = refs.mag_attention(st["Q"], st["K"], st["V"], LL_H)
-    check_bound(bf16(_host(A)), bf16(st["A"]), mag, RTOL_BF16, what="attention")
+    S, D = st["A"].shape
+    check_bf16_stage(_host(A), st["exact"]["A"], mag, S + D // LL_H, what="attention")
     # causal: row 0 attends only to key 0, so it equals V's row 0 exactly
     assert np.array_equal(_host(A)[0], st["V"][0])
 
@@ -420,7 +440,7 @@ def test_c5_stage_oproj_residual(cuda, llama_case):
     groups.fused_llama_matmul_residual(d["A"], d["wo"], d["x"], h)
     torch.cuda.synchronize()
     mag = refs.mag_residual(st["A"], inp["wo"], inp["x"])
-    check_bound(bf16(_host(h)), bf16(st["h"]), mag, RTOL_BF16, what="h")
+    check_bf16_rounded(_host(h), st["exact"]["h"], mag, inp["wo"].shape[0] + 1, what="h")
 
 
 def test_c5_stage_swiglu(cuda, llama_case):
@@ -431,7 +451,7 @@ def test_c5_stage_swiglu(cuda, llama_case):
     torch.cuda.synchronize()
     hn = refs.normed_bf16(st["h"], inp["g2"], LL_EPS)
     mag = refs.mag_swiglu(hn, inp["wg"], inp["wu"])
-    check_bound(bf16(_host(act)), bf16(st["act"]), mag, RTOL_BF16, what="act")
+    check_bf16_stage(_host(act), st["exact"]["act"], mag, inp["wg"].shape[0] + 4, what="act")
 
 
 def test_c5_stage_down_residual(cuda, llama_case):
@@ -441,7 +461,7 @@ def test_c5_stage_down_residual(cuda, llama_case):
     groups.fused_llama_matmul_residual(d["act"], d["wd"], d["h"], out)
     torch.cuda.synchronize()
     mag = refs.mag_residual(st["act"], inp["wd"], st["h"])
-    check_bound(bf16(_host(out)), bf16(st["out"]), mag, RTOL_BF16, what="out")
+    check_bf16_rounded(_host(out), st["exact"]["out"], mag, inp["wd"].shape[0] + 1, what="out")
 
 
 def test_c5_layer_end_to_end(cuda, llama_case):

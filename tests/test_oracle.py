@@ -503,3 +503,42 @@ def test_bf16_rounding_bound_rejects_one_dropped_channel_of_one_tap():
     bad32, _ = refs.conv_bias_act(xf, w_bad, a["bias"], 1, "relu")
     with pytest.raises(AssertionError, match="outside the bf16 rounding bound"):
         check_bf16_rounded(rng.to_bf16_bits(bad32), ref32, mag, 9 * 64 + 1, what="planted")
+
+
+def test_llama_stage_bound_accepts_the_oracle_and_rejects_dropped_terms():
+    """The Llama stage bound the GPU tests apply: the oracle's own sub-group
+    outputs pass it against the float64 stage values, and planted mistakes
+    fail it: a 1 % gain on the down projection's and on attention's output,
+    which the 2e-2 bound lets through."""
+    import refs
+    from npu_amd import configs
+    from tolerance import check_bf16_rounded, check_bf16_stage
+    H, eps = 2, 1e-5
+    w = configs.llama_layer(S=64, D=128, H=H, F=192, seed=5)
+    inp = w.make_inputs()
+    st = refs.llama_stages(inp, H, eps)
+    ex = refs.llama_stage_exact(inp, st, H, eps)
+    xn = refs.normed_bf16(inp["x"], inp["g1"], eps)
+    hn = refs.normed_bf16(st["h"], inp["g2"], eps)
+    for name, wname, rope in (("Q", "wq", True), ("K", "wk", True), ("V", "wv", False)):
+        mag = refs.mag_qkv(xn, inp[wname], inp["cos_t"], inp["sin_t"], rope)
+        check_bf16_stage(st[name], ex[name], mag, 128 + 2, what=name)
+    check_bf16_stage(st["A"], ex["A"], refs.mag_attention(st["Q"], st["K"], st["V"], H), 64 + 64,
+                     what="A")
+    m_h = refs.mag_residual(st["A"], inp["wo"], inp["x"])
+    check_bf16_rounded(st["h"], ex["h"], m_h, 128 + 1, what="h")
+    check_bf16_stage(st["act"], ex["act"], refs.mag_swiglu(hn, inp["wg"], inp["wu"]), 128 + 4,
+                     what="act")
+    m_out = refs.mag_residual(st["act"], inp["wd"], st["h"])
+    check_bf16_rounded(st["out"], ex["out"], m_out, 192 + 1, what="out")
+    # planted: a 1 % gain on the output (inside 2e-2 mag, since mag >= |out|)
+    bad = rng.to_bf16_bits(bf16(st["out"]) * 1.01)
+    check_bound(bf16(bad), bf16(st["out"]), m_out, RTOL_BF16, what="2e-2 lets it through")
+    with pytest.raises(AssertionError, match="bf16 rounding bound"):
+        check_bf16_rounded(bad, ex["out"], m_out, 192 + 1, what="planted")
+    # planted: a 1 % gain on attention's output
+    badA = rng.to_bf16_bits(bf16(st["A"]) * 1.01)
+    m_a = refs.mag_attention(st["Q"], st["K"], st["V"], H)
+    check_bound(bf16(badA), bf16(st["A"]), m_a, RTOL_BF16, what="2e-2 lets it through")
+    with pytest.raises(AssertionError, match="bf16 stage bound"):
+        check_bf16_stage(badA, ex["A"], m_a, 128, what="planted A")
