@@ -109,7 +109,7 @@ npu_status fused_matmul_bias_act(const npu_memref *A, const npu_memref *B,
  *   bias f32 [F] (aligned may be NULL)
  *   out  [N,Ho,Wo,F] same dtype as x (bf16: fp32 accumulate, one rounding)
  * Stride 1, symmetric zero padding `pad`; Ho = H + 2*pad - KH + 1.
- * Requires C % 16 == 0 (f32) / C % 32 == 0 (bf16) and F % 16 == 0.
+ * Requires C % 4 == 0 (f32) / C % 8 == 0 (bf16).
  * f32 results are within f32 accuracy of the sequential f32 sum.  Batched
  * 3x3 launches with 32 or 64 channels and F % 64 == 0 compute the products
  * on the bf16 matrix pipe from exact three-part bf16 splits of every value;
@@ -119,6 +119,19 @@ npu_status fused_conv2d_nhwc_bias_act(const npu_memref *x, const npu_memref *w,
                                       const npu_memref *bias,
                                       const npu_memref *out, int32_t pad,
                                       int32_t act, npu_stream stream);
+
+/* The same group with a residual term in its generic:
+ * `fill -> conv_2d -> generic(conv + bias + res, act)`, the residual add of a
+ * ResNet block and of the projection conv of an inverted residual block
+ * (test/resnet_block.mlir, test/models/mobilenetv2.mlir:211-226, where the
+ * generic adds the block's input to the last convolution).
+ *   res  [N,Ho,Wo,F] same dtype as out
+ *   out  = act(conv(x, w) + bias + res), f32 sums, bf16: one rounding
+ * Same limits as fused_conv2d_nhwc_bias_act. */
+npu_status fused_conv2d_nhwc_bias_res_act(const npu_memref *x, const npu_memref *w,
+                                          const npu_memref *bias, const npu_memref *res,
+                                          const npu_memref *out, int32_t pad, int32_t act,
+                                          npu_stream stream);
 
 /* Group chain of the int8 ResNet-50 bottleneck (int8 restatement of
  * test/resnet50_block.mlir:5-105, NHWC, zero points 0), fused across both
@@ -261,8 +274,9 @@ typedef struct npu_group_attrs {
  *   fill_matmul_generic repeated k <= 4 times (test/mlp.mlir: one group of
  *     two matmul -> ReLU chains)          -> k fused_matmul_bias_act calls
  *     (cst, init1, x, w1, [b1], dest1, init2, w2, [b2], dest2, ...) -> (out)
- *   fill_linalg_conv_2d_nhwc_fhwc_generic -> fused_conv2d_nhwc_bias_act
- *     (cst, init, x, w, [bias f32 [F]], dest) -> (out)
+ *   fill_linalg_conv_2d_nhwc_fhwc_generic -> fused_conv2d_nhwc_bias_act, or
+ *     with a residual term in the generic fused_conv2d_nhwc_bias_res_act
+ *     (cst, init, x, w, [bias f32 [F]], [res [N,Ho,Wo,F]], dest) -> (out)
  *   fill_linalg_conv_2d_nhwc_fhwc_generic + the depthwise / project group(s)
  *     of an inverted residual block after its tensor.pad -> fused_irb_f32
  *     (cst, init_e, x, we[E,1,1,C], dest_e, init_d, wdw[3,3,E], dest_d,

@@ -191,15 +191,20 @@ npu_status fused_matmul_bias_act(const npu_memref *A, const npu_memref *B,
                     "fused_matmul_bias_act launch");
 }
 
-npu_status fused_conv2d_nhwc_bias_act(const npu_memref *x, const npu_memref *w,
-                                      const npu_memref *bias, const npu_memref *out,
-                                      int32_t pad, int32_t act, npu_stream stream) {
+namespace {
+
+// fused_conv2d_nhwc_bias_act and its residual variant: checks, then the LDS
+// halo kernel for 3x3 / pad 1 rows of at most 64 pixels without a residual,
+// the implicit-GEMM kernel otherwise.
+npu_status conv_entry(const npu_memref *x, const npu_memref *w, const npu_memref *bias,
+                      const npu_memref *res, const npu_memref *out, int32_t pad, int32_t act,
+                      npu_stream stream, const char *name) {
   npu::plans_reset();
   if (!x) return fail(NPU_ERR_INVALID_ARG, "x: null descriptor");
   const int32_t dt = x->dtype;
   if (dt != NPU_F32 && dt != NPU_BF16)
     return fail(NPU_ERR_UNSUPPORTED, "x: dtype %s, expected f32 or bf16", dtype_name(dt));
-  const void *px, *pw, *pbias = nullptr, *po;
+  const void *px, *pw, *pbias = nullptr, *pres = nullptr, *po;
   NPU_TRY(check_memref(x, "x", 4, dt, &px));
   NPU_TRY(check_memref(w, "w", 4, dt, &pw));
   NPU_TRY(check_memref(out, "out", 4, dt, &po));
@@ -224,22 +229,47 @@ npu_status fused_conv2d_nhwc_bias_act(const npu_memref *x, const npu_memref *w,
       return fail(NPU_ERR_INVALID_ARG, "bias: size %lld, expected F = %lld",
                   (long long)bias->sizes[0], (long long)F);
   }
-  const int64_t cstep = dt == NPU_F32 ? 16 : 32;
+  if (res) {
+    NPU_TRY(check_memref(res, "res", 4, dt, &pres));
+    for (int d = 0; d < 4; ++d)
+      if (res->sizes[d] != out->sizes[d])
+        return fail(NPU_ERR_INVALID_ARG, "res: [%lld,%lld,%lld,%lld], expected the output's shape",
+                    (long long)res->sizes[0], (long long)res->sizes[1], (long long)res->sizes[2],
+                    (long long)res->sizes[3]);
+  }
+  // a lane's operand is one 16-byte run of channels: 4 f32 or 8 bf16
+  const int64_t cstep = dt == NPU_F32 ? 4 : 8;
   if (C % cstep != 0)
     return fail(NPU_ERR_UNSUPPORTED, "C = %lld must be a multiple of %lld for %s", (long long)C,
                 (long long)cstep, dtype_name(dt));
-  if (F % 16 != 0)
-    return fail(NPU_ERR_UNSUPPORTED, "F = %lld must be a multiple of 16", (long long)F);
   npu::ConvArgs a{px, pw, static_cast<const float *>(pbias), const_cast<void *>(po),
                   (int)N, (int)H, (int)W, (int)C, (int)F, (int)KH, (int)KW, pad,
-                  (int)Ho, (int)Wo, act};
+                  (int)Ho, (int)Wo, act, pres};
   hipStream_t s = static_cast<hipStream_t>(stream);
   hipError_t e;
-  if (npu::conv3x3_rows_supported(a, dt == NPU_F32 ? 4 : 2))
+  if (!pres && npu::conv3x3_rows_supported(a, dt == NPU_F32 ? 4 : 2))
     e = dt == NPU_F32 ? npu::launch_conv3x3_f32(a, s) : npu::launch_conv3x3_bf16(a, s);
   else
     e = dt == NPU_F32 ? npu::launch_conv2d_nhwc_f32(a, s) : npu::launch_conv2d_nhwc_bf16(a, s);
-  return hip_status(e, "fused_conv2d_nhwc_bias_act launch");
+  return hip_status(e, name);
+}
+
+}  // namespace
+
+npu_status fused_conv2d_nhwc_bias_act(const npu_memref *x, const npu_memref *w,
+                                      const npu_memref *bias, const npu_memref *out,
+                                      int32_t pad, int32_t act, npu_stream stream) {
+  return conv_entry(x, w, bias, nullptr, out, pad, act, stream,
+                    "fused_conv2d_nhwc_bias_act launch");
+}
+
+npu_status fused_conv2d_nhwc_bias_res_act(const npu_memref *x, const npu_memref *w,
+                                          const npu_memref *bias, const npu_memref *res,
+                                          const npu_memref *out, int32_t pad, int32_t act,
+                                          npu_stream stream) {
+  if (!res) return fail(NPU_ERR_INVALID_ARG, "res: null descriptor");
+  return conv_entry(x, w, bias, res, out, pad, act, stream,
+                    "fused_conv2d_nhwc_bias_res_act launch");
 }
 
 npu_status fused_qbottleneck_i8(const npu_memref *x, const npu_memref *w1,

@@ -122,6 +122,7 @@ class Cursor {
  public:
   Cursor(std::vector<Arg> &args) : a_(args) {}
   size_t pos() const { return i_; }
+  size_t left() const { return a_.size() - i_; }
   bool done() const { return i_ == a_.size(); }
   const Arg *peek() const { return i_ < a_.size() ? &a_[i_] : nullptr; }
   // The fill constant: a scalar 0.0.
@@ -237,7 +238,18 @@ npu_status run_conv(Cursor &c, const npu_group_attrs &at, const npu_memref *out,
   G_TRY(c.memref(4, "conv accumulator (tensor.empty)", &init));
   G_TRY(c.memref(4, "x", &x));
   G_TRY(c.memref(4, "w", &w));
-  if (c.next_is_rank1()) G_TRY(c.memref(1, "bias", &bias));
+  // the generic's other operands, in its order: a bias (rank 1) and / or a
+  // residual (the output's shape); the destination comes last
+  const npu_memref *res = nullptr;
+  while (c.left() > 1) {
+    if (c.next_is_rank1()) {
+      if (bias) return gfail(NPU_ERR_INVALID_ARG, "in[%zu]: a second bias", c.pos());
+      G_TRY(c.memref(1, "bias", &bias));
+    } else {
+      if (res) return gfail(NPU_ERR_INVALID_ARG, "in[%zu]: a second residual", c.pos());
+      G_TRY(c.memref(4, "residual", &res));
+    }
+  }
   G_TRY(c.dest({out->sizes[0], out->sizes[1], out->sizes[2], out->sizes[3]},
                "generic destination (tensor.empty)"));
   if (!c.done())
@@ -247,8 +259,12 @@ npu_status run_conv(Cursor &c, const npu_group_attrs &at, const npu_memref *out,
                  shape_str(*init).c_str(), shape_str(*out).c_str());
   npu_memref none{};
   none.rank = 1;
-  G_TRY(typed(fused_conv2d_nhwc_bias_act(x, w, bias ? bias : &none, out, at.pad, at.act[0],
-                                         stream)));
+  if (res)
+    G_TRY(typed(fused_conv2d_nhwc_bias_res_act(x, w, bias ? bias : &none, res, out, at.pad,
+                                               at.act[0], stream)));
+  else
+    G_TRY(typed(fused_conv2d_nhwc_bias_act(x, w, bias ? bias : &none, out, at.pad, at.act[0],
+                                           stream)));
   log.take();
   return NPU_OK;
 }

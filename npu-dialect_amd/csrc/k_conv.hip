@@ -10,8 +10,11 @@
 // becomes the grid's y dimension; the pixel dimension is the grid's x.
 //
 // Workgroup tile: 64 pixels x 64 filters, 4 waves as 2 x 2, each wave
-// 32 x 32 = four 16x16 MFMA tiles.  The epilogue (bias add, act, and the
-// bf16 rounding of the bf16 variant) runs on the accumulators.
+// 32 x 32 = four 16x16 MFMA tiles.  The epilogue (bias add, residual add,
+// act, and the bf16 rounding of the bf16 variant) runs on the accumulators.
+// C need not be a multiple of an MFMA fragment's 16 (f32) or 32 (bf16)
+// channels: a lane's 16-byte run past C loads zeros.  F need not be a
+// multiple of 16 either: filters past F are zero and not stored.
 #include "kernels.hpp"
 #include "npu_device.hpp"
 #include "plans.hpp"
@@ -23,8 +26,8 @@ namespace {
 template <class MM, typename T>
 __global__ __launch_bounds__(256) void conv2d_nhwc_kernel(
     const T *__restrict__ x, const T *__restrict__ w, const float *__restrict__ bias,
-    T *__restrict__ out, int Nb, int H, int W, int C, int F, int KH, int KW, int pad,
-    int Ho, int Wo, int act) {
+    const T *__restrict__ res, T *__restrict__ out, int Nb, int H, int W, int C, int F, int KH,
+    int KW, int pad, int Ho, int Wo, int act) {
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const int r = lane & 15, q = lane >> 4;
@@ -73,11 +76,12 @@ __global__ __launch_bounds__(256) void conv2d_nhwc_kernel(
       }
       const int woff = (kh * KW + kw) * C + cl;
       for (int c0 = 0; c0 < C; c0 += MM::kPerFrag) {
+        const bool cin = c0 + cl < C;  // this lane's run lies within the C channels
         Frag16 a[2], b[2];
 #pragma unroll
-        for (int i = 0; i < 2; ++i) a[i] = aok[i] ? load16(x + aoff[i] + c0) : frag_zero();
+        for (int i = 0; i < 2; ++i) a[i] = aok[i] && cin ? load16(x + aoff[i] + c0) : frag_zero();
 #pragma unroll
-        for (int j = 0; j < 2; ++j) b[j] = fok[j] ? load16(w + fbase[j] + woff + c0) : frag_zero();
+        for (int j = 0; j < 2; ++j) b[j] = fok[j] && cin ? load16(w + fbase[j] + woff + c0) : frag_zero();
 #pragma unroll
         for (int i = 0; i < 2; ++i)
 #pragma unroll
@@ -98,11 +102,13 @@ __global__ __launch_bounds__(256) void conv2d_nhwc_kernel(
       for (int e = 0; e < 4; ++e) {
         const int p = p0 + 16 * i + 4 * q + e;
         if (p >= P) continue;
-        float v = act_apply(acc[i][j][e] + bv, act);
+        float v = acc[i][j][e] + bv;
         if constexpr (sizeof(T) == 4) {
-          out[(size_t)p * F + f] = v;
+          if (res) v += res[(size_t)p * F + f];
+          out[(size_t)p * F + f] = act_apply(v, act);
         } else {
-          out[(size_t)p * F + f] = f32_to_bf16(v);
+          if (res) v += bf16_to_f32(res[(size_t)p * F + f]);
+          out[(size_t)p * F + f] = f32_to_bf16(act_apply(v, act));
         }
       }
     }
@@ -122,12 +128,12 @@ hipError_t launch_conv(const ConvArgs &a, hipStream_t s) {
   p.tile_load_bytes = iters * 4.0 * 4 * 1024;  // per wave 2 A and 2 B fragments of 1 KB
   p.tile_store_bytes = 64.0 * 64 * sizeof(T);
   p.hbm_bytes = (double)sizeof(T) * ((double)a.N * a.H * a.W * a.C + (double)a.F * a.KH * a.KW * a.C +
-                                     (double)P * a.F) + (a.bias ? 4.0 * a.F : 0.0);
+                                     (double)P * a.F * (a.res ? 2 : 1)) + (a.bias ? 4.0 * a.F : 0.0);
   plans_add(p);
   hipLaunchKernelGGL((conv2d_nhwc_kernel<MM, T>), grid, dim3(256), 0, s,
                      static_cast<const T *>(a.x), static_cast<const T *>(a.w), a.bias,
-                     static_cast<T *>(a.out), a.N, a.H, a.W, a.C, a.F, a.KH, a.KW, a.pad,
-                     a.Ho, a.Wo, a.act);
+                     static_cast<const T *>(a.res), static_cast<T *>(a.out), a.N, a.H, a.W, a.C,
+                     a.F, a.KH, a.KW, a.pad, a.Ho, a.Wo, a.act);
   return hipGetLastError();
 }
 

@@ -20,6 +20,7 @@ struct ConvArgs {
   const float *bias;   // may be null
   void *out;
   int N, H, W, C, F, KH, KW, pad, Ho, Wo, act;
+  const void *res = nullptr;  // residual [N,Ho,Wo,F], the output's type (may be null)
 };
 hipError_t launch_conv2d_nhwc_f32(const ConvArgs &a, hipStream_t s);
 hipError_t launch_conv2d_nhwc_bf16(const ConvArgs &a, hipStream_t s);

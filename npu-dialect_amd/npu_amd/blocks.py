@@ -423,3 +423,53 @@ def llama_layer(S, D, H, F, eps=1e-05, dh=None):
                "%t = arith.truncf %m : f32 to bf16"], "%t")
     t += _mm("%da", "%act", "%wd", S, F, D) + _residual("%out", "%h", "%da", S, D)
     return t + f"  return %out : {_t([S, D], 'bf16')}\n}}\n"
+
+
+def _nchw_conv(res, x, w, xs, ws, os_, elem):
+    return (f"  {res}_i = tensor.empty() : {_t(os_, elem)}\n"
+            f"  {res}_f = linalg.fill ins(%cst : {elem}) outs({res}_i : {_t(os_, elem)}) -> "
+            f"{_t(os_, elem)}\n"
+            f"  {res} = linalg.conv_2d_nchw_fchw {{dilations = dense<1> : tensor<2xi64>, "
+            f"strides = dense<1> : tensor<2xi64>}}\n"
+            f"    ins({x}, {w} : {_t(xs, elem)}, {_t(ws, elem)}) outs({res}_f : {_t(os_, elem)}) "
+            f"-> {_t(os_, elem)}\n")
+
+
+def _nchw_eltwise(res, ins, shape, elem, body, yielded):
+    ids = ", ".join(f"d{i}" for i in range(4))
+    full = f"affine_map<({ids}) -> ({ids})>"
+    args = ", ".join([f"%a{i}: {elem}" for i in range(len(ins))] + [f"%out: {elem}"])
+    its = ", ".join(['"parallel"'] * 4)
+    return (f"  {res}_e = tensor.empty() : {_t(shape, elem)}\n"
+            f"  {res} = linalg.generic {{indexing_maps = [{', '.join([full] * (len(ins) + 1))}],\n"
+            f"    iterator_types = [{its}]}} "
+            f"ins({', '.join(ins)} : {', '.join([_t(shape, elem)] * len(ins))}) "
+            f"outs({res}_e : {_t(shape, elem)}) {{\n  ^bb0({args}):\n" +
+            "".join(f"    {b}\n" for b in body) + f"    linalg.yield {yielded} : {elem}\n"
+            f"  }} -> {_t(shape, elem)}\n")
+
+
+def model_zoo_irb(N, C, E, H, W, elem="f16"):
+    """An inverted residual block of stride 1 in the form of the reference's
+    model-zoo texts (tools/gen_model_mlir.py's output, e.g.
+    test/models/mobilenetv2.mlir:166-226): NCHW, f16, the expand 1x1 conv,
+    ReLU, a zero pad of 1, a 3x3 conv written as a dense C x C conv (the
+    generator does not emit depthwise convolutions), ReLU, the project 1x1
+    conv, and a generic adding the block's input.  Written by this builder
+    with the same ops, shapes, maps and bodies."""
+    xs, es = [N, C, H, W], [N, E, H, W]
+    ps = [N, E, H + 2, W + 2]
+    t = (f"func.func @irb(%x: {_t(xs, elem)}, %w_exp: {_t([E, C, 1, 1], elem)}, "
+         f"%w_dw: {_t([E, E, 3, 3], elem)}, %w_proj: {_t([C, E, 1, 1], elem)}) -> "
+         f"{_t(xs, elem)} {{\n  %cst = arith.constant 0.0 : {elem}\n")
+    relu = [f"%z = arith.constant 0.0 : {elem}", f"%m = arith.maximumf %a0, %z : {elem}"]
+    t += _nchw_conv("%c1", "%x", "%w_exp", xs, [E, C, 1, 1], es, elem)
+    t += _nchw_eltwise("%r1", ["%c1"], es, elem, relu, "%m")
+    t += (f"  %p = tensor.pad %r1 low[0, 0, 1, 1] high[0, 0, 1, 1] {{\n"
+          f"  ^bb0(%i0: index, %i1: index, %i2: index, %i3: index):\n"
+          f"    tensor.yield %cst : {elem}\n  }} : {_t(es, elem)} to {_t(ps, elem)}\n")
+    t += _nchw_conv("%c2", "%p", "%w_dw", ps, [E, E, 3, 3], es, elem)
+    t += _nchw_eltwise("%r2", ["%c2"], es, elem, relu, "%m")
+    t += _nchw_conv("%c3", "%r2", "%w_proj", es, [C, E, 1, 1], xs, elem)
+    t += _nchw_eltwise("%y", ["%c3", "%x"], xs, elem, [f"%s = arith.addf %a0, %a1 : {elem}"], "%s")
+    return t + f"  return %y : {_t(xs, elem)}\n}}\n"

@@ -16,7 +16,8 @@ that runs those calls on the GPU.  Matched:
   per chain, in order;
 * {fill, conv_2d_nhwc_fhwc, generic...}, its input optionally a tensor.pad of
   zeros symmetric in H and W -> fused_conv2d_nhwc_bias_act (f32 / bf16), the pad
-  folded into the call;
+  folded into the call; with a residual term in the generic (a ResNet block's
+  add) -> fused_conv2d_nhwc_bias_res_act;
 * the inverted residual chain: {fill, 1x1 conv, ReLU6 generic} -> tensor.pad ->
   depthwise 3x3 -> ReLU6 generic -> 1x1 conv -> generic adding the chain's
   input (one group after the pad, or two: the fusion decision depends on the
@@ -479,16 +480,20 @@ def lower(func: mlir.MFunc, target=None) -> "Program":
                 covered.update(r for f2 in chain.functions for o in groups[f2] for r in o.results)
                 covered.update(fn.op(chain.params["padded"]).results)
                 continue
-            if res is not None:
-                raise NotImplementedError(f"{name}: residual add after a convolution")
             e = _elem(fn, x, ("f32", "bf16"), name)
             params = {"pad": pad, "act": act}
             if bias is not None and fn.ty(bias).elem != "f32":
                 if fn.ty(bias).elem != e:
                     raise NotImplementedError(f"{name}: bias type {fn.ty(bias).elem}")
                 params["bias_to_f32"] = True  # exact widening; the group adds in f32
-            calls.append(Call("fused_conv2d_nhwc_bias_act", [name], [x, a.ins[1], bias], out,
-                              params))
+            if res is not None:
+                if fn.ty(res).elem != e:
+                    raise NotImplementedError(f"{name}: residual type {fn.ty(res).elem}")
+                calls.append(Call("fused_conv2d_nhwc_bias_res_act", [name],
+                                  [x, a.ins[1], bias, res], out, params))
+            else:
+                calls.append(Call("fused_conv2d_nhwc_bias_act", [name], [x, a.ins[1], bias], out,
+                                  params))
             if pad:
                 covered.add(a.ins[0])
         covered.update(r for o in ops for r in o.results)
@@ -539,7 +544,7 @@ def _launches(fn: _Fn, rep, calls, dests):
         L = Launch("+".join(names), ins, cs[-1].out,
                    [c.params.get("act", "none") for c in cs])
         c0 = cs[0]
-        if c0.entry == "fused_conv2d_nhwc_bias_act" and c0.params.get("pad"):
+        if c0.entry.startswith("fused_conv2d_nhwc_bias") and c0.params.get("pad"):
             conv_in = [v for v in ins if fn.op(v) is not None and fn.op(v).name == "tensor.pad"]
             L.pad, L.padded, L.pad_source = c0.params["pad"], conv_in[0], c0.args[0]
         if c0.params.get("bias_to_f32"):

@@ -95,11 +95,15 @@ def test_conv_rejects_bad_descriptors():
     assert call(x, w, b, _mr([1, 7, 8, 16])) == 1 and "out" in _err()
     assert call(x, _mr([16, 3, 3, 8]), b, o) == 1 and "channels" in _err()
     assert call(_mr([1, 8, 8, 16], I8), w, b, o) == 2 and "f32 or bf16" in _err()
-    assert call(_mr([1, 8, 8, 24]), _mr([16, 3, 3, 24]), b, o) == 2 and "multiple of 16" in _err()
-    assert call(x, _mr([8, 3, 3, 16]), _mr([8]), _mr([1, 8, 8, 8])) == 2 and "F = 8" in _err()
+    assert call(_mr([1, 8, 8, 22]), _mr([16, 3, 3, 22]), b, o) == 2 and "multiple of 4" in _err()
     assert call(x, w, b, o, pad=-1) == 1 and "negative" in _err()
-    xb = _mr([1, 8, 8, 16], BF16)
-    assert call(xb, _mr([16, 3, 3, 16], BF16), b, _mr([1, 8, 8, 16], BF16)) == 2 and "32" in _err()
+    xb = _mr([1, 8, 8, 12], BF16)
+    assert call(xb, _mr([16, 3, 3, 12], BF16), b, _mr([1, 8, 8, 16], BF16)) == 2 and "8" in _err()
+    # the residual variant checks the residual against the output
+    res = lambda r_: lib.fused_conv2d_nhwc_bias_res_act(
+        C.byref(x), C.byref(w), C.byref(b), C.byref(r_), C.byref(o), 1, 1, None)
+    assert res(_mr([1, 8, 7, 16])) == 1 and "res" in _err()
+    assert res(_mr([1, 8, 8, 16], BF16)) == 1 and "res" in _err()
 
 
 def test_python_mirror_raises_with_library_message():

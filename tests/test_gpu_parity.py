@@ -15,7 +15,7 @@ import torch
 
 import oracle
 import refs
-from npu_amd import blocks, configs, groups, lower
+from npu_amd import blocks, configs, frontend, groups, lower, mlir
 from npu_amd import inputs as rng
 from tolerance import RTOL_BF16, RTOL_F32, bf16, check_bf16_rounded, check_bf16_stage, check_bound
 
@@ -664,3 +664,111 @@ def test_lowered_int8_bottleneck_is_bit_exact(cuda, N, H, W, C):
     torch.cuda.synchronize()
     ref = refs.qbottleneck(a)
     assert np.array_equal(_host(out), ref)
+
+
+# ------------------------------------------------------------------ frontends
+def _f64_nchw(t):
+    return t.double().permute(0, 3, 1, 2)
+
+
+@pytest.mark.parametrize("which", ["basic_block", "inverted_residual", "mlp"])
+def test_torch_frontend_runs_on_the_gpu(cuda, which):
+    """A torch module traced to NHWC linalg (npu_amd.frontend), lowered and run
+    on the GPU, against the module itself in float64 on the CPU.  The bound
+    is 1e-5 of the chain's magnitude per contraction stage (each stage's f32
+    error scales with its own magnitude and passes through the later stages'
+    linear maps, which the magnitude recursion bounds)."""
+    import torch.nn.functional as Fn
+    from test_frontend import MLP, BasicBlock, InvertedResidual, randomize_bn
+    torch.manual_seed(7)
+    if which == "basic_block":
+        m, x = randomize_bn(BasicBlock(64)), torch.rand(4, 64, 14, 14)
+    elif which == "inverted_residual":
+        m, x = InvertedResidual(24, 144), torch.rand(2, 24, 28, 28)
+    else:
+        m, x = MLP(256, 512, 128), torch.rand(64, 256) - 0.5
+    import copy
+    text, params = frontend.from_torch(m, x)
+    prog = lower.lower_text(text)
+    (out,) = prog.run({k: v.cuda() for k, v in params.items()}).values()
+    torch.cuda.synchronize()
+    got = out.double().cpu()
+    p = {k: v.double() for k, v in params.items()}
+    with torch.no_grad():
+        ref = copy.deepcopy(m).double()(x.double())
+    if which == "basic_block":
+        ref = ref.permute(0, 2, 3, 1)
+        a = lambda t: t.abs()
+        m1 = Fn.conv2d(_f64_nchw(a(p["x0"])), a(p["w1"]).permute(0, 3, 1, 2), a(p["b2"]), padding=1)
+        mag = Fn.conv2d(m1, a(p["w3"]).permute(0, 3, 1, 2), a(p["b4"]), padding=1) + _f64_nchw(a(p["x0"]))
+        mag, stages = mag.permute(0, 2, 3, 1), 2
+    elif which == "inverted_residual":
+        ref = ref.permute(0, 2, 3, 1)
+        xa = _f64_nchw(p["x0"].abs())
+        me = Fn.conv2d(xa, p["w1"].abs().permute(0, 3, 1, 2))
+        md = Fn.conv2d(me, p["w2"].abs().permute(2, 0, 1).unsqueeze(1), padding=1, groups=144)
+        mag = (Fn.conv2d(md, p["w3"].abs().permute(0, 3, 1, 2)) + xa).permute(0, 2, 3, 1)
+        stages = 3
+    else:
+        m1 = p["x0"].abs() @ p["w1"].abs() + p["b2"].abs()
+        mag, stages = m1 @ p["w3"].abs() + p["b4"].abs(), 2
+    check_bound(got.numpy(), ref.numpy(), mag.numpy(), stages * RTOL_F32, what=which)
+
+
+def test_model_zoo_block_runs_on_the_gpu(cuda):
+    """An inverted residual block in the reference's model-zoo form (NCHW, f16
+    text: test/models/mobilenetv2.mlir:166-226, written by
+    blocks.model_zoo_irb), run the way the reference's harness runs its texts
+    (f16 -> f32) after the NCHW -> NHWC rewrite, against torch's float64 NCHW
+    convolutions of the same data."""
+    import torch.nn.functional as Fn
+    N, C, E, H, W = 2, 24, 144, 56, 56
+    f = mlir.parse_functions(lower.harness_f32(blocks.model_zoo_irb(N, C, E, H, W)))[0]
+    prog = lower.lower(frontend.nchw_to_nhwc(f))
+    g = torch.Generator().manual_seed(11)
+    x = torch.rand(N, C, H, W, generator=g)
+    we = torch.randn(E, C, 1, 1, generator=g) * (2 / C) ** 0.5
+    wd = torch.randn(E, E, 3, 3, generator=g) * (2 / (9 * E)) ** 0.5
+    wp = torch.randn(C, E, 1, 1, generator=g) * (2 / E) ** 0.5
+    nhwc = lambda t: t.permute(0, 2, 3, 1).contiguous().cuda()
+    (out,) = prog.run({"x": nhwc(x), "w_exp": nhwc(we), "w_dw": nhwc(wd),
+                       "w_proj": nhwc(wp)}).values()
+    torch.cuda.synchronize()
+    xd, ed, dd, pd = x.double(), we.double(), wd.double(), wp.double()
+    r1 = Fn.relu(Fn.conv2d(xd, ed))
+    r2 = Fn.relu(Fn.conv2d(r1, dd, padding=1))
+    ref = (Fn.conv2d(r2, pd) + xd).permute(0, 2, 3, 1)
+    m1 = Fn.conv2d(xd.abs(), ed.abs())
+    m2 = Fn.conv2d(m1, dd.abs(), padding=1)
+    mag = (Fn.conv2d(m2, pd.abs()) + xd.abs()).permute(0, 2, 3, 1)
+    check_bound(out.double().cpu().numpy(), ref.numpy(), mag.numpy(), 3 * RTOL_F32,
+                what="model-zoo inverted residual block")
+
+
+@pytest.mark.parametrize("N,H,W,C,F,dtype", [(2, 9, 13, 24, 40, "f32"), (1, 7, 7, 48, 24, "bf16")])
+def test_conv_residual_and_odd_channels(cuda, N, H, W, C, F, dtype):
+    """fused_conv2d_nhwc_bias_res_act with channel counts that are not a
+    multiple of an MFMA fragment (C = 24, 48; F = 40, 24), against the
+    oracle's conv plus the residual."""
+    x = rng.uniform(41, 0, (N, H, W, C), 0, 1)
+    w = rng.normal(41, 1, (F, 3, 3, C), 0, math.sqrt(2 / (9 * C)))
+    b = rng.uniform(41, 2, (F,), -0.1, 0.1)
+    r = rng.uniform(41, 3, (N, H, W, F), -1, 1)
+    ref, mag = refs.conv_bias_act(x, w, b, 1, "none")
+    want = np.maximum(ref.astype(np.float64) + r, 0.0)
+    mag = mag + np.abs(r)
+    if dtype == "bf16":
+        xb, wb, rb = rng.to_bf16_bits(x), rng.to_bf16_bits(w), rng.to_bf16_bits(r)
+        ref32, mag = refs.conv_bias_act(bf16(xb).astype(np.float32), bf16(wb).astype(np.float32), b, 1,
+                                        "none")
+        want = np.maximum(ref32.astype(np.float64) + bf16(rb), 0.0)
+        mag = mag + np.abs(bf16(rb))
+        out = torch.empty(N, H, W, F, device="cuda", dtype=torch.bfloat16)
+        groups.fused_conv2d_nhwc_bias_res_act(_dev(xb), _dev(wb), _dev(b), _dev(rb), out, 1, "relu")
+        torch.cuda.synchronize()
+        check_bf16_rounded(_host(out), want, mag, 9 * C + 2, what="bf16 conv + residual")
+    else:
+        out = torch.empty(N, H, W, F, device="cuda", dtype=torch.float32)
+        groups.fused_conv2d_nhwc_bias_res_act(_dev(x), _dev(w), _dev(b), _dev(r), out, 1, "relu")
+        torch.cuda.synchronize()
+        check_bound(_host(out), want, mag, RTOL_F32, what="f32 conv + residual")
