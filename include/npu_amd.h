@@ -274,9 +274,14 @@ typedef struct npu_group_attrs {
  *   fill_matmul_generic repeated k <= 4 times (test/mlp.mlir: one group of
  *     two matmul -> ReLU chains)          -> k fused_matmul_bias_act calls
  *     (cst, init1, x, w1, [b1], dest1, init2, w2, [b2], dest2, ...) -> (out)
- *   fill_linalg_conv_2d_nhwc_fhwc_generic -> fused_conv2d_nhwc_bias_act, or
- *     with a residual term in the generic fused_conv2d_nhwc_bias_res_act
- *     (cst, init, x, w, [bias f32 [F]], [res [N,Ho,Wo,F]], dest) -> (out)
+ *   fill_linalg_conv_2d_nhwc_fhwc_generic[_generic...] (the epilogue in one
+ *     or several generics: an add of the block input, then a ReLU)
+ *                                         -> fused_conv2d_nhwc_bias_act, or
+ *     with a residual term fused_conv2d_nhwc_bias_res_act
+ *     (cst, init, x, w, then each generic's operands -- [bias f32 [F]],
+ *      [res [N,Ho,Wo,F]] -- and its destination) -> (out); with several
+ *     generics, the destinations before the last are passed without data
+ *     (NULL), which tells them from the residual
  *   fill_linalg_conv_2d_nhwc_fhwc_generic + the depthwise / project group(s)
  *     of an inverted residual block after its tensor.pad -> fused_irb_f32
  *     (cst, init_e, x, we[E,1,1,C], dest_e, init_d, wdw[3,3,E], dest_d,

@@ -231,29 +231,57 @@ npu_status run_matmuls(Cursor &c, const npu_group_attrs &at, int chains, const n
   return NPU_OK;
 }
 
+// A conv group: fill, conv, then n_generic generics holding the epilogue
+// (bias, residual, activation; an add and a ReLU may be two generics).  After
+// (cst, init, x, w) come each generic's other operands and its destination,
+// in first-use order.  A bias has rank 1; the residual and the destinations
+// have the output's shape, the last destination last.  With one generic the
+// residual is the rank-4 argument before the destination; with several, the
+// destinations before the last must be passed without data (NULL), as
+// tensor.empty values are, and the one rank-4 argument with data among them
+// is the residual.
 npu_status run_conv(Cursor &c, const npu_group_attrs &at, const npu_memref *out,
-                    npu_stream stream, PlanLog &log) {
+                    npu_stream stream, PlanLog &log, int n_generic) {
   G_TRY(c.fill_value());
   const npu_memref *init, *x, *w, *bias = nullptr;
   G_TRY(c.memref(4, "conv accumulator (tensor.empty)", &init));
   G_TRY(c.memref(4, "x", &x));
   G_TRY(c.memref(4, "w", &w));
-  // the generic's other operands, in its order: a bias (rank 1) and / or a
-  // residual (the output's shape); the destination comes last
-  const npu_memref *res = nullptr;
-  while (c.left() > 1) {
+  std::vector<const npu_memref *> r4;
+  while (!c.done()) {
     if (c.next_is_rank1()) {
       if (bias) return gfail(NPU_ERR_INVALID_ARG, "in[%zu]: a second bias", c.pos());
       G_TRY(c.memref(1, "bias", &bias));
     } else {
-      if (res) return gfail(NPU_ERR_INVALID_ARG, "in[%zu]: a second residual", c.pos());
-      G_TRY(c.memref(4, "residual", &res));
+      const npu_memref *m;
+      G_TRY(c.memref(4, "residual or generic destination", &m));
+      r4.push_back(m);
     }
   }
-  G_TRY(c.dest({out->sizes[0], out->sizes[1], out->sizes[2], out->sizes[3]},
-               "generic destination (tensor.empty)"));
-  if (!c.done())
-    return gfail(NPU_ERR_INVALID_ARG, "%zu arguments left over after the group's inputs", c.pos());
+  const size_t nd = (size_t)n_generic;
+  if (r4.size() != nd && r4.size() != nd + 1)
+    return gfail(NPU_ERR_INVALID_ARG, "%zu rank-4 arguments after the filter: expected %zu "
+                 "destinations and at most one residual", r4.size(), nd);
+  const npu_memref *res = nullptr;
+  if (r4.size() == nd + 1) {
+    if (nd == 1) {
+      res = r4[0];
+    } else {
+      for (size_t i = 0; i + 1 < r4.size(); ++i)
+        if (r4[i]->aligned) {
+          if (res)
+            return gfail(NPU_ERR_INVALID_ARG, "cannot tell the residual from the generics' "
+                         "destinations: pass the destinations before the last without data");
+          res = r4[i];
+        }
+      if (!res)
+        return gfail(NPU_ERR_INVALID_ARG, "the residual argument has no data");
+    }
+  }
+  for (const npu_memref *d : r4)
+    if (d != res && !same_shape(*d, {out->sizes[0], out->sizes[1], out->sizes[2], out->sizes[3]}))
+      return gfail(NPU_ERR_INVALID_ARG, "generic destination %s does not match the result %s",
+                   shape_str(*d).c_str(), shape_str(*out).c_str());
   if (!same_shape(*init, {out->sizes[0], out->sizes[1], out->sizes[2], out->sizes[3]}))
     return gfail(NPU_ERR_INVALID_ARG, "conv accumulator %s does not match the result %s",
                  shape_str(*init).c_str(), shape_str(*out).c_str());
@@ -398,7 +426,16 @@ extern "C" npu_status npu_group_launch(const char *outlined_name, const npu_grou
                      NPU_GROUP_MAX_CHAINS);
       return run_matmuls(c, *attrs, k, &res.m, stream, log);
     }
-    if (key == kConv) return run_conv(c, *attrs, &res.m, stream, log);
+    // a conv followed by one or more generics
+    if (key.rfind(kConv, 0) == 0) {
+      int ng = 1;
+      size_t at = std::strlen(kConv);
+      while (key.compare(at, 8, "_generic") == 0 && key.size() >= at + 8) {
+        ++ng;
+        at += 8;
+      }
+      if (at == key.size()) return run_conv(c, *attrs, &res.m, stream, log, ng);
+    }
     if (key == kIrb) return run_irb(c, &res.m, stream, log);
     if (key == kQBottleneck) return run_qbottleneck(c, &res.m, stream, log);
     return gfail(NPU_ERR_UNSUPPORTED, "no MI355X group runs the outlined chain '%s'", key.c_str());

@@ -449,27 +449,40 @@ def _nchw_eltwise(res, ins, shape, elem, body, yielded):
             f"  }} -> {_t(shape, elem)}\n")
 
 
-def model_zoo_irb(N, C, E, H, W, elem="f16"):
-    """An inverted residual block of stride 1 in the form of the reference's
-    model-zoo texts (tools/gen_model_mlir.py's output, e.g.
-    test/models/mobilenetv2.mlir:166-226): NCHW, f16, the expand 1x1 conv,
-    ReLU, a zero pad of 1, a 3x3 conv written as a dense C x C conv (the
-    generator does not emit depthwise convolutions), ReLU, the project 1x1
-    conv, and a generic adding the block's input.  Written by this builder
-    with the same ops, shapes, maps and bodies."""
-    xs, es = [N, C, H, W], [N, E, H, W]
-    ps = [N, E, H + 2, W + 2]
-    t = (f"func.func @irb(%x: {_t(xs, elem)}, %w_exp: {_t([E, C, 1, 1], elem)}, "
-         f"%w_dw: {_t([E, E, 3, 3], elem)}, %w_proj: {_t([C, E, 1, 1], elem)}) -> "
+def model_zoo_bottleneck(N, C, M, H, W, final_relu, elem="f16", name="bottleneck"):
+    """A stride-1 residual block in the form of the reference's model-zoo
+    texts (tools/gen_model_mlir.py's output): NCHW, f16, a 1x1 conv C -> M,
+    ReLU, a zero pad of 1, a 3x3 conv M -> M written as a dense conv (the
+    generator emits no depthwise convolutions), ReLU, a 1x1 conv M -> C, a
+    generic adding the block's input and, for a ResNet bottleneck, a ReLU
+    generic after it.  test/models/resnet50.mlir:194-267 (C = 256, M = 64,
+    final ReLU) and test/models/mobilenetv2.mlir:166-226 (the inverted
+    residual block: C = 24, M = 144, none) have this form; this builder
+    writes it with the same ops, shapes, maps and bodies."""
+    xs, es = [N, C, H, W], [N, M, H, W]
+    ps = [N, M, H + 2, W + 2]
+    t = (f"func.func @{name}(%x: {_t(xs, elem)}, %w1: {_t([M, C, 1, 1], elem)}, "
+         f"%w2: {_t([M, M, 3, 3], elem)}, %w3: {_t([C, M, 1, 1], elem)}) -> "
          f"{_t(xs, elem)} {{\n  %cst = arith.constant 0.0 : {elem}\n")
     relu = [f"%z = arith.constant 0.0 : {elem}", f"%m = arith.maximumf %a0, %z : {elem}"]
-    t += _nchw_conv("%c1", "%x", "%w_exp", xs, [E, C, 1, 1], es, elem)
+    t += _nchw_conv("%c1", "%x", "%w1", xs, [M, C, 1, 1], es, elem)
     t += _nchw_eltwise("%r1", ["%c1"], es, elem, relu, "%m")
     t += (f"  %p = tensor.pad %r1 low[0, 0, 1, 1] high[0, 0, 1, 1] {{\n"
           f"  ^bb0(%i0: index, %i1: index, %i2: index, %i3: index):\n"
           f"    tensor.yield %cst : {elem}\n  }} : {_t(es, elem)} to {_t(ps, elem)}\n")
-    t += _nchw_conv("%c2", "%p", "%w_dw", ps, [E, E, 3, 3], es, elem)
+    t += _nchw_conv("%c2", "%p", "%w2", ps, [M, M, 3, 3], es, elem)
     t += _nchw_eltwise("%r2", ["%c2"], es, elem, relu, "%m")
-    t += _nchw_conv("%c3", "%r2", "%w_proj", es, [C, E, 1, 1], xs, elem)
-    t += _nchw_eltwise("%y", ["%c3", "%x"], xs, elem, [f"%s = arith.addf %a0, %a1 : {elem}"], "%s")
-    return t + f"  return %y : {_t(xs, elem)}\n}}\n"
+    t += _nchw_conv("%c3", "%r2", "%w3", es, [C, M, 1, 1], xs, elem)
+    t += _nchw_eltwise("%s", ["%c3", "%x"], xs, elem, [f"%s = arith.addf %a0, %a1 : {elem}"], "%s")
+    y = "%s"
+    if final_relu:
+        t += _nchw_eltwise("%y", ["%s"], xs, elem, relu, "%m")
+        y = "%y"
+    return t + f"  return {y} : {_t(xs, elem)}\n}}\n"
+
+
+def model_zoo_irb(N, C, E, H, W, elem="f16"):
+    """The inverted residual block of stride 1 in the model-zoo form
+    (test/models/mobilenetv2.mlir:166-226): model_zoo_bottleneck with the
+    expansion E as the middle width and no ReLU after the add."""
+    return model_zoo_bottleneck(N, C, E, H, W, False, elem, name="irb")

@@ -102,32 +102,42 @@ def test_torch_frontend_refuses_what_no_entry_point_runs(module, why):
         frontend.from_torch(module, torch.rand(1, 16, 8, 8))
 
 
-def test_model_zoo_block_builder_is_the_reference_block():
-    """blocks.model_zoo_irb writes the form of test/models/mobilenetv2.mlir's
-    inverted residual block 2 (:166-226): the same ops, types, maps, bodies,
-    pads and strides, op for op."""
-    ref = mlir.parse_functions(reference_inputs.read("models/mobilenetv2.mlir"))[0]
-    blk = frontend.extract_block(ref, ["%conv28"], "%add44")
-    ours = mlir.parse_functions(blocks.model_zoo_irb(1, 24, 144, 56, 56))[0]
+def _form(fn):
+    """Op-by-op form of a function: names, types, maps, iterators, body
+    constants, pads and strides (SSA names aside)."""
+    out = []
+    for op in fn.ops:
+        d = (op.name, tuple(str(fn.types[r]) for r in op.results),
+             tuple(str(fn.types.get(v)) for v in op.ins + op.outs + op.operands))
+        if op.name == "linalg.generic":
+            d += (str(op.attrs["maps"]), tuple(op.iterators),
+                  tuple((b.name, b.value if b.name == "arith.constant" else None)
+                        for b in op.attrs["body"]))
+        if op.name == "tensor.pad":
+            d += (tuple(op.attrs["low"]), tuple(op.attrs["high"]))
+        if "conv" in op.name:
+            d += (tuple(op.attrs.get("strides", [1, 1])),)
+        out.append(d)
+    return out
 
-    def form(fn):
-        out = []
-        for op in fn.ops:
-            d = (op.name, tuple(str(fn.types[r]) for r in op.results),
-                 tuple(str(fn.types.get(v)) for v in op.ins + op.outs + op.operands))
-            if op.name == "linalg.generic":
-                d += (str(op.attrs["maps"]), tuple(op.iterators),
-                      tuple((b.name, b.value if b.name == "arith.constant" else None)
-                            for b in op.attrs["body"]))
-            if op.name == "tensor.pad":
-                d += (tuple(op.attrs["low"]), tuple(op.attrs["high"]))
-            if "conv" in op.name:
-                d += (tuple(op.attrs.get("strides", [1, 1])),)
-            out.append(d)
-        return out
 
-    assert [a for a, _ in blk.args] == ["%conv28", "%w_blk2_exp", "%w_blk2_dw", "%w_blk2_proj"]
-    assert form(ours) == form(blk)
+@pytest.mark.parametrize("model,inp,out,args,ours", [
+    ("mobilenetv2.mlir", "%conv28", "%add44",
+     ["%conv28", "%w_blk2_exp", "%w_blk2_dw", "%w_blk2_proj"],
+     lambda: blocks.model_zoo_irb(1, 24, 144, 56, 56)),
+    ("resnet50.mlir", "%relu32", "%relu50",
+     ["%relu32", "%w_s0_b1_c1", "%w_s0_b1_c2", "%w_s0_b1_c3"],
+     lambda: blocks.model_zoo_bottleneck(1, 256, 64, 56, 56, True)),
+])
+def test_model_zoo_block_builder_is_the_reference_block(model, inp, out, args, ours):
+    """blocks.model_zoo_bottleneck writes the form of the reference's
+    model-zoo blocks -- mobilenetv2.mlir's inverted residual block 2
+    (:166-226), resnet50.mlir's second stage-0 bottleneck (:194-267) -- op for
+    op: the same ops, types, maps, bodies, pads and strides."""
+    ref = mlir.parse_functions(reference_inputs.read("models/" + model))[0]
+    blk = frontend.extract_block(ref, [inp], out)
+    assert [a for a, _ in blk.args] == args
+    assert _form(mlir.parse_functions(ours())[0]) == _form(blk)
 
 
 def test_nchw_to_nhwc_permutes_shapes_maps_and_pads():
@@ -154,6 +164,15 @@ def test_nchw_to_nhwc_permutes_shapes_maps_and_pads():
     (gen,) = [op for op in h.ops if op.name == "linalg.generic"]
     assert gen.attrs["maps"] == [[0, 1, 2, 3], [3], [0, 1, 2, 3]]
     assert str(h.types["%y"]) == "tensor<1x4x5x8xf32>"
+
+
+def test_model_zoo_bottleneck_lowers_with_the_final_relu_in_the_residual_conv():
+    f = mlir.parse_functions(lower.harness_f32(blocks.model_zoo_bottleneck(2, 256, 64, 56, 56,
+                                                                           True)))[0]
+    prog = lower.lower(frontend.nchw_to_nhwc(f))
+    assert [(c.entry, c.params["act"]) for c in prog.calls] == [
+        ("fused_conv2d_nhwc_bias_act", "relu"), ("fused_conv2d_nhwc_bias_act", "relu"),
+        ("fused_conv2d_nhwc_bias_res_act", "relu")]
 
 
 def test_model_zoo_block_lowers_to_three_conv_launches():

@@ -715,34 +715,37 @@ def test_torch_frontend_runs_on_the_gpu(cuda, which):
     check_bound(got.numpy(), ref.numpy(), mag.numpy(), stages * RTOL_F32, what=which)
 
 
-def test_model_zoo_block_runs_on_the_gpu(cuda):
-    """An inverted residual block in the reference's model-zoo form (NCHW, f16
-    text: test/models/mobilenetv2.mlir:166-226, written by
-    blocks.model_zoo_irb), run the way the reference's harness runs its texts
-    (f16 -> f32) after the NCHW -> NHWC rewrite, against torch's float64 NCHW
-    convolutions of the same data."""
+@pytest.mark.parametrize("C,M,final_relu", [(24, 144, False), (256, 64, True)])
+def test_model_zoo_block_runs_on_the_gpu(cuda, C, M, final_relu):
+    """Residual blocks in the reference's model-zoo form (NCHW, f16 text:
+    test/models/mobilenetv2.mlir:166-226's inverted residual block,
+    resnet50.mlir:194-267's bottleneck; written by
+    blocks.model_zoo_bottleneck), run the way the reference's harness runs its
+    texts (f16 -> f32) after the NCHW -> NHWC rewrite, against torch's float64
+    NCHW convolutions of the same data."""
     import torch.nn.functional as Fn
-    N, C, E, H, W = 2, 24, 144, 56, 56
-    f = mlir.parse_functions(lower.harness_f32(blocks.model_zoo_irb(N, C, E, H, W)))[0]
+    N, H, W = 2, 56, 56
+    f = mlir.parse_functions(lower.harness_f32(
+        blocks.model_zoo_bottleneck(N, C, M, H, W, final_relu)))[0]
     prog = lower.lower(frontend.nchw_to_nhwc(f))
-    g = torch.Generator().manual_seed(11)
+    g = torch.Generator().manual_seed(11 + C)
     x = torch.rand(N, C, H, W, generator=g)
-    we = torch.randn(E, C, 1, 1, generator=g) * (2 / C) ** 0.5
-    wd = torch.randn(E, E, 3, 3, generator=g) * (2 / (9 * E)) ** 0.5
-    wp = torch.randn(C, E, 1, 1, generator=g) * (2 / E) ** 0.5
+    w1 = torch.randn(M, C, 1, 1, generator=g) * (2 / C) ** 0.5
+    w2 = torch.randn(M, M, 3, 3, generator=g) * (2 / (9 * M)) ** 0.5
+    w3 = torch.randn(C, M, 1, 1, generator=g) * (2 / M) ** 0.5
     nhwc = lambda t: t.permute(0, 2, 3, 1).contiguous().cuda()
-    (out,) = prog.run({"x": nhwc(x), "w_exp": nhwc(we), "w_dw": nhwc(wd),
-                       "w_proj": nhwc(wp)}).values()
+    (out,) = prog.run({"x": nhwc(x), "w1": nhwc(w1), "w2": nhwc(w2), "w3": nhwc(w3)}).values()
     torch.cuda.synchronize()
-    xd, ed, dd, pd = x.double(), we.double(), wd.double(), wp.double()
-    r1 = Fn.relu(Fn.conv2d(xd, ed))
-    r2 = Fn.relu(Fn.conv2d(r1, dd, padding=1))
-    ref = (Fn.conv2d(r2, pd) + xd).permute(0, 2, 3, 1)
-    m1 = Fn.conv2d(xd.abs(), ed.abs())
-    m2 = Fn.conv2d(m1, dd.abs(), padding=1)
-    mag = (Fn.conv2d(m2, pd.abs()) + xd.abs()).permute(0, 2, 3, 1)
+    xd, d1, d2, d3 = x.double(), w1.double(), w2.double(), w3.double()
+    r1 = Fn.relu(Fn.conv2d(xd, d1))
+    r2 = Fn.relu(Fn.conv2d(r1, d2, padding=1))
+    ref = Fn.conv2d(r2, d3) + xd
+    ref = (Fn.relu(ref) if final_relu else ref).permute(0, 2, 3, 1)
+    m1 = Fn.conv2d(xd.abs(), d1.abs())
+    m2 = Fn.conv2d(m1, d2.abs(), padding=1)
+    mag = (Fn.conv2d(m2, d3.abs()) + xd.abs()).permute(0, 2, 3, 1)
     check_bound(out.double().cpu().numpy(), ref.numpy(), mag.numpy(), 3 * RTOL_F32,
-                what="model-zoo inverted residual block")
+                what=f"model-zoo block C={C} M={M}")
 
 
 @pytest.mark.parametrize("N,H,W,C,F,dtype", [(2, 9, 13, 24, 40, "f32"), (1, 7, 7, 48, 24, "bf16")])
