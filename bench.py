@@ -27,7 +27,16 @@ Per configuration (the headline and every entry of ``blocks``):
   MI355X published peak, with the measured HBM ``traffic`` per launch
   (rocprofv3 counters, profiles/<workload>_hbm_traffic.txt);
 * ``cost_model``: the MI355X launch model's prediction from the launch plans
-  the entry points record, against ``graph_us``;
+  the entry points record, against ``graph_us``; the headline's
+  ``cost_model.holdout`` does the same on shapes outside the nine
+  configurations (configs.holdout_workloads), which no work term of the
+  model was written against;
+* ``reference_cost_model``: the reference's own cost model
+  (CostModel.cpp, restated in libnpu_host.so) on the block's linalg form
+  through the reference's pipeline, at the MI355X target
+  (npu_hw_target_mi355x): ``one_core_us`` is the sum of its outlined
+  functions' ``time_sec``, which prices the whole op on one core, and
+  ``per_core_share_us`` that divided by the target's 256 cores;
 * ``cpu_baseline``: the CPU restatement of the reference's execution path
   (the oracle: unfused scalar loop nests) on this host, one thread, on the
   full workload when that fits about 30 s (else as many images as fit,
@@ -58,6 +67,9 @@ def parse():
     ap.add_argument("--quick", action="store_true",
                     help="time only the K back-to-back launches of each configuration (for "
                          "counter and trace runs: every launch is then the workload itself)")
+    ap.add_argument("--model-check", action="store_true",
+                    help="only the launch model against graph times: the nine configurations "
+                         "and the held-out shapes, one JSON line")
     ap.add_argument("--dump-plans", default=None,
                     help="write every configuration's launch plans and graph time to this JSON file")
     return ap.parse_args()
@@ -217,6 +229,35 @@ def model_prediction(w):
                    for k, c in parts], plans
 
 
+def reference_model(w):
+    """The reference's cost model on the workload's linalg form at the MI355X
+    target, next to the measured time (see the module docstring)."""
+    from npu_amd import configs, host, mlir, pipeline
+    bits = {"f32": 32, "bf16": 16, "i8": 8}[w.dtype]
+    t = host.mi355x_target(bits)
+    rep = pipeline.run(mlir.parse_functions(configs.linalg_text(w))[0], t)
+    one = sum(f["cost"].time_sec for f in rep["functions"]) * 1e6
+    return {"target": f"npu_hw_target_mi355x({bits})", "functions": len(rep["functions"]),
+            "one_core_us": round(one, 2), "cores": t.num_cores,
+            "per_core_share_us": round(one / t.num_cores, 3)}
+
+
+def holdouts():
+    """Launch-model prediction against the graph time on shapes outside the
+    nine configurations."""
+    from npu_amd import configs
+    out = []
+    for w in configs.holdout_workloads():
+        gsec, _ = time_graph(w, 20)
+        pred, parts, _ = model_prediction(w)
+        out.append({"workload": w.name, "desc": w.desc, "graph_us": round(gsec * 1e6, 3),
+                    "model_us": round(pred, 3), "model_error": round(pred / (gsec * 1e6) - 1, 3),
+                    "model_kernels": parts, "reference_cost_model": reference_model(w)})
+        print(f"# holdout {w.name}: graph {gsec * 1e6:.2f} us, model {pred:.2f} us",
+              file=sys.stderr, flush=True)
+    return out
+
+
 def cpu_threads():
     """Threads the all-cores baseline uses: OMP_NUM_THREADS when set (the GPU
     box sets it to its CPU share), else every logical CPU visible."""
@@ -331,7 +372,7 @@ def measure(w, steps, warmup, cpu=True, quick=False):
          "roofline": rl, "median_frac": round(w.roofline(med)["frac"], 4),
          "cold_frac": round(w.roofline(cold_us)["frac"], 4),
          "model_us": round(pred, 3), "model_error": round(pred / (gsec * 1e6) - 1, 3),
-         "model_kernels": parts, "plans": plans}
+         "model_kernels": parts, "plans": plans, "reference_cost_model": reference_model(w)}
     if cpu:
         m["cpu_baseline"] = cpu_sample(w)
         m["cpu_all_cores"] = cpu_sample(w, budget_s=15.0, threaded=True)
@@ -351,6 +392,19 @@ def main():
     import npu_amd
     npu_amd.lib()  # fail loudly if the HIP library is missing
     torch.cuda.set_device(0)
+
+    if args.model_check:
+        rows = []
+        for w in configs.all_workloads():
+            gsec, _ = time_graph(w, 20)
+            pred, parts, _ = model_prediction(w)
+            rows.append({"workload": w.name, "graph_us": round(gsec * 1e6, 3),
+                         "model_us": round(pred, 3), "model_error": round(pred / (gsec * 1e6) - 1, 3),
+                         "model_kernels": parts})
+            print(f"# {w.name}: graph {gsec * 1e6:.2f} us, model {pred:.2f} us", file=sys.stderr,
+                  flush=True)
+        print(json.dumps({"configs": rows, "holdout": holdouts()}), flush=True)
+        return
 
     name = args.workload or configs.HEADLINE
     w = configs.by_name(name)
@@ -383,6 +437,7 @@ def main():
         "graph_matches_eager": head["graph_matches_eager"],
         "cost_model": {"predicted_us": head["model_us"], "measured_us": head["graph_us"],
                        "error": head["model_error"], "kernels": head["model_kernels"]},
+        "reference_cost_model": head.get("reference_cost_model"),
     }
     if "cpu_baseline" in head:
         line["cpu_baseline"] = head["cpu_baseline"]
@@ -404,6 +459,12 @@ def main():
         line["blocks"] = blocks
         errs = [abs(line["cost_model"]["error"])] + [abs(b["model_error"]) for b in blocks]
         line["cost_model"]["within_25pct"] = f"{sum(e <= 0.25 for e in errs)}/{len(errs)}"
+        if not args.quick:
+            hold = holdouts()
+            herrs = [abs(h["model_error"]) for h in hold]
+            line["cost_model"]["holdout"] = hold
+            line["cost_model"]["holdout_within_25pct"] = f"{sum(e <= 0.25 for e in herrs)}/{len(herrs)}"
+            line["cost_model"]["holdout_mean_abs_error"] = round(sum(herrs) / len(herrs), 3)
     if args.dump_plans:
         with open(args.dump_plans, "w") as f:
             json.dump(dumped, f, indent=1)

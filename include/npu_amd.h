@@ -321,14 +321,17 @@ typedef struct npu_launch_plan {
   double tile_valu;         /* vector-ALU instructions per tile besides the
                                MFMAs, summed over the workgroup's waves
                                (index arithmetic, epilogues, depthwise taps,
-                               norms, softmax, requant): the instruction budget
-                               of the code as written, counted with the
-                               SQ_INSTS_VALU counter                           */
+                               norms, softmax, requant): the kernel's loop
+                               bodies, per iteration as compiled, times the
+                               trip counts the launch's shape gives            */
   double tile_lds_bytes;    /* LDS bytes read and written per tile             */
   double tile_load_bytes;   /* global bytes loaded per tile                    */
   double tile_store_bytes;  /* global bytes stored per tile                    */
   double wg_setup_bytes;    /* global bytes a persistent workgroup loads once  */
   double hbm_bytes;         /* compulsory HBM bytes of the launch              */
+  double wg_setup_valu;     /* vector-ALU instructions a persistent workgroup
+                               runs once before its first tile (filter splits,
+                               tables), summed over its waves                  */
 } npu_launch_plan;
 
 /* Copies up to max_plans plans of the calling thread's most recent fused_*

@@ -262,7 +262,9 @@ int32_t npu_pass_cost_evaluate(const npu_graph *g, const npu_hw_target *t, const
  *   throughput = n * max(lds, mfma + valu (k waves per SIMD), xfer)
  *   rounds     = ceil(n / k) * serial       (a workgroup runs its tiles in turn)
  *   setup      = latency + k * setup bytes / burst rate  (if it has setup data:
- *                the k workgroups of a CU fetch theirs at once)
+ *                the k workgroups of a CU fetch theirs at once), then the
+ *                set-up vector instructions per SIMD, one wave at a time
+ *                (setup valu / 4 * wave_valu_clk)
  *   cu         = setup + max(throughput, rounds)
  *   time       = max(cu / clock, HBM bytes / HBM bandwidth)
  * The machine constants come from the MI355X data sheet (CUs, MFMA rates)

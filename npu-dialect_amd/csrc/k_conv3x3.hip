@@ -800,11 +800,13 @@ __global__ __launch_bounds__(512, 1) void conv3x3_x6_kernel(
     tile(g, std::integral_constant<bool, false>{});
 }
 
-// Vector-ALU instructions per wave and output row of the persistent kernel
-// (counted with SQ_INSTS_VALU less SQ_INSTS_MFMA): a fixed part (epilogue,
-// loop control) and a part per 64-byte input chunk (halo commit, fetch).
-constexpr double STREAM_VALU_ROW_FIXED = 127.6;
-constexpr double STREAM_VALU_ROW_PER_CHUNK = 0.45;
+// Vector-ALU instructions per wave of the persistent kernel, from its
+// compiled loops: per 2-row tile 151 (epilogue: bias, activation, bf16
+// packing; slot and loop control) plus 35 per 64-byte input chunk (the next
+// rows' fetch, commit and halo write addresses); 250 once (filter loads).
+constexpr double STREAM_VALU_TILE_FIXED = 151.0;
+constexpr double STREAM_VALU_TILE_PER_CHUNK = 35.0;
+constexpr double STREAM_VALU_SETUP = 250.0;
 
 template <class MM, typename T, int WMAX, int NCH, int WFIX>
 hipError_t launch_stream(const ConvArgs &a, int wgs, hipStream_t s) {
@@ -824,7 +826,8 @@ hipError_t launch_stream(const ConvArgs &a, int wgs, hipStream_t s) {
     p.load_phases = 0;  // the next tile's halo is fetched during this tile
     p.tile_macs = 4.0 * (PBW / 2.0) * 256 * 9 * a.C;
     // vector-ALU instructions per row, summed over the four waves
-    p.tile_valu = 4.0 * (STREAM_VALU_ROW_FIXED + STREAM_VALU_ROW_PER_CHUNK * NCH);
+    p.tile_valu = 4.0 * (STREAM_VALU_TILE_FIXED + STREAM_VALU_TILE_PER_CHUNK * NCH) / TR;
+    p.wg_setup_valu = 4.0 * STREAM_VALU_SETUP;
     p.tile_lds_bytes = 2.0 * (a.W + 2) * REC +                  // halo written
                        2.0 * PBW * 9 * NCH * 1024 +             // B fragments read
                        2.0 * a.W * (64 * es + 32);              // output staged and read
@@ -841,10 +844,15 @@ hipError_t launch_stream(const ConvArgs &a, int wgs, hipStream_t s) {
   return hipGetLastError();
 }
 
-// Vector-ALU instructions per wave and output row of the f32 walk on the
-// bf16 pipe (SQ_INSTS_VALU less SQ_INSTS_MFMA over the 32x56x56x64 -> 64
-// launch: 1592 per wave for 7 rows).
-constexpr double X6_VALU_ROW_WAVE = 227.4;
+// Vector-ALU instructions per wave of the f32 walk on the bf16 pipe, from
+// its compiled loops: per tile 24 per 16-byte new-row run split into three
+// parts and written (TR x LPR runs), 20 per 16-pixel block (activation,
+// store address, the partial-sum exchange), 64 for slots, read bases and
+// the prefetch; once, 24 per filter run split (9 taps x 2 runs) plus 120.
+constexpr double X6_VALU_SPLIT_RUN = 24.0;
+constexpr double X6_VALU_BLOCK = 20.0;
+constexpr double X6_VALU_TILE = 64.0;
+constexpr double X6_VALU_SETUP = 9 * 2 * 24.0 + 120.0;
 
 template <int WMAX, int NCX, int WFIX>
 hipError_t launch_x6(const ConvArgs &a, hipStream_t s) {
@@ -863,7 +871,11 @@ hipError_t launch_x6(const ConvArgs &a, hipStream_t s) {
                                   wg_per_cu(conv3x3_x6_kernel<WMAX, NCX, WFIX>, 512), nrows * grid.y, 16);
     p.load_phases = 0;  // the next tile's new rows are fetched a tile ahead
     p.tile_macs = 6.0 * 4.0 * BLOCKS_ROW * 256 * 9 * a.C;
-    p.tile_valu = 8.0 * X6_VALU_ROW_WAVE;  // eight waves
+    constexpr int LPR = ((WMAX + 2) * 8 * NCX + 511) / 512;  // 16-byte runs per lane and input row
+    constexpr int NBW = NCX == 2 ? NBT : (NBT + 1) / 2;           // blocks per wave
+    // per row, eight waves
+    p.tile_valu = 8.0 * (X6_VALU_SPLIT_RUN * TR * LPR + X6_VALU_BLOCK * NBW + X6_VALU_TILE) / TR;
+    p.wg_setup_valu = 8.0 * X6_VALU_SETUP;
     p.tile_lds_bytes = (a.W + 2.0) * RECB +                           // halo row written
                        4.0 * BLOCKS_ROW * 9 * NCX * 3 * 1024 +        // pixel parts read (four filter groups)
                        (NCX == 2 ? 2.0 * 4.0 * BLOCKS_ROW / 2 * 1024 : 0.0);  // partial sums exchanged
@@ -897,8 +909,11 @@ hipError_t launch_rows(const ConvArgs &a, hipStream_t s) {
                                   grid.x * grid.y, 8 * sizeof(T));
     p.load_phases = 1;  // later stages are fetched while the previous one computes
     p.tile_macs = 4.0 * PBW * 256 * 9 * a.C;
-    // counted per wave: 570 (f32, one chunk per stage, four stages), 554 (bf16, one stage)
-    p.tile_valu = 4.0 * (540.0 + 8.0 * nstages * PBW);
+    // Vector instructions per wave, from the compiled loops: the first
+    // stages' halo and filter staging (260 f32, 400 bf16: twice the 16-byte
+    // runs), 41 per stage, the epilogue (bias, activation, conversion and
+    // the stores of the tile's pixel blocks) 137.
+    p.tile_valu = 4.0 * ((sizeof(T) == 4 ? 260.0 : 400.0) + 41.0 * nstages + 137.0);
     p.tile_lds_bytes = (TR + 2.0) * (a.W + 2) * REC * nstages + 4.0 * PBW * 9 * NCH * 1024 * nstages;
     p.tile_load_bytes = (TR + 2.0) * (a.W + 2) * a.C * es + 4.0 * 16 * 9 * a.C * es;
     p.tile_store_bytes = (double)TR * a.W * 16 * WF * es;
@@ -919,19 +934,24 @@ hipError_t launch_persistent(const ConvArgs &a, hipStream_t s) {
   return launch_stream<MM, T, WMAX, NCH, WFIX>(a, g, s);
 }
 
-// Launch shapes.  With many row tiles (batched images) and C of two or four
-// chunks, a persistent kernel (filter fragments held in registers): for f32
-// the one on the bf16 pipe (32 or 64 channels), for bf16 the stream kernel;
-// else
-// one workgroup per tile: 2 rows x 64 filters (waves split the filters) when
-// tiles are many, 1 row x 16 filters (waves split the row) when few (batch
-// 1), so the grid still spreads over the CUs.  Rows of up to 56 pixels use
-// tiles sized for 56 (7 pixel blocks for 2 rows, none wasted); a row width
-// of exactly 56 is also compiled in, so index arithmetic folds.
+// Launch shapes.  With C of two or four chunks, F a multiple of 64 and at
+// least 48 row pairs (two 56-row images), a persistent kernel (filter
+// fragments held in registers): for f32 the one on the bf16 pipe (32 or 64
+// channels), for bf16 the stream kernel.  Its per-workgroup set-up (filters
+// loaded, for f32 split) costs about 2.5 us once, where the one-workgroup-per-
+// tile kernels refetch the filters and re-stage the halo per tile: on
+// 56x56x64 -> 64 those take 5.4 (f32) and 2.3 us (bf16) per further image,
+// the persistent kernels 1.1 and 0.3.  Else one workgroup per tile: 2 rows x
+// 64 filters (waves split the filters) when tiles are many, 1 row x 16
+// filters (waves split the row) when few, so the grid still spreads over the
+// CUs.  Rows of up to 56 pixels use tiles sized for 56 (7 pixel blocks for 2
+// rows, none wasted); a row width of exactly 56 is also compiled in, so
+// index arithmetic folds.
 template <class MM, typename T, int WMAX, int WFIX>
 hipError_t launch_w(const ConvArgs &a, hipStream_t s) {
-  const bool big = a.N * ((a.H + 1) / 2) >= 512;
-  if (big && a.F % 64 == 0) {
+  const int pairs = a.N * ((a.H + 1) / 2);
+  const bool big = pairs >= 512;
+  if (pairs >= 48 && a.F % 64 == 0) {
     if constexpr (sizeof(T) == 4) {  // f32: on the bf16 pipe
       if (a.C == 32) return launch_x6<WMAX, 1, WFIX>(a, s);
       if (a.C == 64) return launch_x6<WMAX, 2, WFIX>(a, s);

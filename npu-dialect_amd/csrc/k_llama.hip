@@ -557,14 +557,7 @@ __global__ __launch_bounds__(256) void llama_attention_kernel(const uint16_t *__
 }
 
 // ---- launch plans ---------------------------------------------------------------
-// Per-tile work of a GEMM launch, from the kernel's own loops: a tile is one
-// workgroup (one per CU at these sizes).  Vector-ALU instructions per wave:
-// per B piece staged (address, masked store) 4, per A piece 4, per k step
-// the fragment reads' address math and repacking (12 per weight fragment, 2
-// per activation fragment), per output group of four the epilogue (RoPE 12,
-// residual 8, SwiGLU 4 + 2 x 14 for two SiLUs' exp and division); the
-// RMSNorm prologue 8 per element piece (square-sum, scale, pack) plus the
-// 64-lane reduction (10) per row.
+// Per-tile work of a GEMM launch, from the kernel's own loops.
 template <class Sh, class Kern>
 void plan_gemm(const char *name, Kern kern, const LlamaGemmArgs &a, int grid, int pro, int epi) {
   // A tile is one workgroup of 16 waves, planned as four 4-wave units side

@@ -89,7 +89,12 @@ hipError_t launch_matmul_bias_act_f32(const MatmulArgs &a, hipStream_t s) {
                                 wg_per_cu(matmul_bias_act_f32_kernel), grid.x * grid.y, 32);
   p.load_phases = ((nchunks + kWaves - 1) / kWaves + kBatch - 1) / kBatch;
   p.tile_macs = 16.0 * 16 * nchunks * 16;
-  p.tile_valu = kWaves * (100.0 + 173.0 * a.K / 512);          // counted: 273 per wave at K = 512
+  // Vector instructions per wave, from the compiled loops: 40 to set up and
+  // write the split-K partials; 209 per batch of kBatch K chunks (a chunk's
+  // five loads: 64-bit addresses, eight mask selects, the bounds tests; a
+  // short last batch runs the whole unrolled body); 19 per epilogue pass.
+  const int batches = ((nchunks + kWaves - 1) / kWaves + kBatch - 1) / kBatch;
+  p.tile_valu = kWaves * (40.0 + 209.0 * batches + 19.0 * ((256 + kWaves * 64 - 1) / (kWaves * 64)));
   p.tile_lds_bytes = 2.0 * kWaves * 256 * 4;                   // partials written, read
   p.tile_load_bytes = 2.0 * 16 * nchunks * 16 * 4;             // 16 rows of A, 16 columns of B
   p.tile_store_bytes = 16.0 * 16 * 4;

@@ -270,15 +270,26 @@ hipError_t launch_qb(const QBottleneckArgs &a, hipStream_t s) {
     npu_launch_plan p = make_plan("int8_bottleneck", grid, wg_per_cu(kern), ntiles, 8);
     p.load_phases = 1;  // the halo of the next tile is fetched during this one
     p.tile_macs = (double)HP * M1 * C + (double)TH * 16 * M1 * 9 * M1 + (double)TH * 16 * C * M1;
-    // per wave: 4 requant instructions per channel value (multiply-add,
-    // shift, clamp, accumulator read) + packing, over conv1's 9 halo blocks,
-    // conv2's 7 blocks and conv3's 7 blocks x C/64 filter blocks, plus the
-    // halo and store addressing
+    // per wave: 4.75 vector instructions per requantized channel value
+    // (64-bit multiply-add, shift, clamp, packing), four values per lane and
+    // block, over conv1's HH halo blocks, conv2's TH blocks and conv3's TH
+    // blocks x C/64 filter blocks; 12 per halo run committed and per output
+    // row stored (addresses)
     const double vals = 4.0 * (HH + TH + TH * C / 64);
     const int segs = (HP * C / 16 + 255) / 256;
     p.tile_valu = 4.0 * (vals * 4.75 + 12.0 * (segs + TH));
-    p.tile_lds_bytes = 4.0 * 1024 * (HH * C / 64 + TH * 9 + TH * C / 64) + HP * (double)C +
-                       2.0 * TH * 16 * C + 2.0 * TH * 16 * C;
+    // LDS: halo written; 1 KiB per wave and MFMA operand read (conv1 HH x
+    // C/64, conv2 TH x 9 taps, conv3 TH x C/64); y1 and y2 written; the
+    // residual read and overwritten; the output read for the stores; the
+    // requant parameters (64 bytes per lane and scale set: conv1, conv2 and
+    // one per conv3 filter block)
+    p.tile_lds_bytes = HP * (double)C + 4.0 * 1024 * (HH * C / 64 + TH * 9 + TH * C / 64) +
+                       (HP + TH * 16.0) * M1 + 2.0 * TH * TW * C + (double)TH * TW * C +
+                       (2.0 + C / 64) * 256 * 64;
+    // set-up: every workgroup loads the three filters (its waves' shares)
+    // and the requant tables, and fills the tables (192 per wave)
+    p.wg_setup_bytes = (double)M1 * C * 2 + 9.0 * M1 * M1 + 2.0 * 4 * (2 * M1 + C);
+    p.wg_setup_valu = 4.0 * 192.0;
     p.tile_load_bytes = HP * (double)C;
     p.tile_store_bytes = (double)TH * TW * C;
     p.hbm_bytes = 2.0 * a.N * a.H * a.W * C + (double)M1 * C * 2 + 9.0 * M1 * M1 + 4.0 * 2 * (2 * M1 + C);

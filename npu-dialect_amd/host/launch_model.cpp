@@ -62,9 +62,10 @@ bool predict_launch(const npu_launch_plan &pl, const npu_gpu_params &g, npu_laun
   const double c_serial = c_lat + c_xfer + c_mfma + c_valu_wave + c_lds;
   const double c_thru = tiles_cu * std::max(c_comp, c_xfer);
   const double c_rounds = std::ceil(tiles_cu / k) * c_serial;
-  const double setup = pl.wg_setup_bytes > 0
-                           ? g.mem_latency_us * clk_per_us + k * pl.wg_setup_bytes / g.burst_bytes_per_clk_cu
-                           : 0.0;
+  const double setup = (pl.wg_setup_bytes > 0
+                            ? g.mem_latency_us * clk_per_us + k * pl.wg_setup_bytes / g.burst_bytes_per_clk_cu
+                            : 0.0) +
+                       pl.wg_setup_valu / 4.0 * g.wave_valu_clk;
   const double cu = setup + std::max(c_thru, c_rounds);
   const double hbm_us = pl.hbm_bytes / (g.hbm_gbs * 1e3);
   out->hbm_us = hbm_us;

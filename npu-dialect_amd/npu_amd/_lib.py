@@ -54,6 +54,7 @@ class NpuLaunchPlan(C.Structure):
         ("tile_store_bytes", C.c_double),
         ("wg_setup_bytes", C.c_double),
         ("hbm_bytes", C.c_double),
+        ("wg_setup_valu", C.c_double),
     ]
 
 def strided_memref_type(rank: int):

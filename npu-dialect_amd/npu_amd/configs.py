@@ -153,9 +153,9 @@ def conv3x3_bias_relu(N=1, dtype="f32", H=56, W=56, C=64, F=64,
         groups.fused_conv2d_nhwc_bias_act(d["x"], d["w"], d["bias"], o["out"], 1, "relu", stream)
 
     P = N * H * W
-    # the f32 persistent launch (many row pairs, F a multiple of 64, 32 or
+    # the f32 persistent launch (>= 48 row pairs, F a multiple of 64, 32 or
     # 64 channels) multiplies on the bf16 pipe, six products per f32 product
-    on_bf16 = dtype == "f32" and N * ((H + 1) // 2) >= 512 and F % 64 == 0 and C in (32, 64) and W <= 64
+    on_bf16 = dtype == "f32" and N * ((H + 1) // 2) >= 48 and F % 64 == 0 and C in (32, 64) and W <= 64
     return Workload(
         name=f"conv3x3_bias_relu_{dtype}_n{N}", config=2, dtype=dtype,
         flops=2 * P * F * KH * KW * C + 2 * P * F,
@@ -346,6 +346,55 @@ def all_workloads() -> list:
         qbottleneck(32),
         llama_layer(),
     ]
+
+
+def holdout_workloads() -> list:
+    """Shapes outside the nine configurations, each run by the same entry
+    points through other launch shapes or template instances: other matmul
+    aspect ratios, the conv's one-row and two-row tile kernels at other
+    batches, the persistent conv at a 64-pixel and a 28-pixel row with 128
+    channels, the block's other channel pairs, the int8 block at 28x28x128,
+    and shorter and longer decoder layers.  The launch model's work terms are
+    written from the kernels' code, not from timings of any of these."""
+    import dataclasses
+
+    def tag(w, name):
+        return dataclasses.replace(w, name=name)
+
+    return [
+        matmul_bias_relu(M=512, K=1024, N=512),
+        matmul_bias_relu(M=128, K=2048, N=128),
+        tag(conv3x3_bias_relu(8, "f32"), "conv3x3_bias_relu_f32_n8"),
+        tag(conv3x3_bias_relu(32, "f32", H=32, W=64), "conv3x3_bias_relu_f32_n32_32x64"),
+        tag(conv3x3_bias_relu(16, "bf16"), "conv3x3_bias_relu_bf16_n16"),
+        tag(conv3x3_bias_relu(64, "bf16", H=28, W=28, C=128, F=128),
+            "conv3x3_bias_relu_bf16_n64_28x28x128"),
+        tag(irb(8), "mbv2_irb_f32_n8"),
+        tag(irb(16, H=28, W=28, C=32, E=192), "mbv2_irb_f32_n16_28x28x32x192"),
+        tag(irb(4, H=112, W=112, C=16, E=96), "mbv2_irb_f32_n4_112x112x16x96"),
+        tag(qbottleneck(8), "qbottleneck_i8_n8"),
+        tag(qbottleneck(16, H=28, W=28, C=128), "qbottleneck_i8_n16_28x28x128"),
+        llama_layer(S=256),
+        llama_layer(S=1024),
+    ]
+
+
+def linalg_text(w: Workload) -> str:
+    """The linalg form of a workload (npu_amd.blocks), the input of the
+    reference's pipeline and cost model."""
+    from . import blocks
+    m = w.meta
+    if w.config == 1:
+        return blocks.matmul_bias_act(m["M"], m["K"], m["N"])
+    if w.config == 2:
+        return blocks.conv_bias_act(m["N"], m["H"], m["W"], m["C"], m["F"], elem=w.dtype)
+    if w.config == 3:
+        return blocks.inverted_residual(m["N"], m["H"], m["W"], m["C"], m["E"])
+    if w.config == 4:
+        return blocks.qbottleneck(m["N"], m["H"], m["W"], m["C"], m["M1"])
+    if w.config == 5:
+        return blocks.llama_layer(m["S"], m["D"], m["H"], m["F"], m["eps"])
+    raise KeyError(w.name)
 
 
 HEADLINE = "conv3x3_bias_relu_f32_n32"

@@ -132,10 +132,15 @@ def test_c2_conv_config_n32(cuda, dtype):
     # pairs; an odd H leaves a half tile at the bottom of each image
     (64, 17, 9, 16, 64, 3, 1, "relu", True, "f32"),
     (64, 17, 9, 32, 80, 3, 1, "relu", True, "bf16"),
-    # the persistent kernel (>= 512 row pairs, F a multiple of 64, C two or
+    # the persistent kernel (>= 48 row pairs, F a multiple of 64, C two or
     # four 64-byte chunks) at a run-time width, an odd H, two 64-filter
-    # blocks, a 64-wide row and four bf16 chunks
+    # blocks, a 64-wide row and four bf16 chunks; and with fewer rows than
+    # workgroups (ranges of zero or one row)
     (64, 17, 9, 32, 128, 3, 1, "relu", True, "f32"),
+    (2, 56, 56, 64, 64, 3, 1, "relu", True, "f32"),
+    (3, 33, 56, 32, 64, 3, 1, "relu", True, "f32"),
+    (2, 56, 56, 64, 64, 3, 1, "relu", True, "bf16"),
+    (4, 28, 28, 128, 128, 3, 1, "relu", True, "bf16"),
     (64, 17, 30, 64, 64, 3, 1, "relu", True, "f32"),  # 64 channels at a run-time width
     (32, 32, 64, 64, 64, 3, 1, "relu", True, "f32"),
     (40, 26, 60, 64, 64, 3, 1, "relu6", False, "bf16"),
