@@ -61,6 +61,9 @@ def test_c1_matmul_bias_relu_config(cuda):
     (16, 4, 16, "none", False),      # smallest K, no bias
     (64, 4096, 32, "relu6", True),   # long K, ReLU6
     (1, 512, 256, "relu", True),     # single row
+    (20, 400, 36, "relu", True),     # K in whole chunks, a wave's last batch partial
+    (5, 64, 4, "none", True),        # N = 4: the narrowest 16-byte B rows
+    (33, 48, 3, "relu", False),      # N < 4: B read a value at a time
 ])
 def test_c1_matmul_shapes(cuda, M, K, N, act, bias):
     A = rng.uniform(11, 0, (M, K), -1, 1)
