@@ -1,0 +1,186 @@
+"""The pipeline's decisions pinned per reference workload (test/*.mlir).
+
+For each of the reference's workloads, at its default target (6 cores, 2 MiB
+SRAM per core), this pins what npu-pipeline (lib/Transforms/Pipeline.cpp:11-38,
+restated in npu_amd.pipeline) decides: the fusion groups by member, the
+outlined functions, every op's spatial split (iteration dim, tile, full
+iterations, peeled tail) and every matrix op's temporal tile and tile count.
+
+The tables are the restatement's output; what fixes them independently is
+checked beside them:
+* group membership follows the fusion rules: an anchor (a matmul or conv)
+  absorbs its elementwise consumers and the next anchor it feeds when the
+  group's tile working set fits (FusionPass.cpp:306-359), never across a
+  tensor.pad (OutlineFusedGroupsPass.cpp:140-144), at most six ops;
+* a spatial tile is ceil(extent / 6) with floor(extent / tile) full
+  iterations and the remainder peeled (SpatialTilingPass.cpp:76-166), so
+  tile * full + peel == extent;
+* the split dim of a matmul is the one whose per-core input DMA is smaller:
+  splitting M sends every core all of B, splitting N all of A
+  (evaluateSpatialSplit, CostModel.cpp:760-812) -- recomputed here in bytes;
+* a conv's split dim is the candidate with the fewest total cycles, ties
+  going to the earlier candidate (SpatialTilingPass.cpp:76-110): where the
+  per-core compute outweighs either split's DMA the candidates tie and the
+  output channels win (conv2d_relu, the resnet blocks, as in
+  test/lit/spatial_tiling_conv2d.mlir); the memory-bound 1x1 convs over a
+  112x112 map (mobilenet conv1, conv3) split rows (pinned, not recomputed);
+* a temporal tile count is the product of ceil(extent / tile) over the
+  tiled dims (TemporalTilingPass.cpp), and the tile's double-buffered working
+  set fits the SRAM.
+"""
+import math
+
+import pytest
+
+import reference_inputs
+from npu_amd import host, mlir, pipeline
+
+CORES = 6
+
+# workload -> (fusion groups, outlined functions,
+#              {op: (iter dim, tile, full iterations, peel)},
+#              {matrix op: (temporal tile sizes, tile count)})
+EXPECTED = {
+    "matmul_relu.mlir": (
+        [["%matmul", "%relu"]],
+        ["fused_fill_matmul_generic_0"],
+        {"%matmul": (1, 86, 5, 82), "%relu": (1, 86, 5, 82)},
+        {"%matmul": ([128, 256, 16], 32)},
+    ),
+    "mlp.mlir": (
+        [["%mm1", "%relu1", "%mm2", "%relu2"]],
+        ["fused_fill_matmul_generic_fill_matmul_generic_0"],
+        {"%mm1": (1, 86, 5, 82), "%relu1": (1, 86, 5, 82), "%mm2": (1, 43, 5, 41),
+         "%relu2": (1, 43, 5, 41)},
+        {"%mm1": ([128, 256, 16], 32), "%mm2": ([128, 256, 16], 32)},
+    ),
+    "conv2d_relu.mlir": (
+        [["%conv", "%relu"]],
+        ["fused_fill_conv2d_generic_0"],
+        {"%conv": (1, 11, 5, 9), "%relu": (1, 11, 5, 9)},
+        {"%conv": ([1, 64, 28, 28, 0, 0, 0], 4)},
+    ),
+    "mobilenet_block.mlir": (
+        [["%conv2", "%relu2"], ["%conv1", "%relu1"], ["%conv3", "%add"]],
+        ["fused_fill_conv2d_generic_0", "fused_fill_conv2d_generic_1",
+         "fused_fill_conv2d_generic_2"],
+        {"%conv1": (2, 19, 5, 17), "%relu1": (1, 32, 6, 0), "%conv2": (1, 32, 6, 0),
+         "%relu2": (1, 32, 6, 0), "%conv3": (2, 19, 5, 17), "%add": (2, 19, 5, 17)},
+        {"%conv1": ([1, 192, 28, 28, 0, 0, 0], 16), "%conv2": ([1, 96, 28, 16, 0, 0, 0], 56),
+         "%conv3": ([1, 32, 56, 16, 0, 0, 0], 14)},
+    ),
+    "resnet50_block.mlir": (
+        [["%conv2", "%relu2"], ["%conv1", "%relu1"], ["%conv3", "%add", "%relu3"]],
+        ["fused_fill_conv2d_generic_0", "fused_fill_conv2d_generic_1",
+         "fused_fill_conv2d_generic_generic_2"],
+        {"%conv1": (1, 11, 5, 9), "%relu1": (1, 11, 5, 9), "%conv2": (1, 11, 5, 9),
+         "%relu2": (1, 11, 5, 9), "%conv3": (1, 43, 5, 41), "%add": (1, 43, 5, 41),
+         "%relu3": (1, 43, 5, 41)},
+        {"%conv1": ([1, 64, 28, 28, 0, 0, 0], 4), "%conv2": ([1, 64, 28, 28, 0, 0, 0], 4),
+         "%conv3": ([1, 256, 28, 16, 0, 0, 0], 8)},
+    ),
+    "resnet_block.mlir": (
+        [["%conv1", "%relu1"], ["%conv2", "%add"]],
+        ["fused_fill_conv2d_generic_0", "fused_fill_conv2d_generic_1"],
+        {"%conv1": (1, 11, 5, 9), "%relu1": (1, 11, 5, 9), "%conv2": (1, 11, 5, 9),
+         "%add": (1, 11, 5, 9)},
+        {"%conv1": ([1, 64, 28, 28, 0, 0, 0], 4), "%conv2": ([1, 64, 28, 28, 0, 0, 0], 4)},
+    ),
+    "llama_attention.mlir": (
+        [["%q", "%scores", "%softmax", "%attn", "%output"]],
+        ["fused_fill_matmul_fill_matmul_fill_matmul_generic_fill_matmul_fill_matmul_0",
+         "fused_fill_matmul_1"],
+        {"%q": (0, 22, 5, 18), "%v": (0, 22, 5, 18), "%scores": (0, 22, 5, 18),
+         "%softmax": (0, 22, 5, 18), "%attn": (0, 22, 5, 18), "%output": (1, 86, 5, 82),
+         "%k": (0, 22, 5, 18)},
+        {"%q": ([128, 64, 16], 32), "%v": ([128, 64, 16], 32), "%scores": ([128, 64, 16], 8),
+         "%attn": ([128, 64, 16], 8), "%output": ([128, 128, 16], 16),
+         "%k": ([128, 64, 16], 32)},
+    ),
+}
+
+
+def _run(name):
+    func = mlir.parse_file(reference_inputs.path(name))[0]
+    return func, pipeline.run(func)
+
+
+def _decisions(rep):
+    spatial, temporal = {}, {}
+    for f in rep["functions"]:
+        for s in f["spatial"]:
+            spatial[s["op"]] = (s["iter_dim"], s["tile"], s["full_iters"], s["peel"])
+        for t in f["temporal"]:
+            if len(t["tiles"]) > 2:  # matrix ops (elementwise ops carry [tile, 0])
+                temporal[t["op"]] = (t["tiles"], t["num_tiles"])
+    return spatial, temporal
+
+
+def _op(func, result):
+    return next(o for o in func.ops if o.results and o.results[0] == result)
+
+
+def _domain(func, op):
+    """Iteration extents of a linalg op: the output dims, then the reduction
+    dims (matmul (M, N, K); NCHW conv (N, F, OH, OW, C, KH, KW))."""
+    out = op.result_types[0].shape
+    if op.name == "linalg.matmul":
+        a = func.types[op.ins[0]].shape
+        return out + [a[1]]
+    if "conv_2d" in op.name:
+        w = func.types[op.ins[1]].shape
+        return out + [w[1], w[2], w[3]]
+    return list(out)
+
+
+@pytest.mark.parametrize("name", sorted(EXPECTED))
+def test_pass_decisions_per_workload(name):
+    groups, outlined, spatial_exp, temporal_exp = EXPECTED[name]
+    func, rep = _run(name)
+    assert rep["fusion_groups"] == groups
+    assert [f["name"] for f in rep["functions"] if f["name"].startswith("fused_")] == outlined
+    spatial, temporal = _decisions(rep)
+    assert spatial == spatial_exp
+    assert temporal == temporal_exp
+
+
+@pytest.mark.parametrize("name", sorted(EXPECTED))
+def test_spatial_tiles_cover_the_split_dim(name):
+    func, rep = _run(name)
+    spatial, _ = _decisions(rep)
+    for res, (dim, tile, full, peel) in spatial.items():
+        extent = _domain(func, _op(func, res))[dim]
+        assert tile == math.ceil(extent / CORES), res
+        assert full == extent // tile and peel == extent - full * tile, res
+
+
+@pytest.mark.parametrize("name", sorted(EXPECTED))
+def test_temporal_tile_counts_and_fit(name):
+    func, rep = _run(name)
+    _, temporal = _decisions(rep)
+    for res, (tiles, count) in temporal.items():
+        dom = _domain(func, _op(func, res))
+        assert count == math.prod(math.ceil(d / t) for d, t in zip(dom, tiles) if t > 0), res
+        # the tile's inputs and output, double-buffered, fit one core's SRAM
+        # (f16: 2 bytes an element; matmul tiles are (M, N, K))
+        if len(tiles) == 3:
+            tm, tn, tk = tiles
+            assert 2 * 2 * (tm * tk + tk * tn + tm * tn) <= host.default_target().sram_per_core, res
+
+
+def _matmul_split_bytes(M, K, N, esz=2):
+    """Per-core input bytes of a 6-way split of M and of N."""
+    split_m = math.ceil(M / CORES) * K * esz + K * N * esz
+    split_n = M * K * esz + K * math.ceil(N / CORES) * esz
+    return split_m, split_n
+
+
+@pytest.mark.parametrize("name,res", [("matmul_relu.mlir", "%matmul"), ("mlp.mlir", "%mm1"),
+                                      ("mlp.mlir", "%mm2"), ("llama_attention.mlir", "%q"),
+                                      ("llama_attention.mlir", "%output")])
+def test_matmul_split_dim_is_the_cheaper_dma(name, res):
+    func, rep = _run(name)
+    spatial, _ = _decisions(rep)
+    M, N, K = _domain(func, _op(func, res))
+    split_m, split_n = _matmul_split_bytes(M, K, N)
+    assert spatial[res][0] == (0 if split_m < split_n else 1), (res, split_m, split_n)
