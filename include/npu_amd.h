@@ -200,6 +200,41 @@ npu_status fused_llama_rmsnorm_swiglu(const npu_memref *h, const npu_memref *g2,
                                       const npu_memref *act, float eps,
                                       npu_stream stream);
 
+/* ---- the reference's SRAM plan as the LDS layout --------------------------
+ * The group `fill -> matmul -> generic(bias add, act)` run as the tile loop
+ * that npu-temporal-tiling and npu-bufferize make of it (per output tile of
+ * tm x tn, a K loop of tk steps, each step a DMA of the A and B slices into
+ * SRAM and a matmul into the SRAM accumulator; then the generic into the
+ * output slice and its DMA back; BufferizePass.cpp:97-222), with every
+ * buffer at the byte offset NPUSRAMAllocationPass's dual-end plan gives it
+ * (SRAMAllocationPass.cpp:172-342: sram_offset, sram_offset_pong) in one
+ * workgroup's LDS, in the slice's own row-major f32 layout.  Each K step is
+ * one npu-barrier-alloc subgraph (DMASchedulingPass.cpp:92-147) and one
+ * s_barrier; the step uses the ping buffers when even, the pong ones when
+ * odd.  The plan is checked before the launch: every buffer inside
+ * [0, lds_bytes), lds_bytes <= 163840 (the reference simulator's bound,
+ * tools/harness/sram_simulator.py:243-256), no two buffers overlapping.
+ * This path keeps the reference's layout and schedule; fused_matmul_bias_act
+ * is the fast kernel for the same group. */
+typedef struct npu_tile_plan {
+  int32_t tm, tn, tk;      /* output tile rows, columns; K step            */
+  int32_t lds_bytes;       /* SRAM (LDS) size the plan was made for         */
+  int64_t off_a, off_a_pong; /* A slice [tm][tk]                            */
+  int64_t off_b, off_b_pong; /* B slice [tk][tn]                            */
+  int64_t off_bias;        /* bias slice [tn]; -1: the group has no bias    */
+  int64_t off_c;           /* accumulator tile [tm][tn]                     */
+  int64_t off_y;           /* output tile [tm][tn]                          */
+} npu_tile_plan;
+/* A f32 [M,K], B f32 [K,N], bias f32 [N] (aligned may be NULL), out f32
+ * [M,N] = act(A @ B + bias).  Any tile sizes with at most 64 16x16 output
+ * blocks per tile (ceil(tm/16) * ceil(tn/16) <= 64).  lds_dump (device memory of lds_bytes, may be
+ * NULL) receives output tile (0, 0)'s whole LDS at the end: the layout the
+ * launch used. */
+npu_status npu_planned_matmul_bias_act(const npu_memref *A, const npu_memref *B,
+                                       const npu_memref *bias, const npu_memref *out,
+                                       int32_t act, const npu_tile_plan *plan,
+                                       void *lds_dump, npu_stream stream);
+
 /* ---- the outlined-group boundary -----------------------------------------
  * A host module produced by the reference's pipeline calls each fused group
  * as `func.call @fused_<ops>_<idx>(external inputs...)` with the group's

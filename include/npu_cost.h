@@ -236,6 +236,14 @@ typedef struct npu_kernel_cost {
   int64_t dma_in_bytes, dma_out_bytes, matrix_cycles, dsp_cycles;
   int64_t peak_sram_bytes, num_tile_iterations, num_linalg_ops, sram_budget;
 } npu_kernel_cost;
+/* npu-barrier-alloc (DMASchedulingPass.cpp:92-147): kinds[i] is op i's
+ * scheduling class in program order (0 DMA into SRAM, 1 compute, 2 DMA out of
+ * SRAM, 3 ignored); subgraph, barrier_id and generation (i % pool, i / pool
+ * of its subgraph) are written per op, -1 for ignored ops.  Returns the
+ * number of subgraphs, or -1 (pool < 1). */
+int32_t npu_pass_barrier_alloc(const int32_t *kinds, int32_t n, int64_t pool, int64_t *subgraph,
+                               int64_t *barrier_id, int64_t *generation);
+
 /* The COST_JSON record of a function whose body is ops, its SRAM plan bufs,
  * its tile loops running tile_iterations times. */
 int32_t npu_pass_cost_evaluate(const npu_graph *g, const npu_hw_target *t, const int32_t *ops,

@@ -191,6 +191,80 @@ npu_status fused_matmul_bias_act(const npu_memref *A, const npu_memref *B,
                     "fused_matmul_bias_act launch");
 }
 
+npu_status npu_planned_matmul_bias_act(const npu_memref *A, const npu_memref *B,
+                                       const npu_memref *bias, const npu_memref *out,
+                                       int32_t act, const npu_tile_plan *plan, void *lds_dump,
+                                       npu_stream stream) {
+  npu::plans_reset();
+  const void *pa, *pb, *pbias = nullptr, *po;
+  NPU_TRY(check_memref(A, "A", 2, NPU_F32, &pa));
+  NPU_TRY(check_memref(B, "B", 2, NPU_F32, &pb));
+  NPU_TRY(check_memref(out, "out", 2, NPU_F32, &po));
+  NPU_TRY(check_act(act));
+  const int64_t M = A->sizes[0], K = A->sizes[1], N = B->sizes[1];
+  if (B->sizes[0] != K)
+    return fail(NPU_ERR_INVALID_ARG, "B: sizes[0] = %lld, expected K = %lld",
+                (long long)B->sizes[0], (long long)K);
+  if (out->sizes[0] != M || out->sizes[1] != N)
+    return fail(NPU_ERR_INVALID_ARG, "out: [%lld,%lld], expected [%lld,%lld]",
+                (long long)out->sizes[0], (long long)out->sizes[1], (long long)M, (long long)N);
+  if (!absent(bias)) {
+    NPU_TRY(check_memref(bias, "bias", 1, NPU_F32, &pbias));
+    if (bias->sizes[0] != N)
+      return fail(NPU_ERR_INVALID_ARG, "bias: size %lld, expected N = %lld",
+                  (long long)bias->sizes[0], (long long)N);
+  }
+  if (!plan) return fail(NPU_ERR_INVALID_ARG, "plan is NULL");
+  const npu_tile_plan &p = *plan;
+  if (!npu::planned_matmul_tiles_ok(p.tm, p.tn, p.tk))
+    return fail(NPU_ERR_UNSUPPORTED,
+                "tile (%d, %d, %d): sizes must be positive with at most 64 16x16 output blocks",
+                p.tm, p.tn, p.tk);
+  if (p.lds_bytes <= 0 || p.lds_bytes > 163840 || p.lds_bytes % 4 != 0)
+    return fail(NPU_ERR_INVALID_ARG, "lds_bytes = %d: must be in (0, 163840], a multiple of 4",
+                p.lds_bytes);
+  struct Buf {
+    const char *name;
+    int64_t off, bytes;
+  };
+  const int64_t t = 4;
+  const Buf bufs[7] = {{"A", p.off_a, t * p.tm * p.tk},     {"A pong", p.off_a_pong, t * p.tm * p.tk},
+                       {"B", p.off_b, t * p.tk * p.tn},     {"B pong", p.off_b_pong, t * p.tk * p.tn},
+                       {"bias", p.off_bias, t * p.tn},       {"C", p.off_c, t * p.tm * p.tn},
+                       {"Y", p.off_y, t * p.tm * p.tn}};
+  // a plan without a bias buffer (off_bias < 0) is for a group without a bias
+  const bool has_bias = p.off_bias >= 0;
+  if (has_bias != (pbias != nullptr))
+    return fail(NPU_ERR_INVALID_ARG, has_bias ? "plan has a bias buffer but bias is absent"
+                                              : "bias given but the plan has no bias buffer");
+  const int nbufs = 7;
+  for (int i = 0; i < nbufs; ++i) {
+    const Buf &b = bufs[i];
+    if (i == 4 && !has_bias) continue;
+    if (b.off < 0 || b.off % 4 != 0 || b.off + b.bytes > p.lds_bytes)
+      return fail(NPU_ERR_INVALID_ARG,
+                  "plan: %s at %lld (+%lld bytes) is not a 4-byte aligned offset inside the %d "
+                  "bytes of SRAM", b.name, (long long)b.off, (long long)b.bytes, p.lds_bytes);
+  }
+  for (int i = 0; i < nbufs; ++i)
+    for (int j = i + 1; j < nbufs; ++j)
+      if ((has_bias || (i != 4 && j != 4)) && bufs[i].off < bufs[j].off + bufs[j].bytes && bufs[j].off < bufs[i].off + bufs[i].bytes)
+        return fail(NPU_ERR_INVALID_ARG, "plan: %s and %s overlap", bufs[i].name, bufs[j].name);
+  npu::PlannedMatmulArgs a{};
+  a.A = static_cast<const float *>(pa);
+  a.B = static_cast<const float *>(pb);
+  a.bias = static_cast<const float *>(pbias);
+  a.out = static_cast<float *>(const_cast<void *>(po));
+  a.M = (int)M; a.N = (int)N; a.K = (int)K; a.act = act;
+  a.tm = p.tm; a.tn = p.tn; a.tk = p.tk; a.lds_bytes = p.lds_bytes;
+  a.off_a[0] = (int)p.off_a; a.off_a[1] = (int)p.off_a_pong;
+  a.off_b[0] = (int)p.off_b; a.off_b[1] = (int)p.off_b_pong;
+  a.off_bias = has_bias ? (int)p.off_bias : -1; a.off_c = (int)p.off_c; a.off_y = (int)p.off_y;
+  a.lds_dump = lds_dump;
+  return hip_status(npu::launch_planned_matmul(a, static_cast<hipStream_t>(stream)),
+                    "npu_planned_matmul_bias_act launch");
+}
+
 namespace {
 
 // fused_conv2d_nhwc_bias_act and its residual variant: checks, then the LDS

@@ -46,6 +46,19 @@ struct IrbArgs {
 bool irb_supported(int C, int E);
 hipError_t launch_irb_f32(const IrbArgs &a, hipStream_t s);
 
+// fill -> matmul -> generic(bias, act) as the reference's bufferized tile
+// loop, every SRAM buffer at its planned LDS byte offset (k_planned.hip).
+struct PlannedMatmulArgs {
+  const float *A, *B, *bias;  // bias may be null
+  float *out;
+  int M, N, K, act;
+  int tm, tn, tk, lds_bytes;
+  int off_a[2], off_b[2], off_bias, off_c, off_y;  // off_bias -1: no bias
+  void *lds_dump;             // may be null: else tile (0,0)'s LDS, lds_bytes
+};
+bool planned_matmul_tiles_ok(int tm, int tn, int tk);
+hipError_t launch_planned_matmul(const PlannedMatmulArgs &a, hipStream_t s);
+
 // Llama layer GEMM variants: A prologue and epilogue kinds.
 enum { kProPlain = 0, kProRmsnorm = 1 };
 enum { kEpiQkvRope = 0, kEpiResidual = 1, kEpiSwiglu = 2 };

@@ -532,4 +532,22 @@ int32_t npu_pass_temporal(const npu_graph *g, const npu_hw_target *t, int32_t op
   return (int32_t)c.tile_sizes.size();
 }
 
+int32_t npu_pass_barrier_alloc(const int32_t *kinds, int32_t n, int64_t pool, int64_t *subgraph,
+                               int64_t *barrier_id, int64_t *generation) {
+  if (pool < 1 || n < 0 || (n > 0 && (!kinds || !subgraph || !barrier_id || !generation)))
+    return fail("barrier alloc: pool must be >= 1 and the arrays non-null");
+  std::vector<npu::SchedKind> ops(n);
+  for (int32_t i = 0; i < n; ++i)
+    ops[i] = kinds[i] >= 0 && kinds[i] <= 2 ? static_cast<npu::SchedKind>(kinds[i]) : npu::SchedKind::Ignore;
+  const auto a = npu::barrier_alloc(ops, pool);
+  int64_t subs = 0;
+  for (int32_t i = 0; i < n; ++i) {
+    subgraph[i] = a[i].subgraph;
+    barrier_id[i] = a[i].barrier_id;
+    generation[i] = a[i].generation;
+    subs = std::max<int64_t>(subs, a[i].subgraph + 1);
+  }
+  return (int32_t)subs;
+}
+
 }  // extern "C"

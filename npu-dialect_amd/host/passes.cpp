@@ -432,4 +432,26 @@ bool temporal_decision(const ir::Graph &g, const CostModel &cm, int32_t op, Tile
   return true;
 }
 
+std::vector<BarrierAssignment> barrier_alloc(const std::vector<SchedKind> &ops, int64_t pool) {
+  std::vector<BarrierAssignment> out(ops.size());
+  int64_t sub = -1;
+  bool open = false;  // the current subgraph holds an op
+  SchedKind prev = SchedKind::Ignore;
+  for (size_t i = 0; i < ops.size(); ++i) {
+    const SchedKind k = ops[i];
+    if (k == SchedKind::Ignore) continue;
+    const bool cut = k == SchedKind::DmaIn && (prev == SchedKind::DmaOut || prev == SchedKind::Compute);
+    if (!open || (cut && open)) {
+      ++sub;
+      open = true;
+    }
+    out[i].subgraph = sub;
+    out[i].barrier_id = sub % pool;
+    out[i].generation = sub / pool;
+    prev = k;
+  }
+  return out;
+}
+
 }  // namespace npu
+

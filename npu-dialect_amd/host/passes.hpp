@@ -55,4 +55,15 @@ bool spatial_decision(const ir::Graph &g, const CostModel &cm, int32_t op, int64
 // stays untiled (no valid config or a single tile).
 bool temporal_decision(const ir::Graph &g, const CostModel &cm, int32_t op, TileConfig *out);
 
+// DMASchedulingPass.cpp:92-147 (npu-barrier-alloc): the schedulable ops of
+// a function in program order -- DMA into SRAM, compute (linalg ops and
+// memref copies), DMA out of SRAM -- are cut into subgraphs, a new one
+// starting at a DMA-in that follows a DMA-out or a compute op; subgraph i
+// gets barrier id i % pool and generation i / pool.  Ignored ops keep -1.
+enum class SchedKind : int32_t { DmaIn = 0, Compute = 1, DmaOut = 2, Ignore = 3 };
+struct BarrierAssignment {
+  int64_t subgraph = -1, barrier_id = -1, generation = -1;
+};
+std::vector<BarrierAssignment> barrier_alloc(const std::vector<SchedKind> &ops, int64_t pool);
+
 }  // namespace npu

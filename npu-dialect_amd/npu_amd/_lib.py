@@ -91,6 +91,17 @@ class NpuGroupAttrs(C.Structure):
     ]
 
 
+class NpuTilePlan(C.Structure):
+    """npu_tile_plan: the temporal tile and each SRAM buffer's LDS offset."""
+
+    _fields_ = [
+        ("tm", C.c_int32), ("tn", C.c_int32), ("tk", C.c_int32), ("lds_bytes", C.c_int32),
+        ("off_a", C.c_int64), ("off_a_pong", C.c_int64),
+        ("off_b", C.c_int64), ("off_b_pong", C.c_int64),
+        ("off_bias", C.c_int64), ("off_c", C.c_int64), ("off_y", C.c_int64),
+    ]
+
+
 _ARG = C.POINTER(NpuArg)
 
 SIGNATURES = {
@@ -99,6 +110,8 @@ SIGNATURES = {
     "npu_status_string": (C.c_char_p, [_I32]),
     "npu_device_count": (_I32, []),
     "fused_matmul_bias_act": (_I32, [_MR, _MR, _MR, _MR, _I32, _P]),
+    "npu_planned_matmul_bias_act": (_I32, [_MR, _MR, _MR, _MR, _I32, C.POINTER(NpuTilePlan), _P,
+                                           _P]),
     "fused_conv2d_nhwc_bias_act": (_I32, [_MR, _MR, _MR, _MR, _I32, _I32, _P]),
     "fused_conv2d_nhwc_bias_res_act": (_I32, [_MR, _MR, _MR, _MR, _MR, _I32, _I32, _P]),
     "fused_qbottleneck_i8": (_I32, [_MR] * 11 + [_P]),

@@ -73,6 +73,19 @@ def fused_matmul_bias_act(A, B, bias, out, act="relu", stream=None):
     return out
 
 
+def planned_matmul_bias_act(A, B, bias, out, plan, act="relu", lds_dump=None, stream=None):
+    """out = act(A @ B + bias) as the reference's bufferized tile loop, every
+    SRAM buffer at the LDS offset `plan` (an NpuTilePlan, see
+    npu_amd.tileplan) gives it; `lds_dump` (a device tensor of
+    plan.lds_bytes bytes) receives tile (0, 0)'s LDS at the end."""
+    mA, mB, mb, mo = from_tensor(A), from_tensor(B), _opt(bias), from_tensor(out)
+    dump = None if lds_dump is None else lds_dump.data_ptr()
+    st = _lib.lib().npu_planned_matmul_bias_act(ref(mA), ref(mB), ref(mb), ref(mo), ACT[act],
+                                                C.byref(plan), dump, _stream(stream))
+    _check(st, "npu_planned_matmul_bias_act")
+    return out
+
+
 def fused_conv2d_nhwc_bias_act(x, w, bias, out, pad=1, act="relu", stream=None):
     """out = act(conv_2d_nhwc_fhwc(pad(x), w) + bias); f32 or bf16."""
     mx, mw, mb, mo = from_tensor(x), from_tensor(w), _opt(bias), from_tensor(out)

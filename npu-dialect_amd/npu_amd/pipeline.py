@@ -13,9 +13,10 @@ library (libnpu_host.so) and returns them as data: the fusion groups, the
 outlined functions (name, signature), each function's spatial and temporal
 tile decisions, its DMA/SRAM plan and its COST_JSON record, and -- for the
 MI355X -- the entry point that executes the outlined group.  Canonicalize/CSE
-only fold the constants peeling leaves behind, and barrier allocation
-numbers hardware barriers a GPU kernel places itself (s_barrier), so neither
-has a decision to restate.  Core mapping tags each spatial tile with its core
+only fold the constants peeling leaves behind, so they have no decision to
+restate; barrier allocation cuts a tile loop's DMA and compute ops into
+subgraphs, which ``tileplan`` applies to one tile loop (host.barrier_alloc)
+next to the loop's SRAM plan at its slice sizes.  Core mapping tags each spatial tile with its core
 id, (iv - lb) / step (CoreMappingPass.cpp:33-73); on the GPU that is the
 workgroup index, so the report gives the core (CU) count of each tiled op.
 

@@ -500,6 +500,71 @@ def test_c5_layer_small_shapes(cuda, S, D, H, F):
         check_bound(bf16(_host(o[name])), bf16(ref), mag, RTOL_BF16, what=f"layer {name}")
 
 
+# ------------------------------------------------------------------ SRAM plan as LDS layout
+def _planned_case(M, K, N, seed, bias=True):
+    from npu_amd import tileplan
+    A = rng.uniform(seed, 0, (M, K), -1, 1)
+    B = rng.uniform(seed, 1, (K, N), -1, 1)
+    b = rng.uniform(seed, 2, (N,), -1, 1) if bias else None
+    text = blocks.matmul_bias_act(M, K, N, act="relu") if bias else None
+    plan = tileplan.matmul_group_plan(mlir.parse_functions(text)[0])
+    return A, B, b, plan
+
+
+@pytest.mark.parametrize("M,K,N", [(256, 512, 256), (100, 36, 52), (64, 1000, 80)])
+def test_planned_matmul_layout_is_the_plan(cuda, M, K, N):
+    """The group run as the reference's tile loop with its SRAM plan as the
+    LDS layout: the output within the f32 bound of the oracle, and tile
+    (0, 0)'s LDS holding each slice at its planned offset -- the bias slice,
+    the last K step's A and B slices in the buffer of that step's parity,
+    the accumulator tile and the output tile, which is what was stored."""
+    A, B, b, p = _planned_case(M, K, N, 40 + M)
+    plan = p["plan"]
+    tm, tn, tk = p["tile"]
+    out = torch.empty((M, N), dtype=torch.float32, device="cuda")
+    dump = torch.zeros(plan.lds_bytes // 4, dtype=torch.float32, device="cuda")
+    groups.planned_matmul_bias_act(_dev(A), _dev(B), _dev(b), out, plan, "relu", lds_dump=dump)
+    torch.cuda.synchronize()
+    ref, mag = refs.matmul_bias_act(A, B, b, "relu")
+    got = _host(out)
+    check_bound(got, ref, mag, RTOL_F32, what="planned matmul")
+    lds = _host(dump)
+    at = lambda off, rows, cols: lds[off // 4: off // 4 + rows * cols].reshape(rows, cols)
+    mt, nt = min(tm, M), min(tn, N)
+    assert np.array_equal(at(plan.off_bias, 1, tn)[0, :nt], b[:nt].astype(np.float32))
+    nk = -(-K // tk)
+    last = (nk - 1) % 2
+    k0 = (nk - 1) * tk
+    a_last = at(plan.off_a_pong if last else plan.off_a, tm, tk)
+    b_last = at(plan.off_b_pong if last else plan.off_b, tk, tn)
+    kk = min(tk, K - k0)
+    assert np.array_equal(a_last[:mt, :kk], A[:mt, k0:k0 + kk].astype(np.float32))
+    assert not a_last[:mt, kk:].any()  # K past the operand: zeros
+    assert np.array_equal(b_last[:kk, :nt], B[k0:k0 + kk, :nt].astype(np.float32))
+    c = at(plan.off_c, tm, tn)[:mt, :nt]
+    r0, m0 = refs.matmul_bias_act(A[:mt], B[:, :nt], None, "none")
+    check_bound(c, r0, m0, RTOL_F32, what="accumulator tile in SRAM")
+    assert np.array_equal(at(plan.off_y, tm, tn)[:mt, :nt], got[:mt, :nt])
+
+
+def test_planned_matmul_relu_mlir_closed_form(cuda):
+    """test/matmul_relu.mlir (the builder's text of it, checked against the
+    reference's file on the CPU) under the harness's rules (f16 -> f32,
+    argument i filled with 0.01 (i + 1)) through its own plan: every output
+    is K * 0.01 * 0.02 = 0.0512 (e2e_verify.py:288-309)."""
+    from npu_amd import tileplan
+    f = mlir.parse_functions(lower.harness_f32(blocks.reference_workload("matmul_relu.mlir")))[0]
+    p = tileplan.matmul_group_plan(f)
+    (na, ta), (nb, tb) = f.args[:2]
+    A = torch.full(ta.shape, 0.01, dtype=torch.float32, device="cuda")
+    B = torch.full(tb.shape, 0.02, dtype=torch.float32, device="cuda")
+    out = torch.empty((ta.shape[0], tb.shape[1]), dtype=torch.float32, device="cuda")
+    groups.planned_matmul_bias_act(A, B, None, out, p["plan"], "relu")
+    torch.cuda.synchronize()
+    got = _host(out)
+    assert np.allclose(got, ta.shape[1] * 0.01 * 0.02, rtol=1e-5, atol=1e-7)
+
+
 # ------------------------------------------------------------------ host lowering
 @pytest.mark.parametrize("case", ["matmul", "conv_f32", "conv_bf16", "inverted_residual"])
 def test_lowered_blocks_match_the_oracle(cuda, case):
