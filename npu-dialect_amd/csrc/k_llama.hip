@@ -98,14 +98,15 @@ constexpr int GT = 1024;  // GEMM workgroup: 16 waves, four per SIMD
 // WR row strips of 16 rows x WC column groups x WK parts of K.  Every global
 // load of the tile is issued up front -- the RMSNorm A panel, then all of B
 // (and A) in chunks of KC rows (at most NCH chunks), then the epilogue's own
-// inputs -- and the chunks are stored to LDS one after another as their
-// loads arrive.  The WK partial sums go to a dense [WK][BM][NB BN] array in
-// LDS, and every thread sums and finishes whole quads (four consecutive
-// columns of one row) of the tile, so the epilogue's vector work is spread
-// over all 16 waves.  kProRmsnorm keeps the whole A panel (K <= KMAX) in LDS.
+// inputs -- and the chunks are stored to LDS as their loads arrive, into two
+// buffers when there are several (one barrier per chunk).  With K split
+// (WK > 1) the partial sums go to a dense [WK][BM][NB BN] array in LDS and
+// every thread sums and finishes whole quads (four consecutive columns of one
+// row) of the tile; with WK = 1 each lane finishes its own accumulator quads.
+// kProRmsnorm keeps the whole A panel (K <= KMAX) in LDS.
 template <int PRO, int EPI, int BM, int BN, int WR, int WC, int WK, int KC, int NCH, int KMAX>
 struct GemmShape {
-  static constexpr int kBM = BM, kBN = BN;
+  static constexpr int kBM = BM, kBN = BN, kWK = WK, kWC = WC;
   static constexpr int PPL = KMAX / 512;  // RMSNorm panel: 8-element pieces per lane and row
   static constexpr int NB = EPI == kEpiSwiglu ? 2 : 1;
   static constexpr int TMW = BM / WR / 16, TNW = BN / WC / 16;  // MFMA tiles of a wave
@@ -117,15 +118,19 @@ struct GemmShape {
   static constexpr int ALD = KC + APAD;                          // plain A chunk row stride
   static constexpr int AITEMS = BM * KC / 8, APER = (AITEMS + GT - 1) / GT;
   static constexpr int RLD = NB * BN + 4;                        // partial-sum row stride (floats)
-  static constexpr int RED = WK * BM * RLD * 4;                  // bytes of the partial sums
+  static constexpr int RED = WK > 1 ? WK * BM * RLD * 4 : 0;     // bytes of the partial sums
   static constexpr int QUADS = BM * BN / 4, QPER = (QUADS + GT - 1) / GT;
   static_assert(WR * WC * WK == 16 && TMW >= 1 && TNW >= 1, "sixteen waves cover the tile");
   static_assert(BN % 16 == 0 && BM % 16 == 0 && KC % 32 == 0, "MFMA tiles");
+  // K chunks staged in LDS: two buffers when there are several chunks (the
+  // next chunk is written while the current one is multiplied)
+  static constexpr int NBUF = NCH > 1 ? 2 : 1;
+  static constexpr int ACHUNK = BM * ALD * 2;  // bytes of one plain A chunk
   __host__ __device__ static size_t abytes(int K) {
-    return PRO == kProRmsnorm ? (size_t)BM * (K + APAD) * 2 : (size_t)BM * ALD * 2;
+    return PRO == kProRmsnorm ? (size_t)BM * (K + APAD) * 2 : (size_t)NBUF * ACHUNK;
   }
   static size_t lds_bytes(int K) {
-    const size_t main = abytes(K) + (size_t)BCHUNK;
+    const size_t main = abytes(K) + (size_t)NBUF * BCHUNK;
     return main > (size_t)RED ? main : (size_t)RED;
   }
 };
@@ -224,14 +229,33 @@ __global__ __launch_bounds__(GT) void llama_gemm_kernel(const LlamaGemmArgs a, i
           areg[c][i] = *reinterpret_cast<const u32x4 *>(asrc[i] + min(c * KC + akc[i], K - 8));
   }
 
-  // ---- the epilogue's inputs of this thread's quads: quad q = tid + GT e is
-  // row q / (BN / 4), columns 4 (q % (BN / 4)) .. +3 of the tile
-  uint2 res[S::QPER];
-  float2 cs[S::QPER], sn[S::QPER];
+  // wave (wr, wc, wk): rows wr * BM/WR .., columns wc * BN/WC .., k steps wk, wk + WK, ...
+  const int wr = wave % WR, wc = (wave / WR) % WC, wk = wave / (WR * WC);
+  const int ml = lane & 15, ng = 4 * (lane >> 4);  // accumulator: row ml, columns ng .. ng+3
+
+  // ---- the epilogue's quads (four consecutive columns of one row of the
+  // tile).  With K split over the waves (WK > 1), quad q = tid + GT e of the
+  // summed tile, row q / (BN / 4), columns 4 (q % (BN / 4)) .. +3; without
+  // (WK = 1), the lane's own accumulator quads, one per 16 x 16 block (i, j)
+  // with e = i TNW + j.  Their inputs are loaded here, before the K loop.
+  constexpr int NQ = WK > 1 ? S::QPER : TMW * TNW;
+  auto quad_of = [&](int e, int &row, int &col) __attribute__((always_inline)) {
+    if constexpr (WK > 1) {
+      const int q = min(tid + GT * e, S::QUADS - 1);
+      row = q / (BN / 4);
+      col = 4 * (q % (BN / 4));
+    } else {
+      row = wr * (BM / WR) + 16 * (e / TNW) + ml;
+      col = wc * (BN / WC) + 16 * (e % TNW) + ng;
+    }
+  };
+  uint2 res[NQ];
+  float2 cs[NQ], sn[NQ];
 #pragma unroll
-  for (int e = 0; e < S::QPER; ++e) {
-    const int q = min(tid + GT * e, S::QUADS - 1);
-    const int m = min(m0 + q / (BN / 4), M - 1), n = n0 + 4 * (q % (BN / 4));
+  for (int e = 0; e < NQ; ++e) {
+    int row, col;
+    quad_of(e, row, col);
+    const int m = min(m0 + row, M - 1), n = n0 + col;
     if constexpr (EPI == kEpiResidual)
       res[e] = *reinterpret_cast<const uint2 *>(a.res + (size_t)m * Np + n);
     if constexpr (EPI == kEpiQkvRope) {
@@ -276,9 +300,6 @@ __global__ __launch_bounds__(GT) void llama_gemm_kernel(const LlamaGemmArgs a, i
     }
   }
 
-  // wave (wr, wc, wk): rows wr * BM/WR .., columns wc * BN/WC .., k steps wk, wk + WK, ...
-  const int wr = wave % WR, wc = (wave / WR) % WC, wk = wave / (WR * WC);
-  const int ml = lane & 15, ng = 4 * (lane >> 4);  // accumulator: row ml, columns ng .. ng+3
   f32x4 acc[NB][TMW][TNW];
 #pragma unroll
   for (int b = 0; b < NB; ++b)
@@ -287,20 +308,29 @@ __global__ __launch_bounds__(GT) void llama_gemm_kernel(const LlamaGemmArgs a, i
 #pragma unroll
       for (int j = 0; j < TNW; ++j) acc[b][i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-#pragma unroll
-  for (int chunk = 0; chunk < NCH; ++chunk) {
-    if (chunk >= nchunks) break;
-    if (chunk > 0) __syncthreads();  // every wave is done with the previous chunk
+  // chunk c lives in buffer c % NBUF; with two buffers, chunk c + 2 is
+  // written once every wave is done with chunk c, so each chunk costs one
+  // barrier
+  auto write_chunk = [&](int chunk, int buf) __attribute__((always_inline)) {
 #pragma unroll
     for (int i = 0; i < S::BPER; ++i)
-      if (bdst[i] >= 0) *reinterpret_cast<u32x4 *>(Bs + bdst[i]) = breg[chunk][i];
+      if (bdst[i] >= 0) *reinterpret_cast<u32x4 *>(Bs + (size_t)buf * S::BCHUNK + bdst[i]) = breg[chunk][i];
     if constexpr (PRO != kProRmsnorm) {
 #pragma unroll
       for (int i = 0; i < S::APER; ++i)
-        if (adst[i] >= 0) *reinterpret_cast<u32x4 *>(As + adst[i]) = areg[chunk][i];
+        if (adst[i] >= 0) *reinterpret_cast<u32x4 *>(As + (size_t)buf * S::ACHUNK + adst[i]) = areg[chunk][i];
     }
-    __syncthreads();
-    const unsigned char *abuf = PRO == kProRmsnorm ? As + (size_t)chunk * KC * 2 : As;
+  };
+  write_chunk(0, 0);
+  if constexpr (S::NBUF == 2)
+    if (nchunks > 1) write_chunk(1, 1);
+  __syncthreads();
+#pragma unroll
+  for (int chunk = 0; chunk < NCH; ++chunk) {
+    if (chunk >= nchunks) break;
+    const int buf = chunk % S::NBUF;
+    const unsigned char *abuf = PRO == kProRmsnorm ? As + (size_t)chunk * KC * 2 : As + (size_t)buf * S::ACHUNK;
+    const unsigned char *bbuf = Bs + (size_t)buf * S::BCHUNK;
     const int steps = min(KC, K - chunk * KC) / 32;
     for (int s = wk; s < steps; s += WK) {
       Frag16 xf[TMW], wf[NB][TNW];
@@ -313,7 +343,7 @@ __global__ __launch_bounds__(GT) void llama_gemm_kernel(const LlamaGemmArgs a, i
       for (int b = 0; b < NB; ++b)
 #pragma unroll
         for (int j = 0; j < TNW; ++j)
-          wf[b][j] = read_wfrag(Bs + (b * S::STRIPS + wc * TNW + j) * S::SB, s, lane);
+          wf[b][j] = read_wfrag(bbuf + (b * S::STRIPS + wc * TNW + j) * S::SB, s, lane);
 #pragma unroll
       for (int b = 0; b < NB; ++b)
 #pragma unroll
@@ -322,34 +352,50 @@ __global__ __launch_bounds__(GT) void llama_gemm_kernel(const LlamaGemmArgs a, i
           for (int j = 0; j < TNW; ++j)
             acc[b][i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wf[b][j].h, xf[i].h, acc[b][i][j], 0, 0, 0);
     }
+    if (chunk + 1 < nchunks) {
+      __syncthreads();  // every wave is done with this chunk's buffer
+      if constexpr (S::NBUF == 1) {
+        write_chunk(chunk + 1, 0);
+        __syncthreads();
+      } else if (chunk + 2 < nchunks) {
+        write_chunk(chunk + 2, buf);  // read after the next chunk's barrier
+      }
+    }
   }
 
-  // ---- partial sums -> LDS [WK][BM][NB BN], then whole quads per thread
-  __syncthreads();  // LDS is free
-  float *red = reinterpret_cast<float *>(smem);
+  // ---- with K split, the partial sums -> LDS [WK][BM][NB BN], summed per quad
+  [[maybe_unused]] float *red = reinterpret_cast<float *>(smem);
+  if constexpr (WK > 1) {
+    __syncthreads();  // LDS is free
 #pragma unroll
-  for (int b = 0; b < NB; ++b)
+    for (int b = 0; b < NB; ++b)
 #pragma unroll
-    for (int i = 0; i < TMW; ++i)
+      for (int i = 0; i < TMW; ++i)
 #pragma unroll
-      for (int j = 0; j < TNW; ++j) {
-        const int row = wr * (BM / WR) + 16 * i + ml;
-        const int col = b * BN + wc * (BN / WC) + 16 * j + ng;
-        *reinterpret_cast<f32x4 *>(red + ((size_t)wk * BM + row) * S::RLD + col) = acc[b][i][j];
-      }
-  __syncthreads();
+        for (int j = 0; j < TNW; ++j) {
+          const int row = wr * (BM / WR) + 16 * i + ml;
+          const int col = b * BN + wc * (BN / WC) + 16 * j + ng;
+          *reinterpret_cast<f32x4 *>(red + ((size_t)wk * BM + row) * S::RLD + col) = acc[b][i][j];
+        }
+    __syncthreads();
+  }
 #pragma unroll
-  for (int e = 0; e < S::QPER; ++e) {
-    const int q = tid + GT * e;
-    if (q >= S::QUADS) break;
-    const int row = q / (BN / 4), col = 4 * (q % (BN / 4));
+  for (int e = 0; e < NQ; ++e) {
+    if (WK > 1 && tid + GT * e >= S::QUADS) break;
+    int row, col;
+    quad_of(e, row, col);
     const int m = m0 + row, n = n0 + col;
     if (m >= M) continue;
     f32x4 v = f32x4{0.f, 0.f, 0.f, 0.f}, u = f32x4{0.f, 0.f, 0.f, 0.f};
+    if constexpr (WK > 1) {
 #pragma unroll
-    for (int w = 0; w < WK; ++w) {
-      v += *reinterpret_cast<const f32x4 *>(red + ((size_t)w * BM + row) * S::RLD + col);
-      if constexpr (NB == 2) u += *reinterpret_cast<const f32x4 *>(red + ((size_t)w * BM + row) * S::RLD + BN + col);
+      for (int w = 0; w < WK; ++w) {
+        v += *reinterpret_cast<const f32x4 *>(red + ((size_t)w * BM + row) * S::RLD + col);
+        if constexpr (NB == 2) u += *reinterpret_cast<const f32x4 *>(red + ((size_t)w * BM + row) * S::RLD + BN + col);
+      }
+    } else {
+      v = acc[0][e / TNW][e % TNW];
+      if constexpr (NB == 2) u = acc[NB - 1][e / TNW][e % TNW];
     }
     uint2 o;
     uint16_t *dst;
@@ -574,15 +620,16 @@ void plan_gemm(const char *name, Kern kern, const LlamaGemmArgs &a, int grid, in
   p.load_phases = a.K > (int)Sh::SB / 32 ? 2 : 1;  // one exposed load round trip per chunk beyond one
   p.tile_macs = BM * BN * Sh::NB * a.K / units;
   const double bpieces = a.K * BN * Sh::NB / 8.0, apieces = BM * a.K / 8.0;
-  const double per_wave_steps = ksteps / 4.0;  // WK = 4 parts of K
+  const double per_wave_steps = ksteps / Sh::kWK;  // K in kWK parts
   const double frag_valu = per_wave_steps * (Sh::TNW * Sh::NB * 4.0 + Sh::TMW * 2.0) * 4;  // 4 waves/unit
   const double quads = BM * BN / 4.0 / 64.0 / units;  // quads per wave of a unit
   const double epi_cost = epi == kEpiQkvRope ? 14 : (epi == kEpiResidual ? 8 : 32);
-  const double red_cost = Sh::NB * 4 * 4.0 / 4.0;  // per quad: WK loads and adds, spread over 16 waves
+  // per quad: kWK loads and adds when K is split (none without a split)
+  const double red_cost = Sh::kWK > 1 ? Sh::NB * Sh::kWK * 4.0 / 4.0 : 0.0;
   const double norm = pro == kProRmsnorm ? (apieces * 6.0 / 64.0 + BM * 14.0) / units : 0.0;
   p.tile_valu = 4.0 * ((bpieces + apieces) * 4.0 / 64.0 / units + frag_valu + quads * (epi_cost + red_cost) + norm);
   p.tile_lds_bytes = (2.0 * (bpieces + apieces) * 16 +
-                      ksteps * (Sh::TNW * Sh::NB * 1024.0 * 4 / (BN / 16 / Sh::TNW) + Sh::TMW * 1024.0 * 4) +
+                      ksteps * 4.0 / Sh::kWK * (Sh::TNW * Sh::NB * 1024.0 * 4 / Sh::kWC + Sh::TMW * 1024.0 * 4) +
                       2.0 * Sh::RED) / units;
   p.tile_load_bytes = ((bpieces + apieces) * 16 + (pro == kProRmsnorm ? 4.0 * a.K : 0.0)) / units;
   p.tile_store_bytes = BM * BN * 2 / units;
@@ -620,21 +667,24 @@ hipError_t run_gemm(const char *name, const LlamaGemmArgs &a, hipStream_t s) {
 
 }  // namespace
 
-// Tiles (16 waves each, K split four ways): QKV 64 x 48 (256 workgroups at
-// the layer's 512 x 1536, all of K in one chunk), SwiGLU 64 x 64 per weight
-// (176 workgroups, K in chunks of 256), residual GEMMs 32 x 32 (256
+// Tiles (16 waves each).  At d_model <= 512 the RMSNorm GEMMs give each wave
+// one 16 x 16 block (per weight) over all of K, no K split: QKV 64 x 64 (192
+// workgroups at the layer's 512 x 1536, K in one chunk), SwiGLU 64 x 64 per
+// weight (176 workgroups, K in chunks of 128); beyond, K split four ways
+// (QKV 64 x 48, SwiGLU 32 x 64, chunks of 128, K <= 1024: the whole A panel
+// is in LDS).  Residual GEMMs 32 x 32 with K split four ways (256
 // workgroups; K in chunks of 512, the down projection's 1408 in three, at
-// most 2048).  The RMSNorm GEMMs hold all of K in LDS (K <= 1024).
+// most 2048).  Chunk sizes keep two chunk buffers within the 160 KiB of LDS.
 hipError_t launch_llama_gemm(const LlamaGemmArgs &a, int pro, int epi, hipStream_t s) {
   if (pro == kProRmsnorm && epi == kEpiQkvRope) {
     if (a.K <= 512)
-      return run_gemm<kProRmsnorm, kEpiQkvRope, 64, 48, 4, 1, 4, 512, 1, 512>("llama_rmsnorm_qkv_rope", a, s);
-    return run_gemm<kProRmsnorm, kEpiQkvRope, 64, 48, 4, 1, 4, 256, 4, 1024>("llama_rmsnorm_qkv_rope", a, s);
+      return run_gemm<kProRmsnorm, kEpiQkvRope, 64, 64, 4, 4, 1, 512, 1, 512>("llama_rmsnorm_qkv_rope", a, s);
+    return run_gemm<kProRmsnorm, kEpiQkvRope, 64, 48, 4, 1, 4, 128, 8, 1024>("llama_rmsnorm_qkv_rope", a, s);
   }
   if (pro == kProRmsnorm && epi == kEpiSwiglu) {
     if (a.K <= 512)
-      return run_gemm<kProRmsnorm, kEpiSwiglu, 64, 64, 4, 1, 4, 256, 2, 512>("llama_rmsnorm_swiglu", a, s);
-    return run_gemm<kProRmsnorm, kEpiSwiglu, 32, 64, 2, 2, 4, 256, 4, 1024>("llama_rmsnorm_swiglu", a, s);
+      return run_gemm<kProRmsnorm, kEpiSwiglu, 64, 64, 4, 4, 1, 128, 4, 512>("llama_rmsnorm_swiglu", a, s);
+    return run_gemm<kProRmsnorm, kEpiSwiglu, 32, 64, 2, 2, 4, 128, 8, 1024>("llama_rmsnorm_swiglu", a, s);
   }
   if (pro == kProPlain && epi == kEpiResidual) {
     if (a.K <= 512)
