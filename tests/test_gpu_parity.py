@@ -486,9 +486,12 @@ def test_c5_layer_end_to_end(cuda, llama_case):
 # attention's four key groups five steps (an odd count), with K/V blocks
 # refetched into both register slots on the way.  D = 448: the single-panel
 # RMSNorm GEMMs with a half-filled last K chunk; D = 576: K past one panel,
-# the general RMSNorm GEMM kernel.
+# the general RMSNorm GEMM kernel.  F = 1088 and 1600: the down projection's
+# K in three and four chunks (the last one ragged) through its two LDS
+# buffers.
 @pytest.mark.parametrize("S,D,H,F", [(64, 128, 2, 192), (128, 64, 1, 64), (96, 128, 2, 128),
-                                     (1088, 128, 2, 128), (64, 448, 7, 128), (64, 576, 9, 192)])
+                                     (1088, 128, 2, 128), (64, 448, 7, 128), (64, 576, 9, 192),
+                                     (64, 128, 2, 1088), (32, 128, 2, 1600)])
 def test_c5_layer_small_shapes(cuda, S, D, H, F):
     w = configs.llama_layer(S=S, D=D, H=H, F=F, seed=91 + S)
     inp = w.make_inputs()
