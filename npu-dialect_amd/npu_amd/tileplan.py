@@ -16,8 +16,6 @@ each buffer at its planned byte offset in the workgroup's LDS.
 """
 from __future__ import annotations
 
-import ctypes as C
-
 from . import _lib, host, mlir, pipeline
 
 LDS_BYTES = 163840
@@ -76,6 +74,11 @@ def matmul_group_plan(func: mlir.MFunc, target: host.HWTarget = None, sram: int 
     nk = -(-func.types[names["A"]].shape[1] // tk)
     trip = ["dma_in"] * (3 if names["bias"] else 2) + ["compute"] * 3 + ["dma_out"]
     barriers = host.barrier_alloc(trip * nk, pool)
+    for key in ("A", "B"):
+        if not layout[key]["double_buffered"]:
+            # the launch fetches K step i + 1 into the other buffer while
+            # step i is multiplied: it needs both halves of the pair
+            raise NotImplementedError(f"the plan gives {key} no ping/pong pair at {sram} bytes")
     plan = _lib.NpuTilePlan()
     plan.tm, plan.tn, plan.tk, plan.lds_bytes = tm, tn, tk, sram
     plan.off_a, plan.off_a_pong = layout["A"]["offset"], layout["A"]["offset_pong"]

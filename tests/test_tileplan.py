@@ -108,3 +108,12 @@ def test_planned_entry_checks_the_plan_before_launch():
     assert _call(_plan(off_bias=-1)) == 1 and "bias" in _err()
     assert _call(_plan(), bias=False) == 1 and "bias" in _err()
     assert _call(_plan(), A=(64, 30), B=(31, 48)) == 1 and "expected K" in _err()
+
+
+def test_plan_that_spills_is_refused():
+    """At an SRAM size the group's slices do not fit, the reference's
+    allocator spills a buffer to DRAM; a launch has no DRAM buffers to place,
+    so the plan is refused by name instead of launched."""
+    f = mlir.parse_functions(blocks.matmul_bias_act(256, 512, 256, act="relu"))[0]
+    with pytest.raises(NotImplementedError, match="spills"):
+        tileplan.matmul_group_plan(f, sram=16384)
