@@ -271,8 +271,11 @@ template <int C, int E>
 hipError_t launch_irb_t(const IrbArgs &a, hipStream_t s) {
   const int tiles_w = (a.W + TW - 1) / TW, tiles_h = (a.H + TH - 1) / TH;
   const int per_image = tiles_w * tiles_h, ntiles = a.N * per_image;
-  const int g = persistent_grid(irb_kernel<C, E>);
-  if (g == 0) return hipErrorInvalidDeviceFunction;
+  const int full = persistent_grid(irb_kernel<C, E>);
+  if (full == 0) return hipErrorInvalidDeviceFunction;
+  // one tile per workgroup when there are fewer tiles than resident slots
+  // (rounded up to whole XCD rounds: the walk gives the spare ones nothing)
+  const int g = ntiles < full ? (ntiles + kXcds - 1) / kXcds * kXcds : full;
   {
     constexpr int KC1 = (C + 15) / 16, FB2 = (C + 15) / 16, FB1 = E / 16;
     npu_launch_plan p = make_plan("mbv2_inverted_residual", g, wg_per_cu(irb_kernel<C, E>), ntiles, 32);
