@@ -7,7 +7,9 @@ accepts: any M, N and K a multiple of 4 (matmul); 1x1 and 3x3 filters with
 and without padding, f32 channels a multiple of 4 and bf16 a multiple of 8,
 any filter count, rows up to 70 pixels and batches large enough to reach the
 persistent kernels (conv); the inverted residual block's three channel pairs;
-the int8 bottleneck's three channel counts; Llama layers of 1-4 heads.  They
+the int8 bottleneck's three channel counts; Llama layers of 1-4 heads; the
+plan-driven launch at the reference's own tile plans; and linalg text lowered
+to npu_group_launch calls (matmul and conv, f32 and bf16).  They
 cross the launch-shape boundaries the hand-picked cases sit on (row pairs
 around 48 and 512, widths around 56 and 64, F around multiples of 16 and 64)
 at places no one chose.
@@ -21,7 +23,8 @@ import torch
 
 import oracle
 import refs
-from npu_amd import configs, groups
+import npu_amd
+from npu_amd import blocks, configs, groups, lower, mlir, tileplan
 from npu_amd import inputs as rng
 from test_gpu_parity import _dev, _host, _qb_inputs, _qb_run, _widened_conv
 from tolerance import RTOL_BF16, RTOL_F32, bf16, check_bf16_rounded, check_bound
@@ -71,6 +74,26 @@ def _qb_cases(n=6, seed=2029):
     r = random.Random(seed)
     return [(r.randint(1, 3), r.randint(1, 20), r.randint(1, 20), r.choice((64, 128, 256)))
             for _ in range(n)]
+
+
+def _planned_cases(n=8, seed=2031):
+    r = random.Random(seed)
+    return [(r.randint(1, 400), r.randint(1, 1200), r.randint(1, 400)) for _ in range(n)]
+
+
+def _lowered_cases(n=8, seed=2032):
+    r = random.Random(seed)
+    cases = []
+    for _ in range(n):
+        if r.random() < 0.4:
+            cases.append(("matmul", r.randint(1, 200), 4 * r.randint(1, 100), r.randint(1, 200),
+                          r.choice(ACTS), "f32"))
+        else:
+            elem = r.choice(("f32", "bf16"))
+            C = (4 if elem == "f32" else 8) * r.randint(1, 12)
+            cases.append(("conv", r.randint(1, 6), r.randint(1, 20), r.randint(1, 64), C,
+                          r.randint(1, 100), elem))
+    return cases
 
 
 def _llama_cases(n=5, seed=2030):
@@ -147,3 +170,65 @@ def test_sweep_llama_layer(cuda, S, H, F):
     torch.cuda.synchronize()
     for name, (ref, mag) in refs.llama_reference(inp, H, 1e-5).items():
         check_bound(bf16(_host(o[name])), bf16(ref), mag, RTOL_BF16, what=f"layer S{S} H{H} F{F} {name}")
+
+
+@pytest.mark.parametrize("M,K,N", _planned_cases())
+def test_sweep_planned_matmul(cuda, M, K, N):
+    """The group through the reference's own plan for its shape: within the
+    f32 bound of the oracle, or refused by name before any launch (a plan
+    that spills to DRAM, or a tile of more 16x16 blocks than the launch
+    holds)."""
+    try:
+        p = tileplan.matmul_group_plan(mlir.parse_functions(blocks.matmul_bias_act(M, K, N))[0])
+    except NotImplementedError as e:
+        assert "spills" in str(e), e
+        return
+    seed = 1000 + M + K + N
+    A = rng.uniform(seed, 0, (M, K), -1, 1)
+    B = rng.uniform(seed, 1, (K, N), -1, 1)
+    b = rng.uniform(seed, 2, (N,), -1, 1)
+    out = torch.empty((M, N), dtype=torch.float32, device="cuda")
+    try:
+        groups.planned_matmul_bias_act(_dev(A), _dev(B), _dev(b), out, p["plan"], "relu")
+    except npu_amd.NpuError as e:
+        assert "blocks" in str(e), e
+        return
+    torch.cuda.synchronize()
+    ref, mag = refs.matmul_bias_act(A, B, b, "relu")
+    check_bound(_host(out), ref, mag, RTOL_F32, what=f"planned matmul {M}x{K}x{N} tile {p['tile']}")
+
+
+@pytest.mark.parametrize("case", _lowered_cases())
+def test_sweep_lowered(cuda, case):
+    """linalg text -> npu_amd.lower -> npu_group_launch, against the oracle."""
+    kind = case[0]
+    if kind == "matmul":
+        _, M, K, N, act, _ = case
+        seed = 1100 + M + K + N
+        A = rng.uniform(seed, 0, (M, K), -1, 1)
+        B = rng.uniform(seed, 1, (K, N), -1, 1)
+        b = rng.uniform(seed, 2, (N,), -1, 1)
+        prog = lower.lower_text(blocks.matmul_bias_act(M, K, N, act=act))
+        out = prog.run({"A": _dev(A), "B": _dev(B), "bias": _dev(b)})["%y"]
+        torch.cuda.synchronize()
+        ref, mag = refs.matmul_bias_act(A, B, b, act)
+        check_bound(_host(out), ref, mag, RTOL_F32, what=f"lowered matmul {M}x{K}x{N}")
+        return
+    _, N, H, W, C, F, elem = case
+    seed = 1200 + N * H + W + C + F
+    x = rng.uniform(seed, 0, (N, H, W, C), 0, 1)
+    w = rng.normal(seed, 1, (F, 3, 3, C), 0, math.sqrt(2 / (9 * C)))
+    b = rng.uniform(seed, 2, (F,), -0.1, 0.1)
+    if elem == "bf16":
+        x, w, b = rng.to_bf16_bits(x), rng.to_bf16_bits(w), rng.to_bf16_bits(b)
+    prog = lower.lower_text(blocks.conv_bias_act(N, H, W, C, F, elem=elem))
+    out = prog.run({"x": _dev(x), "w": _dev(w), "bias": _dev(b)})["%y"]
+    torch.cuda.synchronize()
+    bias32 = bf16(b).astype(np.float32) if elem == "bf16" else b
+    ref, mag = refs.conv_bias_act(x, w, bias32, 1, "relu")
+    what = f"lowered conv {elem} {N}x{H}x{W}x{C}->{F}"
+    if elem == "f32":
+        check_bound(_host(out), ref, mag, RTOL_F32, what=what)
+    else:
+        ref32, _ = _widened_conv(x, w, bias32, 1, "relu")
+        check_bf16_rounded(_host(out), ref32, mag, 9 * C + 1, what=what)
