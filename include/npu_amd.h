@@ -110,11 +110,17 @@ npu_status fused_matmul_bias_act(const npu_memref *A, const npu_memref *B,
  *   out  [N,Ho,Wo,F] same dtype as x (bf16: fp32 accumulate, one rounding)
  * Stride 1, symmetric zero padding `pad`; Ho = H + 2*pad - KH + 1.
  * Requires C % 4 == 0 (f32) / C % 8 == 0 (bf16).
- * f32 results are within f32 accuracy of the sequential f32 sum.  Batched
- * 3x3 launches with 32 or 64 channels and F % 64 == 0 compute the products
- * on the bf16 matrix pipe from exact three-part bf16 splits of every value;
- * there an infinite input or filter value gives NaN (not +-Inf) in the
- * outputs it reaches.  NaN propagates everywhere. */
+ * f32 results are within f32 accuracy of the sequential f32 sum (the
+ * parity bound 1e-5 * sum |x w|), with +-Inf and NaN where the f32 loops give
+ * them.  3x3 / pad-1 launches with 32 or 64 channels, F % 64 == 0 and at
+ * least 48 row pairs (N * ceil(H/2) >= 48) compute the products on the bf16
+ * matrix pipe from exact three-part bf16 splits of every value.  The split
+ * is exact for zero and magnitudes in [2^-55, 2^55); a launch in which an
+ * input or filter value lies outside that (Inf, NaN, |v| >= 2^55,
+ * 0 < |v| < 2^-55) or a bias is an f32 subnormal recomputes the rows that
+ * value's workgroup owns on a scalar path bit-identical to the sequential
+ * f32 loops -- correct, but about two orders of magnitude slower for those
+ * rows. */
 npu_status fused_conv2d_nhwc_bias_act(const npu_memref *x, const npu_memref *w,
                                       const npu_memref *bias,
                                       const npu_memref *out, int32_t pad,
@@ -287,6 +293,9 @@ typedef struct npu_group_attrs {
   int32_t n_heads; /* attention: heads of 64                                   */
   float eps;       /* RMSNorm epsilon                                          */
   float scale;     /* attention score scale                                    */
+  int32_t res_arg; /* conv groups: index in `in` of the residual operand a
+                      generic adds, 0 when none is named (in[0] is always the
+                      fill constant, never a residual)                        */
 } npu_group_attrs;
 
 /* Runs one outlined group, or a chain of outlined groups that the host
@@ -315,8 +324,9 @@ typedef struct npu_group_attrs {
  *     with a residual term fused_conv2d_nhwc_bias_res_act
  *     (cst, init, x, w, then each generic's operands -- [bias f32 [F]],
  *      [res [N,Ho,Wo,F]] -- and its destination) -> (out); with several
- *     generics, the destinations before the last are passed without data
- *     (NULL), which tells them from the residual
+ *     generics, attrs->res_arg names the residual's index in `in` (when it
+ *     is 0, the destinations before the last must be passed without data,
+ *     NULL, which tells them from the residual)
  *   fill_linalg_conv_2d_nhwc_fhwc_generic + the depthwise / project group(s)
  *     of an inverted residual block after its tensor.pad -> fused_irb_f32
  *     (cst, init_e, x, we[E,1,1,C], dest_e, init_d, wdw[3,3,E], dest_d,

@@ -110,6 +110,17 @@ npu_status check_memref(const npu_memref *m, const char *name, int32_t rank, int
   return NPU_OK;
 }
 
+}  // namespace
+
+namespace npu {
+npu_status memref_check(const npu_memref *m, const char *name, int32_t rank, int32_t dtype) {
+  const void *p;
+  return check_memref(m, name, rank, dtype, &p);
+}
+}  // namespace npu
+
+namespace {
+
 // An optional operand: a null descriptor or a null data pointer means absent.
 bool absent(const npu_memref *m) { return !m || !m->aligned; }
 

@@ -208,6 +208,20 @@ npu_status run_matmuls(Cursor &c, const npu_group_attrs &at, int chains, const n
     G_TRY(c.memref(2, "B", &s.B));
     if (c.next_is_rank1()) G_TRY(c.memref(1, "bias", &s.bias));
     const int64_t M = s.A->sizes[0], N = s.B->sizes[1];
+    // What each chain's typed call checks is checked here for every chain
+    // first, so that no chain launches before all of them are known good.
+    if (k == 0) G_TRY(typed(npu::memref_check(s.A, "A", 2, NPU_F32)));
+    G_TRY(typed(npu::memref_check(s.B, "B", 2, NPU_F32)));
+    if (s.bias) G_TRY(typed(npu::memref_check(s.bias, "bias", 1, NPU_F32)));
+    if (s.B->sizes[0] != s.A->sizes[1])
+      return gfail(NPU_ERR_INVALID_ARG, "matmul %d: B %s against A %s (K differs)", k,
+                   shape_str(*s.B).c_str(), shape_str(*s.A).c_str());
+    if (s.bias && s.bias->sizes[0] != N)
+      return gfail(NPU_ERR_INVALID_ARG, "matmul %d: bias %s, expected [%lld]", k,
+                   shape_str(*s.bias).c_str(), (long long)N);
+    if (s.A->sizes[1] % 4 != 0)
+      return gfail(NPU_ERR_UNSUPPORTED, "matmul %d: K = %lld (a multiple of 4 is required)", k,
+                   (long long)s.A->sizes[1]);
     if (!same_shape(*s.init, {M, N}))
       return gfail(NPU_ERR_INVALID_ARG, "matmul %d: accumulator %s, expected [%lld,%lld]", k,
                    shape_str(*s.init).c_str(), (long long)M, (long long)N);
@@ -215,11 +229,16 @@ npu_status run_matmuls(Cursor &c, const npu_group_attrs &at, int chains, const n
     if (k + 1 < chains && !s.dest->aligned)
       return gfail(NPU_ERR_INVALID_ARG, "matmul %d: its destination holds the intermediate "
                    "result and must have data", k);
+    if (k + 1 < chains) G_TRY(typed(npu::memref_check(s.dest, "intermediate destination", 2, NPU_F32)));
     steps.push_back(s);
     x = s.dest;  // the next chain reads this chain's result
   }
   if (!c.done())
     return gfail(NPU_ERR_INVALID_ARG, "%zu arguments left over after the group's inputs", c.pos());
+  G_TRY(typed(npu::memref_check(out, "out", 2, NPU_F32)));
+  if (!same_shape(*out, {steps.back().A->sizes[0], steps.back().B->sizes[1]}))
+    return gfail(NPU_ERR_INVALID_ARG, "result %s: expected [%lld,%lld]", shape_str(*out).c_str(),
+                 (long long)steps.back().A->sizes[0], (long long)steps.back().B->sizes[1]);
   for (int k = 0; k < chains; ++k) {
     const Step &s = steps[k];
     const npu_memref *dst = k + 1 == chains ? out : s.dest;
@@ -236,10 +255,11 @@ npu_status run_matmuls(Cursor &c, const npu_group_attrs &at, int chains, const n
 // (cst, init, x, w) come each generic's other operands and its destination,
 // in first-use order.  A bias has rank 1; the residual and the destinations
 // have the output's shape, the last destination last.  With one generic the
-// residual is the rank-4 argument before the destination; with several, the
-// destinations before the last must be passed without data (NULL), as
-// tensor.empty values are, and the one rank-4 argument with data among them
-// is the residual.
+// residual is the rank-4 argument before the destination; with several,
+// attrs.res_arg names its index in `in` (a bufferized host module passes
+// allocated buffers for every destination), or, when it is 0, the
+// destinations before the last must be passed without data (NULL) and the
+// one rank-4 argument with data among them is the residual.
 npu_status run_conv(Cursor &c, const npu_group_attrs &at, const npu_memref *out,
                     npu_stream stream, PlanLog &log, int n_generic) {
   G_TRY(c.fill_value());
@@ -248,12 +268,14 @@ npu_status run_conv(Cursor &c, const npu_group_attrs &at, const npu_memref *out,
   G_TRY(c.memref(4, "x", &x));
   G_TRY(c.memref(4, "w", &w));
   std::vector<const npu_memref *> r4;
+  std::vector<size_t> r4_pos;
   while (!c.done()) {
     if (c.next_is_rank1()) {
       if (bias) return gfail(NPU_ERR_INVALID_ARG, "in[%zu]: a second bias", c.pos());
       G_TRY(c.memref(1, "bias", &bias));
     } else {
       const npu_memref *m;
+      r4_pos.push_back(c.pos());
       G_TRY(c.memref(4, "residual or generic destination", &m));
       r4.push_back(m);
     }
@@ -263,7 +285,14 @@ npu_status run_conv(Cursor &c, const npu_group_attrs &at, const npu_memref *out,
     return gfail(NPU_ERR_INVALID_ARG, "%zu rank-4 arguments after the filter: expected %zu "
                  "destinations and at most one residual", r4.size(), nd);
   const npu_memref *res = nullptr;
-  if (r4.size() == nd + 1) {
+  if (at.res_arg != 0) {
+    for (size_t i = 0; i + 1 < r4.size(); ++i)
+      if (r4_pos[i] == (size_t)at.res_arg) res = r4[i];
+    if (!res || r4.size() != nd + 1)
+      return gfail(NPU_ERR_INVALID_ARG, "res_arg %d does not name a rank-4 operand before the "
+                   "last destination (with %zu generics)", at.res_arg, nd);
+    if (!res->aligned) return gfail(NPU_ERR_INVALID_ARG, "the residual argument has no data");
+  } else if (r4.size() == nd + 1) {
     if (nd == 1) {
       res = r4[0];
     } else {

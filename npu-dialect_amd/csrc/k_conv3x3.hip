@@ -451,6 +451,47 @@ __global__ __launch_bounds__(256, NCH <= 2 && WMAX <= 56 ? 2 : 1) void conv3x3_s
   }
 }
 
+// Output rows [first, end) of the 3x3 / pad-1 conv for 64 filters from f0,
+// computed the way the sequential f32 loops compute them: the accumulator
+// starts at +0, every tap row, tap column and channel in that order adds
+// the rounded product of the padded input (zero outside the image) and the
+// filter value as a separate f32 multiply and add, then the bias and the
+// activation.  Bit-identical to those loops, so +-Inf, NaN and values the
+// bf16 split cannot carry come out as they do there.  The x6 kernel runs it
+// over its rows when a split value fell outside the split's domain.
+template <int C>
+__device__ __forceinline__ void conv3x3_exact_rows(
+    const float *__restrict__ x, const float *__restrict__ w, const float *__restrict__ bias,
+    float *__restrict__ out, int H, int W, int F, int act, int f0, int first, int end) {
+#pragma clang fp contract(off)
+  const int f = f0 + (threadIdx.x & 63);
+  const float *const wf = w + (size_t)f * 9 * C;
+  const ActBounds ab = act_bounds(act);
+  const float b = bias ? bias[f] : 0.0f;
+  for (int p = first * W + (int)(threadIdx.x >> 6); p < end * W; p += (int)(blockDim.x >> 6)) {
+    const int g = p / W, ow = p - g * W;  // g = n * H + oh
+    const int n = g / H, oh = g - n * H;
+    float acc = 0.0f;
+    for (int kh = 0; kh < 3; ++kh) {
+      const int ih = oh + kh - 1;
+      for (int kw = 0; kw < 3; ++kw) {
+        const int iw = ow + kw - 1;
+        const bool in = ih >= 0 && ih < H && iw >= 0 && iw < W;
+        const float *xp = x + ((size_t)(n * H + (in ? ih : 0)) * W + (in ? iw : 0)) * C;
+        const float *wp = wf + (kh * 3 + kw) * C;
+#pragma unroll 4
+        for (int c = 0; c < C; ++c) {
+          const float a = in ? xp[c] : 0.0f;
+          const float prod = a * wp[c];
+          acc = acc + prod;
+        }
+      }
+    }
+    const float v = bias ? acc + b : acc;
+    out[(size_t)p * F + f] = act_clamp(v, ab);
+  }
+}
+
 // f32 variant of the persistent walk on the bf16 matrix pipe.  Every input
 // and filter value is split into its three bf16 parts (split_parts) and each
 // 32-channel run is multiplied with the six part products (mma_x6): 6 x 16
@@ -505,10 +546,12 @@ __global__ __launch_bounds__(512, 1) void conv3x3_x6_kernel(
   constexpr int XB_SUM = KSPLIT ? 4 * NXB * 64 * 16 : 0;
   constexpr int XB_STAGE = 8 * 16 * WSR;
   constexpr int XB = XB_SUM > XB_STAGE ? XB_SUM : XB_STAGE;  // partial sums, or filter staging (before the walk)
-  static_assert(HALOB + TRASHB + XB <= 160 * 1024, "LDS");
-  __shared__ __attribute__((aligned(16))) char lds[HALOB + TRASHB + XB];
+  constexpr int FLAGB = 16;                          // set when a value fell outside the split's domain
+  static_assert(HALOB + TRASHB + XB + FLAGB <= 160 * 1024, "LDS");
+  __shared__ __attribute__((aligned(16))) char lds[HALOB + TRASHB + XB + FLAGB];
   char *const halo = lds;
   char *const xch = lds + HALOB + TRASHB;
+  int *const miss_flag = reinterpret_cast<int *>(lds + HALOB + TRASHB + XB);
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int r = lane & 15, q = lane >> 4;
@@ -570,6 +613,10 @@ __global__ __launch_bounds__(512, 1) void conv3x3_x6_kernel(
   // All halo rows of the tile at g (fetch_tile), written to slots b, b+1,
   // ... (mod NSLOT) by put_tile; rows outside the image are zero.  Used where
   // no prefetch could run: the first tile, and a tile that starts an image.
+  // Lanes whose split values fell outside the split's domain (Inf, NaN, or
+  // magnitudes the split does not carry), over the whole walk: such a
+  // workgroup recomputes its rows on the exact path at the end.
+  uint64_t miss = 0;
   u32x4 fraw[TR + 2][LPR];
   auto fetch_tile = [&](int g) __attribute__((always_inline)) {
     const int n = g / H, h0 = g - n * H;
@@ -577,21 +624,22 @@ __global__ __launch_bounds__(512, 1) void conv3x3_x6_kernel(
     for (int hr = 0; hr < TR + 2; ++hr) load_row(fraw[hr], n * H + min(max(h0 + hr - 1, 0), H - 1));
   };
   // run j of halo row hr of the tile at g, into slot b + hr
-  auto put_fraw = [&](int g, int b, int hr, int j) __attribute__((always_inline)) {
+  auto put_fraw = [&](int g, int b, int hr, int j, SplitDomainBounds &bd) __attribute__((always_inline)) {
     const int rows = tile_rows(g), ih = g % H + hr - 1, slot = (b + hr) % NSLOT;
     if (hr > rows + 1) {
       // not a halo row of a short tile
     } else if (ih >= 0 && ih < H) {
       put_run(waddr(slot, j), split_parts(fraw[hr][j]));
+      bd.fold(fraw[hr][j]);
     } else {
       zero_run(waddr(slot, j));
     }
   };
-  auto put_tile = [&](int g, int b, int hr0, int hr1) __attribute__((always_inline)) {
+  auto put_tile = [&](int g, int b, int hr0, int hr1, SplitDomainBounds &bd) __attribute__((always_inline)) {
 #pragma unroll
     for (int hr = hr0; hr < hr1; ++hr)
 #pragma unroll
-      for (int j = 0; j < LPR; ++j) put_fraw(g, b, hr, j);
+      for (int j = 0; j < LPR; ++j) put_fraw(g, b, hr, j, bd);
   };
   // The next tile's new rows (its halo rows 2..TR+1: image rows gn+1..gn+TR
   // for a tile starting at gn), fetched a tile ahead.  Unconditional (rows
@@ -633,6 +681,7 @@ __global__ __launch_bounds__(512, 1) void conv3x3_x6_kernel(
   const int g1 = range.first + tile_rows(range.first);
   prefetch(g1 < range.end ? g1 : range.first);
   Frag16 fr[9][3];  // [tap][part]
+  SplitDomainBounds wbd;  // this wave's filter values (and the first tile's first rows)
   {
     char *const wslot = xch + wave * 16 * WSR;
     const int fl = lane / 8, pc = lane - fl * 8;
@@ -640,7 +689,10 @@ __global__ __launch_bounds__(512, 1) void conv3x3_x6_kernel(
     for (int t = 0; t < 9; ++t) {
       Parts4 p[NWI];
 #pragma unroll
-      for (int i = 0; i < NWI; ++i) p[i] = split_parts(wraw[t][i]);
+      for (int i = 0; i < NWI; ++i) {
+        p[i] = split_parts(wraw[t][i]);
+        wbd.fold(wraw[t][i]);
+      }
 #pragma unroll
       for (int k = 0; k < 3; ++k) {
 #pragma unroll
@@ -656,7 +708,7 @@ __global__ __launch_bounds__(512, 1) void conv3x3_x6_kernel(
   // index registers and those rows held over would not fit without spills.
   constexpr bool EARLY = WFIX > 0;
   int base = 0;  // slot of the current tile's halo row 0
-  put_tile(range.first, base, 0, EARLY ? 2 : TR + 2);
+  put_tile(range.first, base, 0, EARLY ? 2 : TR + 2, wbd);
   // zero-padding columns 0 and W+1 of every slot (lanes write no record there)
   constexpr int ZR = 3 * PST / 16;  // 16-byte runs of a record's parts
   for (int i = tid; i < NSLOT * 2 * ZR; i += NT) {
@@ -669,6 +721,19 @@ __global__ __launch_bounds__(512, 1) void conv3x3_x6_kernel(
   for (int t = 0; t < 9; ++t)
 #pragma unroll
     for (int k = 0; k < 3; ++k) settle(fr[t][k].u);
+  // The accumulators start at the bias: a subnormal bias is carried by the
+  // exact path (the MFMA's treatment of it is not the f32 add's).
+  {
+    bool sub = false;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const uint32_t t = __float_as_uint(bv[e]) << 1;
+      sub |= (t != 0u) & (t < (1u << 24));
+    }
+    miss |= __builtin_amdgcn_ballot_w64(sub);
+  }
+  miss |= __builtin_amdgcn_ballot_w64(wbd.miss());
+  if (tid == 0) *miss_flag = 0;
   __syncthreads();  // halo, padding and every wave's filter staging done (staging shares the exchange area)
 
   auto tile = [&](int g, auto first) __attribute__((always_inline)) {
@@ -692,6 +757,7 @@ __global__ __launch_bounds__(512, 1) void conv3x3_x6_kernel(
     f32x4 acc[NBW];
 #pragma unroll
     for (int ii = 0; ii < NBW; ++ii) acc[ii] = f32x4{bv[0], bv[1], bv[2], bv[3]};
+    SplitDomainBounds nb;  // the new rows split during this tile
     // Steps s = (tap t, block ii) in order; each reads its block's three
     // pixel parts from LDS D steps ahead and issues six MFMAs.  From a third
     // of the way in, one new-row run is split and written every SPS steps.
@@ -719,17 +785,22 @@ __global__ __launch_bounds__(512, 1) void conv3x3_x6_kernel(
           // the first tile's halo rows 2 and 3, then a barrier before tap row 1
           constexpr int NF = TR * LPR, SPF = (3 * NB - 1) / NF > 0 ? (3 * NB - 1) / NF : 1;
           static_assert(SPF * (NF - 1) < 3 * NB - 1, "the first tile's last rows are written before tap row 1");
-          if constexpr (s % SPF == 0 && s / SPF < NF) put_fraw(g, 0, 2 + (s / SPF) / LPR, (s / SPF) % LPR);
+          if constexpr (s % SPF == 0 && s / SPF < NF) put_fraw(g, 0, 2 + (s / SPF) / LPR, (s / SPF) % LPR, nb);
           if constexpr (s == 3 * NB - 1) __syncthreads();
         }
         if constexpr (s >= S0 && (s - S0) % SPS == 0 && (s - S0) / SPS < NSPL) {
+          // Branch-free, so the split's vector work stays in this step's
+          // region beside its MFMAs: a row past the image is written as
+          // zeros by a uniform select.
           constexpr int e = (s - S0) / SPS, k = e / LPR, j = e % LPR;
-          const Parts4 p = split_parts(nraw[k][j]);
-          const uint32_t a = waddr((bnext + 2 + k) % NSLOT, j);
-          if ((nok >> k) & 1u)
-            put_run(a, p);
-          else
-            zero_run(a);
+          const bool ok = (nok >> k) & 1u;
+          Parts4 p = split_parts(nraw[k][j]);
+          nb.fold(nraw[k][j]);  // (a row past the image is the clamped last row: checked anyway)
+          const uint2 z = make_uint2(0u, 0u);
+          p.h = ok ? p.h : z;
+          p.m = ok ? p.m : z;
+          p.l = ok ? p.l : z;
+          put_run(waddr((bnext + 2 + k) % NSLOT, j), p);
         }
         __builtin_amdgcn_sched_barrier(0);
       });
@@ -757,6 +828,8 @@ __global__ __launch_bounds__(512, 1) void conv3x3_x6_kernel(
       // finished by half 0, [NXB, NBW) by half 1, in two rounds through an
       // exchange area of NXB blocks per filter group.
       char *const xg = xch + fg * NXB * 1024 + lane * 16;
+      miss |= __builtin_amdgcn_ballot_w64(nb.miss());
+      if (miss != 0 && lane == 0) *miss_flag = 1;  // read after the walk
       if (half == 1) {
 #pragma unroll
         for (int ii = 0; ii < NXB; ++ii) *reinterpret_cast<f32x4 *>(xg + ii * 1024) = acc[ii];
@@ -779,6 +852,8 @@ __global__ __launch_bounds__(512, 1) void conv3x3_x6_kernel(
     } else {
 #pragma unroll
       for (int ii = 0; ii < NBW; ++ii) store(half + 2 * ii, acc[ii]);
+      miss |= __builtin_amdgcn_ballot_w64(nb.miss());
+      if (miss != 0 && lane == 0) *miss_flag = 1;  // read after the walk
       __syncthreads();  // every wave's multiply (halo reads) and new-row writes are done
     }
     // The tile after next: fetched now, written during the next tile.  With
@@ -790,7 +865,10 @@ __global__ __launch_bounds__(512, 1) void conv3x3_x6_kernel(
     prefetch(g2 < range.end ? g2 : g);
     if (gn < range.end && hn == 0) {  // the next tile starts an image: its rows were not prefetched
       fetch_tile(gn);
-      put_tile(gn, bnext, 0, TR + 2);
+      SplitDomainBounds ib;
+      put_tile(gn, bnext, 0, TR + 2, ib);
+      miss |= __builtin_amdgcn_ballot_w64(ib.miss());
+      if (miss != 0 && lane == 0) *miss_flag = 1;
       __syncthreads();
     }
     base = bnext;
@@ -798,6 +876,15 @@ __global__ __launch_bounds__(512, 1) void conv3x3_x6_kernel(
   tile(range.first, std::integral_constant<bool, EARLY>{});
   for (int g = range.first + tile_rows(range.first); g < range.end; g += tile_rows(g))
     tile(g, std::integral_constant<bool, false>{});
+  // A value outside the split's domain anywhere in the walk (every split
+  // precedes the last tile's barrier, which also published the flag): once
+  // every wave's stores have completed, the range is computed again on the
+  // exact path, whose stores then land after them.
+  if (*miss_flag != 0) {
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    conv3x3_exact_rows<C>(x, w, bias, out, H, W, F, act, blockIdx.y * 64, range.first, range.end);
+  }
 }
 
 // Vector-ALU instructions per wave of the persistent kernel, from its

@@ -106,6 +106,10 @@ __global__ __launch_bounds__(kWaves * 64) void matmul_bias_act_f32_kernel(
 #pragma unroll
     for (int u = 0; u < kBatch; ++u) {
       *reinterpret_cast<u32x4 *>(myb + (u * 16 + br) * kBRow + 4 * bq) = bv[u].u;
+      // the reads below take values other lanes of this wave just wrote:
+      // order them after the writes explicitly
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
 #pragma unroll
       for (int s = 0; s < 4; ++s)
         acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a[u].f[s], myb[(u * 16 + 4 * q + s) * kBRow + r], acc, 0, 0, 0);

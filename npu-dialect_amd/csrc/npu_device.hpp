@@ -205,11 +205,20 @@ __device__ __forceinline__ Frag16 load16(const void *p) {
 // does the 16x work of an f32 MFMA (32 clocks for 16x16x4), so the six
 // products take 6 * 16 clocks where the f32 instructions take 8 * 32.
 //
-// Special values: a NaN gives a NaN h (or, when its payload lies in the low
-// bits only, an infinite h and NaN r, m, l), so NaN propagates.  An
-// infinite a gives h = a and r = Inf - Inf = NaN: an infinite operand gives
-// NaN where the f32 sum gives +-Inf.  (Splitting it into (a, 0, 0) would not
-// help: the products of a with the zero parts of a finite b are Inf * 0.)
+// The split's domain: zero, or a finite magnitude in [2^-E, 2^E) with
+// E = kSplitDomainLog2.  There every part is exact (a's low part keeps its
+// bits far above bf16's subnormals), every part product that mma_x6 keeps
+// is exact in f32 or rounds at f32's subnormal spacing (the MFMA keeps f32
+// subnormals), every product of two such values is at least 2^-2E, and no
+// sum of products comes near the f32 range: the six products give the
+// f32 sum to f32 accuracy.  Outside it the split is not used: an infinite
+// a gives h = a and r = Inf - Inf = NaN (and splitting it into (a, 0, 0)
+// would not help: its products with the zero parts of a finite b are
+// Inf * 0), a value below 2^-102 loses its low part under bf16's
+// subnormals, and products of tiny values round differently from the f32
+// products.  A kernel that splits tests every value (SplitDomainBounds) and
+// computes the outputs such values reach without the split.
+constexpr int kSplitDomainLog2 = 55;
 struct Parts4 {  // parts of four f32 values, two bf16 per dword
   uint2 h, m, l;
 };
@@ -239,6 +248,34 @@ __device__ __forceinline__ Parts4 split_parts(u32x4 v) {
   p.l = make_uint2(cvt_pk_bf16(s0, s1), cvt_pk_bf16(s2, s3));
   return p;
 }
+// The domain test, spread over the runs a lane splits: fold() takes a
+// 16-byte run into two running bounds, the largest magnitude by IEEE
+// maximum (NaN in, NaN out, so NaN and Inf fail `< 2^E`) and the smallest
+// 2|bits| - 1 (the sign shifted out; zero wraps to 0xffffffff, above every
+// nonzero value); miss() compares them once with 2^E and 2 bits(2^-E) - 1.
+// Four values cost four shifts, a min3 and two maximum3.
+struct SplitDomainBounds {
+  uint32_t umin = 0xffffffffu;
+  float amax = 0.0f;
+  __device__ __forceinline__ void fold(u32x4 v) {
+    uint32_t u[4];
+    float a[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      u[e] = (v[e] << 1) + 0xffffffffu;
+      a[e] = __builtin_fabsf(__uint_as_float(v[e]));
+    }
+    umin = min(min(umin, u[0]), min(min(u[1], u[2]), u[3]));
+    amax = __builtin_elementwise_maximum(__builtin_elementwise_maximum(amax, a[0]),
+                                         __builtin_elementwise_maximum(a[1], __builtin_elementwise_maximum(a[2], a[3])));
+  }
+  __device__ __forceinline__ bool miss() const {
+    constexpr uint32_t LO2 = (uint32_t)(127 - kSplitDomainLog2) << 24;
+    const float big = __uint_as_float((uint32_t)(127 + kSplitDomainLog2) << 23);
+    return (umin < LO2 - 1u) | !(amax < big);
+  }
+};
+
 // acc += A * B over one 32-long k run, A and B given as their three parts.
 __device__ __forceinline__ void mma_x6(f32x4 &acc, const Frag16 (&a)[3], const Frag16 (&b)[3]) {
   acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[1].h, b[1].h, acc, 0, 0, 0);

@@ -19,6 +19,10 @@ void plans_reset();
 void plans_add(const npu_launch_plan &p);
 // Sets the calling thread's npu_last_error() message (defined in abi.hip).
 void set_last_error(const char *msg);
+// The typed entry points' descriptor check (rank, dtype, row-major
+// contiguity, alignment, element limit); on failure the message is the
+// thread's last error.
+npu_status memref_check(const npu_memref *m, const char *name, int32_t rank, int32_t dtype);
 
 // Per-kernel, per-device launch facts cached by kernel address (kernels of
 // one signature share a function type, so the type cannot be the key).

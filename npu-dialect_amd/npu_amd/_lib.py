@@ -80,7 +80,8 @@ class NpuArg(C.Structure):
 
 
 class NpuGroupAttrs(C.Structure):
-    """npu_group_attrs: per-chain activations, folded pad, heads, eps, scale."""
+    """npu_group_attrs: per-chain activations, folded pad, heads, eps, scale,
+    the residual operand's argument index."""
 
     _fields_ = [
         ("act", C.c_int32 * 4),
@@ -88,6 +89,7 @@ class NpuGroupAttrs(C.Structure):
         ("n_heads", C.c_int32),
         ("eps", C.c_float),
         ("scale", C.c_float),
+        ("res_arg", C.c_int32),
     ]
 
 

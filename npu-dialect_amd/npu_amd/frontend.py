@@ -284,6 +284,10 @@ def from_torch(module, x, elem="f32", name="model"):
         res, act, last = None, "none", n
         u = single_user(last)
         if u is not None and kind(u) == "add":
+            if u.kwargs:
+                # torch.add(y, x, alpha=a) scales x: not a plain residual add
+                raise NotImplementedError(f"{u.name}: add with {sorted(u.kwargs)} "
+                                          "(only a plain residual add is lowered)")
             other = [a for a in u.args if a is not last]
             if len(other) != 1 or len(u.args) != 2 or other[0] not in vals:
                 raise NotImplementedError(f"{u.name}: an add that is not a residual of a "

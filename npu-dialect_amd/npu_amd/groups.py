@@ -194,11 +194,12 @@ def _group_arg(x, keep):
 
 
 def group_launch(outlined_name, ins, outs, act=("none",), pad=0, n_heads=0, eps=0.0, scale=0.0,
-                 stream=None):
+                 stream=None, res_arg=0):
     """npu_group_launch: runs the outlined group(s) `outlined_name` ('+'-joined
     for a chain) on its arguments in the outlined function's order: ``ins``
     are tensors, Empty placeholders and the fill value (a float); ``outs`` the
-    result tensors."""
+    result tensors.  ``res_arg``: the index in ``ins`` of a conv group's
+    residual operand (0: none named)."""
     keep = []
     ia = (_lib.NpuArg * max(len(ins), 1))(*[_group_arg(x, keep) for x in ins])
     oa = (_lib.NpuArg * max(len(outs), 1))(*[_group_arg(x, keep) for x in outs])
@@ -206,6 +207,7 @@ def group_launch(outlined_name, ins, outs, act=("none",), pad=0, n_heads=0, eps=
     for i, a in enumerate(act):
         at.act[i] = ACT[a]
     at.pad, at.n_heads, at.eps, at.scale = int(pad), int(n_heads), float(eps), float(scale)
+    at.res_arg = int(res_arg)
     st = _lib.lib().npu_group_launch(outlined_name.encode(), C.byref(at), ia, len(ins), oa,
                                      len(outs), _stream(stream))
     _check(st, f"npu_group_launch({outlined_name})")

@@ -57,6 +57,27 @@ static npu_arg mem2(npu_strided_memref_2d *d, void *data, int64_t r, int64_t c) 
   return a;
 }
 
+static npu_arg mem4(npu_strided_memref_4d *d, void *data, int64_t n, int64_t h, int64_t w,
+                    int64_t c) {
+  npu_arg a;
+  memset(&a, 0, sizeof a);
+  d->allocated = d->aligned = data;
+  d->offset = 0;
+  d->sizes[0] = n;
+  d->sizes[1] = h;
+  d->sizes[2] = w;
+  d->sizes[3] = c;
+  d->strides[3] = 1;
+  d->strides[2] = c;
+  d->strides[1] = w * c;
+  d->strides[0] = h * w * c;
+  a.rank = 4;
+  a.descriptor = d;
+  a.dtype = NPU_F32;
+  a.kind = NPU_ARG_MEMREF;
+  return a;
+}
+
 static npu_arg mem1(npu_strided_memref_1d *d, void *data, int64_t n) {
   npu_arg a;
   memset(&a, 0, sizeof a);
@@ -108,7 +129,7 @@ static void validate(void) {
 
   in[3] = mem2(&dBad, B, 255, 512);
   s = npu_group_launch("fused_fill_matmul_generic_0", &at, in, 5, out, 1, NULL);
-  CHECK(s == NPU_ERR_INVALID_ARG && strstr(npu_last_error(), "expected K"),
+  CHECK(s == NPU_ERR_INVALID_ARG && strstr(npu_last_error(), "K differs"),
         "B rows != K: status %d (%s)", s, npu_last_error());
   in[3] = mem2(&dB, B, 256, 512);
 
@@ -141,6 +162,46 @@ static void validate(void) {
                        NULL);
   CHECK(s == NPU_ERR_INVALID_ARG && strstr(npu_last_error(), "intermediate"),
         "mlp without storage: status %d (%s)", s, npu_last_error());
+  /* every chain is checked before the first launches: a second chain whose
+   * weight does not match the first chain's result is rejected as such (on a
+   * machine without a GPU a launch of the first chain would fail instead) */
+  npu_strided_memref_2d dW2b;
+  in2[4] = mem2(&dE, A, 128, 512);
+  in2[6] = mem2(&dW2b, B, 500, 256);
+  s = npu_group_launch("fused_fill_matmul_generic_fill_matmul_generic_0", &at, in2, 8, out2, 1,
+                       NULL);
+  CHECK(s == NPU_ERR_INVALID_ARG && strstr(npu_last_error(), "K differs"),
+        "mlp, second weight: status %d (%s)", s, npu_last_error());
+  in2[6] = mem2(&dW2, B, 512, 256);
+  npu_strided_memref_2d dO3;
+  npu_arg out3[1] = {mem2(&dO3, O, 128, 255)};
+  s = npu_group_launch("fused_fill_matmul_generic_fill_matmul_generic_0", &at, in2, 8, out3, 1,
+                       NULL);
+  CHECK(s == NPU_ERR_INVALID_ARG && strstr(npu_last_error(), "result"),
+        "mlp, result shape: status %d (%s)", s, npu_last_error());
+  /* a conv group's residual named by index must be a rank-4 operand before
+   * the last destination */
+  {
+    npu_strided_memref_4d dI4, dX4, dW4, dR4, dE41, dE42, dO4;
+    void *X = (void *)0x400000, *W = (void *)0x500000, *R = (void *)0x600000;
+    npu_arg ic[7] = {scalar(0.0), mem4(&dI4, NULL, 2, 8, 8, 16), mem4(&dX4, X, 2, 8, 8, 16),
+                     mem4(&dW4, W, 16, 3, 3, 16), mem4(&dR4, R, 2, 8, 8, 16),
+                     mem4(&dE41, O, 2, 8, 8, 16), mem4(&dE42, O, 2, 8, 8, 16)};
+    npu_arg oc[1] = {mem4(&dO4, O, 2, 8, 8, 16)};
+    npu_group_attrs ac = relu_attrs();
+    ac.pad = 1;
+    ac.res_arg = 6;
+    s = npu_group_launch("fused_fill_linalg_conv_2d_nhwc_fhwc_generic_generic_0", &ac, ic, 7, oc, 1,
+                         NULL);
+    CHECK(s == NPU_ERR_INVALID_ARG && strstr(npu_last_error(), "res_arg"),
+          "res_arg at the last destination: status %d (%s)", s, npu_last_error());
+    /* without res_arg, destinations with data leave the residual ambiguous */
+    ac.res_arg = 0;
+    s = npu_group_launch("fused_fill_linalg_conv_2d_nhwc_fhwc_generic_generic_0", &ac, ic, 7, oc, 1,
+                         NULL);
+    CHECK(s == NPU_ERR_INVALID_ARG && strstr(npu_last_error(), "residual"),
+          "ambiguous residual: status %d (%s)", s, npu_last_error());
+  }
 }
 
 /* --- launches ------------------------------------------------------------ */
@@ -253,6 +314,60 @@ static void gpu(void) {
     CHECK(npu_last_launch_plans(p, 4) == 1, "one launch plan recorded");
     free(h); free(hA); free(hB); free(hb); free(ref);
     hipFree(A); hipFree(B); hipFree(b); hipFree(O);
+  }
+  /* a ResNet-style conv group (add of the block input, then ReLU, in two
+   * generics) called the way a bufferized host module calls it: every
+   * destination allocated, the residual named by attrs.res_arg */
+  {
+    const int64_t N = 2, H = 8, W = 8, C = 16, F = 16;
+    const int64_t nx = N * H * W * C, nw = F * 9 * C, no = N * H * W * F;
+    float *hx = malloc(nx * 4), *hw = malloc(nw * 4), *hr = malloc(no * 4);
+    float *conv = malloc(no * 4);
+    uint64_t seed = 0x4e505502;
+    for (int64_t i = 0; i < nx; ++i) hx[i] = urand(&seed);
+    for (int64_t i = 0; i < nw; ++i) hw[i] = urand(&seed) * 0.1f;
+    for (int64_t i = 0; i < no; ++i) hr[i] = urand(&seed);
+    orc_block_conv_bias_act_f32(hx, hw, NULL, conv, N, H, W, C, F, 3, 3, 1, 0);
+    float *X = dev_from(hx, nx), *Wt = dev_from(hw, nw), *R = dev_from(hr, no);
+    float *D1 = dev_filled(no, 7), *D2 = dev_filled(no, 7), *I = dev_filled(no, 7);
+    float *O = dev_filled(no, -1);
+    npu_strided_memref_4d dI, dX, dW, dR, dD1, dD2, dO;
+    npu_arg in[7] = {scalar(0.0), mem4(&dI, I, N, H, W, F), mem4(&dX, X, N, H, W, C),
+                     mem4(&dW, Wt, F, 3, 3, C), mem4(&dR, R, N, H, W, F),
+                     mem4(&dD1, D1, N, H, W, F), mem4(&dD2, D2, N, H, W, F)};
+    npu_arg out[1] = {mem4(&dO, O, N, H, W, F)};
+    npu_group_attrs ac = relu_attrs();
+    ac.pad = 1;
+    ac.res_arg = 4;
+    npu_status s = npu_group_launch("fused_fill_linalg_conv_2d_nhwc_fhwc_generic_generic_3", &ac,
+                                    in, 7, out, 1, NULL);
+    CHECK(s == NPU_OK, "conv + residual + relu: %s", npu_last_error());
+    float *h = host_of(O, no);
+    int bad = 0;
+    double worst = 0;
+    for (int64_t n = 0; n < N; ++n)
+      for (int64_t y = 0; y < H; ++y)
+        for (int64_t x = 0; x < W; ++x)
+          for (int64_t f = 0; f < F; ++f) {
+            const int64_t o = ((n * H + y) * W + x) * F + f;
+            double mag = fabs(hr[o]);
+            for (int64_t ky = 0; ky < 3; ++ky)
+              for (int64_t kx = 0; kx < 3; ++kx) {
+                const int64_t iy = y + ky - 1, ix = x + kx - 1;
+                if (iy < 0 || iy >= H || ix < 0 || ix >= W) continue;
+                for (int64_t c = 0; c < C; ++c)
+                  mag += fabs((double)hx[((n * H + iy) * W + ix) * C + c] * hw[((f * 3 + ky) * 3 + kx) * C + c]);
+              }
+            float ref = conv[o] + hr[o];
+            ref = ref > 0.0f ? ref : 0.0f;
+            const double err = fabs((double)h[o] - ref);
+            worst = fmax(worst, err / mag);
+            bad += err > 1e-5 * mag;
+          }
+    CHECK(bad == 0, "conv + residual + relu: %d outputs outside 1e-5 * mag (worst %.3g)", bad, worst);
+    printf("conv + residual + relu (res_arg) vs oracle: worst |err|/mag = %.3g\n", worst);
+    free(h); free(hx); free(hw); free(hr); free(conv);
+    hipFree(X); hipFree(Wt); hipFree(R); hipFree(D1); hipFree(D2); hipFree(I); hipFree(O);
   }
 }
 

@@ -91,6 +91,22 @@ def test_torch_mlp_is_a_matmul_chain():
     assert list(params["w1"].shape) == [64, 128]   # nn.Linear's [out, in], transposed
 
 
+class _ScaledResidual(nn.Module):
+    """conv -> torch.add(y, x, alpha=2): the residual is scaled, not added."""
+
+    def __init__(self):
+        super().__init__()
+        self.c = nn.Conv2d(16, 16, 3, padding=1)
+
+    def forward(self, x):
+        return torch.relu(torch.add(self.c(x), x, alpha=2))
+
+
+def test_torch_add_with_alpha_is_refused():
+    with pytest.raises(NotImplementedError, match="alpha"):
+        frontend.from_torch(_ScaledResidual(), torch.rand(1, 16, 8, 8))
+
+
 @pytest.mark.parametrize("module,why", [
     (nn.Sequential(nn.Conv2d(16, 16, 3, stride=2, padding=1)), "stride"),
     (nn.Sequential(nn.Conv2d(16, 16, 3, padding=1, groups=4)), "grouped"),
