@@ -139,6 +139,29 @@ npu_status fused_conv2d_nhwc_bias_res_act(const npu_memref *x, const npu_memref 
                                           const npu_memref *out, int32_t pad, int32_t act,
                                           npu_stream stream);
 
+/* The reference's own layout: group `pad -> fill -> conv_2d_nchw_fchw ->
+ * generic...` (test/conv2d_relu.mlir:7-42, test/resnet_block.mlir,
+ * test/resnet50_block.mlir, test/mobilenet_block.mlir; outlined as
+ * @fused_fill_conv2d_generic[_generic]_<idx>,
+ * OutlineFusedGroupsPass.cpp:69-82), with the zero pad folded into the
+ * launch.  f32 (f16 text runs as f32, tools/harness/e2e_verify.py:163-164).
+ *   x    f32 [N,C,H,W]       w f32 [F,C,KH,KW], KH = KW = 1 or 3
+ *   bias f32 [F] (aligned may be NULL)
+ *   out  f32 [N,F,Ho,Wo] = act(conv(pad(x), w) + bias), Ho = H + 2*pad - KH + 1
+ * Stride 1.  Computed on the f32 matrix pipe: within f32 accuracy of the
+ * sequential f32 sum, +-Inf and NaN as there. */
+npu_status fused_conv2d_nchw_bias_act(const npu_memref *x, const npu_memref *w,
+                                      const npu_memref *bias, const npu_memref *out,
+                                      int32_t pad, int32_t act, npu_stream stream);
+
+/* The same with the residual term of a ResNet block's add generic
+ * (test/resnet_block.mlir:55-67, test/resnet50_block.mlir:77-102):
+ *   res  f32 [N,F,Ho,Wo]     out = act(conv(pad(x), w) + bias + res) */
+npu_status fused_conv2d_nchw_bias_res_act(const npu_memref *x, const npu_memref *w,
+                                          const npu_memref *bias, const npu_memref *res,
+                                          const npu_memref *out, int32_t pad, int32_t act,
+                                          npu_stream stream);
+
 /* Group chain of the int8 ResNet-50 bottleneck (int8 restatement of
  * test/resnet50_block.mlir:5-105, NHWC, zero points 0), fused across both
  * tensor.pads into one launch:
@@ -327,6 +350,11 @@ typedef struct npu_group_attrs {
  *     generics, attrs->res_arg names the residual's index in `in` (when it
  *     is 0, the destinations before the last must be passed without data,
  *     NULL, which tells them from the residual)
+ *   fill_conv2d_generic[_generic...] (the reference's linalg.conv_2d_nchw_fchw,
+ *     test/conv2d_relu.mlir, test/resnet_block.mlir, test/resnet50_block.mlir,
+ *     test/mobilenet_block.mlir)          -> fused_conv2d_nchw_bias_act, or
+ *     with a residual term fused_conv2d_nchw_bias_res_act; the same argument
+ *     order as the NHWC group, every tensor NCHW / FCHW
  *   fill_linalg_conv_2d_nhwc_fhwc_generic + the depthwise / project group(s)
  *     of an inverted residual block after its tensor.pad -> fused_irb_f32
  *     (cst, init_e, x, we[E,1,1,C], dest_e, init_d, wdw[3,3,E], dest_d,

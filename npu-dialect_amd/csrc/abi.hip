@@ -357,6 +357,73 @@ npu_status fused_conv2d_nhwc_bias_res_act(const npu_memref *x, const npu_memref 
                     "fused_conv2d_nhwc_bias_res_act launch");
 }
 
+namespace {
+
+// fused_conv2d_nchw_bias_act and its residual variant.
+npu_status conv_nchw_entry(const npu_memref *x, const npu_memref *w, const npu_memref *bias,
+                           const npu_memref *res, const npu_memref *out, int32_t pad, int32_t act,
+                           npu_stream stream, const char *name) {
+  npu::plans_reset();
+  const void *px, *pw, *pbias = nullptr, *pres = nullptr, *po;
+  NPU_TRY(check_memref(x, "x", 4, NPU_F32, &px));
+  NPU_TRY(check_memref(w, "w", 4, NPU_F32, &pw));
+  NPU_TRY(check_memref(out, "out", 4, NPU_F32, &po));
+  NPU_TRY(check_act(act));
+  const int64_t N = x->sizes[0], C = x->sizes[1], H = x->sizes[2], W = x->sizes[3];
+  const int64_t F = w->sizes[0], KH = w->sizes[2], KW = w->sizes[3];
+  if (w->sizes[1] != C)
+    return fail(NPU_ERR_INVALID_ARG, "w: channels %lld, expected C = %lld",
+                (long long)w->sizes[1], (long long)C);
+  if (!npu::conv2d_nchw_supported((int)KH, (int)KW))
+    return fail(NPU_ERR_UNSUPPORTED, "w: %lldx%lld filter (1x1 and 3x3 are supported)",
+                (long long)KH, (long long)KW);
+  if (pad < 0) return fail(NPU_ERR_INVALID_ARG, "pad %d is negative", pad);
+  const int64_t Ho = H + 2 * pad - KH + 1, Wo = W + 2 * pad - KW + 1;
+  if (Ho <= 0 || Wo <= 0) return fail(NPU_ERR_INVALID_ARG, "empty output (%lld x %lld)",
+                                      (long long)Ho, (long long)Wo);
+  if (out->sizes[0] != N || out->sizes[1] != F || out->sizes[2] != Ho || out->sizes[3] != Wo)
+    return fail(NPU_ERR_INVALID_ARG, "out: [%lld,%lld,%lld,%lld], expected [%lld,%lld,%lld,%lld]",
+                (long long)out->sizes[0], (long long)out->sizes[1], (long long)out->sizes[2],
+                (long long)out->sizes[3], (long long)N, (long long)F, (long long)Ho,
+                (long long)Wo);
+  if (!absent(bias)) {
+    NPU_TRY(check_memref(bias, "bias", 1, NPU_F32, &pbias));
+    if (bias->sizes[0] != F)
+      return fail(NPU_ERR_INVALID_ARG, "bias: size %lld, expected F = %lld",
+                  (long long)bias->sizes[0], (long long)F);
+  }
+  if (res) {
+    NPU_TRY(check_memref(res, "res", 4, NPU_F32, &pres));
+    for (int d = 0; d < 4; ++d)
+      if (res->sizes[d] != out->sizes[d])
+        return fail(NPU_ERR_INVALID_ARG, "res: [%lld,%lld,%lld,%lld], expected the output's shape",
+                    (long long)res->sizes[0], (long long)res->sizes[1], (long long)res->sizes[2],
+                    (long long)res->sizes[3]);
+  }
+  npu::ConvArgs a{px, pw, static_cast<const float *>(pbias), const_cast<void *>(po),
+                  (int)N, (int)H, (int)W, (int)C, (int)F, (int)KH, (int)KW, pad,
+                  (int)Ho, (int)Wo, act, pres};
+  return hip_status(npu::launch_conv2d_nchw_f32(a, static_cast<hipStream_t>(stream)), name);
+}
+
+}  // namespace
+
+npu_status fused_conv2d_nchw_bias_act(const npu_memref *x, const npu_memref *w,
+                                      const npu_memref *bias, const npu_memref *out,
+                                      int32_t pad, int32_t act, npu_stream stream) {
+  return conv_nchw_entry(x, w, bias, nullptr, out, pad, act, stream,
+                         "fused_conv2d_nchw_bias_act launch");
+}
+
+npu_status fused_conv2d_nchw_bias_res_act(const npu_memref *x, const npu_memref *w,
+                                          const npu_memref *bias, const npu_memref *res,
+                                          const npu_memref *out, int32_t pad, int32_t act,
+                                          npu_stream stream) {
+  if (!res) return fail(NPU_ERR_INVALID_ARG, "res: null descriptor");
+  return conv_nchw_entry(x, w, bias, res, out, pad, act, stream,
+                         "fused_conv2d_nchw_bias_res_act launch");
+}
+
 npu_status fused_qbottleneck_i8(const npu_memref *x, const npu_memref *w1,
                                 const npu_memref *w2, const npu_memref *w3,
                                 const npu_memref *m1, const npu_memref *s1,

@@ -261,7 +261,7 @@ npu_status run_matmuls(Cursor &c, const npu_group_attrs &at, int chains, const n
 // destinations before the last must be passed without data (NULL) and the
 // one rank-4 argument with data among them is the residual.
 npu_status run_conv(Cursor &c, const npu_group_attrs &at, const npu_memref *out,
-                    npu_stream stream, PlanLog &log, int n_generic) {
+                    npu_stream stream, PlanLog &log, int n_generic, bool nchw) {
   G_TRY(c.fill_value());
   const npu_memref *init, *x, *w, *bias = nullptr;
   G_TRY(c.memref(4, "conv accumulator (tensor.empty)", &init));
@@ -316,12 +316,20 @@ npu_status run_conv(Cursor &c, const npu_group_attrs &at, const npu_memref *out,
                  shape_str(*init).c_str(), shape_str(*out).c_str());
   npu_memref none{};
   none.rank = 1;
-  if (res)
+  if (nchw) {
+    if (res)
+      G_TRY(typed(fused_conv2d_nchw_bias_res_act(x, w, bias ? bias : &none, res, out, at.pad,
+                                                 at.act[0], stream)));
+    else
+      G_TRY(typed(fused_conv2d_nchw_bias_act(x, w, bias ? bias : &none, out, at.pad, at.act[0],
+                                             stream)));
+  } else if (res) {
     G_TRY(typed(fused_conv2d_nhwc_bias_res_act(x, w, bias ? bias : &none, res, out, at.pad,
                                                at.act[0], stream)));
-  else
+  } else {
     G_TRY(typed(fused_conv2d_nhwc_bias_act(x, w, bias ? bias : &none, out, at.pad, at.act[0],
                                            stream)));
+  }
   log.take();
   return NPU_OK;
 }
@@ -405,6 +413,8 @@ npu_status run_qbottleneck(Cursor &c, const npu_memref *out, npu_stream stream, 
 
 const char *kMatmul = "fill_matmul_generic";
 const char *kConv = "fill_linalg_conv_2d_nhwc_fhwc_generic";
+// linalg.conv_2d_nchw_fchw's short name is `conv2d` (OutlineFusedGroupsPass.cpp:69-82)
+const char *kConvNchw = "fill_conv2d_generic";
 const char *kQBottleneck =
     "fill_linalg_conv_2d_nhwc_fhwc_generic_fill_linalg_conv_2d_nhwc_fhwc_generic_"
     "fill_linalg_conv_2d_nhwc_fhwc_generic";
@@ -455,15 +465,17 @@ extern "C" npu_status npu_group_launch(const char *outlined_name, const npu_grou
                      NPU_GROUP_MAX_CHAINS);
       return run_matmuls(c, *attrs, k, &res.m, stream, log);
     }
-    // a conv followed by one or more generics
-    if (key.rfind(kConv, 0) == 0) {
+    // a conv followed by one or more generics, NHWC (authored) or NCHW (the
+    // reference's own)
+    for (const char *kc : {kConv, kConvNchw}) {
+      if (key.rfind(kc, 0) != 0) continue;
       int ng = 1;
-      size_t at = std::strlen(kConv);
+      size_t at = std::strlen(kc);
       while (key.compare(at, 8, "_generic") == 0 && key.size() >= at + 8) {
         ++ng;
         at += 8;
       }
-      if (at == key.size()) return run_conv(c, *attrs, &res.m, stream, log, ng);
+      if (at == key.size()) return run_conv(c, *attrs, &res.m, stream, log, ng, kc == kConvNchw);
     }
     if (key == kIrb) return run_irb(c, &res.m, stream, log);
     if (key == kQBottleneck) return run_qbottleneck(c, &res.m, stream, log);

@@ -116,6 +116,8 @@ SIGNATURES = {
                                            _P]),
     "fused_conv2d_nhwc_bias_act": (_I32, [_MR, _MR, _MR, _MR, _I32, _I32, _P]),
     "fused_conv2d_nhwc_bias_res_act": (_I32, [_MR, _MR, _MR, _MR, _MR, _I32, _I32, _P]),
+    "fused_conv2d_nchw_bias_act": (_I32, [_MR, _MR, _MR, _MR, _I32, _I32, _P]),
+    "fused_conv2d_nchw_bias_res_act": (_I32, [_MR, _MR, _MR, _MR, _MR, _I32, _I32, _P]),
     "fused_qbottleneck_i8": (_I32, [_MR] * 11 + [_P]),
     "fused_irb_f32": (_I32, [_MR] * 5 + [_P]),
     "fused_llama_qkv_rope": (_I32, [_MR] * 10 + [C.c_float, _P]),

@@ -157,14 +157,24 @@ def mlp(M, K, H, N, elem="f32"):
 
 def reference_workload(name):
     """Builder text of a reference test workload, by its file name:
-    test/matmul_relu.mlir (fill -> matmul 128x256 . 256x512 -> ReLU, f16) and
-    test/mlp.mlir.  They run on the GPU where the reference's files are not
+    test/matmul_relu.mlir (fill -> matmul 128x256 . 256x512 -> ReLU, f16),
+    test/mlp.mlir and the NCHW conv workloads test/conv2d_relu.mlir,
+    test/resnet_block.mlir, test/resnet50_block.mlir and
+    test/mobilenet_block.mlir (f16 text, conv_2d_nchw_fchw).  They run on the GPU where the reference's files are not
     present; a CPU test checks that each has the same ops, types, indexing maps
     and generic bodies as the reference's file."""
     if name == "matmul_relu.mlir":
         return matmul_bias_act(128, 256, 512, act="relu", bias=False, elem="f16")
     if name == "mlp.mlir":
         return mlp(128, 256, 512, 256, elem="f16")
+    if name == "conv2d_relu.mlir":
+        return nchw_conv_relu(1, 64, 64, 56, 56)
+    if name == "resnet_block.mlir":
+        return nchw_resnet_block(1, 64, 56, 56)
+    if name == "resnet50_block.mlir":
+        return model_zoo_bottleneck(1, 256, 64, 56, 56, True, name="resnet50_block")
+    if name == "mobilenet_block.mlir":
+        return model_zoo_bottleneck(1, 32, 192, 112, 112, False, name="mobilenet_block")
     raise KeyError(name)
 
 
@@ -479,6 +489,44 @@ def model_zoo_bottleneck(N, C, M, H, W, final_relu, elem="f16", name="bottleneck
         t += _nchw_eltwise("%y", ["%s"], xs, elem, relu, "%m")
         y = "%y"
     return t + f"  return {y} : {_t(xs, elem)}\n}}\n"
+
+
+def _nchw_pad(res, x, shape, p, elem):
+    ps = [shape[0], shape[1], shape[2] + 2 * p, shape[3] + 2 * p]
+    return (f"  {res} = tensor.pad {x} low[0, 0, {p}, {p}] high[0, 0, {p}, {p}] {{\n"
+            f"  ^bb0(%i0: index, %i1: index, %i2: index, %i3: index):\n"
+            f"    tensor.yield %cst : {elem}\n  }} : {_t(shape, elem)} to {_t(ps, elem)}\n")
+
+
+def nchw_conv_relu(N, C, F, H, W, elem="f16"):
+    """test/conv2d_relu.mlir's form: a zero pad of 1 in H and W, then fill ->
+    conv_2d_nchw_fchw 3x3 -> ReLU generic (`arith.maximumf` with 0)."""
+    xs, os_, ps = [N, C, H, W], [N, F, H, W], [N, C, H + 2, W + 2]
+    relu = [f"%z = arith.constant 0.0 : {elem}", f"%m = arith.maximumf %a0, %z : {elem}"]
+    return (f"func.func @conv2d_relu(%input: {_t(xs, elem)}, %filter: {_t([F, C, 3, 3], elem)}) "
+            f"-> {_t(os_, elem)} {{\n  %cst = arith.constant 0.0 : {elem}\n" +
+            _nchw_pad("%p", "%input", xs, 1, elem) +
+            _nchw_conv("%c", "%p", "%filter", ps, [F, C, 3, 3], os_, elem) +
+            _nchw_eltwise("%r", ["%c"], os_, elem, relu, "%m") +
+            f"  return %r : {_t(os_, elem)}\n}}\n")
+
+
+def nchw_resnet_block(N, C, H, W, elem="f16"):
+    """test/resnet_block.mlir's form: pad -> 3x3 conv -> ReLU -> pad -> 3x3
+    conv -> generic adding the block's input (no ReLU after it)."""
+    xs, ps = [N, C, H, W], [N, C, H + 2, W + 2]
+    ws = [C, C, 3, 3]
+    relu = [f"%z = arith.constant 0.0 : {elem}", f"%m = arith.maximumf %a0, %z : {elem}"]
+    return (f"func.func @resnet_block(%input: {_t(xs, elem)}, %w1: {_t(ws, elem)}, "
+            f"%w2: {_t(ws, elem)}) -> {_t(xs, elem)} {{\n  %cst = arith.constant 0.0 : {elem}\n" +
+            _nchw_pad("%p1", "%input", xs, 1, elem) +
+            _nchw_conv("%c1", "%p1", "%w1", ps, ws, xs, elem) +
+            _nchw_eltwise("%r1", ["%c1"], xs, elem, relu, "%m") +
+            _nchw_pad("%p2", "%r1", xs, 1, elem) +
+            _nchw_conv("%c2", "%p2", "%w2", ps, ws, xs, elem) +
+            _nchw_eltwise("%s", ["%c2", "%input"], xs, elem,
+                          [f"%s = arith.addf %a0, %a1 : {elem}"], "%s") +
+            f"  return %s : {_t(xs, elem)}\n}}\n")
 
 
 def model_zoo_irb(N, C, E, H, W, elem="f16"):

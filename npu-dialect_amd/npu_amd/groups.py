@@ -104,6 +104,24 @@ def fused_conv2d_nhwc_bias_res_act(x, w, bias, res, out, pad=1, act="relu", stre
     return out
 
 
+def fused_conv2d_nchw_bias_act(x, w, bias, out, pad=1, act="relu", stream=None):
+    """out = act(conv_2d_nchw_fchw(pad(x), w) + bias); f32, NCHW / FCHW."""
+    mx, mw, mb, mo = from_tensor(x), from_tensor(w), _opt(bias), from_tensor(out)
+    st = _lib.lib().fused_conv2d_nchw_bias_act(ref(mx), ref(mw), ref(mb), ref(mo), int(pad),
+                                               ACT[act], _stream(stream))
+    _check(st, "fused_conv2d_nchw_bias_act")
+    return out
+
+
+def fused_conv2d_nchw_bias_res_act(x, w, bias, res, out, pad=1, act="relu", stream=None):
+    """out = act(conv_2d_nchw_fchw(pad(x), w) + bias + res); f32, NCHW / FCHW."""
+    mx, mw, mb, mr, mo = from_tensor(x), from_tensor(w), _opt(bias), from_tensor(res), from_tensor(out)
+    st = _lib.lib().fused_conv2d_nchw_bias_res_act(ref(mx), ref(mw), ref(mb), ref(mr), ref(mo),
+                                                   int(pad), ACT[act], _stream(stream))
+    _check(st, "fused_conv2d_nchw_bias_res_act")
+    return out
+
+
 def fused_qbottleneck_i8(x, w1, w2, w3, m1, s1, m2, s2, m3, s3, out, stream=None):
     """int8 bottleneck: three convs with per-channel requant, residual, ReLU."""
     ms = [from_tensor(t) for t in (x, w1, w2, w3, m1, s1, m2, s2, m3, s3, out)]

@@ -18,6 +18,11 @@ that runs those calls on the GPU.  Matched:
   zeros symmetric in H and W -> fused_conv2d_nhwc_bias_act (f32 / bf16), the pad
   folded into the call; with a residual term in the generic (a ResNet block's
   add) -> fused_conv2d_nhwc_bias_res_act;
+* {fill, conv_2d_nchw_fchw, generic...} -- the reference's own layout
+  (test/conv2d_relu.mlir, test/resnet_block.mlir, test/resnet50_block.mlir,
+  test/mobilenet_block.mlir), 1x1 or 3x3 -> fused_conv2d_nchw_bias_act (f32),
+  the pad folded, or with the residual of an add generic (and a ReLU after it
+  in a second generic) -> fused_conv2d_nchw_bias_res_act;
 * the inverted residual chain: {fill, 1x1 conv, ReLU6 generic} -> tensor.pad ->
   depthwise 3x3 -> ReLU6 generic -> 1x1 conv -> generic adding the chain's
   input (one group after the pad, or two: the fusion decision depends on the
@@ -73,6 +78,7 @@ class Launch:
     entry: str = "npu_group_launch"   # or a typed entry point taking `ins`, `outs`, `params`
     outs: list = None
     params: dict = field(default_factory=dict)
+    res_arg: int = 0           # index of a conv group's residual in `ins` (0: none)
 
 
 _TORCH_DTYPE = {"f32": "float32", "bf16": "bfloat16", "i8": "int8", "i32": "int32"}
@@ -274,9 +280,12 @@ def _sum_leaves(e):
     return [e]
 
 
-def _match_generic(fn: _Fn, g, v, shape):
-    """(bias, residual, act) of one epilogue generic applied to chain value v."""
+def _match_generic(fn: _Fn, g, v, shape, cdim=-1):
+    """(bias, residual, act) of one epilogue generic applied to chain value v;
+    a bias is indexed by the channel dimension `cdim` alone (the last for
+    NHWC and matrices, 1 for NCHW)."""
     rank = len(shape)
+    cdim = cdim % rank
     ident = list(range(rank))
     name = g.results[0]
     maps = g.attrs.get("maps", [])
@@ -310,7 +319,7 @@ def _match_generic(fn: _Fn, g, v, shape):
         t = fn.ty(operand)
         if operand == v and m == ident and not seen_chain:
             seen_chain = True
-        elif m == [rank - 1] and t.shape == [shape[-1]] and bias is None:
+        elif m == [cdim] and t.shape == [shape[cdim]] and bias is None:
             bias = operand
         elif m == ident and t.shape == list(shape) and residual is None:
             residual = operand
@@ -322,14 +331,14 @@ def _match_generic(fn: _Fn, g, v, shape):
     return bias, residual, act
 
 
-def _epilogue(fn: _Fn, generics, src, shape):
+def _epilogue(fn: _Fn, generics, src, shape, cdim=-1):
     """Bias, residual and activation of the generics that follow `src` in a
     group, applied in order; returns (bias, residual, act, last value)."""
     bias = residual = None
     act = "none"
     v = src
     for g in generics:
-        b, r, a = _match_generic(fn, g, v, shape)
+        b, r, a = _match_generic(fn, g, v, shape, cdim)
         if act != "none" and (b or r or a != "none"):
             raise NotImplementedError(f"{g.results[0]}: epilogue after the activation")
         if b is not None:
@@ -352,17 +361,20 @@ def _check_fill(fn: _Fn, fill):
                                   "(accumulators start at 0.0)")
 
 
-def _pad_of(fn: _Fn, v):
-    """(source, pad) when v is a tensor.pad of zeros by p in H and W only."""
+def _pad_of(fn: _Fn, v, nchw=False):
+    """(source, pad) when v is a tensor.pad of zeros by p in H and W only
+    (dimensions 1 and 2 of NHWC, 2 and 3 of NCHW)."""
     op = fn.op(v)
     if op is None or op.name != "tensor.pad":
         return v, 0
     lo, hi = op.attrs.get("low", []), op.attrs.get("high", [])
-    if len(lo) != 4 or lo != hi or lo[0] or lo[3] or lo[1] != lo[2]:
+    h, w_ = (2, 3) if nchw else (1, 2)
+    if (len(lo) != 4 or lo != hi or lo[h] != lo[w_]
+            or any(lo[d] for d in range(4) if d not in (h, w_))):
         raise NotImplementedError(f"{v}: pad low {lo} high {hi} (entry points pad H and W equally)")
     if _const(fn, op.attrs.get("yield")) != 0.0:
         raise NotImplementedError(f"{v}: tensor.pad yields {op.attrs.get('yield')} (zero padding)")
-    return op.operands[0], lo[1]
+    return op.operands[0], lo[h]
 
 
 def _check_conv(op):
@@ -384,7 +396,7 @@ def _elem(fn, v, allowed, what):
     return e
 
 
-ANCHORS = ("linalg.matmul", "linalg.conv_2d_nhwc_fhwc")
+ANCHORS = ("linalg.matmul", "linalg.conv_2d_nhwc_fhwc", "linalg.conv_2d_nchw_fchw")
 
 
 def _segments(name, ops):
@@ -458,7 +470,31 @@ def lower(func: mlir.MFunc, target=None) -> "Program":
                 covered.update(r for f2 in chain.functions for o in groups[f2] for r in o.results)
                 covered.update(fn.op(chain.params["padded"]).results)
                 break
-            bias, res, act, out = _epilogue(fn, s["generics"], a.results[0], shape)
+            nchw = a.name == "linalg.conv_2d_nchw_fchw"
+            bias, res, act, out = _epilogue(fn, s["generics"], a.results[0], shape,
+                                            1 if nchw else -1)
+            if nchw:
+                _check_conv(a)
+                x, pad = _pad_of(fn, a.ins[0], nchw=True)
+                _elem(fn, x, ("f32",), name)
+                kh, kw = fn.ty(a.ins[1]).shape[2:]
+                if (kh, kw) not in ((1, 1), (3, 3)):
+                    raise NotImplementedError(f"{name}: {kh}x{kw} NCHW filter "
+                                              "(1x1 and 3x3 are run)")
+                for v in (bias, res):
+                    if v is not None and fn.ty(v).elem != "f32":
+                        raise NotImplementedError(f"{name}: {v} of type {fn.ty(v).elem}")
+                params = {"pad": pad, "act": act}
+                if res is not None:
+                    calls.append(Call("fused_conv2d_nchw_bias_res_act", [name],
+                                      [x, a.ins[1], bias, res], out, params))
+                else:
+                    calls.append(Call("fused_conv2d_nchw_bias_act", [name], [x, a.ins[1], bias],
+                                      out, params))
+                if pad:
+                    covered.add(a.ins[0])
+                covered.update(r for o in ops for r in o.results)
+                continue
             if a.name == "linalg.matmul":
                 _check_matmul(a)
                 if res is not None:
@@ -544,12 +580,14 @@ def _launches(fn: _Fn, rep, calls, dests):
         L = Launch("+".join(names), ins, cs[-1].out,
                    [c.params.get("act", "none") for c in cs])
         c0 = cs[0]
-        if c0.entry.startswith("fused_conv2d_nhwc_bias") and c0.params.get("pad"):
+        if c0.entry.startswith("fused_conv2d_n") and c0.params.get("pad"):
             conv_in = [v for v in ins if fn.op(v) is not None and fn.op(v).name == "tensor.pad"]
             L.pad, L.padded, L.pad_source = c0.params["pad"], conv_in[0], c0.args[0]
         if c0.params.get("bias_to_f32"):
             L.widen.append(c0.args[2])
         L.stores = [dests[id(c)] for c in cs[:-1]]
+        if c0.entry.endswith("_res_act"):  # the residual operand, by its argument index
+            L.res_arg = ins.index(c0.args[3])
         out.append(L)
         i = j
     return out
@@ -748,7 +786,8 @@ class Program:
         oty = types[L.out]
         if L.out not in vals:
             vals[L.out] = torch.empty(oty.shape, dtype=tdt(oty.elem), device=dev)
-        groups.group_launch(L.name, ins, [vals[L.out]], act=L.acts, pad=L.pad, stream=stream)
+        groups.group_launch(L.name, ins, [vals[L.out]], act=L.acts, pad=L.pad, stream=stream,
+                            res_arg=L.res_arg)
 
     def run(self, inputs: dict, stream=None) -> dict:
         """inputs: argument name (with or without %) -> tensor.  Runs every

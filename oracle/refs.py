@@ -48,6 +48,53 @@ def conv_bias_act(x, w, bias, pad=1, act="relu"):
     return out, mag
 
 
+def conv_nchw_act(x, w, bias=None, res=None, pad=1, act="relu"):
+    """One NCHW conv group as the oracle runs it: tensor.pad, fill 0,
+    conv_2d_nchw_fchw, then bias, residual and activation generics; mag is
+    the same chain on absolute values."""
+    xp = oracle.pad_nchw(x, (pad, pad, pad, pad)) if pad else np.asarray(x, np.float32)
+    out = oracle.conv2d_nchw_fchw(xp, w)
+    axp = oracle.pad_nchw(np.abs(x), (pad, pad, pad, pad)) if pad else np.abs(x)
+    mag = oracle.conv2d_nchw_fchw(axp, np.abs(w)).astype(np.float64)
+    if bias is not None:
+        out = oracle.add(out, np.broadcast_to(np.asarray(bias, np.float32)[None, :, None, None],
+                                              out.shape))
+        mag = mag + np.abs(bias)[None, :, None, None]
+    if res is not None:
+        out = oracle.add(out, res)
+        mag = mag + np.abs(res)
+    if act == "relu":
+        out = oracle.relu(out)
+    elif act == "relu6":
+        out = oracle.relu6(out)
+    return out, mag
+
+
+def nchw_workload(name, args):
+    """The oracle's result and magnitude bound for the reference's NCHW conv
+    workloads (test/conv2d_relu.mlir, test/resnet_block.mlir,
+    test/resnet50_block.mlir, test/mobilenet_block.mlir) on argument arrays
+    in the function's order; a later conv's bound carries the earlier
+    stage's through its filter (conv of the magnitude)."""
+    if name == "conv2d_relu.mlir":
+        x, w = args
+        return conv_nchw_act(x, w, pad=1)
+    if name == "resnet_block.mlir":
+        x, w1, w2 = args
+        r1, m1 = conv_nchw_act(x, w1, pad=1)
+        out, _ = conv_nchw_act(r1, w2, res=x, pad=1, act="none")
+        mag = oracle.conv2d_nchw_fchw(oracle.pad_nchw(m1, (1, 1, 1, 1)), np.abs(w2)) + np.abs(x)
+        return out, mag.astype(np.float64)
+    x, w1, w2, w3 = args
+    r1, m1 = conv_nchw_act(x, w1, pad=0)
+    r2, _ = conv_nchw_act(r1, w2, pad=1)
+    m2 = oracle.conv2d_nchw_fchw(oracle.pad_nchw(m1, (1, 1, 1, 1)), np.abs(w2))
+    act = "relu" if name == "resnet50_block.mlir" else "none"
+    out, _ = conv_nchw_act(r2, w3, res=x, pad=0, act=act)
+    mag = oracle.conv2d_nchw_fchw(m2, np.abs(w3)) + np.abs(x)
+    return out, mag.astype(np.float64)
+
+
 def irb(x, we, wdw, wp):
     out = oracle.block_irb(x, we, wdw, wp)
     ax = np.abs(x)

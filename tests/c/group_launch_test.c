@@ -114,9 +114,14 @@ static void validate(void) {
   in[4] = mem2(&dE, NULL, 128, 512);
   out[0] = mem2(&dO, O, 128, 512);
 
-  npu_status s = npu_group_launch("fused_fill_conv2d_generic_0", &at, in, 5, out, 1, NULL);
-  CHECK(s == NPU_ERR_UNSUPPORTED, "NCHW chain: status %d", s);
-  CHECK(strstr(npu_last_error(), "fill_conv2d_generic") != NULL, "message: %s", npu_last_error());
+  npu_status s = npu_group_launch("fused_fill_batch_matmul_generic_0", &at, in, 5, out, 1, NULL);
+  CHECK(s == NPU_ERR_UNSUPPORTED, "unknown chain: status %d", s);
+  CHECK(strstr(npu_last_error(), "fill_batch_matmul_generic") != NULL, "message: %s",
+        npu_last_error());
+  /* the reference's NCHW conv group takes rank-4 operands */
+  s = npu_group_launch("fused_fill_conv2d_generic_0", &at, in, 5, out, 1, NULL);
+  CHECK(s == NPU_ERR_INVALID_ARG && strstr(npu_last_error(), "rank-4"),
+        "NCHW group with matrices: status %d (%s)", s, npu_last_error());
 
   s = npu_group_launch("fused_fill_matmul_generic_0", &at, in, 4, out, 1, NULL);
   CHECK(s == NPU_ERR_INVALID_ARG, "missing destination: status %d", s);

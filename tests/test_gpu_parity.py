@@ -702,6 +702,87 @@ def test_reference_workloads_run_on_the_gpu(cuda, name):
     assert np.all(np.abs(got - ref) <= 1e-5 * np.abs(ref) * 2)
 
 
+NCHW_WORKLOADS = ["conv2d_relu.mlir", "resnet_block.mlir", "resnet50_block.mlir",
+                  "mobilenet_block.mlir"]
+
+
+@pytest.mark.parametrize("fills", ["harness", "seeded"])
+@pytest.mark.parametrize("name", NCHW_WORKLOADS)
+def test_reference_nchw_workloads_run_on_the_gpu(cuda, name, fills):
+    """The reference's own conv workloads -- linalg.conv_2d_nchw_fchw groups
+    outlined as @fused_fill_conv2d_generic[_generic]_<idx>, f16 run as f32 --
+    lowered and launched group by group through npu_group_launch (the pads
+    folded, the ResNet adds as residual terms), against the oracle's unfused
+    NCHW loops: with the harness's fills 0.01 (i + 1) (e2e_verify.py:186-203)
+    and with seeded inputs (U(0, 1) activations, He-normal filters)."""
+    prog = lower.lower_text(blocks.reference_workload(name))
+    if fills == "harness":
+        ins = _harness_fills(prog)
+    else:
+        ins = {}
+        for i, (a, t) in enumerate(prog.func.args):
+            if i == 0:
+                arr = rng.uniform(31, i, tuple(t.shape), 0, 1)
+            else:
+                fan = int(np.prod(t.shape[1:]))
+                arr = rng.normal(31, i, tuple(t.shape), 0, math.sqrt(2 / fan))
+            ins[a] = _dev(arr)
+    (res,) = prog.run(ins).values()
+    torch.cuda.synchronize()
+    host_ins = [_host(ins[a]) for a, _ in prog.func.args]
+    with oracle.threaded():
+        ref, mag = refs.nchw_workload(name, host_ins)
+    check_bound(_host(res), ref, mag, RTOL_F32, what=f"{name} ({fills})")
+    assert all(L.name.startswith("fused_fill_conv2d_generic") for L in prog.launches)
+
+
+@pytest.mark.parametrize("N,C,H,W,F,K,pad,act,bias,res", [
+    (2, 20, 9, 37, 40, 3, 1, "relu", True, False),    # C and F off the 16 / 64 blocks, ragged segments
+    (1, 64, 56, 56, 64, 3, 1, "relu", False, True),   # the reference's conv, with a residual
+    (1, 256, 14, 14, 64, 1, 0, "relu6", True, False),  # 1x1, sixteen channel chunks
+    (3, 8, 5, 70, 24, 3, 0, "none", False, True),     # valid conv, rows past one segment
+    (1, 192, 28, 112, 192, 3, 1, "relu", False, False),  # 64-pixel segments (large grid)
+    (1, 4, 3, 3, 4, 1, 0, "none", True, False),       # a handful of values
+])
+def test_nchw_conv_shapes(cuda, N, C, H, W, F, K, pad, act, bias, res):
+    x = rng.uniform(32, 0, (N, C, H, W), -1, 1)
+    w = rng.normal(32, 1, (F, C, K, K), 0, math.sqrt(2 / (K * K * C)))
+    b = rng.uniform(32, 2, (F,), -0.1, 0.1) if bias else None
+    Ho, Wo = H + 2 * pad - K + 1, W + 2 * pad - K + 1
+    r = rng.uniform(32, 3, (N, F, Ho, Wo), -1, 1) if res else None
+    out = torch.empty(N, F, Ho, Wo, device="cuda")
+    if res:
+        groups.fused_conv2d_nchw_bias_res_act(_dev(x), _dev(w), None if b is None else _dev(b),
+                                              _dev(r), out, pad, act)
+    else:
+        groups.fused_conv2d_nchw_bias_act(_dev(x), _dev(w), None if b is None else _dev(b), out,
+                                          pad, act)
+    torch.cuda.synchronize()
+    ref, mag = refs.conv_nchw_act(x, w, b, r, pad, act)
+    check_bound(_host(out), ref, mag, RTOL_F32, what=f"nchw conv {N}x{C}x{H}x{W} -> {F} {K}x{K}")
+
+
+def test_nchw_conv_non_finite(cuda):
+    """NaN and +-Inf through the NCHW conv on the f32 matrix pipe: the same
+    positions and values as the oracle's f32 loops."""
+    N, C, H, W, F = 1, 32, 12, 20, 32
+    x = rng.uniform(33, 0, (N, C, H, W), 0, 1)
+    x[0, 3, 4, 5] = np.nan
+    x[0, 7, 9, 15] = np.inf
+    w = rng.normal(33, 1, (F, C, 3, 3), 0, 0.1)
+    out = torch.empty(N, F, H, W, device="cuda")
+    groups.fused_conv2d_nchw_bias_act(_dev(x), _dev(w), None, out, 1, "none")
+    torch.cuda.synchronize()
+    got = _host(out)
+    ref, mag = refs.conv_nchw_act(x, w, None, None, 1, "none")
+    hit = ~np.isfinite(ref)
+    assert hit.sum() > 9 * F
+    assert np.array_equal(np.isnan(got), np.isnan(ref))
+    fin = hit & ~np.isnan(ref)
+    assert np.array_equal(got[fin], ref[fin])
+    check_bound(got[~hit], ref[~hit], mag[~hit], RTOL_F32, what="nchw conv next to NaN / Inf")
+
+
 def test_compiled_c_caller_on_the_gpu(cuda):
     """The C program that calls npu_group_launch by outlined name with MLIR
     memref descriptors: the matmul_relu and mlp closed forms and the C1 group

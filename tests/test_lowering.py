@@ -55,10 +55,49 @@ def test_inverted_residual_chain_is_one_call(shape, ngroups):
     assert c.views == {"%we": [144, 24], "%wp": [24, 144]}
 
 
-def test_nchw_conv_is_refused():
-    """test/conv2d_relu.mlir is NCHW: no entry point runs linalg.conv_2d_nchw_fchw."""
-    with pytest.raises(NotImplementedError, match="no MI355X entry point"):
-        lower.lower_text(reference_inputs.read("conv2d_relu.mlir"))
+@pytest.mark.parametrize("name,calls", [
+    ("conv2d_relu.mlir", [("fused_fill_conv2d_generic_0", "fused_conv2d_nchw_bias_act", 1, "relu", 0)]),
+    ("resnet_block.mlir", [("fused_fill_conv2d_generic_0", "fused_conv2d_nchw_bias_act", 1, "relu", 0),
+                           ("fused_fill_conv2d_generic_1", "fused_conv2d_nchw_bias_res_act", 1,
+                            "none", 4)]),
+    ("resnet50_block.mlir", [("fused_fill_conv2d_generic_0", "fused_conv2d_nchw_bias_act", 0, "relu", 0),
+                             ("fused_fill_conv2d_generic_1", "fused_conv2d_nchw_bias_act", 1, "relu", 0),
+                             ("fused_fill_conv2d_generic_generic_2", "fused_conv2d_nchw_bias_res_act",
+                              0, "relu", 4)]),
+    ("mobilenet_block.mlir", [("fused_fill_conv2d_generic_0", "fused_conv2d_nchw_bias_act", 0, "relu", 0),
+                              ("fused_fill_conv2d_generic_1", "fused_conv2d_nchw_bias_act", 1, "relu", 0),
+                              ("fused_fill_conv2d_generic_2", "fused_conv2d_nchw_bias_res_act", 0,
+                               "none", 4)]),
+])
+def test_reference_nchw_workloads_lower_to_their_groups(name, calls):
+    """The reference's own conv workloads (linalg.conv_2d_nchw_fchw, the
+    tensor.pad outside the groups) lower group by group to the NCHW entry
+    points under the outliner's names (OutlineFusedGroupsPass.cpp:69-82):
+    the pad folded into the launch, a ResNet add (and the ReLU after it, in
+    its own generic) as the residual term, named by its argument index."""
+    p = lower.lower_text(reference_inputs.read(name))
+    got = [(L.name, c.entry, L.pad, L.acts[0], L.res_arg) for L, c in zip(p.launches, p.calls)]
+    assert got == calls
+    for L, c in zip(p.launches, p.calls):
+        if L.res_arg:
+            assert L.ins[L.res_arg] == c.args[3] == p.func.args[0][0]
+
+
+def test_nchw_conv_refusals():
+    """What the NCHW entry points do not run is refused by name: a 5x5
+    filter, a stride of 2, a pad that is not symmetric in H and W."""
+    t = blocks.nchw_conv_relu(1, 16, 16, 8, 8, elem="f32")
+    five = t.replace("16x16x3x3", "16x16x5x5").replace("x10x10xf32", "x12x12xf32") \
+        .replace("low[0, 0, 1, 1] high[0, 0, 1, 1]", "low[0, 0, 2, 2] high[0, 0, 2, 2]")
+    with pytest.raises(NotImplementedError, match="5x5"):
+        lower.lower_text(five)
+    strided = t.replace("strides = dense<1>", "strides = dense<2>").replace("1x16x8x8xf32> -> ",
+                                                                            "1x16x8x8xf32> -> ")
+    with pytest.raises(NotImplementedError, match="strided"):
+        lower.lower_text(strided)
+    lopsided = t.replace("high[0, 0, 1, 1]", "high[0, 0, 1, 2]")
+    with pytest.raises(NotImplementedError, match="pad"):
+        lower.lower_text(lopsided)
 
 
 def test_reference_matmul_relu_lowers_through_the_harness_rule():
@@ -83,7 +122,8 @@ def test_reference_mlp_is_two_calls():
 
 def _shape_of(func):
     """The function with SSA names replaced by first-appearance numbers: op
-    names, operand/result types, indexing maps, iterators, generic bodies."""
+    names, operand/result types, indexing maps, iterators, generic bodies,
+    pad widths and strides."""
     ids = {}
 
     def n(v):
@@ -99,11 +139,14 @@ def _shape_of(func):
         body = [(b.name, b.value) for b in op.attrs.get("body", [])]
         out.append((op.name, [n(v) for v in op.ins + op.operands if v in ids],
                     [str(func.types[r]) for r in op.results], op.attrs.get("maps"),
-                    op.iterators, body, op.attrs.get("value")))
+                    op.iterators, body, op.attrs.get("value"), op.attrs.get("low"),
+                    op.attrs.get("high"), op.attrs.get("strides")))
     return out
 
 
-@pytest.mark.parametrize("name", ["matmul_relu.mlir", "mlp.mlir"])
+@pytest.mark.parametrize("name", ["matmul_relu.mlir", "mlp.mlir", "conv2d_relu.mlir",
+                                  "resnet_block.mlir", "resnet50_block.mlir",
+                                  "mobilenet_block.mlir"])
 def test_builder_text_is_the_reference_workload(name):
     """The GPU box has no reference checkout, so the GPU runs the builder's
     text of these workloads; here it is checked against the reference's file."""
