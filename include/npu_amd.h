@@ -141,26 +141,31 @@ npu_status fused_conv2d_nhwc_bias_res_act(const npu_memref *x, const npu_memref 
 
 /* The reference's own layout: group `pad -> fill -> conv_2d_nchw_fchw ->
  * generic...` (test/conv2d_relu.mlir:7-42, test/resnet_block.mlir,
- * test/resnet50_block.mlir, test/mobilenet_block.mlir; outlined as
- * @fused_fill_conv2d_generic[_generic]_<idx>,
- * OutlineFusedGroupsPass.cpp:69-82), with the zero pad folded into the
- * launch.  f32 (f16 text runs as f32, tools/harness/e2e_verify.py:163-164).
- *   x    f32 [N,C,H,W]       w f32 [F,C,KH,KW], KH = KW = 1 or 3
+ * test/resnet50_block.mlir, test/mobilenet_block.mlir, and every network of
+ * test/models/, e.g. resnet18.mlir; outlined as
+ * @fused_fill_conv2d[_generic...]_<idx>, OutlineFusedGroupsPass.cpp:69-82),
+ * with the zero pad folded into the launch.  f32 (f16 text runs as f32,
+ * tools/harness/e2e_verify.py:163-164).
+ *   x    f32 [N,C,H,W]       w f32 [F,C,KH,KW], any KH, KW
  *   bias f32 [F] (aligned may be NULL)
- *   out  f32 [N,F,Ho,Wo] = act(conv(pad(x), w) + bias), Ho = H + 2*pad - KH + 1
- * Stride 1.  Computed on the f32 matrix pipe: within f32 accuracy of the
- * sequential f32 sum, +-Inf and NaN as there. */
+ *   out  f32 [N,F,Ho,Wo] = act(conv(pad(x), w, stride) + bias),
+ *        Ho = (H + 2*pad - KH) / stride + 1 (the `strides` attribute, the
+ *        same in both dimensions)
+ * 1x1 and 3x3 filters at stride 1 or 2 stage their halo in LDS; other shapes
+ * read their operands directly.  Computed on the f32 matrix pipe: within f32
+ * accuracy of the sequential f32 sum, +-Inf and NaN as there. */
 npu_status fused_conv2d_nchw_bias_act(const npu_memref *x, const npu_memref *w,
                                       const npu_memref *bias, const npu_memref *out,
-                                      int32_t pad, int32_t act, npu_stream stream);
+                                      int32_t pad, int32_t stride, int32_t act,
+                                      npu_stream stream);
 
 /* The same with the residual term of a ResNet block's add generic
  * (test/resnet_block.mlir:55-67, test/resnet50_block.mlir:77-102):
- *   res  f32 [N,F,Ho,Wo]     out = act(conv(pad(x), w) + bias + res) */
+ *   res  f32 [N,F,Ho,Wo]     out = act(conv(pad(x), w, stride) + bias + res) */
 npu_status fused_conv2d_nchw_bias_res_act(const npu_memref *x, const npu_memref *w,
                                           const npu_memref *bias, const npu_memref *res,
-                                          const npu_memref *out, int32_t pad, int32_t act,
-                                          npu_stream stream);
+                                          const npu_memref *out, int32_t pad, int32_t stride,
+                                          int32_t act, npu_stream stream);
 
 /* Group chain of the int8 ResNet-50 bottleneck (int8 restatement of
  * test/resnet50_block.mlir:5-105, NHWC, zero points 0), fused across both
@@ -305,7 +310,7 @@ typedef struct npu_arg {
 
 /* What the outlined body computes beyond its signature: constants inside the
  * generic regions and the folding of a feeding tensor.pad. */
-#define NPU_GROUP_MAX_CHAINS 4
+#define NPU_GROUP_MAX_CHAINS 16
 typedef struct npu_group_attrs {
   int32_t act[NPU_GROUP_MAX_CHAINS]; /* NPU_ACT_* of each matmul/conv chain of
                                         the group, in order                    */
@@ -319,6 +324,7 @@ typedef struct npu_group_attrs {
   int32_t res_arg; /* conv groups: index in `in` of the residual operand a
                       generic adds, 0 when none is named (in[0] is always the
                       fill constant, never a residual)                        */
+  int32_t stride;  /* NCHW conv groups: the conv's `strides` (0 or 1: 1)      */
 } npu_group_attrs;
 
 /* Runs one outlined group, or a chain of outlined groups that the host
@@ -338,9 +344,11 @@ typedef struct npu_group_attrs {
  * Groups (chain key = the names with `fused_` and the index removed):
  *   fill_matmul_generic                   -> fused_matmul_bias_act
  *     (cst, init[M,N], A[M,K], B[K,N], [bias[N]], dest[M,N]) -> (out[M,N])
- *   fill_matmul_generic repeated k <= 4 times (test/mlp.mlir: one group of
- *     two matmul -> ReLU chains)          -> k fused_matmul_bias_act calls
- *     (cst, init1, x, w1, [b1], dest1, init2, w2, [b2], dest2, ...) -> (out)
+ *   fill_matmul[_generic] repeated k <= 16 times (test/mlp.mlir: one group
+ *     of two matmul -> ReLU chains; test/models/autoencoder.mlir: eight, the
+ *     last without a generic)             -> k fused_matmul_bias_act calls
+ *     (cst, init1, x, w1, [b1], dest1, init2, w2, [b2], dest2, ...) -> (out);
+ *     a chain without a generic has no dest, its result is its init
  *   fill_linalg_conv_2d_nhwc_fhwc_generic[_generic...] (the epilogue in one
  *     or several generics: an add of the block input, then a ReLU)
  *                                         -> fused_conv2d_nhwc_bias_act, or
@@ -350,11 +358,14 @@ typedef struct npu_group_attrs {
  *     generics, attrs->res_arg names the residual's index in `in` (when it
  *     is 0, the destinations before the last must be passed without data,
  *     NULL, which tells them from the residual)
- *   fill_conv2d_generic[_generic...] (the reference's linalg.conv_2d_nchw_fchw,
+ *   fill_conv2d[_generic...] (the reference's linalg.conv_2d_nchw_fchw,
  *     test/conv2d_relu.mlir, test/resnet_block.mlir, test/resnet50_block.mlir,
- *     test/mobilenet_block.mlir)          -> fused_conv2d_nchw_bias_act, or
+ *     test/mobilenet_block.mlir, the networks of test/models/)
+ *                                         -> fused_conv2d_nchw_bias_act, or
  *     with a residual term fused_conv2d_nchw_bias_res_act; the same argument
- *     order as the NHWC group, every tensor NCHW / FCHW
+ *     order as the NHWC group, every tensor NCHW / FCHW, attrs->stride the
+ *     conv's stride; without a generic (a classifier conv) the group is
+ *     (cst, init, x, w) -> (out)
  *   fill_linalg_conv_2d_nhwc_fhwc_generic + the depthwise / project group(s)
  *     of an inverted residual block after its tensor.pad -> fused_irb_f32
  *     (cst, init_e, x, we[E,1,1,C], dest_e, init_d, wdw[3,3,E], dest_d,

@@ -361,8 +361,8 @@ namespace {
 
 // fused_conv2d_nchw_bias_act and its residual variant.
 npu_status conv_nchw_entry(const npu_memref *x, const npu_memref *w, const npu_memref *bias,
-                           const npu_memref *res, const npu_memref *out, int32_t pad, int32_t act,
-                           npu_stream stream, const char *name) {
+                           const npu_memref *res, const npu_memref *out, int32_t pad,
+                           int32_t stride, int32_t act, npu_stream stream, const char *name) {
   npu::plans_reset();
   const void *px, *pw, *pbias = nullptr, *pres = nullptr, *po;
   NPU_TRY(check_memref(x, "x", 4, NPU_F32, &px));
@@ -374,13 +374,12 @@ npu_status conv_nchw_entry(const npu_memref *x, const npu_memref *w, const npu_m
   if (w->sizes[1] != C)
     return fail(NPU_ERR_INVALID_ARG, "w: channels %lld, expected C = %lld",
                 (long long)w->sizes[1], (long long)C);
-  if (!npu::conv2d_nchw_supported((int)KH, (int)KW))
-    return fail(NPU_ERR_UNSUPPORTED, "w: %lldx%lld filter (1x1 and 3x3 are supported)",
-                (long long)KH, (long long)KW);
   if (pad < 0) return fail(NPU_ERR_INVALID_ARG, "pad %d is negative", pad);
-  const int64_t Ho = H + 2 * pad - KH + 1, Wo = W + 2 * pad - KW + 1;
-  if (Ho <= 0 || Wo <= 0) return fail(NPU_ERR_INVALID_ARG, "empty output (%lld x %lld)",
-                                      (long long)Ho, (long long)Wo);
+  if (stride < 1) return fail(NPU_ERR_INVALID_ARG, "stride %d must be positive", stride);
+  if (H + 2 * pad < KH || W + 2 * pad < KW)
+    return fail(NPU_ERR_INVALID_ARG, "filter %lldx%lld larger than the padded input",
+                (long long)KH, (long long)KW);
+  const int64_t Ho = (H + 2 * pad - KH) / stride + 1, Wo = (W + 2 * pad - KW) / stride + 1;
   if (out->sizes[0] != N || out->sizes[1] != F || out->sizes[2] != Ho || out->sizes[3] != Wo)
     return fail(NPU_ERR_INVALID_ARG, "out: [%lld,%lld,%lld,%lld], expected [%lld,%lld,%lld,%lld]",
                 (long long)out->sizes[0], (long long)out->sizes[1], (long long)out->sizes[2],
@@ -402,7 +401,7 @@ npu_status conv_nchw_entry(const npu_memref *x, const npu_memref *w, const npu_m
   }
   npu::ConvArgs a{px, pw, static_cast<const float *>(pbias), const_cast<void *>(po),
                   (int)N, (int)H, (int)W, (int)C, (int)F, (int)KH, (int)KW, pad,
-                  (int)Ho, (int)Wo, act, pres};
+                  (int)Ho, (int)Wo, act, pres, stride};
   return hip_status(npu::launch_conv2d_nchw_f32(a, static_cast<hipStream_t>(stream)), name);
 }
 
@@ -410,17 +409,18 @@ npu_status conv_nchw_entry(const npu_memref *x, const npu_memref *w, const npu_m
 
 npu_status fused_conv2d_nchw_bias_act(const npu_memref *x, const npu_memref *w,
                                       const npu_memref *bias, const npu_memref *out,
-                                      int32_t pad, int32_t act, npu_stream stream) {
-  return conv_nchw_entry(x, w, bias, nullptr, out, pad, act, stream,
+                                      int32_t pad, int32_t stride, int32_t act,
+                                      npu_stream stream) {
+  return conv_nchw_entry(x, w, bias, nullptr, out, pad, stride, act, stream,
                          "fused_conv2d_nchw_bias_act launch");
 }
 
 npu_status fused_conv2d_nchw_bias_res_act(const npu_memref *x, const npu_memref *w,
                                           const npu_memref *bias, const npu_memref *res,
-                                          const npu_memref *out, int32_t pad, int32_t act,
-                                          npu_stream stream) {
+                                          const npu_memref *out, int32_t pad, int32_t stride,
+                                          int32_t act, npu_stream stream) {
   if (!res) return fail(NPU_ERR_INVALID_ARG, "res: null descriptor");
-  return conv_nchw_entry(x, w, bias, res, out, pad, act, stream,
+  return conv_nchw_entry(x, w, bias, res, out, pad, stride, act, stream,
                          "fused_conv2d_nchw_bias_res_act launch");
 }
 

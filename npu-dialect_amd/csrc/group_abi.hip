@@ -194,8 +194,12 @@ npu_status typed(npu_status s) {
   return s;
 }
 
-npu_status run_matmuls(Cursor &c, const npu_group_attrs &at, int chains, const npu_memref *out,
-                       npu_stream stream, PlanLog &log) {
+// chains[k]: whether matmul chain k ends in a generic (else its result is
+// the accumulator the fill initialised, as the reference's last layers
+// without an activation are).
+npu_status run_matmuls(Cursor &c, const npu_group_attrs &at, const std::vector<bool> &gen,
+                       const npu_memref *out, npu_stream stream, PlanLog &log) {
+  const int chains = (int)gen.size();
   G_TRY(c.fill_value());
   const npu_memref *x = nullptr;
   struct Step { const npu_memref *init, *A, *B, *bias, *dest; };
@@ -206,7 +210,7 @@ npu_status run_matmuls(Cursor &c, const npu_group_attrs &at, int chains, const n
     if (k == 0) G_TRY(c.memref(2, "A", &x));
     s.A = x;
     G_TRY(c.memref(2, "B", &s.B));
-    if (c.next_is_rank1()) G_TRY(c.memref(1, "bias", &s.bias));
+    if (gen[k] && c.next_is_rank1()) G_TRY(c.memref(1, "bias", &s.bias));
     const int64_t M = s.A->sizes[0], N = s.B->sizes[1];
     // What each chain's typed call checks is checked here for every chain
     // first, so that no chain launches before all of them are known good.
@@ -225,7 +229,10 @@ npu_status run_matmuls(Cursor &c, const npu_group_attrs &at, int chains, const n
     if (!same_shape(*s.init, {M, N}))
       return gfail(NPU_ERR_INVALID_ARG, "matmul %d: accumulator %s, expected [%lld,%lld]", k,
                    shape_str(*s.init).c_str(), (long long)M, (long long)N);
-    G_TRY(c.dest({M, N}, "generic destination (tensor.empty)", &s.dest));
+    if (gen[k])
+      G_TRY(c.dest({M, N}, "generic destination (tensor.empty)", &s.dest));
+    else
+      s.dest = s.init;  // no generic: the result stays in the filled accumulator
     if (k + 1 < chains && !s.dest->aligned)
       return gfail(NPU_ERR_INVALID_ARG, "matmul %d: its destination holds the intermediate "
                    "result and must have data", k);
@@ -244,7 +251,8 @@ npu_status run_matmuls(Cursor &c, const npu_group_attrs &at, int chains, const n
     const npu_memref *dst = k + 1 == chains ? out : s.dest;
     npu_memref none{};
     none.rank = 1;
-    G_TRY(typed(fused_matmul_bias_act(s.A, s.B, s.bias ? s.bias : &none, dst, at.act[k], stream)));
+    G_TRY(typed(fused_matmul_bias_act(s.A, s.B, s.bias ? s.bias : &none, dst,
+                                      gen[k] ? at.act[k] : NPU_ACT_NONE, stream)));
     log.take();
   }
   return NPU_OK;
@@ -281,6 +289,9 @@ npu_status run_conv(Cursor &c, const npu_group_attrs &at, const npu_memref *out,
     }
   }
   const size_t nd = (size_t)n_generic;
+  if (nd == 0 && (bias || !r4.empty()))
+    return gfail(NPU_ERR_INVALID_ARG, "a conv group without a generic takes no bias, residual or "
+                 "destination (its result is the filled accumulator)");
   if (r4.size() != nd && r4.size() != nd + 1)
     return gfail(NPU_ERR_INVALID_ARG, "%zu rank-4 arguments after the filter: expected %zu "
                  "destinations and at most one residual", r4.size(), nd);
@@ -317,12 +328,15 @@ npu_status run_conv(Cursor &c, const npu_group_attrs &at, const npu_memref *out,
   npu_memref none{};
   none.rank = 1;
   if (nchw) {
+    const int32_t st = at.stride > 1 ? at.stride : 1;
     if (res)
-      G_TRY(typed(fused_conv2d_nchw_bias_res_act(x, w, bias ? bias : &none, res, out, at.pad,
+      G_TRY(typed(fused_conv2d_nchw_bias_res_act(x, w, bias ? bias : &none, res, out, at.pad, st,
                                                  at.act[0], stream)));
     else
-      G_TRY(typed(fused_conv2d_nchw_bias_act(x, w, bias ? bias : &none, out, at.pad, at.act[0],
-                                             stream)));
+      G_TRY(typed(fused_conv2d_nchw_bias_act(x, w, bias ? bias : &none, out, at.pad, st,
+                                             at.act[0], stream)));
+  } else if (at.stride > 1) {
+    return gfail(NPU_ERR_UNSUPPORTED, "stride %d: the NHWC conv groups take stride 1", at.stride);
   } else if (res) {
     G_TRY(typed(fused_conv2d_nhwc_bias_res_act(x, w, bias ? bias : &none, res, out, at.pad,
                                                at.act[0], stream)));
@@ -411,10 +425,9 @@ npu_status run_qbottleneck(Cursor &c, const npu_memref *out, npu_stream stream, 
   return NPU_OK;
 }
 
-const char *kMatmul = "fill_matmul_generic";
-const char *kConv = "fill_linalg_conv_2d_nhwc_fhwc_generic";
+const char *kConv = "fill_linalg_conv_2d_nhwc_fhwc";
 // linalg.conv_2d_nchw_fchw's short name is `conv2d` (OutlineFusedGroupsPass.cpp:69-82)
-const char *kConvNchw = "fill_conv2d_generic";
+const char *kConvNchw = "fill_conv2d";
 const char *kQBottleneck =
     "fill_linalg_conv_2d_nhwc_fhwc_generic_fill_linalg_conv_2d_nhwc_fhwc_generic_"
     "fill_linalg_conv_2d_nhwc_fhwc_generic";
@@ -422,20 +435,27 @@ const char *kIrb =
     "fill_linalg_conv_2d_nhwc_fhwc_generic_fill_linalg_depthwise_conv_2d_nhwc_hwc_generic_"
     "fill_linalg_conv_2d_nhwc_fhwc_generic";
 
-// k when key is `fill_matmul_generic` repeated k times, else 0.
-int matmul_chains(const std::string &key) {
-  const std::string one = kMatmul;
-  int k = 0;
+// The chains of a matmul group's key -- `fill_matmul` each, then `_generic`
+// when the chain has an epilogue -- as one flag per chain; empty when the
+// key is not such a sequence.
+std::vector<bool> matmul_chains(const std::string &key) {
+  const std::string one = "fill_matmul", gen = "_generic";
+  std::vector<bool> chains;
   size_t p = 0;
   while (p < key.size()) {
-    if (key.compare(p, one.size(), one) != 0) return 0;
+    if (key.compare(p, one.size(), one) != 0) return {};
     p += one.size();
-    ++k;
-    if (p == key.size()) return k;
-    if (key[p] != '_') return 0;
+    bool g = false;
+    if (key.compare(p, gen.size(), gen) == 0) {
+      g = true;
+      p += gen.size();
+    }
+    chains.push_back(g);
+    if (p == key.size()) return chains;
+    if (key[p] != '_') return {};
     ++p;
   }
-  return 0;
+  return {};
 }
 
 }  // namespace
@@ -459,23 +479,25 @@ extern "C" npu_status npu_group_launch(const char *outlined_name, const npu_grou
     if (res.scalar) return gfail(NPU_ERR_INVALID_ARG, "out[0]: a result must be a memref");
     const std::string key = chain_key(outlined_name);
     Cursor c(args);
-    if (const int k = matmul_chains(key)) {
-      if (k > NPU_GROUP_MAX_CHAINS)
-        return gfail(NPU_ERR_UNSUPPORTED, "%d matmul chains (at most %d)", k,
+    const std::vector<bool> mm = matmul_chains(key);
+    if (!mm.empty()) {
+      if ((int)mm.size() > NPU_GROUP_MAX_CHAINS)
+        return gfail(NPU_ERR_UNSUPPORTED, "%zu matmul chains (at most %d)", mm.size(),
                      NPU_GROUP_MAX_CHAINS);
-      return run_matmuls(c, *attrs, k, &res.m, stream, log);
+      return run_matmuls(c, *attrs, mm, &res.m, stream, log);
     }
-    // a conv followed by one or more generics, NHWC (authored) or NCHW (the
-    // reference's own)
+    // a conv followed by generics (none for the NCHW classifier convs), NHWC
+    // (authored) or NCHW (the reference's own)
     for (const char *kc : {kConv, kConvNchw}) {
       if (key.rfind(kc, 0) != 0) continue;
-      int ng = 1;
+      int ng = 0;
       size_t at = std::strlen(kc);
       while (key.compare(at, 8, "_generic") == 0 && key.size() >= at + 8) {
         ++ng;
         at += 8;
       }
-      if (at == key.size()) return run_conv(c, *attrs, &res.m, stream, log, ng, kc == kConvNchw);
+      if (at == key.size() && (ng > 0 || kc == kConvNchw))
+        return run_conv(c, *attrs, &res.m, stream, log, ng, kc == kConvNchw);
     }
     if (key == kIrb) return run_irb(c, &res.m, stream, log);
     if (key == kQBottleneck) return run_qbottleneck(c, &res.m, stream, log);

@@ -21,13 +21,13 @@ struct ConvArgs {
   void *out;
   int N, H, W, C, F, KH, KW, pad, Ho, Wo, act;
   const void *res = nullptr;  // residual [N,Ho,Wo,F], the output's type (may be null)
+  int stride = 1;             // both spatial dimensions (the NCHW kernels; NHWC takes 1)
 };
 hipError_t launch_conv2d_nhwc_f32(const ConvArgs &a, hipStream_t s);
 hipError_t launch_conv2d_nhwc_bf16(const ConvArgs &a, hipStream_t s);
-// NCHW activations, FCHW filters (conv_2d_nchw_fchw), f32, 1x1 or 3x3,
-// stride 1: ConvArgs with H/W/C/F as named, x [N,C,H,W], w [F,C,KH,KW],
+// NCHW activations, FCHW filters (conv_2d_nchw_fchw), f32, any filter size
+// and stride: ConvArgs with H/W/C/F as named, x [N,C,H,W], w [F,C,KH,KW],
 // out and res [N,F,Ho,Wo].
-bool conv2d_nchw_supported(int KH, int KW);
 hipError_t launch_conv2d_nchw_f32(const ConvArgs &a, hipStream_t s);
 // 3x3 / stride 1 / pad 1 with rows of at most 64 pixels: LDS halo kernel.
 bool conv3x3_rows_supported(const ConvArgs &a, int elem_bytes);

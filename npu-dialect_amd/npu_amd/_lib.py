@@ -81,15 +81,16 @@ class NpuArg(C.Structure):
 
 class NpuGroupAttrs(C.Structure):
     """npu_group_attrs: per-chain activations, folded pad, heads, eps, scale,
-    the residual operand's argument index."""
+    the residual operand's argument index, the conv stride."""
 
     _fields_ = [
-        ("act", C.c_int32 * 4),
+        ("act", C.c_int32 * 16),
         ("pad", C.c_int32),
         ("n_heads", C.c_int32),
         ("eps", C.c_float),
         ("scale", C.c_float),
         ("res_arg", C.c_int32),
+        ("stride", C.c_int32),
     ]
 
 
@@ -116,8 +117,8 @@ SIGNATURES = {
                                            _P]),
     "fused_conv2d_nhwc_bias_act": (_I32, [_MR, _MR, _MR, _MR, _I32, _I32, _P]),
     "fused_conv2d_nhwc_bias_res_act": (_I32, [_MR, _MR, _MR, _MR, _MR, _I32, _I32, _P]),
-    "fused_conv2d_nchw_bias_act": (_I32, [_MR, _MR, _MR, _MR, _I32, _I32, _P]),
-    "fused_conv2d_nchw_bias_res_act": (_I32, [_MR, _MR, _MR, _MR, _MR, _I32, _I32, _P]),
+    "fused_conv2d_nchw_bias_act": (_I32, [_MR, _MR, _MR, _MR, _I32, _I32, _I32, _P]),
+    "fused_conv2d_nchw_bias_res_act": (_I32, [_MR, _MR, _MR, _MR, _MR, _I32, _I32, _I32, _P]),
     "fused_qbottleneck_i8": (_I32, [_MR] * 11 + [_P]),
     "fused_irb_f32": (_I32, [_MR] * 5 + [_P]),
     "fused_llama_qkv_rope": (_I32, [_MR] * 10 + [C.c_float, _P]),

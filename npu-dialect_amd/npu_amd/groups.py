@@ -104,20 +104,21 @@ def fused_conv2d_nhwc_bias_res_act(x, w, bias, res, out, pad=1, act="relu", stre
     return out
 
 
-def fused_conv2d_nchw_bias_act(x, w, bias, out, pad=1, act="relu", stream=None):
-    """out = act(conv_2d_nchw_fchw(pad(x), w) + bias); f32, NCHW / FCHW."""
+def fused_conv2d_nchw_bias_act(x, w, bias, out, pad=1, act="relu", stream=None, stride=1):
+    """out = act(conv_2d_nchw_fchw(pad(x), w, stride) + bias); f32, NCHW / FCHW."""
     mx, mw, mb, mo = from_tensor(x), from_tensor(w), _opt(bias), from_tensor(out)
     st = _lib.lib().fused_conv2d_nchw_bias_act(ref(mx), ref(mw), ref(mb), ref(mo), int(pad),
-                                               ACT[act], _stream(stream))
+                                               int(stride), ACT[act], _stream(stream))
     _check(st, "fused_conv2d_nchw_bias_act")
     return out
 
 
-def fused_conv2d_nchw_bias_res_act(x, w, bias, res, out, pad=1, act="relu", stream=None):
-    """out = act(conv_2d_nchw_fchw(pad(x), w) + bias + res); f32, NCHW / FCHW."""
+def fused_conv2d_nchw_bias_res_act(x, w, bias, res, out, pad=1, act="relu", stream=None,
+                                   stride=1):
+    """out = act(conv_2d_nchw_fchw(pad(x), w, stride) + bias + res); f32, NCHW / FCHW."""
     mx, mw, mb, mr, mo = from_tensor(x), from_tensor(w), _opt(bias), from_tensor(res), from_tensor(out)
     st = _lib.lib().fused_conv2d_nchw_bias_res_act(ref(mx), ref(mw), ref(mb), ref(mr), ref(mo),
-                                                   int(pad), ACT[act], _stream(stream))
+                                                   int(pad), int(stride), ACT[act], _stream(stream))
     _check(st, "fused_conv2d_nchw_bias_res_act")
     return out
 
@@ -212,7 +213,7 @@ def _group_arg(x, keep):
 
 
 def group_launch(outlined_name, ins, outs, act=("none",), pad=0, n_heads=0, eps=0.0, scale=0.0,
-                 stream=None, res_arg=0):
+                 stream=None, res_arg=0, stride=1):
     """npu_group_launch: runs the outlined group(s) `outlined_name` ('+'-joined
     for a chain) on its arguments in the outlined function's order: ``ins``
     are tensors, Empty placeholders and the fill value (a float); ``outs`` the
@@ -225,7 +226,7 @@ def group_launch(outlined_name, ins, outs, act=("none",), pad=0, n_heads=0, eps=
     for i, a in enumerate(act):
         at.act[i] = ACT[a]
     at.pad, at.n_heads, at.eps, at.scale = int(pad), int(n_heads), float(eps), float(scale)
-    at.res_arg = int(res_arg)
+    at.res_arg, at.stride = int(res_arg), int(stride)
     st = _lib.lib().npu_group_launch(outlined_name.encode(), C.byref(at), ia, len(ins), oa,
                                      len(outs), _stream(stream))
     _check(st, f"npu_group_launch({outlined_name})")

@@ -79,6 +79,7 @@ class Launch:
     outs: list = None
     params: dict = field(default_factory=dict)
     res_arg: int = 0           # index of a conv group's residual in `ins` (0: none)
+    stride: int = 1            # an NCHW conv group's stride
 
 
 _TORCH_DTYPE = {"f32": "float32", "bf16": "bfloat16", "i8": "int8", "i32": "int32"}
@@ -377,11 +378,15 @@ def _pad_of(fn: _Fn, v, nchw=False):
     return op.operands[0], lo[h]
 
 
-def _check_conv(op):
-    if any(s != 1 for s in op.attrs.get("strides", [1, 1])):
-        raise NotImplementedError(f"{op.results[0]}: strided convolution")
+def _check_conv(op, strided=False):
+    """The conv's stride (refused unless `strided`: the NCHW entry points
+    take one stride for both spatial dimensions); dilations must be 1."""
+    st = op.attrs.get("strides", [1, 1])
+    if any(s != 1 for s in st) and (not strided or len(set(st)) != 1):
+        raise NotImplementedError(f"{op.results[0]}: strided convolution {st}")
     if "dilations" in op.text and "dilations = dense<1>" not in op.text.replace("  ", " "):
         raise NotImplementedError(f"{op.results[0]}: dilated convolution")
+    return st[0] if st else 1
 
 
 def _check_matmul(op):
@@ -418,10 +423,14 @@ def _segments(name, ops):
             owner[0]["fills"].append(o)
         elif o.name == "linalg.generic":
             owner = [s for s in segs if s["value"] in o.ins]
-            if len(owner) != 1:
+            if not owner:
                 raise NotImplementedError(f"{name}: {o.results[0]} is on no matmul/conv chain")
-            owner[0]["generics"].append(o)
-            owner[0]["value"] = o.results[0]
+            # a generic joining two chains of the group (a ResNet block's add of
+            # its shortcut conv) continues the later one; the earlier chain's
+            # value is then its residual operand
+            owner = max(owner, key=lambda s: ops.index(s["anchor"]))
+            owner["generics"].append(o)
+            owner["value"] = o.results[0]
         else:
             raise NotImplementedError(f"{name}: no MI355X entry point runs {o.name} in a group")
     for s in segs:
@@ -474,17 +483,13 @@ def lower(func: mlir.MFunc, target=None) -> "Program":
             bias, res, act, out = _epilogue(fn, s["generics"], a.results[0], shape,
                                             1 if nchw else -1)
             if nchw:
-                _check_conv(a)
+                stride = _check_conv(a, strided=True)
                 x, pad = _pad_of(fn, a.ins[0], nchw=True)
                 _elem(fn, x, ("f32",), name)
-                kh, kw = fn.ty(a.ins[1]).shape[2:]
-                if (kh, kw) not in ((1, 1), (3, 3)):
-                    raise NotImplementedError(f"{name}: {kh}x{kw} NCHW filter "
-                                              "(1x1 and 3x3 are run)")
                 for v in (bias, res):
                     if v is not None and fn.ty(v).elem != "f32":
                         raise NotImplementedError(f"{name}: {v} of type {fn.ty(v).elem}")
-                params = {"pad": pad, "act": act}
+                params = {"pad": pad, "act": act, "stride": stride}
                 if res is not None:
                     calls.append(Call("fused_conv2d_nchw_bias_res_act", [name],
                                       [x, a.ins[1], bias, res], out, params))
@@ -552,12 +557,23 @@ def _launches(fn: _Fn, rep, calls, dests):
     a call spanning several groups (the inverted residual chain) is one
     launch of their '+'-joined names."""
     by_name = {f["name"]: f for f in rep["functions"]}
+    per_group = {}
+    for c in calls:
+        per_group[tuple(c.functions)] = per_group.get(tuple(c.functions), 0) + 1
     out, i = [], 0
     while i < len(calls):
-        if calls[i].outs is not None:  # a typed Llama entry point
-            c = calls[i]
+        c = calls[i]
+        if c.outs is not None:  # a typed Llama entry point
             out.append(Launch("+".join(c.functions), list(c.args), c.out, [], entry=c.entry,
                               outs=list(c.outs), params=dict(c.params)))
+            i += 1
+            continue
+        if c.entry.startswith("fused_conv2d_nchw") and per_group[tuple(c.functions)] > 1:
+            # an NCHW group of several conv chains (a ResNet downsampling
+            # block's shortcut and second conv): each chain through its typed
+            # entry point, in dataflow order
+            out.append(Launch("+".join(c.functions), list(c.args), c.out, [], entry=c.entry,
+                              outs=[c.out], params=dict(c.params)))
             i += 1
             continue
         j = i + 1
@@ -579,6 +595,7 @@ def _launches(fn: _Fn, rep, calls, dests):
                     ins.append(v)
         L = Launch("+".join(names), ins, cs[-1].out,
                    [c.params.get("act", "none") for c in cs])
+        L.stride = cs[0].params.get("stride", 1)
         c0 = cs[0]
         if c0.entry.startswith("fused_conv2d_n") and c0.params.get("pad"):
             conv_in = [v for v in ins if fn.op(v) is not None and fn.op(v).name == "tensor.pad"]
@@ -762,7 +779,8 @@ class Program:
             for v in L.outs:
                 if v not in vals:
                     vals[v] = torch.empty(types[v].shape, dtype=tdt(types[v].elem), device=dev)
-            ins, outs = [vals[v] for v in L.ins], [vals[v] for v in L.outs]
+            ins = [None if v is None else vals[v] for v in L.ins]
+            outs = [vals[v] for v in L.outs]
             getattr(groups, L.entry)(*ins, *outs, **L.params, stream=stream)
             return
         prod = {r: op for op in self.func.ops for r in op.results}
@@ -787,7 +805,7 @@ class Program:
         if L.out not in vals:
             vals[L.out] = torch.empty(oty.shape, dtype=tdt(oty.elem), device=dev)
         groups.group_launch(L.name, ins, [vals[L.out]], act=L.acts, pad=L.pad, stream=stream,
-                            res_arg=L.res_arg)
+                            res_arg=L.res_arg, stride=L.stride)
 
     def run(self, inputs: dict, stream=None) -> dict:
         """inputs: argument name (with or without %) -> tensor.  Runs every

@@ -48,14 +48,15 @@ def conv_bias_act(x, w, bias, pad=1, act="relu"):
     return out, mag
 
 
-def conv_nchw_act(x, w, bias=None, res=None, pad=1, act="relu"):
+def conv_nchw_act(x, w, bias=None, res=None, pad=1, act="relu", stride=1):
     """One NCHW conv group as the oracle runs it: tensor.pad, fill 0,
-    conv_2d_nchw_fchw, then bias, residual and activation generics; mag is
-    the same chain on absolute values."""
+    conv_2d_nchw_fchw (strided), then bias, residual and activation
+    generics; mag is the same chain on absolute values."""
+    st = (stride, stride)
     xp = oracle.pad_nchw(x, (pad, pad, pad, pad)) if pad else np.asarray(x, np.float32)
-    out = oracle.conv2d_nchw_fchw(xp, w)
+    out = oracle.conv2d_nchw_fchw(xp, w, st)
     axp = oracle.pad_nchw(np.abs(x), (pad, pad, pad, pad)) if pad else np.abs(x)
-    mag = oracle.conv2d_nchw_fchw(axp, np.abs(w)).astype(np.float64)
+    mag = oracle.conv2d_nchw_fchw(axp, np.abs(w), st).astype(np.float64)
     if bias is not None:
         out = oracle.add(out, np.broadcast_to(np.asarray(bias, np.float32)[None, :, None, None],
                                               out.shape))
@@ -93,6 +94,71 @@ def nchw_workload(name, args):
     out, _ = conv_nchw_act(r2, w3, res=x, pad=0, act=act)
     mag = oracle.conv2d_nchw_fchw(m2, np.abs(w3)) + np.abs(x)
     return out, mag.astype(np.float64)
+
+
+def _generic_kind(op):
+    """'relu' or 'add' for the model zoo's two epilogue generics, by body."""
+    body = [b.name for b in op.attrs.get("body", [])]
+    if "arith.maximumf" in body and len(op.ins) == 1:
+        return "relu"
+    if body[:1] == ["arith.addf"] and len(op.ins) == 2:
+        return "add"
+    raise NotImplementedError(f"{op.results[0]}: generic body {body}")
+
+
+def run_network(func, args, given=None):
+    """Runs a parsed linalg function of the model zoo's forms (NCHW
+    conv_2d_nchw_fchw with strides, matmul, zero fills and pads, ReLU and
+    add generics) op by op with the oracle's loops, the way mlir-runner runs
+    the lowered function.  ``given`` maps SSA names to values computed
+    elsewhere (the GPU's results of earlier launches): an op reads a given
+    value instead of the oracle's own, so each op's result is the oracle's
+    for the same inputs.  Returns (vals, mags, depth) by SSA name: mags is
+    the same computation on magnitudes, restarted at every given value (each
+    conv / matmul applied to its inputs' magnitudes and the filters'
+    absolute values, adds summed, ReLU passed through), the scale of the
+    value's error bound; depth counts conv / matmul ops since the last given
+    value."""
+    given = given or {}
+    vals, mags, depth = {}, {}, {}
+
+    def src(v):
+        if v in given:
+            x = np.asarray(given[v], np.float32)
+            return x, np.abs(x), 0
+        return vals[v], mags[v], depth[v]
+    for (a, _), x in zip(func.args, args):
+        vals[a] = np.asarray(x, np.float32)
+        mags[a] = np.abs(vals[a])
+        depth[a] = 0
+    for op in func.ops:
+        r = op.results[0] if op.results else None
+        if op.name in ("arith.constant", "tensor.empty", "linalg.fill", "func.return"):
+            continue
+        if op.name == "tensor.pad":
+            lo, hi = op.attrs["low"], op.attrs["high"]
+            x, m, d = src(op.operands[0])
+            pads = (lo[2], hi[2], lo[3], hi[3])
+            vals[r], mags[r], depth[r] = oracle.pad_nchw(x, pads), oracle.pad_nchw(m, pads), d
+        elif op.name == "linalg.conv_2d_nchw_fchw":
+            (x, mx, dx), (w, mw, dw) = src(op.ins[0]), src(op.ins[1])
+            st = tuple(op.attrs.get("strides", [1, 1]))
+            vals[r] = oracle.conv2d_nchw_fchw(x, w, st)
+            mags[r] = oracle.conv2d_nchw_fchw(mx, mw, st)
+            depth[r] = max(dx, dw) + 1
+        elif op.name == "linalg.matmul":
+            (a, ma, da), (b, mb, db) = src(op.ins[0]), src(op.ins[1])
+            vals[r], mags[r], depth[r] = oracle.matmul(a, b), oracle.matmul(ma, mb), max(da, db) + 1
+        elif op.name == "linalg.generic":
+            if _generic_kind(op) == "relu":
+                x, m, d = src(op.ins[0])
+                vals[r], mags[r], depth[r] = oracle.relu(x), m, d
+            else:
+                (a, ma, da), (b, mb, db) = src(op.ins[0]), src(op.ins[1])
+                vals[r], mags[r], depth[r] = oracle.add(a, b), ma + mb, max(da, db)
+        else:
+            raise NotImplementedError(op.name)
+    return vals, {k: v.astype(np.float64) for k, v in mags.items()}, depth
 
 
 def irb(x, we, wdw, wp):

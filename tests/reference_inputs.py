@@ -15,6 +15,9 @@ TEST_DIR = os.environ.get("NPU_DIALECT_TEST_DIR", "/root/reference/test")
 # test/lit/ (the larger *_full.mlir and model-zoo files are not needed).
 WORKLOADS = ["conv2d_relu.mlir", "llama_attention.mlir", "matmul_relu.mlir", "mlp.mlir",
              "mobilenet_block.mlir", "resnet50_block.mlir", "resnet_block.mlir"]
+MODELS = ["autoencoder.mlir", "autoencoder_deep.mlir", "dcgan_generator.mlir", "espcn.mlir",
+          "resnet18.mlir", "resnet34.mlir", "resnet50.mlir", "resnet_deep_20.mlir", "srcnn.mlir",
+          "vgg11.mlir"]
 LIT = ["batch_matmul_tiling.mlir", "bufferize_dma.mlir", "cost_evaluate.mlir",
        "fusion_matmul_relu.mlir", "outline_groups.mlir", "spatial_tiling_conv2d.mlir",
        "spatial_tiling_matmul.mlir", "static_shapes.mlir", "temporal_tiling_matmul.mlir"]

@@ -736,30 +736,37 @@ def test_reference_nchw_workloads_run_on_the_gpu(cuda, name, fills):
     assert all(L.name.startswith("fused_fill_conv2d_generic") for L in prog.launches)
 
 
-@pytest.mark.parametrize("N,C,H,W,F,K,pad,act,bias,res", [
-    (2, 20, 9, 37, 40, 3, 1, "relu", True, False),    # C and F off the 16 / 64 blocks, ragged segments
-    (1, 64, 56, 56, 64, 3, 1, "relu", False, True),   # the reference's conv, with a residual
-    (1, 256, 14, 14, 64, 1, 0, "relu6", True, False),  # 1x1, sixteen channel chunks
-    (3, 8, 5, 70, 24, 3, 0, "none", False, True),     # valid conv, rows past one segment
-    (1, 192, 28, 112, 192, 3, 1, "relu", False, False),  # 64-pixel segments (large grid)
-    (1, 4, 3, 3, 4, 1, 0, "none", True, False),       # a handful of values
+@pytest.mark.parametrize("N,C,H,W,F,K,pad,st,act,bias,res", [
+    (2, 20, 9, 37, 40, 3, 1, 1, "relu", True, False),    # C and F off the 16 / 64 blocks, ragged segments
+    (1, 64, 56, 56, 64, 3, 1, 1, "relu", False, True),   # the reference's conv, with a residual
+    (1, 256, 14, 14, 64, 1, 0, 1, "relu6", True, False),  # 1x1, sixteen channel chunks
+    (3, 8, 5, 70, 24, 3, 0, 1, "none", False, True),     # valid conv, rows past one segment
+    (1, 192, 28, 112, 192, 3, 1, 1, "relu", False, False),  # 64-pixel segments (large grid)
+    (1, 4, 3, 3, 4, 1, 0, 1, "none", True, False),       # a handful of values
+    (2, 64, 15, 15, 128, 3, 1, 2, "relu", True, True),   # stride 2, odd sizes (staged kernel)
+    (1, 64, 14, 14, 128, 1, 0, 2, "none", False, False),  # the 1x1 stride-2 shortcut
+    (1, 3, 30, 34, 64, 7, 3, 2, "relu", False, False),   # a 7x7/2 stem (direct kernel)
+    (1, 32, 9, 9, 40, 5, 2, 1, "relu6", True, False),    # 5x5 (direct)
+    (1, 20, 11, 13, 24, 9, 4, 1, "relu", False, True),   # 9x9, pad 4 (direct)
+    (1, 512, 7, 7, 100, 7, 0, 1, "none", False, False),  # the classifier as a conv: 1x1 output
 ])
-def test_nchw_conv_shapes(cuda, N, C, H, W, F, K, pad, act, bias, res):
+def test_nchw_conv_shapes(cuda, N, C, H, W, F, K, pad, st, act, bias, res):
     x = rng.uniform(32, 0, (N, C, H, W), -1, 1)
     w = rng.normal(32, 1, (F, C, K, K), 0, math.sqrt(2 / (K * K * C)))
     b = rng.uniform(32, 2, (F,), -0.1, 0.1) if bias else None
-    Ho, Wo = H + 2 * pad - K + 1, W + 2 * pad - K + 1
+    Ho, Wo = (H + 2 * pad - K) // st + 1, (W + 2 * pad - K) // st + 1
     r = rng.uniform(32, 3, (N, F, Ho, Wo), -1, 1) if res else None
     out = torch.empty(N, F, Ho, Wo, device="cuda")
     if res:
         groups.fused_conv2d_nchw_bias_res_act(_dev(x), _dev(w), None if b is None else _dev(b),
-                                              _dev(r), out, pad, act)
+                                              _dev(r), out, pad, act, stride=st)
     else:
         groups.fused_conv2d_nchw_bias_act(_dev(x), _dev(w), None if b is None else _dev(b), out,
-                                          pad, act)
+                                          pad, act, stride=st)
     torch.cuda.synchronize()
-    ref, mag = refs.conv_nchw_act(x, w, b, r, pad, act)
-    check_bound(_host(out), ref, mag, RTOL_F32, what=f"nchw conv {N}x{C}x{H}x{W} -> {F} {K}x{K}")
+    ref, mag = refs.conv_nchw_act(x, w, b, r, pad, act, stride=st)
+    check_bound(_host(out), ref, mag, RTOL_F32,
+                what=f"nchw conv {N}x{C}x{H}x{W} -> {F} {K}x{K}/{st}")
 
 
 def test_nchw_conv_non_finite(cuda):
@@ -781,6 +788,50 @@ def test_nchw_conv_non_finite(cuda):
     fin = hit & ~np.isnan(ref)
     assert np.array_equal(got[fin], ref[fin])
     check_bound(got[~hit], ref[~hit], mag[~hit], RTOL_F32, what="nchw conv next to NaN / Inf")
+
+
+@pytest.mark.parametrize("name", ["resnet18", "resnet50", "vgg11", "srcnn", "espcn",
+                                  "dcgan_generator", "autoencoder", "autoencoder_deep"])
+def test_model_zoo_networks_run_on_the_gpu(cuda, name):
+    """Whole networks of the reference's model zoo (test/models/<name>.mlir,
+    the builder's text, checked op for op against the file on the CPU), f16
+    run as f32: lowered, every group launched through npu_group_launch or,
+    for a group of two conv chains (a ResNet downsampling block's shortcut
+    and second conv), its entry points; U(0, 1) input, He-normal weights.
+    Every launch's result is held to the f32 bound against the oracle's loops
+    run on that launch's own inputs (the GPU's results of the launches
+    before it); the network's output is within a relative 2-norm of 1e-4 of
+    the oracle run end to end (f32 rounding through up to 50 layers stays
+    near 1e-6; a wrong layout, stride, pad or residual gives order 1).  The
+    element-wise magnitude bound end to end would be vacuous here: |W|
+    products grow far faster than the values through the layers."""
+    from npu_amd import model_zoo
+    prog = lower.lower_text(model_zoo.model(name))
+    ins, host = {}, []
+    for i, (a, t) in enumerate(prog.func.args):
+        if i == 0:
+            arr = rng.uniform(34, i, tuple(t.shape), 0, 1)
+        else:
+            fan = int(np.prod(t.shape[1:])) if len(t.shape) == 4 else t.shape[0]
+            arr = rng.normal(34, i, tuple(t.shape), 0, math.sqrt(2 / fan))
+        host.append(arr)
+        ins[a] = _dev(arr)
+    print(f"{name}: {len(prog.launches)} launches", flush=True)
+    vals = prog.check_inputs(ins)
+    for li in range(len(prog.launches)):
+        prog.run_launch(li, vals)
+    torch.cuda.synchronize()
+    gpu = {v: _host(t) for v, t in vals.items() if v not in ins and v.lstrip("%") not in ins}
+    with oracle.threaded():
+        per, mags, _ = refs.run_network(prog.func, host, given=gpu)
+        end, _, depth = refs.run_network(prog.func, host)
+    for L in prog.launches:
+        for v in L.outs or [L.out]:
+            check_bound(gpu[v], per[v], mags[v], RTOL_F32, what=f"{name}: launch {L.name} -> {v}")
+    (out,) = [op.operands[0] for op in prog.func.ops if op.name == "func.return"]
+    rel = np.linalg.norm(gpu[out].astype(np.float64) - end[out]) / np.linalg.norm(end[out])
+    print(f"{name}: depth {depth[out]}, end-to-end relative 2-norm {rel:.3g}", flush=True)
+    assert rel <= 1e-4, f"{name}: end-to-end relative difference {rel:.3g}"
 
 
 def test_compiled_c_caller_on_the_gpu(cuda):

@@ -83,18 +83,34 @@ def test_reference_nchw_workloads_lower_to_their_groups(name, calls):
             assert L.ins[L.res_arg] == c.args[3] == p.func.args[0][0]
 
 
-def test_nchw_conv_refusals():
-    """What the NCHW entry points do not run is refused by name: a 5x5
-    filter, a stride of 2, a pad that is not symmetric in H and W."""
+def test_nchw_conv_any_filter_and_stride_lowers():
+    """A 5x5 filter and a stride of 2 lower to the NCHW entry point with the
+    stride as a launch attribute (the model zoo's 7x7 stems, 9x9 and 5x5
+    filters, stride-2 downsampling convs)."""
     t = blocks.nchw_conv_relu(1, 16, 16, 8, 8, elem="f32")
     five = t.replace("16x16x3x3", "16x16x5x5").replace("x10x10xf32", "x12x12xf32") \
         .replace("low[0, 0, 1, 1] high[0, 0, 1, 1]", "low[0, 0, 2, 2] high[0, 0, 2, 2]")
-    with pytest.raises(NotImplementedError, match="5x5"):
-        lower.lower_text(five)
-    strided = t.replace("strides = dense<1>", "strides = dense<2>").replace("1x16x8x8xf32> -> ",
-                                                                            "1x16x8x8xf32> -> ")
-    with pytest.raises(NotImplementedError, match="strided"):
-        lower.lower_text(strided)
+    (L,) = lower.lower_text(five).launches
+    assert (L.name, L.pad, L.stride) == ("fused_fill_conv2d_generic_0", 2, 1)
+    strided = t.replace("strides = dense<1>", "strides = dense<2>").replace(
+        "tensor<1x16x8x8xf32>) -> tensor<1x16x8x8xf32>", "tensor<1x16x8x8xf32>) -> tensor<1x16x4x4xf32>")
+    strided = strided.replace("outs(%c_f : tensor<1x16x8x8xf32>) -> tensor<1x16x8x8xf32>",
+                              "outs(%c_f : tensor<1x16x4x4xf32>) -> tensor<1x16x4x4xf32>")
+    strided = strided.replace("%c_i = tensor.empty() : tensor<1x16x8x8xf32>",
+                              "%c_i = tensor.empty() : tensor<1x16x4x4xf32>")
+    strided = strided.replace("%c_f = linalg.fill ins(%cst : f32) outs(%c_i : tensor<1x16x8x8xf32>) -> "
+                              "tensor<1x16x8x8xf32>", "%c_f = linalg.fill ins(%cst : f32) outs(%c_i : "
+                              "tensor<1x16x4x4xf32>) -> tensor<1x16x4x4xf32>")
+    (L,) = lower.lower_text(strided).launches
+    assert L.stride == 2
+
+
+def test_nchw_conv_refusals():
+    """What the NCHW entry points do not run is refused by name: a dilated
+    conv, a pad that is not symmetric in H and W."""
+    t = blocks.nchw_conv_relu(1, 16, 16, 8, 8, elem="f32")
+    with pytest.raises(NotImplementedError, match="dilated"):
+        lower.lower_text(t.replace("dilations = dense<1>", "dilations = dense<2>"))
     lopsided = t.replace("high[0, 0, 1, 1]", "high[0, 0, 1, 2]")
     with pytest.raises(NotImplementedError, match="pad"):
         lower.lower_text(lopsided)
