@@ -27,6 +27,16 @@ directly, NCHW and f16.  The kernels here take channels last, so:
   one block of a model-zoo text, e.g. the inverted residual block at
   test/models/mobilenetv2.mlir:166-226.
 
+* ``from_torch_int8(module, calib)`` quantizes a float ResNet bottleneck
+  (1x1 conv, ReLU, 3x3 conv, ReLU, 1x1 conv, + input, ReLU; no conv biases)
+  after training: filters per output channel, symmetric, to [-127, 127];
+  activations with zero point 0, the block's input and output at scale
+  1/127 (so the residual adds directly), the two inner activations at the
+  scale that maps their 99.9th percentile on the calibration batch to 127;
+  each requantization's multiplier and shift the fixed-point form of
+  s_in * s_w[c] / s_out.  Returns the int8 NHWC linalg text the int8
+  bottleneck's lowering runs and its argument arrays.
+
 ``emit(func)`` prints a parsed function back as text.
 """
 from __future__ import annotations
@@ -348,10 +358,10 @@ def from_torch(module, x, elem="f32", name="model"):
                                      name="linalg.depthwise_conv_2d_nhwc_hwc"))
             else:
                 raise NotImplementedError(f"{node.name}: grouped conv, groups {m.groups}")
-            if bias is not None and elem != "f32":
-                raise NotImplementedError(f"{node.name}: a bias (or folded batch norm) on a "
-                                          f"{elem} conv")
-            bn_ = w.arg("b", bias.float()) if bias is not None else None
+            # the bias (or the folded batch norm's) in the text's element type:
+            # a bf16 text holds it rounded to bf16, which the lowering widens
+            # exactly to the f32 bias the entry point adds
+            bn_ = w.arg("b", bias.to(tdt)) if bias is not None else None
             out = w.fresh("y")
             if bn_ is not None or res is not None or act != "none":
                 w.lines.append(_epilogue(out, cn, bn_, os_, elem, act,
@@ -397,3 +407,87 @@ def from_torch(module, x, elem="f32", name="model"):
             raise NotImplementedError(f"{node.name}: {k} (the frontend writes conv, batch norm "
                                       "after a conv, linear, ReLU / ReLU6 and residual adds)")
     raise NotImplementedError("the module has no output")
+
+
+def from_torch_int8(module, calib, name="qbottleneck"):
+    """(text, {argument: numpy array}) of a float ResNet bottleneck quantized
+    after training (module docstring).  `module` has the structure conv1
+    (1x1, C -> M1), ReLU, conv2 (3x3, pad 1), ReLU, conv3 (1x1, M1 -> C), a
+    residual add of the block input and a ReLU, with a batch norm after each
+    conv allowed when it only scales (zero mean and shift): the int8 kernel
+    adds no bias.  `calib` is an NCHW float batch with values in [0, 1]."""
+    import operator
+
+    import numpy as np
+    import torch
+    import torch.fx
+
+    from . import blocks
+    from .configs import _quantize_per_channel, quant_multiplier, requant_np
+
+    module = module.eval()
+    gm = torch.fx.symbolic_trace(module)
+    mods = dict(gm.named_modules())
+    convs, seq = [], []
+    for n in gm.graph.nodes:
+        if n.op == "call_module":
+            m = mods[n.target]
+            k = type(m).__name__
+            if k == "Conv2d":
+                if m.bias is not None and bool(torch.any(m.bias != 0)):
+                    raise NotImplementedError(f"{n.name}: conv bias (the int8 kernel adds none)")
+                if m.stride != (1, 1) or m.groups != 1 or m.dilation != (1, 1):
+                    raise NotImplementedError(f"{n.name}: stride / groups / dilation")
+                convs.append([m.weight.detach().double(), m.padding[0]])
+                seq.append("conv")
+            elif k == "BatchNorm2d":
+                if not convs or seq[-1] != "conv":
+                    raise NotImplementedError(f"{n.name}: batch norm not after a conv")
+                sh = m.bias.detach().double() - m.running_mean.double() * m.weight.detach().double() \
+                    / torch.sqrt(m.running_var.double() + m.eps)
+                if bool(torch.any(sh.abs() > 1e-12)):
+                    raise NotImplementedError(f"{n.name}: batch norm with a shift (a bias)")
+                sc = m.weight.detach().double() / torch.sqrt(m.running_var.double() + m.eps)
+                convs[-1][0] = convs[-1][0] * sc.view(-1, 1, 1, 1)
+            elif k == "ReLU":
+                seq.append("relu")
+            else:
+                raise NotImplementedError(f"{n.name}: {k}")
+        elif n.op == "call_function":
+            if n.target in (operator.add, torch.add):
+                seq.append("add")
+            elif n.target in (torch.relu, torch.nn.functional.relu):
+                seq.append("relu")
+            else:
+                raise NotImplementedError(f"{n.name}: {n.target}")
+        elif n.op == "call_method" and n.target == "relu":
+            seq.append("relu")
+    if seq != ["conv", "relu", "conv", "relu", "conv", "add", "relu"] or len(convs) != 3:
+        raise NotImplementedError(f"not a bottleneck: {seq}")
+    (w1f, p1), (w2f, p2), (w3f, p3) = convs
+    M1, C = w1f.shape[0], w1f.shape[1]
+    if (p1, p2, p3) != (0, 1, 0) or tuple(w1f.shape[2:]) != (1, 1) or \
+            tuple(w2f.shape) != (M1, M1, 3, 3) or tuple(w3f.shape) != (C, M1, 1, 1):
+        raise NotImplementedError("conv shapes are not 1x1 C->M1, 3x3 M1->M1, 1x1 M1->C")
+    # weights per output channel; FHWC / [F, C] layouts of the int8 text
+    w1, sw1 = _quantize_per_channel(w1f[:, :, 0, 0].numpy())
+    w2, sw2 = _quantize_per_channel(w2f.permute(0, 2, 3, 1).numpy())
+    w3, sw3 = _quantize_per_channel(w3f[:, :, 0, 0].numpy())
+    xq = np.clip(np.rint(calib.permute(0, 2, 3, 1).double().numpy() * 127), 0, 127).astype(np.int8)
+    N, H, W, _ = xq.shape
+    sx = 1.0 / 127
+    acc1 = xq.reshape(-1, C).astype(np.int64) @ w1.astype(np.int64).T
+    sy1 = np.percentile(np.maximum(acc1 * (sx * sw1), 0), 99.9) / 127
+    m1, s1 = quant_multiplier(sx * sw1 / sy1)
+    y1 = np.clip(requant_np(acc1, m1, s1), 0, 127).reshape(N, H, W, M1)
+    y1p = np.pad(y1, ((0, 0), (1, 1), (1, 1), (0, 0)))
+    cols = np.concatenate([y1p[:, kh:kh + H, kw:kw + W] for kh in range(3) for kw in range(3)],
+                          -1).reshape(-1, 9 * M1)
+    acc2 = cols @ w2.reshape(M1, -1).astype(np.int64).T
+    sy2 = np.percentile(np.maximum(acc2 * (sy1 * sw2), 0), 99.9) / 127
+    m2, s2 = quant_multiplier(sy1 * sw2 / sy2)
+    m3, s3 = quant_multiplier(sy2 * sw3 / sx)
+    text = blocks.qbottleneck(N, H, W, C, M1).replace("@qbottleneck(", f"@{name}(")
+    args = {"x": xq, "w1": w1.reshape(M1, 1, 1, C), "w2": w2, "w3": w3.reshape(C, 1, 1, M1),
+            "m1": m1, "s1": s1, "m2": m2, "s2": s2, "m3": m3, "s3": s3}
+    return text, args

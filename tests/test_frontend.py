@@ -202,3 +202,65 @@ def test_model_zoo_block_lowers_to_three_conv_launches():
         ("fused_conv2d_nhwc_bias_act", {"pad": 1, "act": "relu"}),
         ("fused_conv2d_nhwc_bias_res_act", {"pad": 0, "act": "none"})]
     assert prog.calls[2].args[3] == "%x"
+
+
+class _FloatBottleneck(nn.Module):
+    """A ResNet bottleneck without conv biases; BatchNorms that only scale."""
+
+    def __init__(self, C=64, M=64, bn=False):
+        super().__init__()
+        self.c1 = nn.Conv2d(C, M, 1, bias=False)
+        self.c2 = nn.Conv2d(M, M, 3, padding=1, bias=False)
+        self.c3 = nn.Conv2d(M, C, 1, bias=False)
+        self.bn = bn
+        if bn:
+            self.b1 = nn.BatchNorm2d(M)
+            with torch.no_grad():
+                self.b1.weight.uniform_(0.5, 1.5)
+                self.b1.running_var.uniform_(0.5, 2.0)
+                self.b1.bias.zero_()
+                self.b1.running_mean.zero_()
+
+    def forward(self, x):
+        y = self.c1(x)
+        if self.bn:
+            y = self.b1(y)
+        y = torch.relu(y)
+        y = torch.relu(self.c2(y))
+        return torch.relu(self.c3(y) + x)
+
+
+@pytest.mark.parametrize("bn", [False, True])
+def test_int8_frontend_quantizes_a_bottleneck(bn):
+    """Post-training quantization of a float bottleneck: the int8 text lowers
+    to the int8 bottleneck entry point, and the oracle's int8 result,
+    dequantized, follows the float module within the quantization error
+    wherever the output is below the output scale's saturation (1.0)."""
+    import numpy as np
+
+    import oracle
+    torch.manual_seed(1)
+    m = _FloatBottleneck(bn=bn)
+    x = torch.rand(2, 64, 8, 8)
+    text, a = frontend.from_torch_int8(m, x)
+    (c,) = lower.lower_text(text).calls
+    assert c.entry == "fused_qbottleneck_i8"
+    assert a["x"].dtype == np.int8 and a["m1"].dtype == np.int32
+    q = oracle.block_qbottleneck(a["x"], a["w1"].reshape(64, 64), a["w2"], a["w3"].reshape(64, 64),
+                                 a["m1"], a["s1"], a["m2"], a["s2"], a["m3"], a["s3"])
+    fl = m(x).detach().permute(0, 2, 3, 1).numpy()
+    ok = fl < 0.99
+    assert ok.mean() > 0.9
+    assert np.abs(q.astype(np.float64)[ok] / 127 - fl[ok]).max() < 0.05
+
+
+def test_int8_frontend_refuses_biases_and_other_graphs():
+    m = _FloatBottleneck()
+    m.c1 = nn.Conv2d(64, 64, 1, bias=True)
+    with torch.no_grad():
+        m.c1.bias.fill_(0.1)
+    with pytest.raises(NotImplementedError, match="bias"):
+        frontend.from_torch_int8(m, torch.rand(1, 64, 8, 8))
+    with pytest.raises(NotImplementedError, match="bottleneck"):
+        frontend.from_torch_int8(nn.Sequential(nn.Conv2d(64, 64, 1, bias=False), nn.ReLU()),
+                                 torch.rand(1, 64, 8, 8))

@@ -834,6 +834,59 @@ def test_model_zoo_networks_run_on_the_gpu(cuda, name):
     assert rel <= 1e-4, f"{name}: end-to-end relative difference {rel:.3g}"
 
 
+def test_int8_frontend_runs_on_the_gpu(cuda):
+    """A float ResNet bottleneck (C = 256, M1 = 64) quantized by the int8
+    frontend, lowered and run: bit-exact against the oracle's int8 loops."""
+    import torch.nn as nn
+    from test_frontend import _FloatBottleneck
+    torch.manual_seed(2)
+    m = _FloatBottleneck(C=256, M=64, bn=True)
+    with torch.no_grad():
+        for c in (m.c1, m.c2, m.c3):
+            nn.init.kaiming_normal_(c.weight)
+    x = torch.rand(4, 256, 14, 14)
+    text, a = frontend.from_torch_int8(m, x)
+    prog = lower.lower_text(text)
+    (res,) = prog.run({k: configs.to_device({k: v})[k] for k, v in a.items()}).values()
+    torch.cuda.synchronize()
+    ref = oracle.block_qbottleneck(a["x"], a["w1"].reshape(64, 256), a["w2"],
+                                   a["w3"].reshape(256, 64), a["m1"], a["s1"], a["m2"], a["s2"],
+                                   a["m3"], a["s3"])
+    assert np.array_equal(_host(res), ref)
+
+
+def test_bf16_frontend_runs_on_the_gpu(cuda):
+    """The torch frontend in bf16: a BasicBlock (conv, batch norm folded,
+    ReLU, conv, batch norm, residual, ReLU) traced to bf16 NHWC linalg,
+    lowered (biases widened to f32) and run, against the block computed in
+    float64 from the same bf16 arguments, stage bound (the first conv's
+    output is rounded to bf16 before the second conv reads it)."""
+    import torch.nn as nn
+    from test_frontend import BasicBlock, randomize_bn
+    torch.manual_seed(3)
+    m = randomize_bn(BasicBlock(64))
+    x = torch.rand(2, 64, 14, 14)
+    text, params = frontend.from_torch(m, x, elem="bf16", name="basic_bf16")
+    prog = lower.lower_text(text)
+    dev = {k: v.cuda() for k, v in params.items()}
+    (res,) = prog.run(dev).values()
+    torch.cuda.synchronize()
+    f = {k: v.double() for k, v in params.items()}
+    y1 = torch.relu(torch.nn.functional.conv2d(f["x0"].permute(0, 3, 1, 2),
+                                               f["w1"].permute(0, 3, 1, 2), f["b2"], padding=1))
+    y1 = y1.to(torch.bfloat16).double()
+    out = torch.nn.functional.conv2d(y1, f["w3"].permute(0, 3, 1, 2), f["b4"], padding=1) + \
+        f["x0"].permute(0, 3, 1, 2)
+    exact = torch.relu(out).permute(0, 2, 3, 1).numpy()
+    a = lambda t: t.abs()
+    m1 = torch.nn.functional.conv2d(a(f["x0"]).permute(0, 3, 1, 2), a(f["w1"]).permute(0, 3, 1, 2),
+                                    a(f["b2"]), padding=1)
+    mag = (torch.nn.functional.conv2d(m1, a(f["w3"]).permute(0, 3, 1, 2), a(f["b4"]), padding=1) +
+           a(f["x0"]).permute(0, 3, 1, 2)).permute(0, 2, 3, 1).numpy()
+    got = _host(res)
+    check_bf16_stage(got, exact, mag, 9 * 64 + 2, what="bf16 BasicBlock")
+
+
 def test_compiled_c_caller_on_the_gpu(cuda):
     """The C program that calls npu_group_launch by outlined name with MLIR
     memref descriptors: the matmul_relu and mlp closed forms and the C1 group
