@@ -89,30 +89,37 @@ HWTarget mi355x_target(int32_t elem_bits) {
 // CostModel.cpp:46-89
 int64_t CostModel::op_macs(int32_t opi) const {
   const ir::Op &op = g_.ops[opi];
+  // The output shape is the result's; an op in memref form has no result,
+  // so its destination (the init operand, last) stands in for it.  The
+  // reference reads getResult(0) for matmul / batch_matmul / conv, which such
+  // an op does not have; a generic without results is priced at the default.
+  const int32_t out = op.results.empty() ? (op.operands.empty() ? -1 : op.operands.back())
+                                         : op.results[0];
+  if (out < 0 && op.kind != OpKind::Generic) return 1024;
   switch (op.kind) {
     case OpKind::Matmul: {
-      const auto &o = g_.type(op.results[0]);
+      const auto &o = g_.type(out);
       const auto &a = g_.type(op.operands[0]);
       return dim_or_one(o, 0) * dim_or_one(o, 1) * dim_or_one(a, 1);
     }
     case OpKind::BatchMatmul: {
-      const auto &o = g_.type(op.results[0]);
+      const auto &o = g_.type(out);
       const auto &a = g_.type(op.operands[0]);
       return dim_or_one(o, 0) * dim_or_one(o, 1) * dim_or_one(o, 2) * dim_or_one(a, 2);
     }
     case OpKind::Conv2dNchwFchw: {
-      const auto &o = g_.type(op.results[0]);
+      const auto &o = g_.type(out);
       const auto &f = g_.type(op.operands[1]);
       return dim_or_one(o, 0) * dim_or_one(o, 1) * dim_or_one(o, 2) * dim_or_one(o, 3) *
              dim_or_one(f, 1) * dim_or_one(f, 2) * dim_or_one(f, 3);
     }
     case OpKind::Conv2dNhwcFhwc: {
-      const auto &o = g_.type(op.results[0]);
+      const auto &o = g_.type(out);
       const auto &f = g_.type(op.operands[1]);
       return safe_product(o) * dim_or_one(f, 1) * dim_or_one(f, 2) * dim_or_one(f, 3);
     }
     case OpKind::DepthwiseNhwcHwc: {
-      const auto &o = g_.type(op.results[0]);
+      const auto &o = g_.type(out);
       const auto &f = g_.type(op.operands[1]);
       return safe_product(o) * dim_or_one(f, 0) * dim_or_one(f, 1);
     }

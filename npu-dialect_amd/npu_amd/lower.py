@@ -356,6 +356,8 @@ def _epilogue(fn: _Fn, generics, src, shape, cdim=-1):
 
 
 def _check_fill(fn: _Fn, fill):
+    if fill.ins and fill.ins[0] in {a for a, _ in fn.f.args}:
+        return  # an outlined kernel's argument: npu_group_launch checks its value
     c = _const(fn, fill.ins[0]) if fill.ins else None
     if c != 0.0:
         raise NotImplementedError(f"{fill.results[0]}: linalg.fill with {fill.ins} "
@@ -440,12 +442,22 @@ def _segments(name, ops):
     return segs
 
 
-def lower(func: mlir.MFunc, target=None) -> "Program":
-    """Matches func's outlined groups to entry points; see the module docstring."""
+def lower(func: mlir.MFunc, target=None, groups=None) -> "Program":
+    """Matches func's outlined groups to entry points; see the module docstring.
+    `groups` ([{name, ops, inputs, outputs}], ops as indices into func.ops)
+    gives the groups instead of the restated pipeline's decisions: the
+    outlined kernels of a module npu-opt has already run (npu_amd.reader)."""
     from . import lower_llama
 
     fn = _Fn(func)
-    rep = pipeline.run(func, target)
+    if groups is None:
+        rep = pipeline.run(func, target)
+    else:
+        inside = {i for g in groups for i in g["ops"]}
+        rest = [i for i, o in enumerate(func.ops) if o.name.startswith("linalg.")
+                and i not in inside]
+        rep = {"functions": [dict(g) for g in groups] +
+               ([{"name": func.name, "ops": rest, "inputs": [], "outputs": []}] if rest else [])}
     groups = {g["name"]: [func.ops[i] for i in g["ops"]] for g in rep["functions"]}
     calls, covered, consumed, dests = [], set(), set(), {}
     # a Llama layer: its calls span the pipeline's groups, which hold only its ops

@@ -337,10 +337,12 @@ def parse_op(stmt: str) -> MOp:
     return op
 
 
-def parse_functions(text: str) -> list:
-    """Every func.func with a body in the text."""
+def split_functions(text: str) -> list:
+    """Every func.func with a body: dicts of name, private (bool), header
+    (the text between the argument list and the body: results and
+    attributes), args [(name, TType)], result_types and body (text)."""
     funcs = []
-    for m in re.finditer(r"func\.func\s+(?:private\s+)?@([\w]+)\s*\(", text):
+    for m in re.finditer(r"func\.func\s+(private\s+)?@([\w]+)\s*\(", text):
         i = m.end()
         depth, j = 1, i
         while depth:
@@ -351,9 +353,14 @@ def parse_functions(text: str) -> list:
             j += 1
         args_txt = text[i:j - 1]
         k = text.index("{", j)
+        # a `{` of an attribute dict before the body: `attributes {npu.fused_kernel} {`
+        while re.search(r"attributes\s*$", text[j:k]):
+            d, e = 1, k + 1
+            while d:
+                d += {"{": 1, "}": -1}.get(text[e], 0)
+                e += 1
+            k = text.index("{", e)
         header = text[j:k]
-        if "attributes" in header and header.strip().startswith("->") is False and "->" not in header:
-            pass
         depth, e = 1, k + 1
         while depth:
             if text[e] == "{":
@@ -361,13 +368,13 @@ def parse_functions(text: str) -> list:
             elif text[e] == "}":
                 depth -= 1
             e += 1
-        body = text[k + 1:e - 1]
-        args = []
+        args, arg_text = [], []
         for a in _split_top(args_txt):
             if not a:
                 continue
             n, t = a.split(":", 1)
             args.append((n.strip(), parse_type(t.split("{")[0])))
+            arg_text.append(t.strip())
         rtypes = []
         rm = re.search(r"->\s*(.*?)(?:attributes|$)", header, re.S)
         if rm and rm.group(1).strip():
@@ -375,12 +382,22 @@ def parse_functions(text: str) -> list:
             if rt.startswith("("):
                 rt = rt[1:-1]
             rtypes = [parse_type(t) for t in _split_top(rt)]
-        ops = [parse_op(s) for s in _statements(body)]
-        types = {n: t for n, t in args}
+        funcs.append({"name": m.group(2), "private": bool(m.group(1)), "header": header,
+                      "args": args, "arg_text": arg_text, "result_types": rtypes,
+                      "body": text[k + 1:e - 1]})
+    return funcs
+
+
+def parse_functions(text: str) -> list:
+    """Every func.func with a body in the text."""
+    funcs = []
+    for f in split_functions(text):
+        ops = [parse_op(s) for s in _statements(f["body"])]
+        types = {n: t for n, t in f["args"]}
         for op in ops:
             for r, t in zip(op.results, op.result_types):
                 types[r] = t
-        funcs.append(MFunc(m.group(1), args, rtypes, ops, types))
+        funcs.append(MFunc(f["name"], f["args"], f["result_types"], ops, types))
     target = parse_target(text)
     for f in funcs:
         f.target = target
