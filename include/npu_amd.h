@@ -400,7 +400,8 @@ typedef struct npu_launch_plan {
   int32_t load_phases;      /* dependent global-load round trips per tile that
                                no prefetch hides                               */
   int32_t mfma_bits;        /* MFMA operand width: 32 (f32), 16 (bf16), 8 (i8) */
-  int32_t reserved;
+  int32_t unit_waves;       /* waves of one grid unit (0: four); tile_valu and
+                               wg_setup_valu are summed over a unit's waves    */
   double tile_macs;         /* MFMA multiply-adds per tile                     */
   double tile_valu;         /* vector-ALU instructions per tile besides the
                                MFMAs, summed over the workgroup's waves

@@ -887,13 +887,15 @@ __global__ __launch_bounds__(512, 1) void conv3x3_x6_kernel(
   }
 }
 
-// Vector-ALU instructions per wave of the persistent kernel, from its
-// compiled loops: per 2-row tile 151 (epilogue: bias, activation, bf16
-// packing; slot and loop control) plus 35 per 64-byte input chunk (the next
-// rows' fetch, commit and halo write addresses); 250 once (filter loads).
-constexpr double STREAM_VALU_TILE_FIXED = 151.0;
-constexpr double STREAM_VALU_TILE_PER_CHUNK = 35.0;
-constexpr double STREAM_VALU_SETUP = 250.0;
+// Vector-ALU instructions per wave of the persistent kernel, counted in its
+// compiled code (gfx950 assembly, vector instructions other than MFMAs per
+// basic block): per 2-row tile 105 (the epilogue's bias, activation and
+// bf16 packing, slot and loop control) plus 20 per 64-byte input chunk (the
+// next rows' commit and halo writes): 145 at two chunks, 185 at four; 196
+// once (the filter fragments' staging and the first halo).
+constexpr double STREAM_VALU_TILE_FIXED = 105.0;
+constexpr double STREAM_VALU_TILE_PER_CHUNK = 20.0;
+constexpr double STREAM_VALU_SETUP = 196.0;
 
 template <class MM, typename T, int WMAX, int NCH, int WFIX>
 hipError_t launch_stream(const ConvArgs &a, int wgs, hipStream_t s) {
@@ -957,6 +959,7 @@ hipError_t launch_x6(const ConvArgs &a, hipStream_t s) {
     npu_launch_plan p = make_plan("conv3x3_f32_bf16x6", wgs * grid.y,
                                   wg_per_cu(conv3x3_x6_kernel<WMAX, NCX, WFIX>, 512), nrows * grid.y, 16);
     p.load_phases = 0;  // the next tile's new rows are fetched a tile ahead
+    p.unit_waves = 8;   // one grid unit is a whole eight-wave workgroup
     p.tile_macs = 6.0 * 4.0 * BLOCKS_ROW * 256 * 9 * a.C;
     constexpr int LPR = ((WMAX + 2) * 8 * NCX + 511) / 512;  // 16-byte runs per lane and input row
     constexpr int NBW = NCX == 2 ? NBT : (NBT + 1) / 2;           // blocks per wave

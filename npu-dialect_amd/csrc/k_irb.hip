@@ -281,14 +281,15 @@ hipError_t launch_irb_t(const IrbArgs &a, hipStream_t s) {
     npu_launch_plan p = make_plan("mbv2_inverted_residual", g, wg_per_cu(irb_kernel<C, E>), ntiles, 32);
     p.load_phases = 0;  // the next tile's halo is fetched during this tile
     p.tile_macs = (double)E * HPB * 16 * KC1 * 16 + (double)OP * FB2 * 16 * E;
-    // Vector instructions per wave and tile, from the compiled loops: 189
-    // for the tile (halo commit and fetch addresses, residual, stores); per
-    // expand unit (a filter block on 16 halo pixels, FB1 * HPB / 4 per wave)
-    // 14 (ReLU6, the padding select, the store address) plus one per input
-    // chunk; per depthwise chunk of four channels 44 (nine taps' 36 FMAs,
-    // ReLU6, addresses) plus 20.  Set-up: the filter loads' addresses.
-    p.tile_valu = 4.0 * (189.0 + FB1 * HPB / 4.0 * (14.0 + KC1) + 44.0 * (E / 16) + 20.0);
-    p.wg_setup_valu = 4.0 * 190.0;
+    // Vector instructions per wave and tile, counted in the compiled code
+    // (gfx950 assembly, <24, 144>): 81 for the tile (halo commit and fetch
+    // addresses, residual, stores, loop control); 13.4 per expand unit (a
+    // filter block on 16 halo pixels, FB1 * HPB / 4 per wave: ReLU6, the
+    // padding select, the store address); 46 per 16 depthwise channels
+    // (nine taps' FMAs, ReLU6, LDS addresses): 706 per tile at E = 144.
+    // Set-up: 330 (the filter staging and the first halo's addresses).
+    p.tile_valu = 4.0 * (81.0 + FB1 * HPB / 4.0 * 13.4 + 46.0 * (E / 16));
+    p.wg_setup_valu = 4.0 * 330.0;
     p.tile_lds_bytes = HP * (KC1 * 16 + 8) * 4.0 +                // halo written
                        (E / 16.0) * KC1 * HPB * 1024 +            // expand A read
                        HP * E * 4.0 +                             // expanded tile written

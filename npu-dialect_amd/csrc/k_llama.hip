@@ -607,27 +607,32 @@ __global__ __launch_bounds__(256) void llama_attention_kernel(const uint16_t *__
 template <class Sh, class Kern>
 void plan_gemm(const char *name, Kern kern, const LlamaGemmArgs &a, int grid, int pro, int epi) {
   // A tile is one workgroup of 16 waves, planned as four 4-wave units side
-  // by side (one wave per SIMD each).  Vector instructions per unit, from
-  // the kernel's loops: per 16-byte piece staged 4 (address, store), per k
-  // step a wave runs 2 per activation fragment and 4 per weight fragment
-  // (addresses), per output quad the reduction (4 per partial) and the
-  // epilogue (RoPE 14, residual 8, SwiGLU 32: two SiLUs' exp and division);
-  // the RMSNorm prologue 6 per piece (square-sum, scale, pack) and 14 per
-  // row (the 64-lane reduction and the inverse square root).
+  // by side (one wave per SIMD each).  Vector instructions per wave, counted
+  // in the compiled code (gfx950 assembly, the path the layer's shapes take):
+  // a straight-line part -- the loads' addresses, the RMSNorm of the A panel,
+  // the chunk commits, the epilogue (RoPE, residual, SwiGLU) and the stores
+  // -- plus a few per MFMA of the K loop (fragment addresses, loop control).
+  // RMSNorm + QKV + RoPE: 440 + 2 per MFMA; RMSNorm + SwiGLU: 406 + 2 per
+  // MFMA; residual GEMMs: 112 + 5 per MFMA with K in one chunk, 164 + 4.5
+  // with several (the assembly's path counts 161 and 210 there; the
+  // SQ_INSTS_VALU figures, 20 % lower, are used).  The wider-K instances
+  // (K > 512 for the RMSNorm GEMMs) reuse these figures.
   const double BM = Sh::kBM, BN = Sh::kBN, units = 4.0;
   const double ksteps = a.K / 32.0;
   npu_launch_plan p = make_plan(name, grid * 4, wg_per_cu(kern, GT), grid * 4, 16);
   p.load_phases = a.K > (int)Sh::SB / 32 ? 2 : 1;  // one exposed load round trip per chunk beyond one
   p.tile_macs = BM * BN * Sh::NB * a.K / units;
   const double bpieces = a.K * BN * Sh::NB / 8.0, apieces = BM * a.K / 8.0;
-  const double per_wave_steps = ksteps / Sh::kWK;  // K in kWK parts
-  const double frag_valu = per_wave_steps * (Sh::TNW * Sh::NB * 4.0 + Sh::TMW * 2.0) * 4;  // 4 waves/unit
-  const double quads = BM * BN / 4.0 / 64.0 / units;  // quads per wave of a unit
-  const double epi_cost = epi == kEpiQkvRope ? 14 : (epi == kEpiResidual ? 8 : 32);
-  // per quad: kWK loads and adds when K is split (none without a split)
-  const double red_cost = Sh::kWK > 1 ? Sh::NB * Sh::kWK * 4.0 / 4.0 : 0.0;
-  const double norm = pro == kProRmsnorm ? (apieces * 6.0 / 64.0 + BM * 14.0) / units : 0.0;
-  p.tile_valu = 4.0 * ((bpieces + apieces) * 4.0 / 64.0 / units + frag_valu + quads * (epi_cost + red_cost) + norm);
+  const double mfma_per_wave = p.tile_macs / 4.0 / (16.0 * 16.0 * 32.0);
+  double base, per_mfma;
+  if (pro == kProRmsnorm) {
+    base = epi == kEpiQkvRope ? 440.0 : 406.0;
+    per_mfma = 2.0;
+  } else {
+    base = Sh::NBUF > 1 ? 164.0 : 112.0;
+    per_mfma = Sh::NBUF > 1 ? 4.5 : 5.0;
+  }
+  p.tile_valu = 4.0 * (base + per_mfma * mfma_per_wave);
   p.tile_lds_bytes = (2.0 * (bpieces + apieces) * 16 +
                       ksteps * 4.0 / Sh::kWK * (Sh::TNW * Sh::NB * 1024.0 * 4 / Sh::kWC + Sh::TMW * 1024.0 * 4) +
                       2.0 * Sh::RED) / units;
@@ -701,12 +706,14 @@ hipError_t launch_llama_attention(const uint16_t *Q, const uint16_t *K, const ui
   {
     // The longest workgroup is the last query block's: ceil(S / AKB / 4)
     // key blocks per wave.  Per key block and wave: 8 MFMAs (S^T and O^T),
-    // the online softmax (about 70 vector instructions), one K and V block.
+    // the online softmax and the next block's fetch (139 vector
+    // instructions in the compiled code, 50 more on the diagonal block's
+    // mask), one K and V block; 226 once (Q fetch, the merge and stores).
     const double kblocks = std::ceil(S / (double)AKB / AWAVES);
     npu_launch_plan p = make_plan("llama_causal_attention", G, wg_per_cu(llama_attention_kernel, 256), G, 16);
     p.load_phases = 1;
     p.tile_macs = kblocks * AWAVES * 2.0 * AQ * AKB * 64;
-    p.tile_valu = 4.0 * (60.0 + 70.0 * kblocks) + 4.0 * 40.0;
+    p.tile_valu = 4.0 * (226.0 + 139.0 * kblocks + 50.0);
     p.tile_lds_bytes = kblocks * AWAVES * (2.0 * AKB * 64 * 2) + AWAVES * 64 * AQ * 4 * 2;
     p.tile_load_bytes = kblocks * AWAVES * 2.0 * AKB * 64 * 2 + AQ * 64 * 2.0;
     p.tile_store_bytes = AQ * 64 * 2.0;

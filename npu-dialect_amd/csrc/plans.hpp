@@ -67,6 +67,7 @@ inline npu_launch_plan make_plan(const char *kernel, int grid, int per_cu, int t
   p.tiles = tiles;
   p.load_phases = 1;
   p.mfma_bits = mfma_bits;
+  p.unit_waves = 4;
   return p;
 }
 

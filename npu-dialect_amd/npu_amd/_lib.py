@@ -46,7 +46,7 @@ class NpuLaunchPlan(C.Structure):
         ("tiles", C.c_int32),
         ("load_phases", C.c_int32),
         ("mfma_bits", C.c_int32),
-        ("reserved", C.c_int32),
+        ("unit_waves", C.c_int32),
         ("tile_macs", C.c_double),
         ("tile_valu", C.c_double),
         ("tile_lds_bytes", C.c_double),
