@@ -26,21 +26,34 @@ namespace npu {
 
 namespace {
 
-constexpr int TH = 8, TW = 8;        // output tile
-constexpr int HW = TW + 2;           // halo tile width (and height)
-constexpr int HP = HW * (TH + 2);    // 100 halo pixels
-constexpr int HPB = (HP + 15) / 16;  // 7 blocks of 16 rows
-constexpr int OP = TH * TW;          // 64 output pixels
+// Output tile TH x TW: 8 x 8 when the batch has tiles enough for every CU,
+// 4 x 4 below that (more workgroups, each with a shorter serial chain; the
+// expand conv is recomputed on 36 halo pixels for 16 outputs instead of 100
+// for 64, which idle CUs pay for).
+template <int TH, int TW>
+struct IrbTile {
+  static constexpr int HW = TW + 2;           // halo tile width
+  static constexpr int HP = HW * (TH + 2);    // halo pixels (100 for 8 x 8)
+  static constexpr int HPB = (HP + 15) / 16;  // blocks of 16 halo pixels
+  static constexpr int OP = TH * TW;          // output pixels
+  static constexpr int OPB = OP / 16;         // blocks of 16 output pixels
+  // the depthwise/project stage: wave w takes output block w % OPB and
+  // channel group w / OPB of CS (CS > 1: partial projections summed in LDS)
+  static constexpr int CS = 4 / OPB;
+  static_assert(OP % 16 == 0 && 4 % OPB == 0, "one to four output blocks");
+};
 
 __device__ __forceinline__ float relu6(float v) { return act_clamp(v, ActBounds{0.0f, 6.0f}); }
 
-template <int C, int E>
+template <int C, int E, int TH, int TW>
 __global__ __launch_bounds__(256, E >= 192 ? 1 : 2) void irb_kernel(const float *__restrict__ x,
                                                   const float *__restrict__ we,
                                                   const float *__restrict__ wdw,
                                                   const float *__restrict__ wp,
                                                   float *__restrict__ out, int H, int W,
                                                   int tiles_w, int tiles_per_image, int ntiles) {
+  using Tl = IrbTile<TH, TW>;
+  constexpr int HW = Tl::HW, HP = Tl::HP, HPB = Tl::HPB, OPB = Tl::OPB, CS = Tl::CS;
   static_assert(C % 4 == 0 && E % 16 == 0, "C must be a multiple of 4, E of 16");
   constexpr int KC1 = (C + 15) / 16;  // expand reduction chunks (C padded to 16)
   // LDS row strides in floats.  A stride of 32 mod 64 bytes keeps the 16-lane
@@ -59,6 +72,8 @@ __global__ __launch_bounds__(256, E >= 192 ? 1 : 2) void irb_kernel(const float 
   __shared__ __attribute__((aligned(16))) float xs[HP * XS];
   __shared__ __attribute__((aligned(16))) float es[HP * ES];
   __shared__ __attribute__((aligned(16))) float wds[9 * E];
+  // partial projections of channel groups 1 .. CS-1 (16 pixels x FB2*16)
+  __shared__ __attribute__((aligned(16))) float part[CS > 1 ? (CS - 1) * 16 * FB2 * 16 : 4];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int r = lane & 15, q = lane >> 4;
@@ -158,8 +173,12 @@ __global__ __launch_bounds__(256, E >= 192 ? 1 : 2) void irb_kernel(const float 
   __syncthreads();
 
   // Per-lane constants of the depthwise/project stage: wave w owns output
-  // pixels 16w .. 16w+15 (p), this lane's pixel p = 16w + r.
-  const int p = wave * 16 + r, py = p / TW, px = p - py * TW;
+  // pixels 16 ob .. 16 ob + 15 (ob = w % OPB) and the expanded channels of
+  // its channel group cg = w / OPB: 16-channel chunks [kc0, kc1) of KC2;
+  // this lane's pixel p = 16 ob + r.
+  const int ob = wave % OPB, cg = wave / OPB;
+  const int kc0 = cg * KC2 / CS, kc1 = (cg + 1) * KC2 / CS;
+  const int p = ob * 16 + r, py = p / TW, px = p - py * TW;
   const int hbase = py * HW + px;
   const uint32_t ooff = (uint32_t)(((py * W + px) * C + 4 * q) * 4);
 
@@ -233,6 +252,7 @@ __global__ __launch_bounds__(256, E >= 192 ? 1 : 2) void irb_kernel(const float 
     for (int fb = 0; fb < FB2; ++fb) acc2[fb] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int kc = 0; kc < KC2; ++kc) {
+      if (CS > 1 && (kc < kc0 || kc >= kc1)) continue;  // another wave's channels
       const int e0 = kc * 16 + 4 * q;
       f32x4 d = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -249,14 +269,29 @@ __global__ __launch_bounds__(256, E >= 192 ? 1 : 2) void irb_kernel(const float 
     }
     // residual added while x is still in LDS; the stores go out after the
     // next halo is committed and the one after it is fetched, so they are
-    // the newest memory operations when the loop comes round
+    // the newest memory operations when the loop comes round.  With channel
+    // groups, groups 1.. leave their partial projections in LDS and group 0
+    // adds them, in group order, after the barrier.
+    if (CS > 1 && cg > 0) {
 #pragma unroll
-    for (int fb = 0; fb < FB2; ++fb)
-      acc2[fb] += *reinterpret_cast<const f32x4 *>(xs + (hbase + HW + 1) * XS + fb * 16 + 4 * q);
+      for (int fb = 0; fb < FB2; ++fb)
+        *reinterpret_cast<f32x4 *>(part + ((cg - 1) * 16 + r) * FB2 * 16 + fb * 16 + 4 * q) = acc2[fb];
+    } else {
+#pragma unroll
+      for (int fb = 0; fb < FB2; ++fb)
+        acc2[fb] += *reinterpret_cast<const f32x4 *>(xs + (hbase + HW + 1) * XS + fb * 16 + 4 * q);
+    }
     __syncthreads();  // every wave is done with xs and es of this tile
+    if (CS > 1 && cg == 0) {
+#pragma unroll
+      for (int g2 = 1; g2 < CS; ++g2)
+#pragma unroll
+        for (int fb = 0; fb < FB2; ++fb)
+          acc2[fb] += *reinterpret_cast<const f32x4 *>(part + ((g2 - 1) * 16 + r) * FB2 * 16 + fb * 16 + 4 * q);
+    }
     commit();
     fetch(next_of(next_of(t)));
-    if (ty0 + py < H && tx0 + px < W) {
+    if ((CS == 1 || cg == 0) && ty0 + py < H && tx0 + px < W) {
       char *ob = reinterpret_cast<char *>(out) + ((size_t)(n * H + ty0) * W + tx0) * C * 4;
 #pragma unroll
       for (int fb = 0; fb < FB2; ++fb)
@@ -267,33 +302,37 @@ __global__ __launch_bounds__(256, E >= 192 ? 1 : 2) void irb_kernel(const float 
   }
 }
 
-template <int C, int E>
-hipError_t launch_irb_t(const IrbArgs &a, hipStream_t s) {
+template <int C, int E, int TH, int TW>
+hipError_t launch_irb_tile(const IrbArgs &a, hipStream_t s) {
+  using Tl = IrbTile<TH, TW>;
+  constexpr int HP = Tl::HP, HPB = Tl::HPB, OP = Tl::OP;
+  auto kern = irb_kernel<C, E, TH, TW>;
   const int tiles_w = (a.W + TW - 1) / TW, tiles_h = (a.H + TH - 1) / TH;
   const int per_image = tiles_w * tiles_h, ntiles = a.N * per_image;
-  const int full = persistent_grid(irb_kernel<C, E>);
+  const int full = persistent_grid(kern);
   if (full == 0) return hipErrorInvalidDeviceFunction;
   // one tile per workgroup when there are fewer tiles than resident slots
   // (rounded up to whole XCD rounds: the walk gives the spare ones nothing)
   const int g = ntiles < full ? (ntiles + kXcds - 1) / kXcds * kXcds : full;
   {
     constexpr int KC1 = (C + 15) / 16, FB2 = (C + 15) / 16, FB1 = E / 16;
-    npu_launch_plan p = make_plan("mbv2_inverted_residual", g, wg_per_cu(irb_kernel<C, E>), ntiles, 32);
+    npu_launch_plan p = make_plan("mbv2_inverted_residual", g, wg_per_cu(kern), ntiles, 32);
     p.load_phases = 0;  // the next tile's halo is fetched during this tile
     p.tile_macs = (double)E * HPB * 16 * KC1 * 16 + (double)OP * FB2 * 16 * E;
     // Vector instructions per wave and tile, counted in the compiled code
-    // (gfx950 assembly, <24, 144>): 81 for the tile (halo commit and fetch
-    // addresses, residual, stores, loop control); 13.4 per expand unit (a
-    // filter block on 16 halo pixels, FB1 * HPB / 4 per wave: ReLU6, the
-    // padding select, the store address); 46 per 16 depthwise channels
-    // (nine taps' FMAs, ReLU6, LDS addresses): 706 per tile at E = 144.
+    // (gfx950 assembly, <24, 144, 8, 8>): 81 for the tile (halo commit and
+    // fetch addresses, residual, stores, loop control); 13.4 per expand unit
+    // (a filter block on 16 halo pixels, FB1 * HPB / 4 per wave: ReLU6, the
+    // padding select, the store address); 46 per 16 depthwise channels of a
+    // block of 16 output pixels (nine taps' FMAs, ReLU6, LDS addresses),
+    // OP / 16 blocks over four waves: 706 per 8 x 8 tile at E = 144.
     // Set-up: 330 (the filter staging and the first halo's addresses).
-    p.tile_valu = 4.0 * (81.0 + FB1 * HPB / 4.0 * 13.4 + 46.0 * (E / 16));
+    p.tile_valu = 4.0 * (81.0 + FB1 * HPB / 4.0 * 13.4 + 46.0 * (E / 16) * (OP / 16) / 4.0);
     p.wg_setup_valu = 4.0 * 330.0;
     p.tile_lds_bytes = HP * (KC1 * 16 + 8) * 4.0 +                // halo written
                        (E / 16.0) * KC1 * HPB * 1024 +            // expand A read
                        HP * E * 4.0 +                             // expanded tile written
-                       2.0 * 4 * (E / 16) * 9 * 1024 +            // depthwise taps and weights read
+                       2.0 * (OP / 16) * (E / 16) * 9 * 1024 +    // depthwise taps and weights read
                        OP * C * 4.0;                              // residual
     p.tile_load_bytes = HP * C * 4.0;
     p.tile_store_bytes = OP * C * 4.0;
@@ -301,9 +340,20 @@ hipError_t launch_irb_t(const IrbArgs &a, hipStream_t s) {
     p.hbm_bytes = 4.0 * (2.0 * a.N * a.H * a.W * C + 2.0 * C * E + 9.0 * E);
     plans_add(p);
   }
-  hipLaunchKernelGGL((irb_kernel<C, E>), dim3(g), dim3(256), 0, s, a.x, a.we, a.wdw, a.wp, a.out,
+  hipLaunchKernelGGL(kern, dim3(g), dim3(256), 0, s, a.x, a.we, a.wdw, a.wp, a.out,
                      a.H, a.W, tiles_w, per_image, ntiles);
   return hipGetLastError();
+}
+
+// 8 x 8 tiles when there are at least as many as CUs, else 4 x 4.
+template <int C, int E>
+hipError_t launch_irb_t(const IrbArgs &a, hipStream_t s) {
+  const long long tiles8 = (long long)a.N * ((a.H + 7) / 8) * ((a.W + 7) / 8);
+  int dev = 0, cus = 256;
+  if (hipGetDevice(&dev) == hipSuccess)
+    (void)hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
+  if (tiles8 < cus) return launch_irb_tile<C, E, 4, 4>(a, s);
+  return launch_irb_tile<C, E, 8, 8>(a, s);
 }
 
 }  // namespace
