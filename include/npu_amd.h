@@ -269,6 +269,45 @@ npu_status npu_planned_matmul_bias_act(const npu_memref *A, const npu_memref *B,
                                        int32_t act, const npu_tile_plan *plan,
                                        void *lds_dump, npu_stream stream);
 
+/* The group `fill -> conv_2d_nchw_fchw -> generic(bias add, act)` as the
+ * reference's temporal tile loop over output-channel tiles, every SRAM
+ * buffer where the reference's SRAM plan puts it in one workgroup's LDS
+ * (SRAMAllocationPass.cpp:172-363: sram_offset, sram_offset_pong,
+ * double_buffered, prefetch_addr, spills).  A workgroup is one core's
+ * share: one output row (n, ho).  Per tile i (output channels i*tco ..
+ * +tco): the input rows [C][KH][Wp], the filter slice [tco][C][KH][KW]
+ * and the bias slice [tco] in their ping (i even) or pong (i odd)
+ * buffers, the tile's MACs into the accumulator row [tco][Wo], the
+ * generic (bias slice, activation) into the output row, DMA'd back.  A
+ * buffer with a prefetch region (prefetch_addr) has tile i+2's copy
+ * fetched from HBM into it after tile i, and tile i+1's copy made
+ * SRAM-to-SRAM from it (the reference's "next tile iteration's data in
+ * free SRAM"); a buffer without a pong reuses its ping; spilled input rows
+ * or filters (offset -1) are read from HBM where they lie; a bias, when
+ * the group has one, is in SRAM.  Stride 1, no dilation; x is the padded
+ * input [N][C][Hp][Wp].  The plan is checked before the launch: every
+ * buffer 4-byte aligned inside [0, lds_bytes), lds_bytes <= 163840, no two
+ * buffers overlapping, no pong or prefetch region for a buffer outside
+ * SRAM. */
+typedef struct npu_conv_tile_plan {
+  int32_t tco;             /* output channels per temporal tile             */
+  int32_t lds_bytes;       /* SRAM (LDS) size the plan was made for         */
+  int64_t off_in, off_in_pong, off_in_prefetch;        /* rows [C][KH][Wp]  */
+  int64_t off_w, off_w_pong, off_w_prefetch;     /* filters [tco][C][KH][KW] */
+  int64_t off_bias, off_bias_pong, off_bias_prefetch;  /* bias [tco]; off_bias
+                              -1: the group has no bias                    */
+  int64_t off_c;           /* accumulator row [tco][Wo]                     */
+  int64_t off_y;           /* output row [tco][Wo]                          */
+} npu_conv_tile_plan;
+/* x f32 [N,C,Hp,Wp] (padded), w f32 [F,C,KH,KW], bias f32 [F] (aligned may
+ * be NULL), out f32 [N,F,Ho,Wo] = act(conv + bias), Ho = Hp-KH+1,
+ * Wo = Wp-KW+1.  lds_dump (device memory of lds_bytes, may be NULL)
+ * receives workgroup 0's (image 0, output row 0) whole LDS at the end. */
+npu_status npu_planned_conv2d_nchw_bias_act(const npu_memref *x, const npu_memref *w,
+                                            const npu_memref *bias, const npu_memref *out,
+                                            int32_t act, const npu_conv_tile_plan *plan,
+                                            void *lds_dump, npu_stream stream);
+
 /* ---- the outlined-group boundary -----------------------------------------
  * A host module produced by the reference's pipeline calls each fused group
  * as `func.call @fused_<ops>_<idx>(external inputs...)` with the group's

@@ -276,6 +276,100 @@ npu_status npu_planned_matmul_bias_act(const npu_memref *A, const npu_memref *B,
                     "npu_planned_matmul_bias_act launch");
 }
 
+npu_status npu_planned_conv2d_nchw_bias_act(const npu_memref *x, const npu_memref *w,
+                                            const npu_memref *bias, const npu_memref *out,
+                                            int32_t act, const npu_conv_tile_plan *plan,
+                                            void *lds_dump, npu_stream stream) {
+  npu::plans_reset();
+  const void *px, *pw, *pbias = nullptr, *po;
+  NPU_TRY(check_memref(x, "x", 4, NPU_F32, &px));
+  NPU_TRY(check_memref(w, "w", 4, NPU_F32, &pw));
+  NPU_TRY(check_memref(out, "out", 4, NPU_F32, &po));
+  NPU_TRY(check_act(act));
+  const int64_t N = x->sizes[0], C = x->sizes[1], Hp = x->sizes[2], Wp = x->sizes[3];
+  const int64_t F = w->sizes[0], KH = w->sizes[2], KW = w->sizes[3];
+  if (w->sizes[1] != C)
+    return fail(NPU_ERR_INVALID_ARG, "w: sizes[1] = %lld, expected C = %lld",
+                (long long)w->sizes[1], (long long)C);
+  if (KH > Hp || KW > Wp)
+    return fail(NPU_ERR_INVALID_ARG, "w: %lldx%lld filter larger than the %lldx%lld input",
+                (long long)KH, (long long)KW, (long long)Hp, (long long)Wp);
+  const int64_t Ho = Hp - KH + 1, Wo = Wp - KW + 1;
+  if (out->sizes[0] != N || out->sizes[1] != F || out->sizes[2] != Ho || out->sizes[3] != Wo)
+    return fail(NPU_ERR_INVALID_ARG, "out: [%lld,%lld,%lld,%lld], expected [%lld,%lld,%lld,%lld]",
+                (long long)out->sizes[0], (long long)out->sizes[1], (long long)out->sizes[2],
+                (long long)out->sizes[3], (long long)N, (long long)F, (long long)Ho, (long long)Wo);
+  if (!absent(bias)) {
+    NPU_TRY(check_memref(bias, "bias", 1, NPU_F32, &pbias));
+    if (bias->sizes[0] != F)
+      return fail(NPU_ERR_INVALID_ARG, "bias: size %lld, expected F = %lld",
+                  (long long)bias->sizes[0], (long long)F);
+  }
+  if (!plan) return fail(NPU_ERR_INVALID_ARG, "plan is NULL");
+  const npu_conv_tile_plan &p = *plan;
+  if (p.tco < 1 || p.tco > F)
+    return fail(NPU_ERR_INVALID_ARG, "plan: tco = %d, expected 1 .. F = %lld", p.tco, (long long)F);
+  if (p.lds_bytes <= 0 || p.lds_bytes > 163840 || p.lds_bytes % 4 != 0)
+    return fail(NPU_ERR_INVALID_ARG, "lds_bytes = %d: must be in (0, 163840], a multiple of 4",
+                p.lds_bytes);
+  struct Buf {
+    const char *name;
+    int64_t off, bytes;
+  };
+  const int64_t t = 4, in_b = t * C * KH * Wp, w_b = t * p.tco * C * KH * KW, row_b = t * p.tco * Wo;
+  constexpr int kBufs = 11;
+  const Buf bufs[kBufs] = {{"input rows", p.off_in, in_b}, {"input rows pong", p.off_in_pong, in_b},
+                           {"input rows prefetch", p.off_in_prefetch, in_b},
+                           {"filters", p.off_w, w_b}, {"filters pong", p.off_w_pong, w_b},
+                           {"filters prefetch", p.off_w_prefetch, w_b},
+                           {"bias", p.off_bias, t * p.tco}, {"bias pong", p.off_bias_pong, t * p.tco},
+                           {"bias prefetch", p.off_bias_prefetch, t * p.tco},
+                           {"C", p.off_c, row_b}, {"Y", p.off_y, row_b}};
+  const bool has_bias = p.off_bias >= 0;
+  if (has_bias != (pbias != nullptr))
+    return fail(NPU_ERR_INVALID_ARG, has_bias ? "plan has a bias buffer but bias is absent"
+                                              : "bias given but the plan has no bias buffer");
+  // -1: the buffer is not in SRAM (a spilled input, no pong, no prefetch
+  // region, no bias); C and Y must be in SRAM, and a buffer not in SRAM has
+  // neither a pong nor a prefetch region
+  if (p.off_c < 0 || p.off_y < 0) return fail(NPU_ERR_INVALID_ARG, "plan: C and Y must be in SRAM");
+  if ((p.off_in < 0 && (p.off_in_pong >= 0 || p.off_in_prefetch >= 0)) ||
+      (p.off_w < 0 && (p.off_w_pong >= 0 || p.off_w_prefetch >= 0)) ||
+      (p.off_bias < 0 && (p.off_bias_pong >= 0 || p.off_bias_prefetch >= 0)))
+    return fail(NPU_ERR_INVALID_ARG, "plan: a buffer outside SRAM with a pong or prefetch buffer");
+  auto used = [&](int i) { return bufs[i].off >= 0; };
+  for (int i = 0; i < kBufs; ++i) {
+    if (!used(i)) continue;
+    const Buf &b = bufs[i];
+    if (b.off % 4 != 0 || b.off + b.bytes > p.lds_bytes)
+      return fail(NPU_ERR_INVALID_ARG,
+                  "plan: %s at %lld (+%lld bytes) is not a 4-byte aligned offset inside the %d "
+                  "bytes of SRAM", b.name, (long long)b.off, (long long)b.bytes, p.lds_bytes);
+  }
+  for (int i = 0; i < kBufs; ++i)
+    for (int j = i + 1; j < kBufs; ++j)
+      if (used(i) && used(j) && bufs[i].off < bufs[j].off + bufs[j].bytes &&
+          bufs[j].off < bufs[i].off + bufs[i].bytes)
+        return fail(NPU_ERR_INVALID_ARG, "plan: %s and %s overlap", bufs[i].name, bufs[j].name);
+  npu::PlannedConvArgs a{};
+  a.x = static_cast<const float *>(px);
+  a.w = static_cast<const float *>(pw);
+  a.bias = static_cast<const float *>(pbias);
+  a.out = static_cast<float *>(const_cast<void *>(po));
+  a.N = (int)N; a.C = (int)C; a.Hp = (int)Hp; a.Wp = (int)Wp; a.F = (int)F;
+  a.KH = (int)KH; a.KW = (int)KW; a.Ho = (int)Ho; a.Wo = (int)Wo; a.act = act;
+  a.tco = p.tco; a.lds_bytes = p.lds_bytes;
+  a.off_in[0] = (int)p.off_in; a.off_in[1] = (int)p.off_in_pong;
+  a.off_w[0] = (int)p.off_w; a.off_w[1] = (int)p.off_w_pong;
+  a.off_in_pre = (int)p.off_in_prefetch; a.off_w_pre = (int)p.off_w_prefetch;
+  a.off_bias[0] = (int)p.off_bias; a.off_bias[1] = (int)p.off_bias_pong;
+  a.off_bias_pre = (int)p.off_bias_prefetch;
+  a.off_c = (int)p.off_c; a.off_y = (int)p.off_y;
+  a.lds_dump = lds_dump;
+  return hip_status(npu::launch_planned_conv(a, static_cast<hipStream_t>(stream)),
+                    "npu_planned_conv2d_nchw_bias_act launch");
+}
+
 namespace {
 
 // fused_conv2d_nhwc_bias_act and its residual variant: checks, then the LDS

@@ -137,6 +137,122 @@ __global__ __launch_bounds__(kPT) void planned_matmul_kernel(const PlannedMatmul
   }
 }
 
+// The conv group's tile loop (see npu_planned_conv2d_nchw_bias_act): one
+// workgroup per output row (n, ho), the loop over output-channel tiles of
+// tco, every buffer at the plan's offset in its slice's own row-major f32
+// layout.  Step i: [barrier] the tile's MACs from its input-rows and filter
+// slots into C, [barrier] the generic C + bias -> Y, [barrier] Y back to
+// HBM and the DMA-in of tile i+1 into the other slots (from the prefetch
+// region, SRAM to SRAM, for a buffer that has one), [barrier] tile i+2's
+// copies from HBM into the prefetch regions.
+__global__ __launch_bounds__(kPT) void planned_conv_kernel(const PlannedConvArgs a) {
+  extern __shared__ __attribute__((aligned(16))) unsigned char sram[];
+  const int tid = threadIdx.x;
+  const int C = a.C, KH = a.KH, KW = a.KW, Wp = a.Wp, Hp = a.Hp, Wo = a.Wo, F = a.F;
+  const int tco = a.tco, CKK = C * KH * KW;
+  const int n = blockIdx.x / a.Ho, ho = blockIdx.x - n * a.Ho;
+  const int nt = (F + tco - 1) / tco;
+  auto at = [&](int off) { return reinterpret_cast<float *>(sram + (off >= 0 ? off : 0)); };
+  const bool in_lds = a.off_in[0] >= 0, w_lds = a.off_w[0] >= 0;
+  const bool in_pre = a.off_in_pre >= 0, w_pre = a.off_w_pre >= 0, has_bias = a.off_bias[0] >= 0;
+  const bool b_pre = has_bias && a.off_bias_pre >= 0;
+  float *const sIn[2] = {at(a.off_in[0]), at(a.off_in[1] >= 0 ? a.off_in[1] : a.off_in[0])};
+  float *const sW[2] = {at(a.off_w[0]), at(a.off_w[1] >= 0 ? a.off_w[1] : a.off_w[0])};
+  float *const sB[2] = {at(a.off_bias[0]), at(a.off_bias[1] >= 0 ? a.off_bias[1] : a.off_bias[0])};
+  float *const sInPre = at(a.off_in_pre), *const sWPre = at(a.off_w_pre);
+  float *const sBPre = at(a.off_bias_pre), *const sC = at(a.off_c), *const sY = at(a.off_y);
+  // the input rows ho .. ho+KH-1 of image n where they lie in HBM
+  const float *const xrow = a.x + (size_t)n * C * Hp * Wp + (size_t)ho * Wp;
+
+  // DMA of the input rows (all channels) into `dst`, as [C][KH][Wp]
+  auto dma_in = [&](float *dst) {
+    for (int e = tid; e < C * KH * Wp; e += kPT) {
+      const int c = e / (KH * Wp), rc = e - c * KH * Wp;
+      dst[e] = xrow[(size_t)c * Hp * Wp + rc];
+    }
+  };
+  // DMA of tile i's filter slice; filters past F are zero
+  auto dma_w = [&](int i, float *dst) {
+    for (int e = tid; e < tco * CKK; e += kPT) {
+      const int f = i * tco + e / CKK;
+      dst[e] = f < F ? a.w[(size_t)f * CKK + e % CKK] : 0.0f;
+    }
+  };
+  auto copy = [&](const float *src, float *dst, int count) {
+    for (int e = tid; e < count; e += kPT) dst[e] = src[e];
+  };
+  // DMA of tile i's bias slice; channels past F are zero
+  auto dma_bias = [&](int i, float *dst) {
+    for (int co = tid; co < tco; co += kPT) dst[co] = i * tco + co < F ? a.bias[i * tco + co] : 0.0f;
+  };
+
+  if (in_lds) dma_in(sIn[0]);
+  if (w_lds) dma_w(0, sW[0]);
+  if (has_bias) dma_bias(0, sB[0]);
+  if (in_pre && nt > 1) dma_in(sInPre);
+  if (w_pre && nt > 1) dma_w(1, sWPre);
+  if (b_pre && nt > 1) dma_bias(1, sBPre);
+  const ActBounds ab = act_bounds(a.act);
+  for (int i = 0; i < nt; ++i) {
+    // operands of tile i: its LDS slots, or HBM for a spilled buffer
+    const float *in = in_lds ? sIn[i & 1] : xrow;
+    const int cstride = in_lds ? KH * Wp : Hp * Wp;
+    const float *wt = w_lds ? sW[i & 1] : a.w + (size_t)i * tco * CKK;
+    const float *bs = sB[i & 1];
+    __syncthreads();
+    for (int o = tid; o < tco * Wo; o += kPT) {
+      const int co = o / Wo, wo = o - co * Wo;
+      float acc = 0.0f;
+      if (i * tco + co < F)
+        for (int c = 0; c < C; ++c)
+          for (int kh = 0; kh < KH; ++kh)
+            for (int kw = 0; kw < KW; ++kw)
+              acc += in[c * cstride + kh * Wp + wo + kw] * wt[co * CKK + (c * KH + kh) * KW + kw];
+      sC[o] = acc;
+    }
+    __syncthreads();
+    for (int o = tid; o < tco * Wo; o += kPT)
+      sY[o] = act_clamp(has_bias ? sC[o] + bs[o / Wo] : sC[o], ab);
+    __syncthreads();
+    for (int o = tid; o < tco * Wo; o += kPT) {
+      const int co = o / Wo, wo = o - co * Wo, f = i * tco + co;
+      if (f < F) a.out[((size_t)(n * F + f) * a.Ho + ho) * Wo + wo] = sY[o];
+    }
+    if (i + 1 < nt) {
+      const int nb = (i + 1) & 1;
+      if (in_lds) {
+        if (in_pre)
+          copy(sInPre, sIn[nb], C * KH * Wp);
+        else
+          dma_in(sIn[nb]);
+      }
+      if (w_lds) {
+        if (w_pre)
+          copy(sWPre, sW[nb], tco * CKK);
+        else
+          dma_w(i + 1, sW[nb]);
+      }
+      if (has_bias) {
+        if (b_pre)
+          copy(sBPre, sB[nb], tco);
+        else
+          dma_bias(i + 1, sB[nb]);
+      }
+    }
+    __syncthreads();
+    if (i + 2 < nt) {
+      if (in_pre) dma_in(sInPre);
+      if (w_pre) dma_w(i + 2, sWPre);
+      if (b_pre) dma_bias(i + 2, sBPre);
+    }
+  }
+  if (a.lds_dump && blockIdx.x == 0) {
+    __syncthreads();
+    for (int e = tid; e < a.lds_bytes / 4; e += kPT)
+      reinterpret_cast<uint32_t *>(a.lds_dump)[e] = reinterpret_cast<const uint32_t *>(sram)[e];
+  }
+}
+
 }  // namespace
 
 bool planned_matmul_tiles_ok(int tm, int tn, int tk) {
@@ -174,6 +290,39 @@ hipError_t launch_planned_matmul(const PlannedMatmulArgs &a, hipStream_t s) {
     plans_add(p);
   }
   hipLaunchKernelGGL(planned_matmul_kernel, grid, dim3(kPT), a.lds_bytes, s, a);
+  return hipGetLastError();
+}
+
+hipError_t launch_planned_conv(const PlannedConvArgs &a, hipStream_t s) {
+  if (a.tco < 1 || a.lds_bytes <= 0 || a.lds_bytes > 160 * 1024 || a.lds_bytes % 4 != 0)
+    return hipErrorInvalidValue;
+  const void *kern = reinterpret_cast<const void *>(planned_conv_kernel);
+  const int ok = cached_per_kernel(kern, [&](int) {
+    return hipFuncSetAttribute(kern, hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024) ==
+                   hipSuccess
+               ? 1 : 0;
+  });
+  if (!ok) return hipErrorInvalidValue;
+  const int grid = a.N * a.Ho;
+  {
+    // per workgroup (one output row): every tile's scalar MACs, the generic
+    // and the copy back; the DMA of the input rows and filter slices
+    const double nt = (a.F + a.tco - 1) / a.tco, macs = (double)a.tco * a.Wo * a.C * a.KH * a.KW;
+    npu_launch_plan p = make_plan("planned_conv2d_nchw_bias_act", grid, wg_per_cu(planned_conv_kernel),
+                                  grid, 32);
+    p.load_phases = 1 + 1;
+    p.tile_macs = 0.0;  // scalar FMAs, priced as vector work below
+    p.tile_valu = nt * (2.0 * macs / 64.0 + 8.0 * a.tco * a.Wo / 64.0 +
+                        3.0 * ((double)a.C * a.KH * a.Wp + a.tco * a.C * a.KH * a.KW) / 64.0);
+    p.tile_lds_bytes = nt * (8.0 * macs + 16.0 * a.tco * a.Wo +
+                             4.0 * ((double)a.C * a.KH * a.Wp + 2.0 * a.tco * a.C * a.KH * a.KW));
+    p.tile_load_bytes = nt * 4.0 * ((double)a.C * a.KH * a.Wp + a.tco * a.C * a.KH * a.KW);
+    p.tile_store_bytes = 4.0 * a.F * a.Wo;
+    p.hbm_bytes = 4.0 * ((double)a.N * a.C * a.Hp * a.Wp + (double)a.F * a.C * a.KH * a.KW +
+                         (double)a.N * a.F * a.Ho * a.Wo + a.F);
+    plans_add(p);
+  }
+  hipLaunchKernelGGL(planned_conv_kernel, dim3(grid), dim3(kPT), a.lds_bytes, s, a);
   return hipGetLastError();
 }
 

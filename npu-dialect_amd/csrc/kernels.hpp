@@ -64,6 +64,17 @@ struct PlannedMatmulArgs {
 bool planned_matmul_tiles_ok(int tm, int tn, int tk);
 hipError_t launch_planned_matmul(const PlannedMatmulArgs &a, hipStream_t s);
 
+struct PlannedConvArgs {
+  const float *x, *w, *bias;  // bias may be null
+  float *out;
+  int N, C, Hp, Wp, F, KH, KW, Ho, Wo, act;
+  int tco, lds_bytes;
+  // -1: spilled (in, w: read from HBM), no prefetch region, no bias
+  int off_in[2], off_w[2], off_bias[2], off_in_pre, off_w_pre, off_bias_pre, off_c, off_y;
+  void *lds_dump;             // may be null: else workgroup 0's LDS, lds_bytes
+};
+hipError_t launch_planned_conv(const PlannedConvArgs &a, hipStream_t s);
+
 // Llama layer GEMM variants: A prologue and epilogue kinds.
 enum { kProPlain = 0, kProRmsnorm = 1 };
 enum { kEpiQkvRope = 0, kEpiResidual = 1, kEpiSwiglu = 2 };

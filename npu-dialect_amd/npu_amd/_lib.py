@@ -105,6 +105,19 @@ class NpuTilePlan(C.Structure):
     ]
 
 
+class NpuConvTilePlan(C.Structure):
+    """npu_conv_tile_plan: the output-channel tile and each SRAM buffer's LDS
+    offset (ping, pong, prefetch region; -1 where the plan has none)."""
+
+    _fields_ = [
+        ("tco", C.c_int32), ("lds_bytes", C.c_int32),
+        ("off_in", C.c_int64), ("off_in_pong", C.c_int64), ("off_in_prefetch", C.c_int64),
+        ("off_w", C.c_int64), ("off_w_pong", C.c_int64), ("off_w_prefetch", C.c_int64),
+        ("off_bias", C.c_int64), ("off_bias_pong", C.c_int64), ("off_bias_prefetch", C.c_int64),
+        ("off_c", C.c_int64), ("off_y", C.c_int64),
+    ]
+
+
 _ARG = C.POINTER(NpuArg)
 
 SIGNATURES = {
@@ -115,6 +128,8 @@ SIGNATURES = {
     "fused_matmul_bias_act": (_I32, [_MR, _MR, _MR, _MR, _I32, _P]),
     "npu_planned_matmul_bias_act": (_I32, [_MR, _MR, _MR, _MR, _I32, C.POINTER(NpuTilePlan), _P,
                                            _P]),
+    "npu_planned_conv2d_nchw_bias_act": (_I32, [_MR, _MR, _MR, _MR, _I32,
+                                                C.POINTER(NpuConvTilePlan), _P, _P]),
     "fused_conv2d_nhwc_bias_act": (_I32, [_MR, _MR, _MR, _MR, _I32, _I32, _P]),
     "fused_conv2d_nhwc_bias_res_act": (_I32, [_MR, _MR, _MR, _MR, _MR, _I32, _I32, _P]),
     "fused_conv2d_nchw_bias_act": (_I32, [_MR, _MR, _MR, _MR, _I32, _I32, _I32, _P]),

@@ -24,9 +24,11 @@ def _maps(rank, bias):
     return f"[{full}, affine_map<({ids}) -> (d{rank - 1})>, {full}]"
 
 
-def _epilogue(res, src, bias, shape, elem, act, residual=None):
-    """`res` = act(src [+ bias] [+ residual]) as one linalg.generic."""
+def _epilogue(res, src, bias, shape, elem, act, residual=None, bias_dim=None):
+    """`res` = act(src [+ bias] [+ residual]) as one linalg.generic; the bias
+    runs along dimension `bias_dim` (default the last)."""
     rank = len(shape)
+    bias_dim = rank - 1 if bias_dim is None else bias_dim
     ins, tys, args, lines = [src], [_t(shape, elem)], ["%in: " + elem], []
     maps = []
     ids = ", ".join(f"d{i}" for i in range(rank))
@@ -35,9 +37,9 @@ def _epilogue(res, src, bias, shape, elem, act, residual=None):
     v = "%in"
     if bias is not None:
         ins.append(bias)
-        tys.append(_t([shape[-1]], elem))
+        tys.append(_t([shape[bias_dim]], elem))
         args.append("%b: " + elem)
-        maps.append(f"affine_map<({ids}) -> (d{rank - 1})>")
+        maps.append(f"affine_map<({ids}) -> (d{bias_dim})>")
         lines.append(f"    %s0 = arith.addf {v}, %b : {elem}")
         v = "%s0"
     if residual is not None:
@@ -508,6 +510,19 @@ def nchw_conv_relu(N, C, F, H, W, elem="f16"):
             _nchw_pad("%p", "%input", xs, 1, elem) +
             _nchw_conv("%c", "%p", "%filter", ps, [F, C, 3, 3], os_, elem) +
             _nchw_eltwise("%r", ["%c"], os_, elem, relu, "%m") +
+            f"  return %r : {_t(os_, elem)}\n}}\n")
+
+
+def nchw_conv_bias_act(N, C, F, H, W, act="relu", elem="f32"):
+    """A zero pad of 1 in H and W, then fill -> conv_2d_nchw_fchw 3x3 ->
+    generic(bias along the output channels, activation)."""
+    xs, os_, ps = [N, C, H, W], [N, F, H, W], [N, C, H + 2, W + 2]
+    return (f"func.func @conv2d_bias_act(%input: {_t(xs, elem)}, %filter: "
+            f"{_t([F, C, 3, 3], elem)}, %bias: {_t([F], elem)}) -> {_t(os_, elem)} {{\n"
+            f"  %cst = arith.constant 0.0 : {elem}\n" +
+            _nchw_pad("%p", "%input", xs, 1, elem) +
+            _nchw_conv("%c", "%p", "%filter", ps, [F, C, 3, 3], os_, elem) +
+            _epilogue("%r", "%c", "%bias", os_, elem, act, bias_dim=1) +
             f"  return %r : {_t(os_, elem)}\n}}\n")
 
 

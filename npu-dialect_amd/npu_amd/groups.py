@@ -73,16 +73,43 @@ def fused_matmul_bias_act(A, B, bias, out, act="relu", stream=None):
     return out
 
 
+def _dump_ptr(lds_dump, plan):
+    """The device address the launch copies a workgroup's LDS to: the kernel
+    writes plan.lds_bytes bytes there, so the tensor must hold them."""
+    if lds_dump is None:
+        return None
+    if not lds_dump.is_cuda or not lds_dump.is_contiguous() or \
+            lds_dump.numel() * lds_dump.element_size() < plan.lds_bytes:
+        raise ValueError(f"lds_dump: a contiguous device tensor of at least {plan.lds_bytes} "
+                         "bytes is needed")
+    return lds_dump.data_ptr()
+
+
 def planned_matmul_bias_act(A, B, bias, out, plan, act="relu", lds_dump=None, stream=None):
     """out = act(A @ B + bias) as the reference's bufferized tile loop, every
     SRAM buffer at the LDS offset `plan` (an NpuTilePlan, see
     npu_amd.tileplan) gives it; `lds_dump` (a device tensor of
     plan.lds_bytes bytes) receives tile (0, 0)'s LDS at the end."""
     mA, mB, mb, mo = from_tensor(A), from_tensor(B), _opt(bias), from_tensor(out)
-    dump = None if lds_dump is None else lds_dump.data_ptr()
+    dump = _dump_ptr(lds_dump, plan)
     st = _lib.lib().npu_planned_matmul_bias_act(ref(mA), ref(mB), ref(mb), ref(mo), ACT[act],
                                                 C.byref(plan), dump, _stream(stream))
     _check(st, "npu_planned_matmul_bias_act")
+    return out
+
+
+def planned_conv2d_nchw_bias_act(x, w, bias, out, plan, act="relu", lds_dump=None, stream=None):
+    """out = act(conv_2d_nchw_fchw(x, w) + bias) (x padded, stride 1) as the
+    reference's tile loop over output-channel tiles, every SRAM buffer at
+    the LDS offset `plan` (an NpuConvTilePlan, see npu_amd.tileplan) gives
+    it, the next tiles' filters through its prefetch region; `lds_dump` (a
+    device tensor of plan.lds_bytes bytes) receives workgroup 0's LDS at
+    the end."""
+    mx, mw, mb, mo = from_tensor(x), from_tensor(w), _opt(bias), from_tensor(out)
+    dump = _dump_ptr(lds_dump, plan)
+    st = _lib.lib().npu_planned_conv2d_nchw_bias_act(ref(mx), ref(mw), ref(mb), ref(mo), ACT[act],
+                                                     C.byref(plan), dump, _stream(stream))
+    _check(st, "npu_planned_conv2d_nchw_bias_act")
     return out
 
 

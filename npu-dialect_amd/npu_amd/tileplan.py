@@ -88,3 +88,103 @@ def matmul_group_plan(func: mlir.MFunc, target: host.HWTarget = None, sram: int 
     return {"function": f["name"], "tile": (tm, tn, tk), "k_steps": nk, "buffers": layout,
             "peak_bytes": summ.peak_bytes, "barriers": barriers,
             "subgraphs": max(s for s, _, _ in barriers) + 1, "plan": plan}
+
+
+def _conv_group(func, f):
+    by = {func.ops[i].name: func.ops[i] for i in f["ops"]}
+    fill, conv = by.get("linalg.fill"), by.get("linalg.conv_2d_nchw_fchw")
+    gen = by.get("linalg.generic")
+    if conv is None or gen is None:
+        raise NotImplementedError("the conv tile plan covers fill -> conv_2d_nchw_fchw -> generic "
+                                  "groups")
+    bias = [v for v in gen.ins if v != conv.results[0]]
+    return conv, {"x": conv.ins[0], "w": conv.ins[1],
+                  "init": fill.outs[0] if fill else conv.outs[0],
+                  "bias": bias[0] if bias else None, "y": gen.outs[0]}
+
+
+def conv_group_plan(func: mlir.MFunc, target: host.HWTarget = None, cores: int = 256,
+                    sram: int = LDS_BYTES) -> dict:
+    """The fill -> conv_2d_nchw_fchw -> generic group of `func` (its input the
+    padded tensor) as `npu-opt --npu-spatial-tiling=num-cores=<cores>
+    --npu-temporal-tiling=sram-size=<sram> --npu-bufferize
+    --npu-sram-allocation=sram-size=<sram>` plans it: the spatial split of the
+    conv over output rows (one row per core: SpatialTilingPass.cpp:38-168),
+    the spec-driven temporal tile of a core's row over output channels
+    (TemporalTilingPass.cpp:76-336), the loop's slice buffers placed by the
+    dual-end allocator -- ping/pong for inputs in the loop, the weight
+    prefetch into the SRAM left over, spills to DRAM
+    (SRAMAllocationPass.cpp:172-363).  Returns the plan, the buffers and the
+    npu_conv_tile_plan a launch uses (-1 for a buffer the plan does not put in
+    SRAM).  `target`: the module's, else the reference's default."""
+    import copy
+    t = target or (host.target_from_params(func.target) if func.target else host.default_target())
+    rep = pipeline.run(func, t, cores=cores, sram_size=sram)
+    f = next((f for f in rep["functions"]
+              if any(func.ops[i].name == "linalg.conv_2d_nchw_fchw" for i in f["ops"])), None)
+    if f is None:
+        raise NotImplementedError("no conv_2d_nchw_fchw group in this function")
+    conv, names = _conv_group(func, f)
+    if conv.attrs.get("strides", [1, 1]) != [1, 1]:
+        raise NotImplementedError(f"{conv.results[0]}: strides {conv.attrs['strides']}")
+    N, C, Hp, Wp = func.types[names["x"]].shape
+    F, _, KH, KW = func.types[names["w"]].shape
+    Ho, Wo = Hp - KH + 1, Wp - KW + 1
+    sp = next((d for d in f["spatial"] if d["op"] == conv.results[0]), None)
+    if sp is None or sp["iter_dim"] != 2 or sp["tile"] != 1:
+        raise NotImplementedError(f"{conv.results[0]}: the spatial split is {sp}, not one output "
+                                  "row per core")
+    # one core's share: output row [1, F, 1, Wo] from input rows [1, C, KH, Wp]
+    share = (f"func.func @row(%x: tensor<1x{C}x{KH}x{Wp}xf32>, %w: tensor<{F}x{C}x{KH}x{KW}xf32>, "
+             f"%o: tensor<1x{F}x1x{Wo}xf32>) -> tensor<1x{F}x1x{Wo}xf32> {{\n"
+             f"  %r = linalg.conv_2d_nchw_fchw {{dilations = dense<1> : tensor<2xi64>, strides = "
+             f"dense<1> : tensor<2xi64>}} ins(%x, %w : tensor<1x{C}x{KH}x{Wp}xf32>, "
+             f"tensor<{F}x{C}x{KH}x{KW}xf32>) outs(%o : tensor<1x{F}x1x{Wo}xf32>) -> "
+             f"tensor<1x{F}x1x{Wo}xf32>\n  return %r : tensor<1x{F}x1x{Wo}xf32>\n}}\n")
+    t2 = copy.copy(t)
+    t2.sram_per_core = sram
+    ts, _ = host.temporal(host.Graph(mlir.parse_functions(share)[0]), t2, 0)
+    if ts is None:
+        # one tile (TemporalTilingPass leaves an op whose best tile count is 1
+        # untiled): the core's whole row in one trip
+        ts = [1, F, 1, Wo, 0, 0, 0]
+    if ts[0] != 1 or ts[2] != 1 or ts[3] != Wo:
+        raise NotImplementedError(f"the temporal tile of a row is {ts}, not output-channel tiles")
+    tco = min(ts[1], F)
+    elem = 4  # f32 (f16 text runs as f32, the reference harness's rule)
+    slice_bytes = {names["x"]: C * KH * Wp * elem, names["w"]: tco * C * KH * KW * elem,
+                   names["init"]: tco * Wo * elem, names["y"]: tco * Wo * elem}
+    if names["bias"]:
+        slice_bytes[names["bias"]] = tco * elem
+    g = host.Graph(func)
+    bufs = host.bufferize(g, f["ops"], slice_bytes)
+    summ = host.sram_allocation(bufs, sram)
+    vname = {v: k for k, v in g.value_id.items()}
+    planned = {vname.get(b.value, str(b.value)): b for b in bufs}
+    layout = {}
+    for key in ("x", "w", "bias", "init", "y"):
+        b = planned.get(names[key]) if names[key] else None
+        if b is None:
+            continue
+        if b.spilled and key not in ("x", "w"):
+            raise NotImplementedError(f"the plan spills {names[key]} to DRAM")
+        layout[key] = {"value": names[key], "bytes": b.bytes, "spilled": bool(b.spilled),
+                       "offset": -1 if b.spilled else b.addr,
+                       "offset_pong": b.addr_pong if b.double_buffered and not b.spilled else -1,
+                       "double_buffered": bool(b.double_buffered) and not b.spilled,
+                       "prefetch_addr": b.prefetch_addr if not b.spilled else -1,
+                       "role": host.ROLES[b.role]}
+    plan = _lib.NpuConvTilePlan()
+    plan.tco, plan.lds_bytes = tco, sram
+    plan.off_in, plan.off_in_pong = layout["x"]["offset"], layout["x"]["offset_pong"]
+    plan.off_in_prefetch = layout["x"]["prefetch_addr"]
+    plan.off_w, plan.off_w_pong = layout["w"]["offset"], layout["w"]["offset_pong"]
+    plan.off_w_prefetch = layout["w"]["prefetch_addr"]
+    nob = {"offset": -1, "offset_pong": -1, "prefetch_addr": -1}
+    bl = layout.get("bias", nob)
+    plan.off_bias, plan.off_bias_pong = bl["offset"], bl["offset_pong"]
+    plan.off_bias_prefetch = bl["prefetch_addr"]
+    plan.off_c, plan.off_y = layout["init"]["offset"], layout["y"]["offset"]
+    return {"function": f["name"], "share": (1, F, 1, Wo), "tile": list(ts), "tco": tco,
+            "tiles": -(-F // tco), "cores": N * Ho, "buffers": layout,
+            "peak_bytes": summ.peak_bytes, "prefetched": summ.prefetched, "plan": plan}

@@ -622,6 +622,91 @@ def test_planned_matmul_relu_mlir_closed_form(cuda):
     assert np.allclose(got, ta.shape[1] * 0.01 * 0.02, rtol=1e-5, atol=1e-7)
 
 
+def _conv_plan_case(shape, bias, seed):
+    from npu_amd import tileplan
+    N, Cc, F, H, W = shape
+    text = (blocks.nchw_conv_bias_act(N, Cc, F, H, W, act="relu6") if bias
+            else lower.harness_f32(blocks.nchw_conv_relu(N, Cc, F, H, W)))
+    p = tileplan.conv_group_plan(mlir.parse_functions(text)[0])
+    x = rng.uniform(seed, 0, (N, Cc, H, W), -1, 1)
+    w = rng.uniform(seed, 1, (F, Cc, 3, 3), -1, 1)
+    b = rng.uniform(seed, 2, (F,), -1, 1) if bias else None
+    return p, oracle.pad_nchw(x, (1, 1, 1, 1)), w, b
+
+
+# (shape N, C, F, H, W; bias): the layouts the reference's plan gives them
+PLANNED_CONV = [
+    ((1, 64, 64, 56, 56), False),   # conv2d_relu.mlir: rows ping/pong/prefetch, filters spilled
+    ((2, 5, 45, 64, 19), True),     # 3 tiles, the last ragged; every input with a prefetch region
+    ((1, 4, 64, 90, 15), True),     # 4 tiles: tile i+2 fetched into the prefetch regions
+    ((1, 64, 96, 112, 20), True),   # filters' ping only, rows without a prefetch region
+    ((1, 128, 64, 56, 56), False),  # rows' ping only, filters spilled, 4 tiles
+    ((1, 256, 64, 56, 56), False),  # rows and filters spilled, one tile
+    ((1, 8, 20, 40, 16), True),     # one tile of all 20 channels
+]
+
+
+@pytest.mark.parametrize("shape,bias", PLANNED_CONV, ids=lambda v: "x".join(map(str, v))
+                         if isinstance(v, tuple) else ("bias" if v else "nobias"))
+def test_planned_conv_layout_is_the_plan(cuda, shape, bias):
+    """The conv group run as the reference's tile loop over output-channel
+    tiles with its SRAM plan as the LDS layout: the output within the f32
+    bound of the oracle (relu6 with a bias, relu without), and workgroup
+    0's LDS (image 0, output row 0) holding each slice at its planned
+    offset: the input rows in every slot the loop filled, the last tile's
+    filter and bias slices in the buffer of that tile's parity, the tile
+    before it in the other, the last tile's copy in the prefetch regions
+    (zeros past F), the accumulator row and the output row, which is what
+    was stored."""
+    p, xp, w, b = _conv_plan_case(shape, bias, 70 + shape[1])
+    plan = p["plan"]
+    N, Cc, F, H, W = shape
+    tco, nt = p["tco"], p["tiles"]
+    print(f"planned conv {shape} tco {tco} tiles {nt}", flush=True)
+    out = torch.empty((N, F, H, W), dtype=torch.float32, device="cuda")
+    dump = torch.zeros(plan.lds_bytes // 4, dtype=torch.float32, device="cuda")
+    act = "relu6" if bias else "relu"
+    groups.planned_conv2d_nchw_bias_act(_dev(xp), _dev(w), _dev(b), out, plan, act, lds_dump=dump)
+    torch.cuda.synchronize()
+    ref, mag = refs.conv_nchw_act(xp, w, b, pad=0, act=act)
+    got = _host(out)
+    check_bound(got, ref, mag, RTOL_F32, what=f"planned conv {shape}")
+    lds = _host(dump)
+    at = lambda off, n: lds[off // 4: off // 4 + n]
+    rows = xp[0, :, 0:3, :].astype(np.float32).ravel()
+    filled = [plan.off_in] + ([plan.off_in_pong, plan.off_in_prefetch] if nt > 1 else [])
+    for off in filled:
+        if off >= 0:
+            assert np.array_equal(at(off, rows.size), rows)
+
+    def slice_of(t, arr, per):
+        v = np.zeros((tco,) + arr.shape[1:], np.float32)
+        f0 = t * tco
+        v[:max(0, min(tco, F - f0))] = arr[f0:f0 + tco]
+        return v.ravel()
+
+    last, prev = nt - 1, nt - 2
+    for arr, ping, pong, pre in ((w, plan.off_w, plan.off_w_pong, plan.off_w_prefetch),
+                                 (b, plan.off_bias, plan.off_bias_pong, plan.off_bias_prefetch)):
+        if arr is None or ping < 0:
+            continue
+        slots = [ping, pong if pong >= 0 else ping]
+        want = slice_of(last, arr, None)
+        assert np.array_equal(at(slots[last & 1], want.size), want)
+        if nt > 1 and pong >= 0:
+            wp = slice_of(prev, arr, None)
+            assert np.array_equal(at(slots[prev & 1], wp.size), wp)
+        if nt > 1 and pre >= 0:
+            assert np.array_equal(at(pre, want.size), want)
+    nl = min(tco, F - last * tco)
+    c = at(plan.off_c, tco * W).reshape(tco, W)[:nl]
+    r0, m0 = refs.conv_nchw_act(xp[:1, :, 0:3], w[last * tco:last * tco + nl], None, pad=0,
+                                act="none")
+    check_bound(c, r0[0, :, 0], m0[0, :, 0], RTOL_F32, what="accumulator row in SRAM")
+    y = at(plan.off_y, tco * W).reshape(tco, W)[:nl]
+    assert np.array_equal(y, got[0, last * tco:last * tco + nl, 0])
+
+
 # ------------------------------------------------------------------ host lowering
 @pytest.mark.parametrize("case", ["matmul", "conv_f32", "conv_bf16", "inverted_residual"])
 def test_lowered_blocks_match_the_oracle(cuda, case):
