@@ -934,14 +934,16 @@ hipError_t launch_stream(const ConvArgs &a, int wgs, hipStream_t s) {
 }
 
 // Vector-ALU instructions per wave of the f32 walk on the bf16 pipe, from
-// its compiled loops: per tile 24 per 16-byte new-row run split into three
-// parts and written (TR x LPR runs), 20 per 16-pixel block (activation,
-// store address, the partial-sum exchange), 64 for slots, read bases and
-// the prefetch; once, 24 per filter run split (9 taps x 2 runs) plus 120.
-constexpr double X6_VALU_SPLIT_RUN = 24.0;
+// its compiled loops: per tile 34 per 16-byte new-row run split into three
+// parts, written and folded into the split-domain bounds (TR x LPR runs),
+// 20 per 16-pixel block (activation, store address, the partial-sum
+// exchange), 64 for slots, read bases and the prefetch; once, 34 per
+// filter run split (9 taps x 2 runs), 160 for the first tile's rows and the
+// addresses, 20 for the bias check and the end-of-walk domain test.
+constexpr double X6_VALU_SPLIT_RUN = 34.0;
 constexpr double X6_VALU_BLOCK = 20.0;
 constexpr double X6_VALU_TILE = 64.0;
-constexpr double X6_VALU_SETUP = 9 * 2 * 24.0 + 120.0;
+constexpr double X6_VALU_SETUP = 9 * 2 * 34.0 + 160.0 + 20.0;
 
 template <int WMAX, int NCX, int WFIX>
 hipError_t launch_x6(const ConvArgs &a, hipStream_t s) {

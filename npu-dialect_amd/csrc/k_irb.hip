@@ -326,9 +326,10 @@ hipError_t launch_irb_tile(const IrbArgs &a, hipStream_t s) {
     // padding select, the store address); 46 per 16 depthwise channels of a
     // block of 16 output pixels (nine taps' FMAs, ReLU6, LDS addresses),
     // OP / 16 blocks over four waves: 706 per 8 x 8 tile at E = 144.
-    // Set-up: 330 (the filter staging and the first halo's addresses).
+    // Set-up: 330 (the filter staging and the first halo's addresses; 254
+    // for the 4 x 4 tile's 36-pixel halo, <24, 144, 4, 4>).
     p.tile_valu = 4.0 * (81.0 + FB1 * HPB / 4.0 * 13.4 + 46.0 * (E / 16) * (OP / 16) / 4.0);
-    p.wg_setup_valu = 4.0 * 330.0;
+    p.wg_setup_valu = 4.0 * (TH == 4 ? 254.0 : 330.0);
     p.tile_lds_bytes = HP * (KC1 * 16 + 8) * 4.0 +                // halo written
                        (E / 16.0) * KC1 * HPB * 1024 +            // expand A read
                        HP * E * 4.0 +                             // expanded tile written
