@@ -393,6 +393,28 @@ def test_c4_requant_extremes(cuda):
     assert np.array_equal(_qb_run(inp), ref)
 
 
+def test_c4_requant_wide_products(cuda):
+    """Shifts from 33 to 62 with multipliers at the int32 limits of either
+    sign and zero, and accumulators at their extremes (x and the filters at
+    +-127): products that need all 64 bits, bit for bit against the
+    oracle's rounding."""
+    N, H, W, C, M1 = 1, 8, 8, 256, 64
+    inp = _qb_inputs(N, H, W, C, M1, 81)
+    inp["x"][:] = 127
+    inp["w1"][::2] = 127
+    inp["w1"][1::2] = -127
+    inp["m1"][:] = rng.randint(82, 0, (M1,), 1 << 24, 1 << 30).astype(np.int32)
+    inp["m1"][:4] = [2 ** 31 - 1, -(2 ** 31), 0, 1]
+    inp["s1"][:] = rng.randint(83, 0, (M1,), 33, 63).astype(np.int32)
+    inp["s1"][:4] = [33, 62, 33, 62]
+    inp["m2"][:] = 2 ** 31 - 1
+    inp["s2"][:] = 33
+    inp["m3"][:] = -(2 ** 30)
+    inp["s3"][:] = rng.randint(84, 0, (C,), 33, 40).astype(np.int32)
+    ref = oracle.block_qbottleneck(**inp)
+    assert np.array_equal(_qb_run(inp), ref)
+
+
 # ------------------------------------------------------------------ C3
 def test_c3_irb_config_n1(cuda):
     w = configs.irb(1)
