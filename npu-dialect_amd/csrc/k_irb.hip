@@ -148,16 +148,24 @@ __global__ __launch_bounds__(256, E >= 192 ? 1 : 2) void irb_kernel(const float 
       b.u = masked(b.u, k < C);
       be[j][kc] = b;
     }
-  // project A operand: output channel fb*16 + r, expanded channels kc*16 + 4q .. +3
-  Frag16 bp[KC2][FB2];
+  // Per-lane constants of the depthwise/project stage: wave w owns output
+  // pixels 16 ob .. 16 ob + 15 (ob = w % OPB) and the expanded channels of
+  // its channel group cg = w / OPB: 16-channel chunks [kc0, kc1) of KC2, at
+  // most KCW; this lane's pixel p = 16 ob + r.
+  const int ob = wave % OPB, cg = wave / OPB;
+  constexpr int KCW = (KC2 + CS - 1) / CS;
+  const int kc0 = CS == 1 ? 0 : cg * KC2 / CS, kc1 = CS == 1 ? KC2 : (cg + 1) * KC2 / CS;
+  // project A operand of the wave's channel group: output channel fb*16 + r,
+  // expanded channels kc*16 + 4q .. +3 (kc = kc0 + j)
+  Frag16 bp[KCW][FB2];
 #pragma unroll
-  for (int kc = 0; kc < KC2; ++kc)
+  for (int j = 0; j < KCW; ++j)
 #pragma unroll
     for (int fb = 0; fb < FB2; ++fb) {
-      const int c = fb * 16 + r;
+      const int c = fb * 16 + r, kc = min(kc0 + j, KC2 - 1);
       Frag16 b = load16(wp + min(c, C - 1) * E + kc * 16 + 4 * q);
       b.u = masked(b.u, c < C);
-      bp[kc][fb] = b;
+      bp[j][fb] = b;
     }
   for (int i = tid; i < 9 * E / 4; i += 256)
     reinterpret_cast<f32x4 *>(wds)[i] = reinterpret_cast<const f32x4 *>(wdw)[i];
@@ -167,17 +175,11 @@ __global__ __launch_bounds__(256, E >= 192 ? 1 : 2) void irb_kernel(const float 
 #pragma unroll
     for (int kc = 0; kc < KC1; ++kc) settle(be[j][kc].u);
 #pragma unroll
-  for (int kc = 0; kc < KC2; ++kc)
+  for (int j = 0; j < KCW; ++j)
 #pragma unroll
-    for (int fb = 0; fb < FB2; ++fb) settle(bp[kc][fb].u);
+    for (int fb = 0; fb < FB2; ++fb) settle(bp[j][fb].u);
   __syncthreads();
 
-  // Per-lane constants of the depthwise/project stage: wave w owns output
-  // pixels 16 ob .. 16 ob + 15 (ob = w % OPB) and the expanded channels of
-  // its channel group cg = w / OPB: 16-channel chunks [kc0, kc1) of KC2;
-  // this lane's pixel p = 16 ob + r.
-  const int ob = wave % OPB, cg = wave / OPB;
-  const int kc0 = cg * KC2 / CS, kc1 = (cg + 1) * KC2 / CS;
   const int p = ob * 16 + r, py = p / TW, px = p - py * TW;
   const int hbase = py * HW + px;
   const uint32_t ooff = (uint32_t)(((py * W + px) * C + 4 * q) * 4);
@@ -251,8 +253,9 @@ __global__ __launch_bounds__(256, E >= 192 ? 1 : 2) void irb_kernel(const float 
 #pragma unroll
     for (int fb = 0; fb < FB2; ++fb) acc2[fb] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int kc = 0; kc < KC2; ++kc) {
-      if (CS > 1 && (kc < kc0 || kc >= kc1)) continue;  // another wave's channels
+    for (int j = 0; j < KCW; ++j) {
+      const int kc = kc0 + j;
+      if (CS > 1 && kc >= kc1) break;  // a group of KCW - 1 chunks
       const int e0 = kc * 16 + 4 * q;
       f32x4 d = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -265,7 +268,7 @@ __global__ __launch_bounds__(256, E >= 192 ? 1 : 2) void irb_kernel(const float 
       Frag16 a;
       a.f = f32x4{relu6(d[0]), relu6(d[1]), relu6(d[2]), relu6(d[3])};
 #pragma unroll
-      for (int fb = 0; fb < FB2; ++fb) MfmaF32::mma(acc2[fb], bp[kc][fb], a);
+      for (int fb = 0; fb < FB2; ++fb) MfmaF32::mma(acc2[fb], bp[j][fb], a);
     }
     // residual added while x is still in LDS; the stores go out after the
     // next halo is committed and the one after it is fetched, so they are
