@@ -435,6 +435,8 @@ def test_c3_irb_config_n32(cuda):
 @pytest.mark.parametrize("N,H,W,C,E", [
     (2, 9, 13, 24, 144),   # ragged tiles (4 x 4 tiles: fewer 8 x 8 tiles than CUs)
     (1, 3, 5, 24, 144),    # image smaller than a tile
+    (4, 33, 30, 24, 144),  # 4 x 4 tiles, more of them than CUs (a walk of one or two per workgroup)
+    (2, 56, 56, 16, 96),
     (2, 8, 8, 16, 96),     # other block widths of the network
     (1, 10, 7, 32, 192),
     (16, 30, 30, 24, 144),  # 8 x 8 tiles (256 of them), ragged at the image edge
