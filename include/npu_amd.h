@@ -194,7 +194,10 @@ npu_status fused_qbottleneck_i8(const npu_memref *x, const npu_memref *w1,
  *   out = conv1x1(d, wp) + x
  *   x f32 [N,H,W,C]; we f32 [E,C]; wdw f32 [3,3,E]; wp f32 [C,E];
  *   out f32 [N,H,W,C].
- * Supported (C, E): (24,144), (16,96), (32,192). */
+ * (C, E) = (24,144), (16,96), (32,192) run on kernels tuned for them; any
+ * other C % 4 == 0, 4 <= C <= 320 with E % 16 == 0 on a kernel that streams
+ * the expanded channels in chunks of 16 (filters read from L2 per chunk);
+ * other channel counts return NPU_ERR_UNSUPPORTED. */
 npu_status fused_irb_f32(const npu_memref *x, const npu_memref *we,
                          const npu_memref *wdw, const npu_memref *wp,
                          const npu_memref *out, npu_stream stream);

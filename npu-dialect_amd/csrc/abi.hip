@@ -592,7 +592,8 @@ npu_status fused_irb_f32(const npu_memref *x, const npu_memref *we, const npu_me
       return fail(NPU_ERR_INVALID_ARG, "out: size[%d] = %lld, expected %lld", d,
                   (long long)out->sizes[d], (long long)x->sizes[d]);
   if (!npu::irb_supported((int)C, (int)E))
-    return fail(NPU_ERR_UNSUPPORTED, "(C, E) = (%lld, %lld) has no kernel instance",
+    return fail(NPU_ERR_UNSUPPORTED,
+                "(C, E) = (%lld, %lld): C must be a multiple of 4 in [4, 320] and E of 16",
                 (long long)C, (long long)E);
   npu::IrbArgs a{static_cast<const float *>(px), static_cast<const float *>(pwe),
                  static_cast<const float *>(pwdw), static_cast<const float *>(pwp),

@@ -360,17 +360,173 @@ hipError_t launch_irb_t(const IrbArgs &a, hipStream_t s) {
   return launch_irb_tile<C, E, 8, 8>(a, s);
 }
 
+// Any (C, E) with C % 4 == 0, C <= 16 CB and E % 16 == 0, for the channel
+// counts the tuned instances above do not cover: the expanded channels are
+// streamed in chunks of 16, so neither the filters nor the expanded tile
+// need to fit in registers or LDS.  A workgroup walks 4 x 4 output tiles;
+// per tile the x halo (6 x 6 pixels, all C channels, zero outside the image
+// and past C) goes to LDS, then wave w takes chunks w, w + 4, ... of E / 16:
+// the expand of the chunk on the halo (its 16 filters as the A operand, from
+// L2), ReLU6 and the zero padding into the wave's own LDS slot, the
+// depthwise of the 16 output pixels in the project MFMA's B layout, and the
+// project of the chunk into the wave's CB accumulator blocks (its columns of
+// wp as the A operand).  Waves 1..3 leave their partial projections in LDS
+// and wave 0 adds them in wave order, then the residual, and stores.
+template <int CB>
+__global__ __launch_bounds__(256, 1) void irb_stream_kernel(
+    const float *__restrict__ x, const float *__restrict__ we, const float *__restrict__ wdw,
+    const float *__restrict__ wp, float *__restrict__ out, int H, int W, int C, int E,
+    int tiles_w, int tiles_per_image, int ntiles) {
+  constexpr int TW = 4, HW = 6, HP = 36, HPB = 3;
+  constexpr int ESS = 24;  // a wave's expanded chunk: 16 channels per pixel + 8 (32 mod 64 bytes)
+  __shared__ __attribute__((aligned(16))) float xs[HP * (16 * CB + 8)];
+  __shared__ __attribute__((aligned(16))) float esw[4][HPB * 16 * ESS];
+  __shared__ __attribute__((aligned(16))) float part[3 * 16 * CB * 16];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int r = lane & 15, q = lane >> 4;
+  const int KC1 = (C + 15) / 16, XV = KC1 * 4, XS = KC1 * 16 + 8;  // x row: 32 mod 64 bytes
+  const int py = r / TW, px = r - py * TW, hbase = py * HW + px;
+  float *const ew = esw[wave];
+  const TileWalk walk = tile_walk(ntiles);
+  for (int t = walk.first; t < walk.end; t += walk.step) {
+    const int n = t / tiles_per_image, tt = t - n * tiles_per_image;
+    const int ty0 = (tt / tiles_w) * 4, tx0 = (tt - (tt / tiles_w) * tiles_w) * TW;
+    for (int idx = tid; idx < HP * XV; idx += 256) {
+      const int hp = idx / XV, cv = idx - hp * XV, hy = hp / HW, hx = hp - hy * HW;
+      const int iy = ty0 + hy - 1, ix = tx0 + hx - 1;
+      const bool inside = (unsigned)iy < (unsigned)H && (unsigned)ix < (unsigned)W && 4 * cv < C;
+      const float *src = x + ((size_t)(n * H + (inside ? iy : 0)) * W + (inside ? ix : 0)) * C +
+                         (inside ? 4 * cv : 0);
+      *reinterpret_cast<u32x4 *>(xs + hp * XS + 4 * cv) = masked(*reinterpret_cast<const u32x4 *>(src), inside);
+    }
+    __syncthreads();
+    f32x4 acc2[CB];
+#pragma unroll
+    for (int ob = 0; ob < CB; ++ob) acc2[ob] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int k = wave; k < E / 16; k += 4) {
+      const int e0 = k * 16;
+      // expand: filters e0 + r (A), halo pixels pb*16 + r (B), channels kc*16 + 4q + s
+      f32x4 acc[HPB];
+#pragma unroll
+      for (int pb = 0; pb < HPB; ++pb) acc[pb] = f32x4{0.f, 0.f, 0.f, 0.f};
+      for (int kc = 0; kc < KC1; ++kc) {
+        const int c = kc * 16 + 4 * q;
+        Frag16 a = load16(we + (size_t)(e0 + r) * C + min(c, C - 4));
+        a.u = masked(a.u, c < C);
+        Frag16 bx[HPB];
+#pragma unroll
+        for (int pb = 0; pb < HPB; ++pb) bx[pb] = load16(xs + min(pb * 16 + r, HP - 1) * XS + c);
+#pragma unroll
+        for (int s2 = 0; s2 < 4; ++s2)
+#pragma unroll
+          for (int pb = 0; pb < HPB; ++pb) MfmaF32::step(acc[pb], a, bx[pb], s2);
+      }
+      // ReLU6, then the zero padding of the expanded tensor outside the image
+#pragma unroll
+      for (int pb = 0; pb < HPB; ++pb) {
+        const int hp = pb * 16 + r, hy = hp / HW, hx = hp - hy * HW;
+        const bool inside = (unsigned)(ty0 + hy - 1) < (unsigned)H && (unsigned)(tx0 + hx - 1) < (unsigned)W;
+        if (hp < HP) {
+          f32x4 v;
+#pragma unroll
+          for (int e = 0; e < 4; ++e) v[e] = inside ? relu6(acc[pb][e]) : 0.0f;
+          *reinterpret_cast<f32x4 *>(ew + hp * ESS + 4 * q) = v;
+        }
+      }
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+      // depthwise: output pixel r, channels e0 + 4q .. +3
+      f32x4 d = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int tap = 0; tap < 9; ++tap)
+        d += *reinterpret_cast<const f32x4 *>(ew + (hbase + (tap / 3) * HW + (tap % 3)) * ESS + 4 * q) *
+             *reinterpret_cast<const f32x4 *>(wdw + tap * E + e0 + 4 * q);
+      Frag16 bd;
+      bd.f = f32x4{relu6(d[0]), relu6(d[1]), relu6(d[2]), relu6(d[3])};
+      // project: output channels ob*16 + r (A: wp rows), the chunk's channels
+#pragma unroll
+      for (int ob = 0; ob < CB; ++ob) {
+        if (ob * 16 < C) {
+          const int co = ob * 16 + r;
+          Frag16 a = load16(wp + (size_t)min(co, C - 1) * E + e0 + 4 * q);
+          a.u = masked(a.u, co < C);
+          MfmaF32::mma(acc2[ob], a, bd);
+        }
+      }
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+    }
+    if (wave > 0) {
+#pragma unroll
+      for (int ob = 0; ob < CB; ++ob)
+        if (ob * 16 < C)
+          *reinterpret_cast<f32x4 *>(part + ((wave - 1) * 16 + r) * CB * 16 + ob * 16 + 4 * q) = acc2[ob];
+    }
+    __syncthreads();
+    if (wave == 0 && ty0 + py < H && tx0 + px < W) {
+      float *o = out + ((size_t)(n * H + ty0 + py) * W + tx0 + px) * C;
+#pragma unroll
+      for (int ob = 0; ob < CB; ++ob) {
+        const int c = ob * 16 + 4 * q;
+        if (ob * 16 < C) {
+          f32x4 v = acc2[ob];
+#pragma unroll
+          for (int w2 = 0; w2 < 3; ++w2)
+            v += *reinterpret_cast<const f32x4 *>(part + (w2 * 16 + r) * CB * 16 + ob * 16 + 4 * q);
+          v += *reinterpret_cast<const f32x4 *>(xs + (hbase + HW + 1) * XS + c);
+          if (c < C) *reinterpret_cast<f32x4 *>(o + c) = v;
+        }
+      }
+    }
+    __syncthreads();  // xs and part are the next tile's
+  }
+}
+
+template <int CB>
+hipError_t launch_irb_stream(const IrbArgs &a, hipStream_t s) {
+  auto kern = irb_stream_kernel<CB>;
+  const int tiles_w = (a.W + 3) / 4, tiles_h = (a.H + 3) / 4;
+  const int per_image = tiles_w * tiles_h, ntiles = a.N * per_image;
+  const int full = persistent_grid(kern);
+  if (full == 0) return hipErrorInvalidDeviceFunction;
+  const int g = ntiles < full ? (ntiles + kXcds - 1) / kXcds * kXcds : full;
+  {
+    const int KC1 = (a.C + 15) / 16, CBr = (a.C + 15) / 16, chunks = a.E / 16;
+    npu_launch_plan p = make_plan("mbv2_inverted_residual_stream", g, wg_per_cu(kern), ntiles, 32);
+    p.load_phases = 1 + (chunks + 3) / 4;  // the halo, then each chunk's filters from L2
+    p.tile_macs = (double)a.E * 48 * KC1 * 16 + 16.0 * CBr * 16 * a.E;
+    p.tile_valu = 4.0 * (40.0 + (chunks + 3) / 4 * (30.0 + 12.0 * KC1 + 8.0 * CBr));
+    p.tile_lds_bytes = 36.0 * KC1 * 16 * 4 * 2 + chunks * (48.0 * 16 * 4 * KC1 + 36.0 * 16 * 4 + 9.0 * 16 * 16 * 4) +
+                       3.0 * 16 * CBr * 16 * 4 * 2;
+    p.tile_load_bytes = 36.0 * a.C * 4 + chunks * 4.0 * (16.0 * a.C + 9.0 * 16 + 16.0 * a.C);
+    p.tile_store_bytes = 16.0 * a.C * 4;
+    p.hbm_bytes = 4.0 * (2.0 * a.N * a.H * a.W * a.C + 2.0 * a.C * a.E + 9.0 * a.E);
+    plans_add(p);
+  }
+  hipLaunchKernelGGL(kern, dim3(g), dim3(256), 0, s, a.x, a.we, a.wdw, a.wp, a.out, a.H, a.W, a.C,
+                     a.E, tiles_w, per_image, ntiles);
+  return hipGetLastError();
+}
+
+bool irb_tuned(int C, int E) {
+  return (C == 24 && E == 144) || (C == 16 && E == 96) || (C == 32 && E == 192);
+}
+
 }  // namespace
 
 bool irb_supported(int C, int E) {
-  return (C == 24 && E == 144) || (C == 16 && E == 96) || (C == 32 && E == 192);
+  return irb_tuned(C, E) || (C >= 4 && C % 4 == 0 && C <= 320 && E >= 16 && E % 16 == 0);
 }
 
 hipError_t launch_irb_f32(const IrbArgs &a, hipStream_t s) {
   if (a.C == 24 && a.E == 144) return launch_irb_t<24, 144>(a, s);
   if (a.C == 16 && a.E == 96) return launch_irb_t<16, 96>(a, s);
   if (a.C == 32 && a.E == 192) return launch_irb_t<32, 192>(a, s);
-  return hipErrorInvalidValue;
+  if (!irb_supported(a.C, a.E)) return hipErrorInvalidValue;
+  if (a.C <= 32) return launch_irb_stream<2>(a, s);
+  if (a.C <= 64) return launch_irb_stream<4>(a, s);
+  if (a.C <= 128) return launch_irb_stream<8>(a, s);
+  return launch_irb_stream<20>(a, s);
 }
 
 }  // namespace npu

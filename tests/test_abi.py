@@ -87,6 +87,21 @@ def test_matmul_rejects_bad_descriptors():
     assert call(_mr([8, 16], ptr=0x10004), B, b, o, 1) == 2 and "aligned" in _err()
 
 
+def test_irb_channel_limits():
+    """fused_irb_f32 takes C % 4 == 0 in [4, 320] and E % 16 == 0 (the tuned
+    (C, E) pairs and the streaming kernel); other counts are refused by name
+    before any launch."""
+    lib = npu_amd.lib()
+
+    def call(ch, e):
+        x, o = _mr([1, 4, 4, ch]), _mr([1, 4, 4, ch])
+        we, wdw, wp = _mr([e, ch]), _mr([3, 3, e]), _mr([ch, e])
+        return lib.fused_irb_f32(*[C.byref(m) for m in (x, we, wdw, wp, o)], None)
+
+    for ch, e in ((324, 1280), (26, 144), (24, 100), (40, 24)):
+        assert call(ch, e) == 2 and "multiple of 4 in [4, 320]" in _err(), (ch, e, _err())
+
+
 def test_conv_rejects_bad_descriptors():
     lib = npu_amd.lib()
     x, w, b, o = _mr([1, 8, 8, 16]), _mr([16, 3, 3, 16]), _mr([16]), _mr([1, 8, 8, 16])

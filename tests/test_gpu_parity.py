@@ -456,6 +456,32 @@ def test_c3_irb_shapes(cuda, N, H, W, C, E):
     check_bound(_host(out), ref, mag, RTOL_F32, what=f"irb {N}x{H}x{W}x{C}/{E}")
 
 
+@pytest.mark.parametrize("N,H,W,C,E", [
+    (2, 9, 13, 64, 384),    # the MobileNetV2 blocks the tuned instances do not cover
+    (1, 14, 14, 96, 576),
+    (1, 7, 7, 160, 960),
+    (3, 10, 11, 40, 240),
+    (1, 12, 12, 28, 64),    # C off the 16-channel blocks
+    (2, 5, 6, 8, 16),       # fewer chunks than waves
+    (1, 6, 5, 320, 1280),   # the largest C
+    (4, 30, 31, 24, 96),    # more tiles than resident workgroups
+])
+def test_c3_irb_any_channels(cuda, N, H, W, C, E):
+    """(C, E) outside the tuned instances run on the kernel that streams the
+    expanded channels in chunks of 16: within the f32 bound of the oracle."""
+    x = rng.uniform(33, 0, (N, H, W, C), -1, 1)
+    we = rng.normal(33, 1, (E, C), 0, math.sqrt(2 / C))
+    wdw = rng.normal(33, 2, (3, 3, E), 0, math.sqrt(2 / 9))
+    wp = rng.normal(33, 3, (C, E), 0, math.sqrt(2 / E))
+    d = configs.to_device({"x": x, "we": we, "wdw": wdw, "wp": wp})
+    out = torch.empty_like(d["x"])
+    print(f"irb stream {N}x{H}x{W}x{C}/{E}", flush=True)
+    groups.fused_irb_f32(d["x"], d["we"], d["wdw"], d["wp"], out)
+    torch.cuda.synchronize()
+    ref, mag = refs.irb(x, we, wdw, wp)
+    check_bound(_host(out), ref, mag, RTOL_F32, what=f"irb {N}x{H}x{W}x{C}/{E}")
+
+
 def test_c3_irb_relu6_clamps_both_sides(cuda):
     """Large weights drive the expand and depthwise stages past 6 and below 0."""
     N, H, W, C, E = 1, 8, 8, 24, 144
@@ -732,7 +758,8 @@ def test_planned_conv_layout_is_the_plan(cuda, shape, bias):
 
 
 # ------------------------------------------------------------------ host lowering
-@pytest.mark.parametrize("case", ["matmul", "conv_f32", "conv_bf16", "inverted_residual"])
+@pytest.mark.parametrize("case", ["matmul", "conv_f32", "conv_bf16", "inverted_residual",
+                                  "inverted_residual_64x384"])
 def test_lowered_blocks_match_the_oracle(cuda, case):
     """linalg text -> npu_amd.lower -> entry-point calls on the GPU, against
     the oracle of the same block."""
@@ -765,7 +792,9 @@ def test_lowered_blocks_match_the_oracle(cuda, case):
             ref32, _ = _widened_conv(x, w, bias32, 1, "relu")
             check_bf16_rounded(_host(out), ref32, mag, 9 * 32 + 1, what="lowered conv")
     else:
-        N, H, W, C, E = 2, 9, 13, 24, 144
+        # the configuration's channels, and a MobileNetV2 block the streaming
+        # kernel runs
+        N, H, W, C, E = (2, 9, 13, 24, 144) if case == "inverted_residual" else (1, 14, 14, 64, 384)
         x = rng.uniform(17, 0, (N, H, W, C), 0, 1)
         we = rng.normal(17, 1, (E, C), 0, math.sqrt(2 / C))
         wdw = rng.normal(17, 2, (3, 3, E), 0, math.sqrt(2 / 9))

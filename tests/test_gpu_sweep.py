@@ -65,9 +65,14 @@ def _conv_cases(n=16, seed=2027):
 
 
 def _irb_cases(n=6, seed=2028):
+    """The tuned (C, E) pairs, then as many with any C % 4 == 0 up to 128 and
+    E % 16 == 0 (the streaming kernel)."""
     r = random.Random(seed)
-    return [(r.randint(1, 4), r.randint(1, 20), r.randint(1, 20)) + r.choice(((24, 144), (16, 96), (32, 192)))
-            for _ in range(n)]
+    tuned = [(r.randint(1, 4), r.randint(1, 20), r.randint(1, 20)) + r.choice(((24, 144), (16, 96), (32, 192)))
+             for _ in range(n)]
+    other = [(r.randint(1, 4), r.randint(1, 20), r.randint(1, 20), 4 * r.randint(1, 32), 16 * r.randint(1, 24))
+             for _ in range(n)]
+    return tuned + other
 
 
 def _qb_cases(n=6, seed=2029):
