@@ -177,8 +177,11 @@ npu_status fused_conv2d_nchw_bias_res_act(const npu_memref *x, const npu_memref 
  *   (int64(acc) * m + (1 << (s - 1))) >> s, per output channel.
  *   x i8 [N,H,W,C]; w1 i8 [M1,C]; w2 i8 [M1,3,3,M1]; w3 i8 [C,M1];
  *   m1,s1,m2,s2 i32 [M1]; m3,s3 i32 [C]; out i8 [N,H,W,C].
- * Supported (C, M1): (256,64), (128,64), (64,64).  Precondition (TOSA):
- * every shift is in [2, 62]. */
+ * (C, M1) = (256,64), (128,64), (64,64) run on kernels tuned for them; any
+ * other C and M1 that are multiples of 64 with C <= 2048 and M1 <= 512 on a
+ * kernel that reads its filter blocks from L2 where they are used; other
+ * counts return NPU_ERR_UNSUPPORTED.  Precondition (TOSA): every shift is in
+ * [2, 62]. */
 npu_status fused_qbottleneck_i8(const npu_memref *x, const npu_memref *w1,
                                 const npu_memref *w2, const npu_memref *w3,
                                 const npu_memref *m1, const npu_memref *s1,

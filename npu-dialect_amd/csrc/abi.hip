@@ -556,7 +556,8 @@ npu_status fused_qbottleneck_i8(const npu_memref *x, const npu_memref *w1,
       return fail(NPU_ERR_INVALID_ARG, "out: size[%d] = %lld, expected %lld", d,
                   (long long)out->sizes[d], (long long)x->sizes[d]);
   if (!npu::qbottleneck_supported((int)C, (int)M1))
-    return fail(NPU_ERR_UNSUPPORTED, "(C, M1) = (%lld, %lld) has no kernel instance",
+    return fail(NPU_ERR_UNSUPPORTED,
+                "(C, M1) = (%lld, %lld): C must be a multiple of 64 up to 2048, M1 up to 512",
                 (long long)C, (long long)M1);
   npu::QBottleneckArgs a{static_cast<const int8_t *>(px), static_cast<const int8_t *>(pw1),
                          static_cast<const int8_t *>(pw2), static_cast<const int8_t *>(pw3),

@@ -300,17 +300,139 @@ hipError_t launch_qb(const QBottleneckArgs &a, hipStream_t s) {
   return hipGetLastError();
 }
 
+// Any C and M1 that are multiples of 64, C <= 2048 and M1 <= 512 (ResNet-50's
+// later stages: 512/128, 1024/256, 2048/512), for the counts the tuned
+// instances above do not cover.  Every filter block is read from L2 where it
+// is used, so nothing scales the registers with the channel counts.  A
+// workgroup walks 4 x 4 output tiles; per tile: the x halo (6 x 6 pixels, all
+// C channels, zero outside the image) to LDS; conv1 on the halo, one unit =
+// 16 output channels x 16 halo pixels, requant + ReLU clamp into y1 (zero
+// outside the image: the pad before conv2); conv2, one unit = 16 channels of
+// the 16 output pixels, into y2; conv3, one unit = 16 output channels, with
+// requant, the residual from the halo and the clamp, stored.  The units of a
+// phase are dealt round-robin over the four waves, one barrier per phase.
+__global__ __launch_bounds__(256, 1) void qb_stream_kernel(
+    const int8_t *__restrict__ x, const int8_t *__restrict__ w1, const int8_t *__restrict__ w2,
+    const int8_t *__restrict__ w3, const int32_t *__restrict__ m1, const int32_t *__restrict__ s1,
+    const int32_t *__restrict__ m2, const int32_t *__restrict__ s2,
+    const int32_t *__restrict__ m3, const int32_t *__restrict__ s3, int8_t *__restrict__ out,
+    int H, int W, int C, int M1, int tiles_w, int tiles_img, int ntiles) {
+  constexpr int SHW = 6, SHP = 36, SHPB = 3, CMAX = 2048, MMAX = 512;
+  __shared__ __attribute__((aligned(16))) int8_t xs[SHP * (CMAX + 32)];
+  __shared__ __attribute__((aligned(16))) int8_t y1[SHPB * 16 * (MMAX + 32)];
+  __shared__ __attribute__((aligned(16))) int8_t y2[16 * (MMAX + 32)];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int r = lane & 15, q = lane >> 4;
+  const int XS = C + 32, YS = M1 + 32;  // 16-byte row reads: 32 mod 64 bytes
+  const int XV = C / 16;                // 16-byte runs per halo pixel
+  const int py = r / 4, px = r - py * 4, hb = py * SHW + px;
+  auto params = [&](const int32_t *m, const int32_t *sh, int c) {
+    Scale4 sc;
+    sc.m = *reinterpret_cast<const i32x4 *>(m + c);
+    sc.s = *reinterpret_cast<const i32x4 *>(sh + c);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) sc.r[e] = 1LL << (sc.s[e] - 1);
+    return sc;
+  };
+  const TileWalk walk = tile_walk(ntiles);
+  for (int t = walk.first; t < walk.end; t += walk.step) {
+    const int n = t / tiles_img, tt = t - n * tiles_img;
+    const int ty0 = (tt / tiles_w) * 4, tx0 = (tt - (tt / tiles_w) * tiles_w) * 4;
+    for (int idx = tid; idx < SHP * XV; idx += 256) {
+      const int hp = idx / XV, cv = idx - hp * XV, hy = hp / SHW, hx = hp - hy * SHW;
+      const int iy = ty0 + hy - 1, ix = tx0 + hx - 1;
+      const bool inside = (unsigned)iy < (unsigned)H && (unsigned)ix < (unsigned)W;
+      const int8_t *src = x + ((size_t)(n * H + (inside ? iy : 0)) * W + (inside ? ix : 0)) * C + 16 * cv;
+      *reinterpret_cast<u32x4 *>(xs + hp * XS + 16 * cv) = masked(*reinterpret_cast<const u32x4 *>(src), inside);
+    }
+    __syncthreads();
+    // conv1: unit u = (filter block fb, halo block pb)
+    for (int u = wave; u < (M1 / 16) * SHPB; u += 4) {
+      const int fb = u / SHPB, pb = u - fb * SHPB;
+      i32x4 acc = {0, 0, 0, 0};
+      for (int c0 = 0; c0 < C; c0 += 64)
+        MfmaI8::mma(acc, load16(w1 + (size_t)(fb * 16 + r) * C + c0 + 16 * q),
+                    load16(xs + min(pb * 16 + r, SHP - 1) * XS + c0 + 16 * q));
+      const int hp = pb * 16 + r, hy = hp / SHW, hx = hp - hy * SHW;
+      const bool inside = hp < SHP && (unsigned)(ty0 + hy - 1) < (unsigned)H &&
+                          (unsigned)(tx0 + hx - 1) < (unsigned)W;
+      const uint32_t v = requant4(acc, params(m1, s1, fb * 16 + 4 * q));
+      *reinterpret_cast<uint32_t *>(y1 + hp * YS + fb * 16 + 4 * q) = inside ? v : 0u;
+    }
+    __syncthreads();
+    // conv2: unit = filter block fb on the 16 output pixels (pixel r: halo hb)
+    for (int fb = wave; fb < M1 / 16; fb += 4) {
+      i32x4 acc = {0, 0, 0, 0};
+      for (int tap = 0; tap < 9; ++tap)
+        for (int c0 = 0; c0 < M1; c0 += 64)
+          MfmaI8::mma(acc, load16(w2 + ((size_t)(fb * 16 + r) * 9 + tap) * M1 + c0 + 16 * q),
+                      load16(y1 + (hb + (tap / 3) * SHW + tap % 3) * YS + c0 + 16 * q));
+      *reinterpret_cast<uint32_t *>(y2 + r * YS + fb * 16 + 4 * q) =
+          requant4(acc, params(m2, s2, fb * 16 + 4 * q));
+    }
+    __syncthreads();
+    // conv3 + requant + residual + clamp: unit = output channel block cb
+    for (int cb = wave; cb < C / 16; cb += 4) {
+      i32x4 acc = {0, 0, 0, 0};
+      for (int c0 = 0; c0 < M1; c0 += 64)
+        MfmaI8::mma(acc, load16(w3 + (size_t)(cb * 16 + r) * M1 + c0 + 16 * q),
+                    load16(y2 + r * YS + c0 + 16 * q));
+      const int c = cb * 16 + 4 * q;
+      const Scale4 sc = params(m3, s3, c);
+      const uint32_t res = *reinterpret_cast<const uint32_t *>(xs + (hb + SHW + 1) * XS + c);
+      uint32_t packed = 0;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int v = requant(acc[e], sc.m[e], sc.r[e], sc.s[e]) + (int)(int8_t)(res >> (8 * e));
+        packed |= (uint32_t)clamp_i(v, 0, 127) << (8 * e);
+      }
+      if (ty0 + py < H && tx0 + px < W)
+        *reinterpret_cast<uint32_t *>(out + ((size_t)(n * H + ty0 + py) * W + tx0 + px) * C + c) = packed;
+    }
+    __syncthreads();  // xs, y1 and y2 are the next tile's
+  }
+}
+
+hipError_t launch_qb_stream(const QBottleneckArgs &a, hipStream_t s) {
+  const int tiles_w = (a.W + 3) / 4, tiles_img = tiles_w * ((a.H + 3) / 4), ntiles = a.N * tiles_img;
+  const int full = persistent_grid(qb_stream_kernel);
+  if (full <= 0) return hipErrorInvalidValue;
+  const int grid = ntiles < full ? (ntiles + kXcds - 1) / kXcds * kXcds : full;
+  {
+    npu_launch_plan p = make_plan("int8_bottleneck_stream", grid, wg_per_cu(qb_stream_kernel), ntiles, 8);
+    p.load_phases = 4;  // the halo, then each phase's filters from L2
+    p.tile_macs = 48.0 * a.M1 * a.C + 16.0 * 9 * a.M1 * a.M1 + 16.0 * a.C * a.M1;
+    p.tile_valu = 4.0 * (40.0 + 30.0 * (3 * a.M1 / 16 + a.M1 / 16 + a.C / 16) / 4.0);
+    p.tile_lds_bytes = 2.0 * 36 * a.C + 1024.0 * (3 * a.M1 / 16 * a.C / 64 + a.M1 / 16 * 9 * a.M1 / 64 +
+                                                  a.C / 16 * a.M1 / 64);
+    p.tile_load_bytes = 36.0 * a.C + 48.0 * a.M1 * a.C / 16 + 9.0 * a.M1 * a.M1 + (double)a.C * a.M1;
+    p.tile_store_bytes = 16.0 * a.C;
+    p.hbm_bytes = 2.0 * a.N * a.H * a.W * a.C + (double)a.M1 * a.C * 2 + 9.0 * a.M1 * a.M1 +
+                  4.0 * 2 * (2 * a.M1 + a.C);
+    plans_add(p);
+  }
+  hipLaunchKernelGGL(qb_stream_kernel, dim3(grid), dim3(256), 0, s, a.x, a.w1, a.w2, a.w3, a.m1,
+                     a.s1, a.m2, a.s2, a.m3, a.s3, a.out, a.H, a.W, a.C, a.M1, tiles_w, tiles_img,
+                     ntiles);
+  return hipGetLastError();
+}
+
+bool qb_tuned(int C, int M1) {
+  return (C == 256 && M1 == 64) || (C == 128 && M1 == 64) || (C == 64 && M1 == 64);
+}
+
 }  // namespace
 
 bool qbottleneck_supported(int C, int M1) {
-  return (C == 256 && M1 == 64) || (C == 128 && M1 == 64) || (C == 64 && M1 == 64);
+  return qb_tuned(C, M1) || (C >= 64 && C % 64 == 0 && C <= 2048 && M1 >= 64 && M1 % 64 == 0 && M1 <= 512);
 }
 
 hipError_t launch_qbottleneck_i8(const QBottleneckArgs &a, hipStream_t s) {
   if (a.C == 256 && a.M1 == 64) return launch_qb<256, 64>(a, s);
   if (a.C == 128 && a.M1 == 64) return launch_qb<128, 64>(a, s);
   if (a.C == 64 && a.M1 == 64) return launch_qb<64, 64>(a, s);
-  return hipErrorInvalidValue;
+  if (!qbottleneck_supported(a.C, a.M1)) return hipErrorInvalidValue;
+  return launch_qb_stream(a, s);
 }
 
 }  // namespace npu

@@ -102,6 +102,22 @@ def test_irb_channel_limits():
         assert call(ch, e) == 2 and "multiple of 4 in [4, 320]" in _err(), (ch, e, _err())
 
 
+def test_qbottleneck_channel_limits():
+    """fused_qbottleneck_i8 takes C % 64 == 0 up to 2048 and M1 % 64 == 0 up
+    to 512; other counts are refused by name before any launch."""
+    from npu_amd.memref import I32
+    lib = npu_amd.lib()
+
+    def call(ch, m1):
+        ms = [_mr([1, 4, 4, ch], I8), _mr([m1, ch], I8), _mr([m1, 3, 3, m1], I8), _mr([ch, m1], I8)]
+        ms += [_mr([m1], I32), _mr([m1], I32), _mr([m1], I32), _mr([m1], I32), _mr([ch], I32),
+               _mr([ch], I32), _mr([1, 4, 4, ch], I8)]
+        return lib.fused_qbottleneck_i8(*[C.byref(m) for m in ms], None)
+
+    for ch, m1 in ((96, 64), (4096, 64), (256, 576), (256, 96)):
+        assert call(ch, m1) == 2 and "multiple of 64" in _err(), (ch, m1, _err())
+
+
 def test_conv_rejects_bad_descriptors():
     lib = npu_amd.lib()
     x, w, b, o = _mr([1, 8, 8, 16]), _mr([16, 3, 3, 16]), _mr([16]), _mr([1, 8, 8, 16])
@@ -143,9 +159,9 @@ def test_qbottleneck_rejects_bad_descriptors():
     assert call(x, w1, _mr([64, 3, 3, 32], I8), w3, *q, o) == 1 and "w2" in _err()
     assert call(x, w1, w2, w3, *q[:4], _mr([64], I32), q[5], o) == 1 and "m3" in _err()
     assert call(x, w1, w2, w3, _mr([64], F32), *q[1:], o) == 1 and "dtype" in _err()
-    xx, ww1 = _mr([1, 8, 8, 192], I8), _mr([64, 192], I8)
-    assert call(xx, ww1, w2, _mr([192, 64], I8), *q[:4], _mr([192], I32), _mr([192], I32),
-                _mr([1, 8, 8, 192], I8)) == 2 and "no kernel instance" in _err()
+    xx, ww1 = _mr([1, 8, 8, 160], I8), _mr([64, 160], I8)
+    assert call(xx, ww1, w2, _mr([160, 64], I8), *q[:4], _mr([160], I32), _mr([160], I32),
+                _mr([1, 8, 8, 160], I8)) == 2 and "multiple of 64" in _err()
 
 
 C_TEST = os.path.join(ROOT, "tests", "c", "group_launch_test")

@@ -415,6 +415,38 @@ def test_c4_requant_wide_products(cuda):
     assert np.array_equal(_qb_run(inp), ref)
 
 
+def _qb_wide_inputs(N, H, W, C, M1, seed):
+    """Inputs for wide channel counts: each stage's shift set from its
+    reduction length K so that requantized values land mid-range (an
+    accumulator's spread grows as sqrt(K)), not all clamped."""
+    inp = _qb_inputs(N, H, W, C, M1, seed)
+    for i, (k, n, K) in enumerate((("1", M1, C), ("2", M1, 9 * M1), ("3", C, M1))):
+        base = int(round(24.5 + math.log2(5329.0 * math.sqrt(K))))
+        inp["s" + k] = rng.randint(seed, 20 + i, (n,), base - 1, base + 1).astype(np.int32)
+    return inp
+
+
+@pytest.mark.parametrize("N,H,W,C,M1", [
+    (1, 9, 10, 512, 128),    # ResNet-50's later bottlenecks
+    (1, 7, 7, 1024, 256),
+    (1, 7, 7, 2048, 512),
+    (2, 6, 13, 192, 64),     # C off the tuned instances
+    (3, 11, 5, 128, 128),
+    (8, 20, 20, 64, 192),    # more tiles than resident workgroups
+])
+def test_c4_qbottleneck_any_channels(cuda, N, H, W, C, M1):
+    """(C, M1) outside the tuned instances run on the kernel that reads its
+    filter blocks from L2 where they are used: bit for bit against the
+    oracle, with most requantized values off the clamp bounds."""
+    inp = _qb_wide_inputs(N, H, W, C, M1, 90 + C // 64)
+    print(f"qbottleneck stream {N}x{H}x{W}x{C}/{M1}", flush=True)
+    ref = oracle.block_qbottleneck(**inp)
+    got = _qb_run(inp)
+    assert np.array_equal(got, ref)
+    inner = ((ref > 0) & (ref < 127)).mean()
+    assert inner > 0.2, f"only {inner:.0%} of the outputs off the clamp bounds"
+
+
 # ------------------------------------------------------------------ C3
 def test_c3_irb_config_n1(cuda):
     w = configs.irb(1)

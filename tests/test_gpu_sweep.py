@@ -26,7 +26,7 @@ import refs
 import npu_amd
 from npu_amd import blocks, configs, groups, lower, mlir, tileplan
 from npu_amd import inputs as rng
-from test_gpu_parity import _dev, _host, _qb_inputs, _qb_run, _widened_conv
+from test_gpu_parity import _dev, _host, _qb_inputs, _qb_run, _qb_wide_inputs, _widened_conv
 from tolerance import RTOL_BF16, RTOL_F32, bf16, check_bf16_rounded, check_bound
 
 pytestmark = pytest.mark.gpu
@@ -79,6 +79,17 @@ def _qb_cases(n=6, seed=2029):
     r = random.Random(seed)
     return [(r.randint(1, 3), r.randint(1, 20), r.randint(1, 20), r.choice((64, 128, 256)))
             for _ in range(n)]
+
+
+def _qb_wide_cases(n=6, seed=2035):
+    """(C, M1) off the tuned instances: multiples of 64 up to 640 and 256."""
+    r = random.Random(seed)
+    cases = []
+    while len(cases) < n:
+        c, m1 = 64 * r.randint(1, 10), 64 * r.randint(1, 4)
+        if (c, m1) not in ((256, 64), (128, 64), (64, 64)):
+            cases.append((r.randint(1, 3), r.randint(1, 16), r.randint(1, 16), c, m1))
+    return cases
 
 
 def _planned_cases(n=8, seed=2031):
@@ -162,6 +173,13 @@ def test_sweep_int8_bottleneck(cuda, N, H, W, C):
     inp = _qb_inputs(N, H, W, C, 64, 800 + N * H + W + C)
     ref = oracle.block_qbottleneck(**inp)
     assert np.array_equal(_qb_run(inp), ref), f"int8 bottleneck {N}x{H}x{W}x{C}"
+
+
+@pytest.mark.parametrize("N,H,W,C,M1", _qb_wide_cases())
+def test_sweep_int8_bottleneck_wide(cuda, N, H, W, C, M1):
+    inp = _qb_wide_inputs(N, H, W, C, M1, 850 + N * H + W + C + M1)
+    ref = oracle.block_qbottleneck(**inp)
+    assert np.array_equal(_qb_run(inp), ref), f"int8 bottleneck {N}x{H}x{W}x{C}/{M1}"
 
 
 @pytest.mark.parametrize("S,H,F", _llama_cases())
