@@ -209,22 +209,23 @@ npu_status fused_irb_f32(const npu_memref *x, const npu_memref *we,
  * elementwise math; bf16 rounding at each group output and at the
  * normalised matmul inputs).  The reference's llama_attention.mlir:5-67
  * replaces softmax by ReLU and has no RMSNorm, RoPE or gating; these groups
- * implement the real layer.  Row-major [S, D] activations, D = H * 64,
- * weights [K, N] as linalg.matmul takes them.  The matmul groups require
- * S % 32 == 0, K % 64 == 0 and N % 64 == 0.
+ * implement the real layer.  Row-major [S, D] activations, D = H * Dh with
+ * head dim Dh = 64 or 128, weights [K, N] as linalg.matmul takes them.  The
+ * matmul groups require S % 32 == 0, K % 64 == 0 and N % 64 == 0.
  *
  * QKV: xn = bf16(rmsnorm(x) * g1) with inv = 1/sqrt(mean(x^2) + eps);
  *      Q = bf16(rope(xn @ wq)), K = bf16(rope(xn @ wk)), V = bf16(xn @ wv).
- *      RoPE rotates interleaved pairs (2t, 2t+1) of each 64-wide head by the
- *      tables cos_t / sin_t f32 [S, 32]. */
+ *      RoPE rotates interleaved pairs (2t, 2t+1) of each Dh-wide head by the
+ *      tables cos_t / sin_t f32 [S, Dh / 2] (their width gives Dh). */
 npu_status fused_llama_qkv_rope(const npu_memref *x, const npu_memref *g1,
                                 const npu_memref *wq, const npu_memref *wk,
                                 const npu_memref *wv, const npu_memref *cos_t,
                                 const npu_memref *sin_t, const npu_memref *Q,
                                 const npu_memref *K, const npu_memref *V,
                                 float eps, npu_stream stream);
-/* Causal attention per head (head dim 64): A = bf16(softmax(Q K^T * scale
- * with keys j <= i) @ V).  Q, K, V, A bf16 [S, H*64]. */
+/* Causal attention per head (head dim Dh = D / n_heads, 64 or 128):
+ * A = bf16(softmax(Q K^T * scale with keys j <= i) @ V).  Q, K, V, A bf16
+ * [S, D]. */
 npu_status fused_llama_attention(const npu_memref *Q, const npu_memref *K,
                                  const npu_memref *V, const npu_memref *A,
                                  int32_t n_heads, float scale,

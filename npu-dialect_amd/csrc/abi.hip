@@ -660,8 +660,17 @@ npu_status fused_llama_qkv_rope(const npu_memref *x, const npu_memref *g1, const
   NPU_TRY(check_2d(wq, "wq", NPU_BF16, D, D, &pq));
   NPU_TRY(check_2d(wk, "wk", NPU_BF16, D, D, &pk));
   NPU_TRY(check_2d(wv, "wv", NPU_BF16, D, D, &pv));
-  NPU_TRY(check_2d(cos_t, "cos_t", NPU_F32, S, 32, &pc));
-  NPU_TRY(check_2d(sin_t, "sin_t", NPU_F32, S, 32, &ps));
+  // the head dim is twice the RoPE tables' width: 64 or 128
+  NPU_TRY(check_memref(cos_t, "cos_t", 2, NPU_F32, &pc));
+  const int64_t half = cos_t->sizes[1];
+  if (half != 32 && half != 64)
+    return fail(NPU_ERR_UNSUPPORTED, "cos_t: %lld columns, expected 32 or 64 (head dim 64 or 128)",
+                (long long)half);
+  if (D % (2 * half) != 0)
+    return fail(NPU_ERR_INVALID_ARG, "D = %lld is not a multiple of the head dim %lld",
+                (long long)D, (long long)(2 * half));
+  NPU_TRY(check_2d(cos_t, "cos_t", NPU_F32, S, half, &pc));
+  NPU_TRY(check_2d(sin_t, "sin_t", NPU_F32, S, half, &ps));
   NPU_TRY(check_2d(Q, "Q", NPU_BF16, S, D, &oq));
   NPU_TRY(check_2d(K, "K", NPU_BF16, S, D, &ok));
   NPU_TRY(check_2d(V, "V", NPU_BF16, S, D, &ov));
@@ -673,7 +682,7 @@ npu_status fused_llama_qkv_rope(const npu_memref *x, const npu_memref *g1, const
   a.eps = eps;
   a.B[0] = u16(pq); a.B[1] = u16(pk); a.B[2] = u16(pv);
   a.nparts = 3;
-  a.M = (int)S; a.K = (int)D; a.Npart = (int)D; a.Dh = 64;
+  a.M = (int)S; a.K = (int)D; a.Npart = (int)D; a.Dh = (int)(2 * half);
   a.cos_t = static_cast<const float *>(pc);
   a.sin_t = static_cast<const float *>(ps);
   a.out[0] = u16w(oq); a.out[1] = u16w(ok); a.out[2] = u16w(ov);
@@ -689,15 +698,16 @@ npu_status fused_llama_attention(const npu_memref *Q, const npu_memref *K, const
   const void *pq, *pk, *pv, *pa;
   NPU_TRY(check_memref(Q, "Q", 2, NPU_BF16, &pq));
   const int64_t S = Q->sizes[0], D = Q->sizes[1];
-  if (n_heads <= 0 || D != (int64_t)n_heads * 64)
-    return fail(NPU_ERR_UNSUPPORTED, "D = %lld must equal n_heads * 64 (n_heads = %d)",
+  if (n_heads <= 0 || D % n_heads != 0 || (D / n_heads != 64 && D / n_heads != 128))
+    return fail(NPU_ERR_UNSUPPORTED, "D = %lld must be n_heads * 64 or n_heads * 128 (n_heads = %d)",
                 (long long)D, n_heads);
+  const int dh = (int)(D / n_heads);
   NPU_TRY(check_2d(K, "K", NPU_BF16, S, D, &pk));
   NPU_TRY(check_2d(V, "V", NPU_BF16, S, D, &pv));
   NPU_TRY(check_2d(A, "A", NPU_BF16, S, D, &pa));
   if (!(scale > 0.0f)) return fail(NPU_ERR_INVALID_ARG, "scale must be positive");
   return hip_status(npu::launch_llama_attention(u16(pq), u16(pk), u16(pv), u16w(pa), (int)S,
-                                                n_heads, scale, static_cast<hipStream_t>(stream)),
+                                                n_heads, dh, scale, static_cast<hipStream_t>(stream)),
                     "fused_llama_attention launch");
 }
 

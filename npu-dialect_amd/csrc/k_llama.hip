@@ -426,8 +426,16 @@ __global__ __launch_bounds__(GT) void llama_gemm_kernel(const LlamaGemmArgs a, i
 // ---- attention ----------------------------------------------------------------
 constexpr int AQ = 16;    // queries per workgroup
 constexpr int AKB = 32;   // keys per block
-constexpr int VLD = 80;   // V block row stride in LDS (elements): 160 bytes
 constexpr int AWAVES = 4;
+// Per head dim DH (64 or 128): Q / K fragments per row (8 dh per lane group,
+// four groups), the V block's LDS row stride (DH + 16 elements: 32 mod 64
+// bytes), 16-byte V pieces per lane of a 32-key block, 16-wide output tiles.
+template <int DH>
+struct AttnShape {
+  static_assert(DH == 64 || DH == 128, "head dims 64 and 128");
+  static constexpr int NQF = DH / 32, VLD = DH + 16, PPR = DH / 8, NVR = AKB * PPR / 64,
+                       NDT = DH / 16;
+};
 
 // S^T tile (16 keys x 16 queries) of key tile t: lane holds keys 4g + r of the
 // tile (g = lane / 16), query lane % 16.  P^T's fragment for the 32-key
@@ -435,6 +443,7 @@ constexpr int AWAVES = 4;
 // V^T's fragment must list the same keys, which the transposing read gives
 // when lane (g, j, a) addresses V row (16 h + 4 g + j), columns 4a .. 4a+3
 // of the dh tile, for halves h = 0, 1.
+template <int VLD>
 __device__ __forceinline__ Frag16 read_vfrag(const uint16_t *vs, int dtile, int lane) {
   const int g = lane >> 4, j = (lane >> 2) & 3, a = lane & 3;
   const uint16_t *p0 = vs + (4 * g + j) * VLD + dtile * 16 + 4 * a;
@@ -445,53 +454,56 @@ __device__ __forceinline__ Frag16 read_vfrag(const uint16_t *vs, int dtile, int 
   return f;
 }
 
+template <int DH>
 __global__ __launch_bounds__(256) void llama_attention_kernel(const uint16_t *__restrict__ Q,
                                                               const uint16_t *__restrict__ Kg,
                                                               const uint16_t *__restrict__ V,
                                                               uint16_t *__restrict__ O, int S,
                                                               int H, float scale) {
+  using Sh = AttnShape<DH>;
+  constexpr int NQF = Sh::NQF, VLD = Sh::VLD, PPR = Sh::PPR, NVR = Sh::NVR, NDT = Sh::NDT;
   __shared__ __attribute__((aligned(16))) uint16_t vbuf[AWAVES][2][AKB * VLD];
   __shared__ float st_m[AWAVES][AQ], st_l[AWAVES][AQ];
-  __shared__ float st_o[AWAVES][64][AQ + 1];
+  __shared__ float st_o[AWAVES][DH][AQ + 1];
   const int nqb = S / AQ, G = nqb * H, per = (G + 7) / 8;
   const int t = (blockIdx.x % 8) * per + blockIdx.x / 8;
   if (t >= G) return;
   const int h = t / nqb, qb = t % nqb;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int g = lane >> 4, ql = lane & 15;
-  const int D = H * 64;
+  const int D = H * DH;
   const int q0 = qb * AQ;
   const int nkb = (q0 + AQ + AKB - 1) / AKB;  // key blocks 0 .. nkb-1 hold keys <= q0 + 15
   const float kscale = scale * 1.4426950408889634f;  // exp(x * scale) = exp2(x * kscale)
 
-  // Q^T fragments (B operand): query ql, dh 8g .. +8 and 32 + 8g .. +8
-  Frag16 qf[2];
+  // Q^T fragments (B operand): query ql, dh 32 k + 8g .. +8
+  Frag16 qf[NQF];
   {
-    const uint16_t *qp = Q + (size_t)(q0 + ql) * D + h * 64 + 8 * g;
-    qf[0] = load16(qp);
-    qf[1] = load16(qp + 32);
+    const uint16_t *qp = Q + (size_t)(q0 + ql) * D + h * DH + 8 * g;
+#pragma unroll
+    for (int k = 0; k < NQF; ++k) qf[k] = load16(qp + 32 * k);
   }
   float m_run = -__builtin_inff(), l_run = 0.0f;
-  f32x4 o[4];
+  f32x4 o[NDT];
 #pragma unroll
-  for (int d = 0; d < 4; ++d) o[d] = f32x4{0.f, 0.f, 0.f, 0.f};
+  for (int d = 0; d < NDT; ++d) o[d] = f32x4{0.f, 0.f, 0.f, 0.f};
 
   // block kb = wave, wave + 4, ...: K fragments (A operand: key 16 t + (lane % 16),
-  // dh 8g .. +8 and +32) and the V block (32 keys x 64 dh, 4 x 16 bytes per lane)
-  Frag16 kf[2][2];
-  u32x4 vr[4];
+  // dh 32 k + 8g .. +8) and the V block (32 keys x DH, NVR x 16 bytes per lane)
+  Frag16 kf[2][NQF];
+  u32x4 vr[NVR];
   auto fetch = [&](int kb) {
     const int k0 = min(kb, nkb - 1) * AKB;
 #pragma unroll
     for (int tt = 0; tt < 2; ++tt) {
-      const uint16_t *kp = Kg + (size_t)(k0 + 16 * tt + ql) * D + h * 64 + 8 * g;
-      kf[tt][0] = load16(kp);
-      kf[tt][1] = load16(kp + 32);
+      const uint16_t *kp = Kg + (size_t)(k0 + 16 * tt + ql) * D + h * DH + 8 * g;
+#pragma unroll
+      for (int k = 0; k < NQF; ++k) kf[tt][k] = load16(kp + 32 * k);
     }
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int item = lane + 64 * i;  // 256 pieces: key item / 8, dh 8 (item % 8)
-      vr[i] = *reinterpret_cast<const u32x4 *>(V + (size_t)(k0 + item / 8) * D + h * 64 + (item % 8) * 8);
+    for (int i = 0; i < NVR; ++i) {
+      const int item = lane + 64 * i;  // AKB * PPR pieces: key item / PPR, dh 8 (item % PPR)
+      vr[i] = *reinterpret_cast<const u32x4 *>(V + (size_t)(k0 + item / PPR) * D + h * DH + (item % PPR) * 8);
     }
   };
   int buf = 0;
@@ -499,18 +511,24 @@ __global__ __launch_bounds__(256) void llama_attention_kernel(const uint16_t *__
   for (int kb = wave; kb < nkb; kb += AWAVES) {
     uint16_t *vs = vbuf[wave][buf];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
+    for (int i = 0; i < NVR; ++i) {
       const int item = lane + 64 * i;
-      *reinterpret_cast<u32x4 *>(vs + (item / 8) * VLD + (item % 8) * 8) = vr[i];
+      *reinterpret_cast<u32x4 *>(vs + (item / PPR) * VLD + (item % PPR) * 8) = vr[i];
     }
-    Frag16 kc[2][2] = {{kf[0][0], kf[0][1]}, {kf[1][0], kf[1][1]}};
+    Frag16 kc[2][NQF];
+#pragma unroll
+    for (int tt = 0; tt < 2; ++tt)
+#pragma unroll
+      for (int k = 0; k < NQF; ++k) kc[tt][k] = kf[tt][k];
     if (kb + AWAVES < nkb) fetch(kb + AWAVES);
     // S^T = K Q^T: two 16-key tiles
     f32x4 s[2];
 #pragma unroll
     for (int tt = 0; tt < 2; ++tt) {
       s[tt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kc[tt][0].h, qf[0].h, f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
-      s[tt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kc[tt][1].h, qf[1].h, s[tt], 0, 0, 0);
+#pragma unroll
+      for (int k = 1; k < NQF; ++k)
+        s[tt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kc[tt][k].h, qf[k].h, s[tt], 0, 0, 0);
     }
     // causal mask on the block that reaches the diagonal: key > query
     const int k0 = kb * AKB, q = q0 + ql;
@@ -544,15 +562,15 @@ __global__ __launch_bounds__(256) void llama_attention_kernel(const uint16_t *__
     l_run = l_run * alpha + psum;
     m_run = m_new;
 #pragma unroll
-    for (int d = 0; d < 4; ++d) o[d] *= alpha;
+    for (int d = 0; d < NDT; ++d) o[d] *= alpha;
     Frag16 pf;  // P^T, k slots: keys 4g + r (tile 0), 16 + 4g + r (tile 1)
     pf.u = u32x4{cvt_pk_bf16(p[0][0], p[0][1]), cvt_pk_bf16(p[0][2], p[0][3]),
                  cvt_pk_bf16(p[1][0], p[1][1]), cvt_pk_bf16(p[1][2], p[1][3])};
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
 #pragma unroll
-    for (int d = 0; d < 4; ++d) {
-      const Frag16 vf = read_vfrag(vs, d, lane);
+    for (int d = 0; d < NDT; ++d) {
+      const Frag16 vf = read_vfrag<VLD>(vs, d, lane);
       o[d] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vf.h, pf.h, o[d], 0, 0, 0);
     }
     buf ^= 1;
@@ -569,13 +587,14 @@ __global__ __launch_bounds__(256) void llama_attention_kernel(const uint16_t *__
     st_l[wave][ql] = l_run;
   }
 #pragma unroll
-  for (int d = 0; d < 4; ++d)
+  for (int d = 0; d < NDT; ++d)
 #pragma unroll
     for (int r = 0; r < 4; ++r) st_o[wave][16 * d + 4 * g + r][ql] = o[d][r];
   __syncthreads();
-  // merge: thread -> query tid / 16, dh 4 (tid % 16) .. +3
-  {
-    const int qq = tid >> 4, d0 = 4 * (tid & 15);
+  // merge: thread -> query tid / 16, dh 64 pass + 4 (tid % 16) .. +3
+#pragma unroll
+  for (int pass = 0; pass < DH / 64; ++pass) {
+    const int qq = tid >> 4, d0 = 64 * pass + 4 * (tid & 15);
     float mw[AWAVES], mmax = -__builtin_inff();
 #pragma unroll
     for (int w = 0; w < AWAVES; ++w) {
@@ -597,7 +616,7 @@ __global__ __launch_bounds__(256) void llama_attention_kernel(const uint16_t *__
       for (int w = 0; w < AWAVES; ++w) acc += st_o[w][d0 + e][qq] * f[w];
       out[e] = acc * invL;
     }
-    *reinterpret_cast<uint2 *>(O + (size_t)(q0 + qq) * D + h * 64 + d0) =
+    *reinterpret_cast<uint2 *>(O + (size_t)(q0 + qq) * D + h * DH + d0) =
         pack4_bf16(out[0], out[1], out[2], out[3]);
   }
 }
@@ -699,9 +718,10 @@ hipError_t launch_llama_gemm(const LlamaGemmArgs &a, int pro, int epi, hipStream
   return hipErrorInvalidValue;
 }
 
-hipError_t launch_llama_attention(const uint16_t *Q, const uint16_t *K, const uint16_t *V,
-                                  uint16_t *O, int S, int H, float scale, hipStream_t s) {
-  if (S % AKB != 0) return hipErrorInvalidValue;
+template <int DH>
+hipError_t launch_attention_dh(const uint16_t *Q, const uint16_t *K, const uint16_t *V,
+                               uint16_t *O, int S, int H, float scale, hipStream_t s) {
+  auto kern = llama_attention_kernel<DH>;
   const int G = (S / AQ) * H, grid = (G + 7) / 8 * 8;
   {
     // The longest workgroup is the last query block's: ceil(S / AKB / 4)
@@ -710,18 +730,26 @@ hipError_t launch_llama_attention(const uint16_t *Q, const uint16_t *K, const ui
     // instructions in the compiled code, 50 more on the diagonal block's
     // mask), one K and V block; 226 once (Q fetch, the merge and stores).
     const double kblocks = std::ceil(S / (double)AKB / AWAVES);
-    npu_launch_plan p = make_plan("llama_causal_attention", G, wg_per_cu(llama_attention_kernel, 256), G, 16);
+    npu_launch_plan p = make_plan("llama_causal_attention", G, wg_per_cu(kern, 256), G, 16);
     p.load_phases = 1;
-    p.tile_macs = kblocks * AWAVES * 2.0 * AQ * AKB * 64;
-    p.tile_valu = 4.0 * (226.0 + 139.0 * kblocks + 50.0);
-    p.tile_lds_bytes = kblocks * AWAVES * (2.0 * AKB * 64 * 2) + AWAVES * 64 * AQ * 4 * 2;
-    p.tile_load_bytes = kblocks * AWAVES * 2.0 * AKB * 64 * 2 + AQ * 64 * 2.0;
-    p.tile_store_bytes = AQ * 64 * 2.0;
-    p.hbm_bytes = 4.0 * S * H * 64 * 2;  // Q, K, V in, O out
+    p.tile_macs = kblocks * AWAVES * 2.0 * AQ * AKB * DH;
+    p.tile_valu = 4.0 * (226.0 + 139.0 * kblocks + 50.0) * (DH / 64);
+    p.tile_lds_bytes = kblocks * AWAVES * (2.0 * AKB * DH * 2) + AWAVES * DH * AQ * 4 * 2;
+    p.tile_load_bytes = kblocks * AWAVES * 2.0 * AKB * DH * 2 + AQ * DH * 2.0;
+    p.tile_store_bytes = AQ * DH * 2.0;
+    p.hbm_bytes = 4.0 * S * H * DH * 2;  // Q, K, V in, O out
     plans_add(p);
   }
-  hipLaunchKernelGGL(llama_attention_kernel, dim3(grid), dim3(256), 0, s, Q, K, V, O, S, H, scale);
+  hipLaunchKernelGGL(kern, dim3(grid), dim3(256), 0, s, Q, K, V, O, S, H, scale);
   return hipGetLastError();
+}
+
+hipError_t launch_llama_attention(const uint16_t *Q, const uint16_t *K, const uint16_t *V,
+                                  uint16_t *O, int S, int H, int dh, float scale, hipStream_t s) {
+  if (S % AKB != 0) return hipErrorInvalidValue;
+  if (dh == 64) return launch_attention_dh<64>(Q, K, V, O, S, H, scale, s);
+  if (dh == 128) return launch_attention_dh<128>(Q, K, V, O, S, H, scale, s);
+  return hipErrorInvalidValue;
 }
 
 }  // namespace npu

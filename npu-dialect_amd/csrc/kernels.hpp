@@ -91,6 +91,6 @@ struct LlamaGemmArgs {
 };
 hipError_t launch_llama_gemm(const LlamaGemmArgs &a, int pro, int epi, hipStream_t s);
 hipError_t launch_llama_attention(const uint16_t *Q, const uint16_t *K, const uint16_t *V,
-                                  uint16_t *O, int S, int H, float scale, hipStream_t s);
+                                  uint16_t *O, int S, int H, int dh, float scale, hipStream_t s);
 
 }  // namespace npu

@@ -296,8 +296,8 @@ def _attention(fn, a):
     Q, qops = _heads(fn, qh, [1, 0, 2])
     K, kops = _heads(fn, kt, [1, 2, 0])
     V, vops = _heads(fn, vh, [1, 0, 2])
-    if Dh != 64 or fn.ty(s).shape != [H, S, S]:
-        _fail(s, f"attention over heads of {Dh} (the entry point's head dimension is 64)")
+    if Dh not in (64, 128) or fn.ty(s).shape != [H, S, S]:
+        _fail(s, f"attention over heads of {Dh} (the entry point's head dimensions are 64 and 128)")
     ops = qops + kops + vops + [fn.op(qk.outs[0]), qk, gs, fn.op(gm.outs[0]), gm, gx,
                                 fn.op(gl.outs[0]), gl, gp, fn.op(pv.outs[0]), pv, tr, col, tg]
     return {"entry": "fused_llama_attention", "ops": ops, "args": [Q, K, V], "outs": [a],

@@ -577,6 +577,35 @@ def test_c5_stage_attention(cuda, llama_case):
     assert np.array_equal(_host(A)[0], st["V"][0])
 
 
+def test_c5_stages_heads_of_128(cuda):
+    """Heads of 128 (RoPE tables [S, 64], four heads of a 512-wide model):
+    the QKV + RoPE and attention stages against the oracle's stage values
+    under the same bounds as the 64-wide heads."""
+    H = 4
+    w = configs.llama_layer(S=256, D=512, H=H, F=384, seed=131)
+    inp = w.make_inputs()
+    assert inp["cos_t"].shape == (256, 64)
+    st = refs.llama_stages(inp, H, LL_EPS)
+    ex = refs.llama_stage_exact(inp, st, H, LL_EPS)
+    d = configs.to_device(inp)
+    S, D = inp["x"].shape
+    Q, K, V = _bf_dev((S, D)), _bf_dev((S, D)), _bf_dev((S, D))
+    groups.fused_llama_qkv_rope(d["x"], d["g1"], d["wq"], d["wk"], d["wv"], d["cos_t"],
+                                d["sin_t"], Q, K, V, LL_EPS)
+    torch.cuda.synchronize()
+    xn = refs.normed_bf16(inp["x"], inp["g1"], LL_EPS)
+    for name, t, wname, rope in (("Q", Q, "wq", True), ("K", K, "wk", True), ("V", V, "wv", False)):
+        mag = refs.mag_qkv(xn, inp[wname], inp["cos_t"], inp["sin_t"], rope)
+        check_bf16_stage(_host(t), ex[name], mag, D + 2, what=f"{name} (heads of 128)")
+    dq = configs.to_device({k: st[k] for k in ("Q", "K", "V")})
+    A = _bf_dev((S, D))
+    groups.fused_llama_attention(dq["Q"], dq["K"], dq["V"], A, H, 128 ** -0.5)
+    torch.cuda.synchronize()
+    mag = refs.mag_attention(st["Q"], st["K"], st["V"], H)
+    check_bf16_stage(_host(A), ex["A"], mag, S + D // H, what="attention (heads of 128)")
+    assert np.array_equal(_host(A)[0], st["V"][0])
+
+
 def test_c5_stage_oproj_residual(cuda, llama_case):
     w, inp, st = llama_case
     d = configs.to_device({"A": st["A"], "wo": inp["wo"], "x": inp["x"]})
@@ -627,7 +656,9 @@ def test_c5_layer_end_to_end(cuda, llama_case):
 # buffers.
 @pytest.mark.parametrize("S,D,H,F", [(64, 128, 2, 192), (128, 64, 1, 64), (96, 128, 2, 128),
                                      (1088, 128, 2, 128), (64, 448, 7, 128), (64, 576, 9, 192),
-                                     (64, 128, 2, 1088), (32, 128, 2, 1600)])
+                                     (64, 128, 2, 1088), (32, 128, 2, 1600),
+                                     # heads of 128 (the head dim is D / H)
+                                     (64, 256, 2, 192), (96, 128, 1, 128), (256, 512, 4, 384)])
 def test_c5_layer_small_shapes(cuda, S, D, H, F):
     w = configs.llama_layer(S=S, D=D, H=H, F=F, seed=91 + S)
     inp = w.make_inputs()
@@ -1116,7 +1147,7 @@ def _llama_text_inputs(inp):
     return d
 
 
-@pytest.mark.parametrize("S,D,H,F", [(64, 128, 2, 192), (256, 512, 8, 1408)])
+@pytest.mark.parametrize("S,D,H,F", [(64, 128, 2, 192), (256, 512, 8, 1408), (64, 256, 2, 192)])
 def test_lowered_llama_layer_matches_the_oracle(cuda, S, D, H, F):
     """The Llama layer's linalg text through the lowering: five calls of the
     Llama entry points, bit-identical to calling them directly, and within

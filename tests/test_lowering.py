@@ -353,6 +353,11 @@ def test_llama_views_and_head_size_are_checked():
     bad = t.replace("permutation = [1, 2, 0]", "permutation = [1, 0, 2]", 1)
     with pytest.raises(NotImplementedError):
         lower.lower_text(bad)
-    # heads of 32: the attention entry point's head dimension is 64
-    with pytest.raises(NotImplementedError, match="head dimension is 64"):
+    # heads of 32: the attention entry point's head dimensions are 64 and 128
+    with pytest.raises(NotImplementedError, match="head dimensions are 64 and 128"):
         lower.lower_text(blocks.llama_layer(64, 128, 4, 192, dh=32))
+    # heads of 128 lower to the same five calls
+    prog = lower.lower_text(blocks.llama_layer(64, 256, 2, 192, dh=128))
+    assert prog.entry_points == ["fused_llama_qkv_rope", "fused_llama_attention",
+                                 "fused_llama_matmul_residual", "fused_llama_rmsnorm_swiglu",
+                                 "fused_llama_matmul_residual"]
