@@ -210,8 +210,8 @@ npu_status fused_irb_f32(const npu_memref *x, const npu_memref *we,
  * normalised matmul inputs).  The reference's llama_attention.mlir:5-67
  * replaces softmax by ReLU and has no RMSNorm, RoPE or gating; these groups
  * implement the real layer.  Row-major [S, D] activations, D = H * Dh with
- * head dim Dh = 64 or 128, weights [K, N] as linalg.matmul takes them.  The
- * matmul groups require S % 32 == 0, K % 64 == 0 and N % 64 == 0.
+ * head dim Dh = 64 or 128, weights [K, N] as linalg.matmul takes them.  Any
+ * sequence length S; the matmul groups require K % 64 == 0 and N % 64 == 0.
  *
  * QKV: xn = bf16(rmsnorm(x) * g1) with inv = 1/sqrt(mean(x^2) + eps);
  *      Q = bf16(rope(xn @ wq)), K = bf16(rope(xn @ wk)), V = bf16(xn @ wv).

@@ -465,7 +465,7 @@ __global__ __launch_bounds__(256) void llama_attention_kernel(const uint16_t *__
   __shared__ __attribute__((aligned(16))) uint16_t vbuf[AWAVES][2][AKB * VLD];
   __shared__ float st_m[AWAVES][AQ], st_l[AWAVES][AQ];
   __shared__ float st_o[AWAVES][DH][AQ + 1];
-  const int nqb = S / AQ, G = nqb * H, per = (G + 7) / 8;
+  const int nqb = (S + AQ - 1) / AQ, G = nqb * H, per = (G + 7) / 8;
   const int t = (blockIdx.x % 8) * per + blockIdx.x / 8;
   if (t >= G) return;
   const int h = t / nqb, qb = t % nqb;
@@ -476,10 +476,14 @@ __global__ __launch_bounds__(256) void llama_attention_kernel(const uint16_t *__
   const int nkb = (q0 + AQ + AKB - 1) / AKB;  // key blocks 0 .. nkb-1 hold keys <= q0 + 15
   const float kscale = scale * 1.4426950408889634f;  // exp(x * scale) = exp2(x * kscale)
 
+  // Rows past S (the last query or key block of a sequence that is not a
+  // multiple of 16 or 32) are read from row S - 1: such keys lie above the
+  // diagonal of every query that is stored, so the causal mask removes them,
+  // and such queries are not stored.
   // Q^T fragments (B operand): query ql, dh 32 k + 8g .. +8
   Frag16 qf[NQF];
   {
-    const uint16_t *qp = Q + (size_t)(q0 + ql) * D + h * DH + 8 * g;
+    const uint16_t *qp = Q + (size_t)min(q0 + ql, S - 1) * D + h * DH + 8 * g;
 #pragma unroll
     for (int k = 0; k < NQF; ++k) qf[k] = load16(qp + 32 * k);
   }
@@ -496,14 +500,15 @@ __global__ __launch_bounds__(256) void llama_attention_kernel(const uint16_t *__
     const int k0 = min(kb, nkb - 1) * AKB;
 #pragma unroll
     for (int tt = 0; tt < 2; ++tt) {
-      const uint16_t *kp = Kg + (size_t)(k0 + 16 * tt + ql) * D + h * DH + 8 * g;
+      const uint16_t *kp = Kg + (size_t)min(k0 + 16 * tt + ql, S - 1) * D + h * DH + 8 * g;
 #pragma unroll
       for (int k = 0; k < NQF; ++k) kf[tt][k] = load16(kp + 32 * k);
     }
 #pragma unroll
     for (int i = 0; i < NVR; ++i) {
       const int item = lane + 64 * i;  // AKB * PPR pieces: key item / PPR, dh 8 (item % PPR)
-      vr[i] = *reinterpret_cast<const u32x4 *>(V + (size_t)(k0 + item / PPR) * D + h * DH + (item % PPR) * 8);
+      vr[i] = *reinterpret_cast<const u32x4 *>(V + (size_t)min(k0 + item / PPR, S - 1) * D + h * DH +
+                                               (item % PPR) * 8);
     }
   };
   int buf = 0;
@@ -616,8 +621,9 @@ __global__ __launch_bounds__(256) void llama_attention_kernel(const uint16_t *__
       for (int w = 0; w < AWAVES; ++w) acc += st_o[w][d0 + e][qq] * f[w];
       out[e] = acc * invL;
     }
-    *reinterpret_cast<uint2 *>(O + (size_t)(q0 + qq) * D + h * DH + d0) =
-        pack4_bf16(out[0], out[1], out[2], out[3]);
+    if (q0 + qq < S)
+      *reinterpret_cast<uint2 *>(O + (size_t)(q0 + qq) * D + h * DH + d0) =
+          pack4_bf16(out[0], out[1], out[2], out[3]);
   }
 }
 
@@ -722,7 +728,7 @@ template <int DH>
 hipError_t launch_attention_dh(const uint16_t *Q, const uint16_t *K, const uint16_t *V,
                                uint16_t *O, int S, int H, float scale, hipStream_t s) {
   auto kern = llama_attention_kernel<DH>;
-  const int G = (S / AQ) * H, grid = (G + 7) / 8 * 8;
+  const int G = (S + AQ - 1) / AQ * H, grid = (G + 7) / 8 * 8;
   {
     // The longest workgroup is the last query block's: ceil(S / AKB / 4)
     // key blocks per wave.  Per key block and wave: 8 MFMAs (S^T and O^T),
@@ -746,7 +752,6 @@ hipError_t launch_attention_dh(const uint16_t *Q, const uint16_t *K, const uint1
 
 hipError_t launch_llama_attention(const uint16_t *Q, const uint16_t *K, const uint16_t *V,
                                   uint16_t *O, int S, int H, int dh, float scale, hipStream_t s) {
-  if (S % AKB != 0) return hipErrorInvalidValue;
   if (dh == 64) return launch_attention_dh<64>(Q, K, V, O, S, H, scale, s);
   if (dh == 128) return launch_attention_dh<128>(Q, K, V, O, S, H, scale, s);
   return hipErrorInvalidValue;

@@ -577,14 +577,15 @@ def test_c5_stage_attention(cuda, llama_case):
     assert np.array_equal(_host(A)[0], st["V"][0])
 
 
-def test_c5_stages_heads_of_128(cuda):
-    """Heads of 128 (RoPE tables [S, 64], four heads of a 512-wide model):
-    the QKV + RoPE and attention stages against the oracle's stage values
-    under the same bounds as the 64-wide heads."""
-    H = 4
-    w = configs.llama_layer(S=256, D=512, H=H, F=384, seed=131)
+@pytest.mark.parametrize("S,D,H", [(256, 512, 4), (100, 256, 2), (40, 128, 2), (1, 128, 2)])
+def test_c5_stages_other_shapes(cuda, S, D, H):
+    """Heads of 128 (RoPE tables [S, 64]) and sequence lengths off the
+    16-query and 32-key blocks, one token included: the QKV + RoPE and
+    attention stages against the oracle's stage values under the same
+    bounds as the configuration's."""
+    w = configs.llama_layer(S=S, D=D, H=H, F=128, seed=131 + S)
     inp = w.make_inputs()
-    assert inp["cos_t"].shape == (256, 64)
+    assert inp["cos_t"].shape == (S, D // H // 2)
     st = refs.llama_stages(inp, H, LL_EPS)
     ex = refs.llama_stage_exact(inp, st, H, LL_EPS)
     d = configs.to_device(inp)
@@ -596,13 +597,13 @@ def test_c5_stages_heads_of_128(cuda):
     xn = refs.normed_bf16(inp["x"], inp["g1"], LL_EPS)
     for name, t, wname, rope in (("Q", Q, "wq", True), ("K", K, "wk", True), ("V", V, "wv", False)):
         mag = refs.mag_qkv(xn, inp[wname], inp["cos_t"], inp["sin_t"], rope)
-        check_bf16_stage(_host(t), ex[name], mag, D + 2, what=f"{name} (heads of 128)")
+        check_bf16_stage(_host(t), ex[name], mag, D + 2, what=f"{name} S={S} dh={D // H}")
     dq = configs.to_device({k: st[k] for k in ("Q", "K", "V")})
     A = _bf_dev((S, D))
-    groups.fused_llama_attention(dq["Q"], dq["K"], dq["V"], A, H, 128 ** -0.5)
+    groups.fused_llama_attention(dq["Q"], dq["K"], dq["V"], A, H, (D // H) ** -0.5)
     torch.cuda.synchronize()
     mag = refs.mag_attention(st["Q"], st["K"], st["V"], H)
-    check_bf16_stage(_host(A), ex["A"], mag, S + D // H, what="attention (heads of 128)")
+    check_bf16_stage(_host(A), ex["A"], mag, S + D // H, what=f"attention S={S} dh={D // H}")
     assert np.array_equal(_host(A)[0], st["V"][0])
 
 
@@ -658,7 +659,10 @@ def test_c5_layer_end_to_end(cuda, llama_case):
                                      (1088, 128, 2, 128), (64, 448, 7, 128), (64, 576, 9, 192),
                                      (64, 128, 2, 1088), (32, 128, 2, 1600),
                                      # heads of 128 (the head dim is D / H)
-                                     (64, 256, 2, 192), (96, 128, 1, 128), (256, 512, 4, 384)])
+                                     (64, 256, 2, 192), (96, 128, 1, 128), (256, 512, 4, 384),
+                                     # sequence lengths off the 16- and 32-row blocks
+                                     (40, 128, 2, 192), (17, 64, 1, 64), (100, 256, 2, 128),
+                                     (1, 128, 2, 64)])
 def test_c5_layer_small_shapes(cuda, S, D, H, F):
     w = configs.llama_layer(S=S, D=D, H=H, F=F, seed=91 + S)
     inp = w.make_inputs()

@@ -113,8 +113,11 @@ def _lowered_cases(n=8, seed=2032):
 
 
 def _llama_cases(n=5, seed=2030):
+    """Sequence lengths in 32-row blocks, then as many of any length."""
     r = random.Random(seed)
-    return [(32 * r.randint(1, 8), r.randint(1, 4), 64 * r.randint(1, 24)) for _ in range(n)]
+    blocks_ = [(32 * r.randint(1, 8), r.randint(1, 4), 64 * r.randint(1, 24)) for _ in range(n)]
+    ragged = [(r.randint(1, 300), r.randint(1, 4), 64 * r.randint(1, 24)) for _ in range(n)]
+    return blocks_ + ragged
 
 
 @pytest.mark.parametrize("M,K,N,act,bias", _matmul_cases())
