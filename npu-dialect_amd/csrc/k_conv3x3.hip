@@ -37,10 +37,14 @@ namespace npu {
 
 namespace {
 
-template <class MM, typename T, int TR, int WF, int WMAX, int NCH, int NBUF>
+template <class MM, typename T, int TR, int WF, int WMAX, int NCH, int NBUF, int WFIX>
 __global__ __launch_bounds__(256) void conv3x3_rows_kernel(
     const T *__restrict__ x, const T *__restrict__ w, const float *__restrict__ bias,
-    T *__restrict__ out, int H, int W, int C, int F, int act) {
+    T *__restrict__ out, int H, int w_rt, int c_rt, int F, int act) {
+  // a row width of WFIX (> 0) and the single stage's channel count are
+  // compile-time, so the halo and output index arithmetic folds
+  const int W = WFIX > 0 ? WFIX : w_rt;
+  const int C = NBUF == 1 ? NCH * MM::kPerFrag : c_rt;
   constexpr int WP = 4 / WF;                  // waves along pixels
   constexpr int KPL = MM::kPerLane;           // elements of one lane's 16-byte run
   constexpr int KC = MM::kPerFrag;            // channels per chunk (64 bytes)
@@ -52,7 +56,14 @@ __global__ __launch_bounds__(256) void conv3x3_rows_kernel(
   constexpr int SEGS = (HR * (WMAX + 2) * SEGP + 255) / 256;
   static_assert(KC * sizeof(T) == 64, "a chunk is 64 bytes per pixel");
   static_assert(NBUF == 1 || NBUF == 2, "single or double buffered");
+  // One f32 stage of 64 channels: the workgroup's 16 filters (all four waves
+  // use the same ones) are loaded once, coalesced, into LDS rather than by
+  // every wave into registers; row stride 9 * 64 + 8 floats (32 mod 64
+  // bytes) keeps the 16 filters' fragment reads conflict-free.
+  constexpr bool WLDS = NBUF == 1 && WF == 1 && sizeof(T) == 4 && NCH == 4;
+  constexpr int WST = 9 * NCH * KC + 8;
   __shared__ __attribute__((aligned(16))) T halo[NBUF][HR * (WMAX + 2) * REC];
+  __shared__ __attribute__((aligned(16))) float wsm[WLDS ? 16 * WST : 4];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int r = lane & 15, q = lane >> 4;
@@ -124,7 +135,16 @@ __global__ __launch_bounds__(256) void conv3x3_rows_kernel(
   for (int i = 0; i < PBW; ++i) acc[i] = typename MM::acc_t{0, 0, 0, 0};
 
   fetch(0);
-  fetch_b(b, 0);
+  if constexpr (WLDS) {
+    const int f0 = blockIdx.y * 16;
+    for (int idx = tid; idx < 16 * 9 * C / 4; idx += 256) {
+      const int fl = idx / (9 * C / 4), e = idx - fl * (9 * C / 4);
+      *reinterpret_cast<u32x4 *>(wsm + fl * WST + 4 * e) =
+          *reinterpret_cast<const u32x4 *>(w + (size_t)min(f0 + fl, F - 1) * 9 * C + 4 * e);
+    }
+  } else {
+    fetch_b(b, 0);
+  }
   commit(0);
   __syncthreads();
   const int nstages = C / (KC * NCH);  // 1 when NBUF == 1 (checked by the launcher)
@@ -146,16 +166,27 @@ __global__ __launch_bounds__(256) void conv3x3_rows_kernel(
 #pragma unroll
       for (int i = 0; i < PBW; ++i) dst[i] = load16(hb + abase[i] + toff);
     };
-    Frag16 a[2][PBW];
+    Frag16 a[2][PBW], bw[2];
+    // filter fragment of (chunk ch, tap t) from LDS: filter r, channels ch*KC + 4q ..
+    auto load_w = [&](int j) { return load16(wsm + r * WST + (j % 9) * NCH * KC + (j / 9) * KC + q * KPL); };
     load_a(a[0], 0);
+    if constexpr (WLDS) bw[0] = load_w(0);
 #pragma unroll
     for (int j = 0; j < NCH * 9; ++j) {
-      if (j + 1 < NCH * 9) load_a(a[(j + 1) & 1], j + 1);
+      if (j + 1 < NCH * 9) {
+        load_a(a[(j + 1) & 1], j + 1);
+        if constexpr (WLDS) bw[(j + 1) & 1] = load_w(j + 1);
+      }
       // independent accumulators between the dependent steps of one fragment
 #pragma unroll
       for (int s = 0; s < MM::kSteps; ++s)
 #pragma unroll
-        for (int i = 0; i < PBW; ++i) MM::step(acc[i], a[j & 1][i], b[j / 9][j % 9], s);
+        for (int i = 0; i < PBW; ++i) {
+          if constexpr (WLDS)
+            MM::step(acc[i], a[j & 1][i], bw[j & 1], s);
+          else
+            MM::step(acc[i], a[j & 1][i], b[j / 9][j % 9], s);
+        }
       __builtin_amdgcn_sched_barrier(0);
     }
     if (more) {
@@ -984,9 +1015,9 @@ hipError_t launch_x6(const ConvArgs &a, hipStream_t s) {
   return hipGetLastError();
 }
 
-template <class MM, typename T, int TR, int WF, int WMAX, int NCH, int NBUF>
+template <class MM, typename T, int TR, int WF, int WMAX, int NCH, int NBUF, int WFIX>
 hipError_t launch_rows(const ConvArgs &a, hipStream_t s) {
-  if (a.W > WMAX || a.C % (MM::kPerFrag * NCH) != 0 ||
+  if (a.W > WMAX || (WFIX > 0 && a.W != WFIX) || a.C % (MM::kPerFrag * NCH) != 0 ||
       (NBUF == 1 && a.C != MM::kPerFrag * NCH))
     return hipErrorInvalidValue;
   const int tiles_h = (a.H + TR - 1) / TR;
@@ -997,23 +1028,31 @@ hipError_t launch_rows(const ConvArgs &a, hipStream_t s) {
     const int nstages = a.C / (MM::kPerFrag * NCH);
     const double es = sizeof(T);
     npu_launch_plan p = make_plan("conv3x3_rows", grid.x * grid.y,
-                                  wg_per_cu(conv3x3_rows_kernel<MM, T, TR, WF, WMAX, NCH, NBUF>),
+                                  wg_per_cu(conv3x3_rows_kernel<MM, T, TR, WF, WMAX, NCH, NBUF, WFIX>),
                                   grid.x * grid.y, 8 * sizeof(T));
     p.load_phases = 1;  // later stages are fetched while the previous one computes
     p.tile_macs = 4.0 * PBW * 256 * 9 * a.C;
-    // Vector instructions per wave, from the compiled loops: the first
-    // stages' halo and filter staging (260 f32, 400 bf16: twice the 16-byte
-    // runs), 41 per stage, the epilogue (bias, activation, conversion and
-    // the stores of the tile's pixel blocks) 137.
-    p.tile_valu = 4.0 * ((sizeof(T) == 4 ? 260.0 : 400.0) + 41.0 * nstages + 137.0);
-    p.tile_lds_bytes = (TR + 2.0) * (a.W + 2) * REC * nstages + 4.0 * PBW * 9 * NCH * 1024 * nstages;
-    p.tile_load_bytes = (TR + 2.0) * (a.W + 2) * a.C * es + 4.0 * 16 * 9 * a.C * es;
+    // Vector instructions per wave, from the compiled loops.  With the row
+    // width compiled in (WFIX, 56), a one-row, single-stage kernel runs
+    // straight-line code: 384 with the filters staged in LDS (f32, 64
+    // channels: the halo's addresses and commit, the staging, the
+    // epilogue), 235 with them in registers (bf16 64 or f32 32 channels).
+    // Otherwise: the first stages' halo and filter staging (260 f32, 400
+    // bf16: twice the 16-byte runs), 41 per stage, the epilogue (bias,
+    // activation, conversion and the stores of the tile's pixel blocks) 137.
+    constexpr bool WLDS = NBUF == 1 && WF == 1 && sizeof(T) == 4 && NCH == 4;
+    p.tile_valu = 4.0 * (WFIX > 0 && NBUF == 1 && TR == 1
+                             ? (WLDS ? 384.0 : 235.0)
+                             : (sizeof(T) == 4 ? 260.0 : 400.0) + 41.0 * nstages + 137.0);
+    p.tile_lds_bytes = (TR + 2.0) * (a.W + 2) * REC * nstages + 4.0 * PBW * 9 * NCH * 1024 * nstages +
+                       (WLDS ? 2.0 * 16 * 9 * a.C * es : 0.0);  // filters staged and read
+    p.tile_load_bytes = (TR + 2.0) * (a.W + 2) * a.C * es + (WLDS ? 1.0 : 4.0) * 16 * 9 * a.C * es;
     p.tile_store_bytes = (double)TR * a.W * 16 * WF * es;
     p.hbm_bytes = es * ((double)a.N * a.H * a.W * a.C + 9.0 * a.F * a.C + (double)a.N * a.H * a.W * a.F) +
                   (a.bias ? 4.0 * a.F : 0.0);
     plans_add(p);
   }
-  hipLaunchKernelGGL((conv3x3_rows_kernel<MM, T, TR, WF, WMAX, NCH, NBUF>), grid, dim3(256), 0, s,
+  hipLaunchKernelGGL((conv3x3_rows_kernel<MM, T, TR, WF, WMAX, NCH, NBUF, WFIX>), grid, dim3(256), 0, s,
                      static_cast<const T *>(a.x), static_cast<const T *>(a.w), a.bias,
                      static_cast<T *>(a.out), a.H, a.W, a.C, a.F, a.act);
   return hipGetLastError();
@@ -1053,8 +1092,10 @@ hipError_t launch_w(const ConvArgs &a, hipStream_t s) {
     }
   }
   if (a.C == 2 * MM::kPerFrag)
-    return big ? launch_rows<MM, T, 2, 4, WMAX, 2, 1>(a, s) : launch_rows<MM, T, 1, 1, WMAX, 2, 1>(a, s);
-  return big ? launch_rows<MM, T, 2, 4, WMAX, 1, 2>(a, s) : launch_rows<MM, T, 1, 1, WMAX, 1, 2>(a, s);
+    return big ? launch_rows<MM, T, 2, 4, WMAX, 2, 1, WFIX>(a, s) : launch_rows<MM, T, 1, 1, WMAX, 2, 1, WFIX>(a, s);
+  if constexpr (sizeof(T) == 4)
+    if (!big && a.C == 4 * MM::kPerFrag) return launch_rows<MM, T, 1, 1, WMAX, 4, 1, WFIX>(a, s);
+  return big ? launch_rows<MM, T, 2, 4, WMAX, 1, 2, WFIX>(a, s) : launch_rows<MM, T, 1, 1, WMAX, 1, 2, WFIX>(a, s);
 }
 
 template <class MM, typename T>
