@@ -136,11 +136,20 @@ __global__ __launch_bounds__(256) void conv3x3_rows_kernel(
 
   fetch(0);
   if constexpr (WLDS) {
+    // every load issued before the first LDS write (a loop that writes each
+    // load's value before issuing the next would wait for every one in turn)
+    constexpr int RPF = 9 * NCH * KC / 4, NWR = 16 * RPF, NWL = (NWR + 255) / 256;
     const int f0 = blockIdx.y * 16;
-    for (int idx = tid; idx < 16 * 9 * C / 4; idx += 256) {
-      const int fl = idx / (9 * C / 4), e = idx - fl * (9 * C / 4);
-      *reinterpret_cast<u32x4 *>(wsm + fl * WST + 4 * e) =
-          *reinterpret_cast<const u32x4 *>(w + (size_t)min(f0 + fl, F - 1) * 9 * C + 4 * e);
+    u32x4 wl[NWL];
+#pragma unroll
+    for (int i = 0; i < NWL; ++i) {
+      const int idx = min(tid + 256 * i, NWR - 1), fl = idx / RPF, e = idx - fl * RPF;
+      wl[i] = *reinterpret_cast<const u32x4 *>(w + (size_t)min(f0 + fl, F - 1) * 9 * C + 4 * e);
+    }
+#pragma unroll
+    for (int i = 0; i < NWL; ++i) {
+      const int idx = tid + 256 * i, fl = idx / RPF, e = idx - fl * RPF;
+      if (idx < NWR) *reinterpret_cast<u32x4 *>(wsm + fl * WST + 4 * e) = wl[i];
     }
   } else {
     fetch_b(b, 0);
@@ -1034,15 +1043,16 @@ hipError_t launch_rows(const ConvArgs &a, hipStream_t s) {
     p.tile_macs = 4.0 * PBW * 256 * 9 * a.C;
     // Vector instructions per wave, from the compiled loops.  With the row
     // width compiled in (WFIX, 56), a one-row, single-stage kernel runs
-    // straight-line code: 384 with the filters staged in LDS (f32, 64
-    // channels: the halo's addresses and commit, the staging, the
-    // epilogue), 235 with them in registers (bf16 64 or f32 32 channels).
+    // straight-line code: 478 with the filters staged in LDS (f32, 64
+    // channels: the halo's addresses and commit, the staging's nine loads
+    // and writes, the epilogue), 235 with them in registers (bf16 64 or f32
+    // 32 channels).
     // Otherwise: the first stages' halo and filter staging (260 f32, 400
     // bf16: twice the 16-byte runs), 41 per stage, the epilogue (bias,
     // activation, conversion and the stores of the tile's pixel blocks) 137.
     constexpr bool WLDS = NBUF == 1 && WF == 1 && sizeof(T) == 4 && NCH == 4;
     p.tile_valu = 4.0 * (WFIX > 0 && NBUF == 1 && TR == 1
-                             ? (WLDS ? 384.0 : 235.0)
+                             ? (WLDS ? 478.0 : 235.0)
                              : (sizeof(T) == 4 ? 260.0 : 400.0) + 41.0 * nstages + 137.0);
     p.tile_lds_bytes = (TR + 2.0) * (a.W + 2) * REC * nstages + 4.0 * PBW * 9 * NCH * 1024 * nstages +
                        (WLDS ? 2.0 * 16 * 9 * a.C * es : 0.0);  // filters staged and read
