@@ -87,7 +87,8 @@ def run(func: mlir.MFunc, target: host.HWTarget = None, cores: int = None,
             if d is not None:
                 sp.append({"op": ops[i].results[0] if ops[i].results else ops[i].name,
                            "iter_dim": d.iter_dim, "tile": d.tile_size, "full_iters": d.full_iters,
-                           "peel": d.peel_size, "cores": cores})
+                           "peel": d.peel_size, "cores": cores,
+                           "candidates": [list(c) for c in d.candidates]})
         f["spatial"] = sp
         # temporal tiling: the spec-driven tile of each matrix op
         tp, trips = [], 1
