@@ -114,6 +114,12 @@ int32_t npu_cm_conv2d_tile(const npu_hw_target *t, int64_t tn, int64_t tco, int6
                            int64_t extra_output_shaped, npu_schedule_cost *out);
 /* Writes up to cap candidates, returns how many there are. */
 int32_t npu_cm_tile_candidates(int64_t dim, int64_t *out, int32_t cap);
+/* The linalg.conv_2d_nchw_fchw tiling spec is built from the first conv it is
+ * asked about and then serves every conv (its kernel size sets the halo of the
+ * row and column splits), as getTilingSpec's function-local static does for
+ * one npu-opt process (OperatorTilingSpec.cpp:531-537).  This forgets it, so
+ * the next module's decisions are those of a fresh npu-opt run.  Returns 0. */
+int32_t npu_spec_reset(void);
 
 /* ---- level 2 (CostModel.cpp:346-823) ---- */
 int32_t npu_cm_best_tile_config(const npu_graph *g, const npu_hw_target *t, int32_t op,

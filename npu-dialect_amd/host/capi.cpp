@@ -323,6 +323,11 @@ int32_t npu_cm_conv2d_tile(const npu_hw_target *t, int64_t tn, int64_t tco, int6
   return 0;
 }
 
+int32_t npu_spec_reset(void) {
+  npu::reset_conv_spec();
+  return 0;
+}
+
 int32_t npu_cm_tile_candidates(int64_t dim, int64_t *out, int32_t cap) {
   const auto c = npu::CostModel::tile_candidates(dim);
   for (int32_t i = 0; i < cap && i < (int32_t)c.size(); ++i) out[i] = c[i];

@@ -4,6 +4,7 @@
 #include "tiling_spec.hpp"
 
 #include <map>
+#include <memory>
 #include <mutex>
 
 namespace npu {
@@ -162,6 +163,19 @@ bool is_reshape_boundary(const ir::Graph &g, int32_t op) {
   return k == OpKind::CollapseShape || k == OpKind::ExpandShape;
 }
 
+namespace {
+// The conv spec in force and every one built so far (a spec handed out stays
+// valid after a reset).
+std::mutex conv_mu;
+std::vector<std::unique_ptr<OperatorTilingSpec>> conv_specs;
+const OperatorTilingSpec *conv_current = nullptr;
+}  // namespace
+
+void reset_conv_spec() {
+  std::lock_guard<std::mutex> lock(conv_mu);
+  conv_current = nullptr;
+}
+
 const OperatorTilingSpec *get_tiling_spec(const ir::Graph &g, int32_t opi) {
   static const OperatorTilingSpec mm = matmul_tiling_spec();
   static const OperatorTilingSpec bmm = batch_matmul_tiling_spec();
@@ -174,11 +188,17 @@ const OperatorTilingSpec *get_tiling_spec(const ir::Graph &g, int32_t opi) {
     case OpKind::BatchMatmul:
       return &bmm;
     case OpKind::Conv2dNchwFchw: {
-      // Built once from the first conv seen, strides taken as 1 (as the
-      // reference's function-local static does).
+      // Built from the first conv asked about, strides taken as 1, and kept
+      // for every later conv until reset_conv_spec (the reference's
+      // function-local static: one spec per npu-opt process).
       const auto &ft = g.type(op.operands[1]).shape;
-      static const OperatorTilingSpec conv = conv2d_nchw_tiling_spec(ft[2], ft[3], 1, 1);
-      return &conv;
+      std::lock_guard<std::mutex> lock(conv_mu);
+      if (!conv_current) {
+        conv_specs.push_back(std::make_unique<OperatorTilingSpec>(
+            conv2d_nchw_tiling_spec(ft[2], ft[3], 1, 1)));
+        conv_current = conv_specs.back().get();
+      }
+      return conv_current;
     }
     default:
       break;

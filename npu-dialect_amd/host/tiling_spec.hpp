@@ -56,6 +56,9 @@ OperatorTilingSpec transpose_tiling_spec(const std::vector<int64_t> &perm, unsig
 // behaviour: the NCHW conv spec is built once per process from the first
 // conv it sees (a function-local static, :536).
 const OperatorTilingSpec *get_tiling_spec(const ir::Graph &g, int32_t op);
+// Forgets the conv spec in force: the next conv asked about builds the next
+// one, as the first conv of a fresh npu-opt process does.
+void reset_conv_spec();
 
 bool is_reshape_boundary(const ir::Graph &g, int32_t op);
 

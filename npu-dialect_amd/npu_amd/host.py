@@ -113,6 +113,7 @@ SIGNATURES = {
     "npu_cm_matmul_tile": (_I32, [_PT] + [_I64] * 8 + [C.POINTER(ScheduleCost)]),
     "npu_cm_conv2d_tile": (_I32, [_PT] + [_I64] * 15 + [C.POINTER(ScheduleCost)]),
     "npu_cm_tile_candidates": (_I32, [_I64, _PI64, _I32]),
+    "npu_spec_reset": (_I32, []),
     "npu_cm_best_tile_config": (_I32, [_P, _PT, _I32, C.POINTER(ScheduleCost)]),
     "npu_cm_fusion_profitable": (_I32, [_P, _PT, _I32, _I32, _PI64]),
     "npu_cm_spatial_split": (_I32, [_P, _PT, _I32, _I32, _I64, C.POINTER(ScheduleCost)]),
@@ -316,6 +317,13 @@ def tile_candidates(dim):
     buf = (C.c_int64 * 64)()
     n = lib().npu_cm_tile_candidates(dim, buf, 64)
     return [buf[i] for i in range(min(n, 64))]
+
+
+def spec_reset():
+    """Forgets the conv tiling spec in force (built from the first conv asked
+    about, as getTilingSpec's function-local static is once per npu-opt
+    process): the next conv builds the next one."""
+    lib().npu_spec_reset()
 
 
 def matmul_tile(target, tm, tn, tk, M, N, K, dtype_bytes, extra=0):

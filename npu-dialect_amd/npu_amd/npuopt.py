@@ -510,6 +510,7 @@ def run_passes(text: str, passes: dict):
     """Runs `passes` ({name: options}, pipeline order) on the module text.
     Returns (module text, COST_JSON lines, remarks)."""
     funcs = mlir.parse_functions(text)
+    host.spec_reset()  # one npu-opt process per module
     tparams = mlir.parse_target(text)
     t = host.target_from_params(tparams) if tparams else host.default_target()
     on = lambda p: p in passes

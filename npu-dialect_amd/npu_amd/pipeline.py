@@ -48,11 +48,16 @@ def _tiles(sizes):
 
 
 def run(func: mlir.MFunc, target: host.HWTarget = None, cores: int = None,
-        sram_size: int = None) -> dict:
+        sram_size: int = None, fresh: bool = True) -> dict:
     """Replays npu-pipeline's decisions on `func`; see the module docstring.
     The target is `target` when given, else the module's #npu.target (as
     CostModelAnalysis reads it, lib/Analysis/CostModel.cpp:985-1000), else
-    the reference's default NPU."""
+    the reference's default NPU.  `fresh`: decide as a new npu-opt process
+    would (the conv tiling spec is rebuilt from this function's first conv);
+    False keeps the spec of the functions run before (later functions of one
+    module)."""
+    if fresh:
+        host.spec_reset()
     if target is not None:
         t = target
     elif func.target:
@@ -120,5 +125,5 @@ def run(func: mlir.MFunc, target: host.HWTarget = None, cores: int = None,
 
 
 def run_file(path: str, target: host.HWTarget = None, **kw) -> list:
-    """`run` on every function of an .mlir file."""
-    return [run(f, target, **kw) for f in mlir.parse_file(path)]
+    """`run` on every function of an .mlir file, as one npu-opt process."""
+    return [run(f, target, fresh=i == 0, **kw) for i, f in enumerate(mlir.parse_file(path))]

@@ -177,6 +177,7 @@ def test_spatial_split_detailed_shared_and_halo(npu):
     g = load("lit/spatial_tiling_conv2d.mlir")
     cm = host.CostModel(g, npu)
     conv = g.find("linalg.conv_2d_nchw_fchw")
+    host.spec_reset()  # this 3x3 conv is the first asked about: its spec is in force
     co = cm.spatial_split_detailed(conv, 1, 6)   # split Co: input shared, filter split
     assert co.shared_data_bytes == 1 * 64 * 58 * 58 * 2
     assert co.split_data_bytes == 64 * 64 * 9 * 2 * 11 // 64

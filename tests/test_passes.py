@@ -43,6 +43,7 @@ def test_spatial_matmul_kat(npu):
 def test_spatial_conv_splits_output_channels(npu):
     g = load("lit/spatial_tiling_conv2d.mlir")
     conv = g.find("linalg.conv_2d_nchw_fchw")
+    host.spec_reset()  # as npu-opt on this file: its 3x3 conv sets the conv spec
     d = host.spatial(g, npu, conv, 6)
     assert d.iter_dim == 1 and d.tile_size == 11  # Co = 64 over 6 cores
     # the Co split keeps the whole padded input (1x64x58x58) on every core
@@ -75,6 +76,7 @@ def test_temporal_matches_best_tile_kat(npu):
     ts, cost = host.temporal(g, npu, g.find("linalg.matmul"))
     assert ts == [128, 256, 16] and cost.total_cycles == 14_464
     g2 = load("conv2d_relu.mlir")
+    host.spec_reset()
     ts2, cost2 = host.temporal(g2, npu, g2.find("linalg.conv_2d_nchw_fchw"))
     assert ts2[:4] == [1, 64, 28, 28] and cost2.total_cycles == 37_264
     # the relu over 1x64x56x56 f16 has no config within 2 MiB: left untiled
