@@ -39,11 +39,11 @@
 // transposing LDS read of the row-major V block.  P is rounded to bf16 for
 // its MFMA (the oracle keeps it in f32).  All heads of one XCD's workgroups
 // are the same, so the L2 of an XCD holds one head's K and V.
-#include <algorithm>
 #include <cmath>
 
 #include "kernels.hpp"
 #include "npu_device.hpp"
+#include "persistent.hpp"
 #include "plans.hpp"
 
 namespace npu {
@@ -80,50 +80,21 @@ __device__ __forceinline__ uint2 pack4_bf16(float a, float b, float c, float d) 
 __device__ __forceinline__ float bf_lo(uint32_t u) { return __uint_as_float(u << 16); }
 __device__ __forceinline__ float bf_hi(uint32_t u) { return __uint_as_float(u & 0xffff0000u); }
 
-// Tile of workgroup `bid` among tiles_m x tiles_n tiles; workgroup bid runs
-// on XCD bid % 8, each with its own L2.  With xm > 0 the tile grid is cut
-// into an xm x (8 / xm) grid of blocks, block x on XCD x (tiles N-major
-// within it), so an XCD reads only its block's rows of A and columns of B;
-// else the N-major tile list is cut into 8 contiguous ranges.  Returns
-// false for the padding workgroups of a grid rounded up to a multiple of 8.
+// Tile of this workgroup among tiles_m x tiles_n tiles: with xm > 0 the 2-D
+// XCD blocks of xcd_block_tile; else the N-major tile list cut into 8
+// contiguous ranges, range x on XCD x (blockIdx.x % 8).  Returns false for
+// the padding workgroups of a grid rounded up to a multiple of 8.
 __device__ __forceinline__ bool xcd_tile(int tiles_m, int tiles_n, int xm, int &tm, int &tn) {
-  const int x = blockIdx.x % 8, l = blockIdx.x / 8;
   if (xm > 0) {
-    const int xn = 8 / xm, rm = tiles_m / xm, rn = tiles_n / xn;
-    tm = (x / xn) * rm + l % rm;
-    tn = (x % xn) * rn + l / rm;
+    xcd_block_tile(tiles_m, tiles_n, xm, tm, tn);
     return true;
   }
   const int G = tiles_m * tiles_n, per = (G + 7) / 8;
-  const int t = x * per + l;
+  const int t = (blockIdx.x % 8) * per + blockIdx.x / 8;
   if (t >= G) return false;
   tn = t / tiles_m;
   tm = t % tiles_m;
   return true;
-}
-
-// The XCD block grid for xcd_tile: the xm (1, 2, 4 or 8, dividing tiles_m,
-// with 8 / xm dividing tiles_n) whose blocks read the fewest A rows plus B
-// columns per XCD (BM rows per tile row, bn_cols per tile column), or 0 --
-// the contiguous ranges -- when none divides or none reads less than the
-// busiest XCD's range does.
-inline int xcd_blocks(int tiles_m, int tiles_n, int bm, int bn_cols) {
-  const int G = tiles_m * tiles_n, per = (G + 7) / 8;
-  long cost = 0;
-  for (int x = 0; x < 8; ++x) {
-    const int t0 = x * per, t1 = std::min(G, t0 + per);
-    if (t0 >= t1) continue;
-    const int rows = std::min(t1 - t0, tiles_m), cols = (t1 - 1) / tiles_m - t0 / tiles_m + 1;
-    cost = std::max(cost, (long)rows * bm + (long)cols * bn_cols);
-  }
-  int best = 0;
-  for (int xm = 1; xm <= 8; xm *= 2) {
-    const int xn = 8 / xm;
-    if (tiles_m % xm || tiles_n % xn) continue;
-    const long c = (long)(tiles_m / xm) * bm + (long)(tiles_n / xn) * bn_cols;
-    if (c < cost) best = xm, cost = c;
-  }
-  return best;
 }
 
 constexpr int APAD = 16;  // A row padding (elements): row stride = 32 mod 64 bytes
@@ -726,7 +697,7 @@ hipError_t run_gemm(const char *name, const LlamaGemmArgs &a, hipStream_t s) {
   });
   if (!ok) return hipErrorInvalidValue;
   plan_gemm<Sh>(name, kern, a, G, PRO, EPI);
-  const int xm = xcd_blocks(tiles_m, tiles_n, BM, BN * Sh::NB);
+  const int xm = xcd_block_grid(tiles_m, tiles_n, BM, BN * Sh::NB, true);
   hipLaunchKernelGGL(kern, dim3(grid), dim3(GT), lds, s, a, tiles_m, tiles_n, xm);
   return hipGetLastError();
 }

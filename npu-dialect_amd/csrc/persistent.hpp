@@ -48,6 +48,47 @@ __device__ __forceinline__ RowRange row_range(int nrows) {
   return r;
 }
 
+// 2-D XCD blocks for a launch of one workgroup per output tile: the
+// tiles_m x tiles_n tile grid cut into an xm x (8 / xm) grid of blocks,
+// block x on XCD x (= blockIdx.x % 8), tiles taken N-major within a block,
+// so an XCD reads only its block's rows of A and columns of B.  The grid is
+// exactly tiles_m * tiles_n workgroups (xcd_block_grid picks xm so that the
+// blocks divide the tile grid).
+__device__ __forceinline__ void xcd_block_tile(int tiles_m, int tiles_n, int xm, int &tm, int &tn) {
+  const int x = blockIdx.x % kXcds, l = blockIdx.x / kXcds;
+  const int xn = kXcds / xm, rm = tiles_m / xm, rn = tiles_n / xn;
+  tm = (x / xn) * rm + l % rm;
+  tn = (x % xn) * rn + l / rm;
+}
+
+// The xm (1, 2, 4 or 8, dividing tiles_m, with 8 / xm dividing tiles_n) for
+// xcd_block_tile whose blocks read the fewest A rows plus B columns per XCD
+// (bm rows per tile row, bn_cols per tile column), or 0 when none divides or
+// none reads less than the busiest XCD does when the tile list -- N-major
+// (tile t is column t / tiles_m) or M-major (row t / tiles_n) -- is cut into
+// 8 contiguous ranges.
+inline int xcd_block_grid(int tiles_m, int tiles_n, int bm, int bn_cols, bool n_major) {
+  const int G = tiles_m * tiles_n, per = (G + kXcds - 1) / kXcds;
+  long cost = 0;
+  for (int x = 0; x < kXcds; ++x) {
+    const int t0 = x * per, t1 = t0 + per < G ? t0 + per : G;
+    if (t0 >= t1) continue;
+    const int minor = n_major ? tiles_m : tiles_n;
+    const int spans = (t1 - 1) / minor - t0 / minor + 1, within = t1 - t0 < minor ? t1 - t0 : minor;
+    const long c = n_major ? (long)within * bm + (long)spans * bn_cols
+                           : (long)spans * bm + (long)within * bn_cols;
+    if (c > cost) cost = c;
+  }
+  int best = 0;
+  for (int xm = 1; xm <= kXcds; xm *= 2) {
+    const int xn = kXcds / xm;
+    if (tiles_m % xm || tiles_n % xn) continue;
+    const long c = (long)(tiles_m / xm) * bm + (long)(tiles_n / xn) * bn_cols;
+    if (c < cost) best = xm, cost = c;
+  }
+  return best;
+}
+
 // Index arithmetic that does not depend on the tile would be hoisted out of
 // a tile loop by the compiler and pinned in registers for its whole length;
 // passing a value through an empty asm makes it be recomputed per tile
