@@ -22,7 +22,10 @@
  *    run concurrently; the library keeps no per-call device state.
  *  - Errors are returned as npu_status; nothing throws across the ABI.  Shape,
  *    dtype and layout mismatches are rejected before any launch, and
- *    npu_last_error() (thread-local) says why.
+ *    npu_last_error() (thread-local) says why.  Every dimension must be
+ *    positive: a memref with a zero-sized dimension is rejected with
+ *    NPU_ERR_INVALID_ARG (the reference's groups have static, nonzero
+ *    shapes; nothing is launched for such a call).
  *  - No entry point allocates device memory.
  */
 #ifndef NPU_AMD_H

@@ -212,3 +212,16 @@ def test_group_launch_reads_strided_memref_layouts():
     st = lib.npu_group_launch(b"fused_fill_linalg_conv_2d_nhwc_fhwc_generic_0", C.byref(at),
                               ia, 6, oa, 1, None)
     assert st == 1 and "accumulator" in _err()
+
+
+def test_zero_sized_dimensions_are_rejected_before_launch():
+    """A memref with a zero-sized dimension is refused with INVALID_ARG (the
+    reference's groups have static, nonzero shapes), whichever operand it
+    is, with no launch."""
+    lib = npu_amd.lib()
+    call = lambda *a: lib.fused_matmul_bias_act(*[C.byref(x) for x in a[:4]], a[4], None)
+    A, B, b, o = _mr([8, 16]), _mr([16, 4]), _mr([4]), _mr([8, 4])
+    for args in ((_mr([0, 16]), B, b, _mr([0, 4])), (A, _mr([16, 0]), _mr([0]), _mr([8, 0])),
+                 (_mr([8, 0]), _mr([0, 4]), b, o)):
+        assert call(*args, 1) == 1
+        assert "must be positive" in _err()
