@@ -56,14 +56,17 @@ __global__ __launch_bounds__(256) void conv3x3_rows_kernel(
   constexpr int SEGS = (HR * (WMAX + 2) * SEGP + 255) / 256;
   static_assert(KC * sizeof(T) == 64, "a chunk is 64 bytes per pixel");
   static_assert(NBUF == 1 || NBUF == 2, "single or double buffered");
-  // One f32 stage of 64 channels: the workgroup's 16 filters (all four waves
-  // use the same ones) are loaded once, coalesced, into LDS rather than by
-  // every wave into registers; row stride 9 * 64 + 8 floats (32 mod 64
-  // bytes) keeps the 16 filters' fragment reads conflict-free.
-  constexpr bool WLDS = NBUF == 1 && WF == 1 && sizeof(T) == 4 && NCH == 4;
-  constexpr int WST = 9 * NCH * KC + 8;
+  // One stage (all of C): the workgroup's 16 filters (all four waves use the
+  // same ones) are loaded once, coalesced, into LDS rather than by every
+  // wave into registers as 16-byte pieces of 16 filter rows (on the critical
+  // path of a one-tile workgroup: bf16 56x56x64 5.1 -> 3.7 us); a row
+  // stride of 9 C channels plus 32 bytes (32 mod 64 bytes) keeps the 16
+  // filters' fragment reads conflict-free.
+  constexpr bool WLDS = NBUF == 1 && WF == 1;
+  constexpr int WST = 9 * NCH * KC + 32 / sizeof(T);
+  constexpr int EPR = 16 / sizeof(T);  // elements per 16-byte run
   __shared__ __attribute__((aligned(16))) T halo[NBUF][HR * (WMAX + 2) * REC];
-  __shared__ __attribute__((aligned(16))) float wsm[WLDS ? 16 * WST : 4];
+  __shared__ __attribute__((aligned(16))) T wsm[WLDS ? 16 * WST : 4];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int r = lane & 15, q = lane >> 4;
@@ -138,18 +141,18 @@ __global__ __launch_bounds__(256) void conv3x3_rows_kernel(
   if constexpr (WLDS) {
     // every load issued before the first LDS write (a loop that writes each
     // load's value before issuing the next would wait for every one in turn)
-    constexpr int RPF = 9 * NCH * KC / 4, NWR = 16 * RPF, NWL = (NWR + 255) / 256;
+    constexpr int RPF = 9 * NCH * KC / EPR, NWR = 16 * RPF, NWL = (NWR + 255) / 256;
     const int f0 = blockIdx.y * 16;
     u32x4 wl[NWL];
 #pragma unroll
     for (int i = 0; i < NWL; ++i) {
       const int idx = min(tid + 256 * i, NWR - 1), fl = idx / RPF, e = idx - fl * RPF;
-      wl[i] = *reinterpret_cast<const u32x4 *>(w + (size_t)min(f0 + fl, F - 1) * 9 * C + 4 * e);
+      wl[i] = *reinterpret_cast<const u32x4 *>(w + (size_t)min(f0 + fl, F - 1) * 9 * C + EPR * e);
     }
 #pragma unroll
     for (int i = 0; i < NWL; ++i) {
       const int idx = tid + 256 * i, fl = idx / RPF, e = idx - fl * RPF;
-      if (idx < NWR) *reinterpret_cast<u32x4 *>(wsm + fl * WST + 4 * e) = wl[i];
+      if (idx < NWR) *reinterpret_cast<u32x4 *>(wsm + fl * WST + EPR * e) = wl[i];
     }
   } else {
     fetch_b(b, 0);
@@ -1043,16 +1046,16 @@ hipError_t launch_rows(const ConvArgs &a, hipStream_t s) {
     p.tile_macs = 4.0 * PBW * 256 * 9 * a.C;
     // Vector instructions per wave, from the compiled loops.  With the row
     // width compiled in (WFIX, 56), a one-row, single-stage kernel runs
-    // straight-line code: 478 with the filters staged in LDS (f32, 64
-    // channels: the halo's addresses and commit, the staging's nine loads
-    // and writes, the epilogue), 235 with them in registers (bf16 64 or f32
-    // 32 channels).
+    // straight-line code, the filters staged in LDS (the halo's addresses
+    // and commit, the staging's loads and writes, the epilogue): 478 for
+    // f32 at 64 channels, 300 for 2304-byte filter rows (f32 32 channels,
+    // bf16 64).
     // Otherwise: the first stages' halo and filter staging (260 f32, 400
     // bf16: twice the 16-byte runs), 41 per stage, the epilogue (bias,
     // activation, conversion and the stores of the tile's pixel blocks) 137.
-    constexpr bool WLDS = NBUF == 1 && WF == 1 && sizeof(T) == 4 && NCH == 4;
+    constexpr bool WLDS = NBUF == 1 && WF == 1;
     p.tile_valu = 4.0 * (WFIX > 0 && NBUF == 1 && TR == 1
-                             ? (WLDS ? 478.0 : 235.0)
+                             ? (WLDS ? (sizeof(T) == 4 && NCH == 4 ? 478.0 : 300.0) : 235.0)
                              : (sizeof(T) == 4 ? 260.0 : 400.0) + 41.0 * nstages + 137.0);
     p.tile_lds_bytes = (TR + 2.0) * (a.W + 2) * REC * nstages + 4.0 * PBW * 9 * NCH * 1024 * nstages +
                        (WLDS ? 2.0 * 16 * 9 * a.C * es : 0.0);  // filters staged and read
